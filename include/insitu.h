@@ -1,0 +1,176 @@
+/* insitu.h -- C ABI of the MI355X compressed-KV decode-attention block.
+ *
+ * The boundary is the reference's seam (kernel.py:253-258 in, :348-353 out):
+ * post-RoPE q/k/v arrive as Q8.16 integers, the block rotates them, appends
+ * the compressed k/v row to an HBM-resident cache, scores the query heads on
+ * the codes, runs the fixed-point softmax and returns Q16 in the rotated
+ * basis, head-major (merge_heads order, ops/project.py:67-74).
+ *
+ * Conventions
+ *   - Every call returns an int status; 0 is OK. The status set follows
+ *     host/attn_proto.py:41 (OK, EBADLEN, ERANGE, EDMA -> EHIP) plus the
+ *     reference's raise sites (capacity, bad format).
+ *   - Pointers named *_dev are device pointers (hipMalloc / torch cuda
+ *     tensors); *_host are host pointers. Device work is ordered on the
+ *     context's stream; a call does not synchronise unless it says so.
+ *   - A handle is not thread-safe. append must precede attend on the same
+ *     stream: the current token attends to itself (hw/vectors.py:22-30).
+ *   - Lengths and the plane layout are owned by the cache handle, as the host
+ *     owns cache_base/head_stride/plane_span in host/attn_proto.h:16-24.
+ */
+#ifndef INSITU_H
+#define INSITU_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    INSITU_OK = 0,
+    INSITU_EBADLEN = 1,    /* shape/length mismatch (attn_proto.py:41 EBADLEN)         */
+    INSITU_ERANGE = 2,     /* value outside the format (attn_proto.py:41 ERANGE)       */
+    INSITU_EHIP = 3,       /* HIP runtime failure (stands where EDMA stood)            */
+    INSITU_EINVAL = 4,     /* unsupported format / bad argument (config.py:45-61,178-207) */
+    INSITU_ECAPACITY = 5,  /* append past capacity (cache/base.py:67-73)               */
+    INSITU_ENOMEM = 6,
+    INSITU_EFAULT = 7      /* a kernel reported an internal error flag                 */
+};
+
+enum {
+    INSITU_SEQUENTIAL = 0, /* CompressedAttention.attend_online, bit-exact (attention.py:451-513) */
+    INSITU_TWO_PASS = 1,   /* CompressedAttention.attend_two_pass, bit-exact (attention.py:429-449) */
+    INSITU_SPLIT = 2,      /* context-split flash-decoding; <= 2 Q16 LSB of SEQUENTIAL */
+    INSITU_SERIAL = 3      /* SEQUENTIAL computed one token at a time per head (slow; reference path) */
+};
+
+typedef struct insitu_ctx insitu_ctx;
+typedef struct insitu_cache insitu_cache;
+
+/* The fixed-point contract (config.py:132-254 QuantConfig + FixedFormat). */
+typedef struct {
+    int32_t head_dim;       /* 64 or 128                                   */
+    int32_t key_bits;       /* 1..8 (config.py:179-181)                    */
+    int32_t value_bits;     /* 1..8                                        */
+    int32_t norm_bits;      /* 16                                          */
+    int32_t norm_frac;      /* 9                                           */
+    int32_t qk_frac;        /* 16                                          */
+    int32_t qk_width;       /* 24                                          */
+    int32_t centroid_frac;  /* 15                                          */
+    int32_t acc_frac;       /* 16                                          */
+    int32_t acc_width;      /* 32                                          */
+    int32_t score_width;    /* 48                                          */
+    int32_t prob_frac;      /* 15                                          */
+    int32_t exp_lut_bits;   /* 8                                           */
+    int32_t rot_rounds;     /* 1 (config.py:169); 0 is the identity         */
+    uint64_t rot_signs[8][2]; /* per round, bit i set = negate channel i (tb/vectors/rot_signs.hex) */
+} insitu_format;
+
+/* cache/compressed.py:42-66 + hw/ddr_layout.py:110-124. Codebooks are the
+ * integers Codebook.build produced (ops/codebook.py:67-120), as the RTL
+ * receives them: centroids 2^bits, boundaries 2^bits - 1, Q(centroid_frac). */
+typedef struct {
+    int64_t capacity;       /* tokens per sequence                         */
+    int32_t batch;          /* sequences                                   */
+    int32_t n_kv_heads;
+    int32_t n_q_heads;      /* multiple of n_kv_heads (config.py:49-53)     */
+    int32_t reserved;
+    insitu_format fmt;
+    const int64_t *key_centroids_host;
+    const int64_t *key_bounds_host;
+    const int64_t *value_centroids_host;
+    const int64_t *value_bounds_host;
+} insitu_cache_desc;
+
+/* hw/ddr_layout.py:261-274 describe(), per sequence region. */
+typedef struct {
+    int32_t row_bytes, n_planes;
+    int32_t plane_lo[16], plane_width[16];
+    int64_t plane_span, head_stride, seq_stride, total_bytes;
+    uint64_t device_base;   /* device address of sequence 0, head 0, plane 0 */
+} insitu_layout;
+
+/* AttentionStats (attention.py:257-274), merged over heads and sequences as
+ * AttentionStats.merge does, plus device flags. */
+typedef struct {
+    int64_t n_tokens, rescale_events, score_overflows, acc_overflows;
+    int64_t max_abs_score, max_abs_acc;
+    int64_t range_errors;      /* q_rot outside the supported +-2^27 range */
+    int64_t serial_fallbacks;  /* heads recomputed on the exact serial path */
+} insitu_stats;
+
+/* --- context ------------------------------------------------------------- */
+/* Binds a device and a stream (NULL = the default stream); holds the exp LUT constants. */
+int insitu_ctx_create(int32_t device, void *hip_stream, insitu_ctx **out);
+int insitu_ctx_destroy(insitu_ctx *ctx);
+int insitu_ctx_sync(insitu_ctx *ctx);
+void *insitu_ctx_stream(insitu_ctx *ctx);
+
+/* --- rotation: Rotation.apply (ops/rotate.py:170-197) -------------------- */
+/* x_dev, y_dev: int32 (n_vec, d). y may alias x. */
+int insitu_rotate(insitu_ctx *ctx, const int32_t *x_dev, int32_t *y_dev, int64_t n_vec,
+                  const insitu_format *fmt);
+
+/* --- encoder: KVQuantizer._norm_wire/_encode_plane (ops/quantize.py:164-196) */
+/* x_dev int32 (n_vec, d) rotated; norm_dev int32 (n_vec); codes_dev uint8 (n_vec, d). */
+int insitu_encode(insitu_ctx *ctx, const int32_t *x_dev, int64_t n_vec, const insitu_format *fmt,
+                  const int64_t *bounds_host, int32_t bits, int32_t *norm_dev, uint8_t *codes_dev);
+
+/* --- qtab: T[h][ch][i] = q_rot[h][ch] * c[i] (hw/vectors.py:485-509) ---------- */
+int insitu_qtab(insitu_ctx *ctx, const int32_t *q_rot_dev, int32_t n_heads, int32_t d,
+                const int64_t *centroids_host, int32_t n_centroids, int64_t *table_dev);
+
+/* --- exp LUT: ExpLut.__call__ (attention.py:153-159) ----------------------- */
+int insitu_exp_lut(insitu_ctx *ctx, const int64_t *delta_dev, int64_t n, int32_t *p_dev);
+
+/* --- finalize: reciprocal + _finalize (attention.py:197-250, 873-880) ----- */
+int insitu_finalize(insitu_ctx *ctx, const int64_t *acc_dev, const int64_t *l_dev, int32_t rows,
+                    int32_t d, int64_t *out_dev, int64_t *recip_dev, int32_t *shift_dev);
+
+/* --- the cache: CompressedCache (cache/compressed.py:42-132) -------------- */
+int insitu_cache_create(insitu_ctx *ctx, const insitu_cache_desc *desc, insitu_cache **out);
+int insitu_cache_destroy(insitu_cache *cache);
+int insitu_cache_reset(insitu_cache *cache);                       /* base.py:64 */
+int insitu_cache_length(const insitu_cache *cache, int32_t seq, int64_t *len);
+int insitu_cache_set_length(insitu_cache *cache, int32_t seq, int64_t len);
+int insitu_cache_layout(const insitu_cache *cache, insitu_layout *out);
+
+/* append_rotated (compressed.py:64-86): encode, pack and write n_tok rows at
+ * each sequence's length. k/v_rot_dev int32 (batch, n_tok, n_kv_heads, d). */
+int insitu_append(insitu_cache *cache, const int32_t *k_rot_dev, const int32_t *v_rot_dev,
+                  int32_t n_tok);
+/* The same for one sequence: k/v_rot_dev int32 (n_tok, n_kv_heads, d). */
+int insitu_append_seq(insitu_cache *cache, int32_t seq, const int32_t *k_rot_dev,
+                      const int32_t *v_rot_dev, int32_t n_tok);
+
+/* attend_online / attend_two_pass over every sequence's cache (kernel.py:337-345,
+ * attention.py:429-513). q_rot_dev int32 (batch, n_q_heads, d) rotated;
+ * out_dev int32 (batch, n_q_heads, d) Q16. stats_host may be NULL (no sync). */
+int insitu_attend(insitu_cache *cache, const int32_t *q_rot_dev, int32_t *out_dev, int32_t mode,
+                  insitu_stats *stats_host);
+
+/* One decode step from the wire (CMD_STEP, host/attn_proto.py:65-72; kernel.py:256-353):
+ * q/k/v_dev int32 Q8.16 (batch, heads, d) -> rotate -> append -> attend -> out_dev. */
+int insitu_step(insitu_cache *cache, const int32_t *q_dev, const int32_t *k_dev,
+                const int32_t *v_dev, int32_t *out_dev, int32_t mode, insitu_stats *stats_host);
+
+/* Byte-exact rows (view_from_buffer, compressed.py:123-129; CMD_LOAD, attn_proto.py:75-78).
+ * rows_host uint8 (n, row_bytes). Synchronous. */
+int insitu_read_rows(insitu_cache *cache, int32_t seq, int32_t head, int64_t t0, int64_t n,
+                     uint8_t *rows_host);
+int insitu_load_rows(insitu_cache *cache, int32_t seq, int32_t head, int64_t t0, int64_t n,
+                     const uint8_t *rows_host);
+
+/* The raw plane image of one sequence (DdrLayout.image / CMD_LOAD, ddr_layout.py:227-248):
+ * nbytes must equal insitu_layout.seq_stride. Synchronous. */
+int insitu_read_image(insitu_cache *cache, int32_t seq, uint8_t *image_host, int64_t nbytes);
+int insitu_load_image(insitu_cache *cache, int32_t seq, const uint8_t *image_host, int64_t nbytes);
+
+/* Message of the last failing call on this thread. */
+const char *insitu_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,99 @@
+"""Attention on the codes, on the GPU.
+
+CompressedAttention mirrors ops/attention.py:281-513 of the reference: the
+same two softmaxes (`attend_online`, the hardware's sequential order, and
+`attend_two_pass`) and the same AttentionStats, computed by libinsitu_hip.so
+over an HBM-resident CompressedCache. Query heads that share a KV head are
+attended together (kernel.py:303-345).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _lib
+from .cache import CompressedCache
+from .runtime import ptr
+
+
+@dataclass
+class AttentionStats:
+    """attention.py:257-274, plus the device's range/fallback counters."""
+
+    n_tokens: int = 0
+    rescale_events: int = 0
+    score_overflows: int = 0
+    acc_overflows: int = 0
+    max_abs_score: int = 0
+    max_abs_acc: int = 0
+    range_errors: int = 0
+    serial_fallbacks: int = 0
+
+    def merge(self, other: "AttentionStats") -> None:
+        self.n_tokens = max(self.n_tokens, other.n_tokens)
+        self.rescale_events += other.rescale_events
+        self.score_overflows += other.score_overflows
+        self.acc_overflows += other.acc_overflows
+        self.max_abs_score = max(self.max_abs_score, other.max_abs_score)
+        self.max_abs_acc = max(self.max_abs_acc, other.max_abs_acc)
+        self.range_errors += other.range_errors
+        self.serial_fallbacks += other.serial_fallbacks
+
+    @classmethod
+    def from_c(cls, s: "_lib.Stats") -> "AttentionStats":
+        return cls(*(int(getattr(s, n)) for n, _ in _lib.Stats._fields_))
+
+
+class CompressedAttention:
+    """Scores and accumulates on codes for every sequence and KV head of a cache."""
+
+    def __init__(self, cache: CompressedCache) -> None:
+        self.cache = cache
+        self.ctx = cache.ctx
+
+    def attend(self, q_rot, mode: str = "online", out=None, stats: bool = True):
+        """q_rot (batch, n_q_heads, d) rotated Q8.16 -> out (batch, n_q_heads, d) Q16.
+
+        mode: "online" (attend_online, bit-exact), "two_pass" (attend_two_pass,
+        bit-exact), "split" (context-split), "serial" (one token at a time).
+        Returns (out torch int32 tensor, AttentionStats or None). With
+        stats=False nothing synchronises.
+        """
+        import torch
+        c = self.cache
+        q = self.ctx.to_device(q_rot, torch.int32)
+        if q.dim() == 2 and c.batch == 1:
+            q = q.unsqueeze(0)
+        if q.shape != (c.batch, c.n_q_heads, c.head_dim):
+            raise ValueError(f"q_rot must be ({c.batch}, {c.n_q_heads}, {c.head_dim}), "
+                             f"got {tuple(q.shape)}")
+        if out is None:
+            out = torch.empty_like(q)
+        st = _lib.Stats() if stats else None
+        _lib.check(self.ctx.lib.insitu_attend(c.handle, ptr(q), ptr(out), _lib.MODES[mode],
+                                              ctypes.byref(st) if st is not None else None))
+        self._keep = q
+        return out, (AttentionStats.from_c(st) if st is not None else None)
+
+    def _group(self, q_rot, kv_head: int, seq: int, mode: str):
+        c = self.cache
+        g = c.n_q_heads // c.n_kv_heads
+        q = np.zeros((c.batch, c.n_q_heads, c.head_dim), dtype=np.int32)
+        qg = np.atleast_2d(np.asarray(q_rot, dtype=np.int64))
+        if qg.shape != (g, c.head_dim):
+            raise ValueError(f"expected the {g} query heads of one KV group, got {qg.shape}")
+        q[seq, kv_head * g:(kv_head + 1) * g] = qg
+        out, st = self.attend(q, mode)
+        res = out[seq, kv_head * g:(kv_head + 1) * g].cpu().numpy().astype(np.int64)
+        return res.reshape(np.shape(q_rot)[:-1] + (c.head_dim,)), st
+
+    def attend_online(self, q_rot, kv_head: int, seq: int = 0):
+        """attention.py:451-513 for one KV group: q_rot (G, d) -> (out (G, d), stats)."""
+        return self._group(q_rot, kv_head, seq, "online")
+
+    def attend_two_pass(self, q_rot, kv_head: int, seq: int = 0):
+        """attention.py:429-449 for one KV group."""
+        return self._group(q_rot, kv_head, seq, "two_pass")

@@ -1,0 +1,85 @@
+"""The seam half of one attention block: wire q/k/v in, Q16 out.
+
+AttentionBlock follows the pipeline order of AttentionKernel.forward
+(kernel.py:253-353 of the reference), the part below the seam:
+
+    rotate k, v, q        kernel.py:271-276
+    append k, v           kernel.py:282-284 (the current token attends to itself)
+    attend per KV group   kernel.py:337-345 (query heads 4h..4h+3 share KV head h)
+    merge_heads           kernel.py:352-353, ops/project.py:67-74
+
+It is one fused C call per decode step (insitu_step), the counterpart of
+the FPGA's CMD_STEP (host/attn_proto.py:65-72).
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from . import _lib
+from .attention import AttentionStats, CompressedAttention
+from .cache import CompressedCache
+from .config import FixedFormat, ModelConfig, QuantConfig
+from .runtime import default_context, ptr
+
+
+class AttentionBlock:
+    def __init__(self, model: ModelConfig, quant: QuantConfig | None = None,
+                 fmt: FixedFormat | None = None, *, capacity: int = 2048, batch: int = 1,
+                 softmax: str = "online", ctx=None) -> None:
+        self.model = model
+        self.quant = quant or QuantConfig()
+        self.fmt = fmt or FixedFormat()
+        self.ctx = ctx or default_context()
+        self.cache = CompressedCache(model.num_kv_heads, model.head_dim, capacity, self.quant,
+                                     self.fmt, batch=batch, n_q_heads=model.num_heads,
+                                     ctx=self.ctx)
+        self.attn = CompressedAttention(self.cache)
+        self.rotation = self.cache.rotation
+        if softmax not in _lib.MODES:
+            raise ValueError(f"softmax={softmax!r}; expected one of {sorted(_lib.MODES)}")
+        self.softmax = softmax
+        self.last_stats: AttentionStats | None = None
+
+    @property
+    def batch(self) -> int:
+        return self.cache.batch
+
+    def step(self, qi, ki, vi, *, stats: bool = True):
+        """One decode token per sequence.
+
+        qi (batch, num_heads, d), ki/vi (batch, num_kv_heads, d): Q8.16 ints
+        from the wire (kernel.py:256-258). Returns merge_heads(out):
+        (batch, num_heads * d) Q16 in the rotated basis, as a torch int32 tensor.
+        """
+        import torch
+        m = self.model
+        q = self.ctx.to_device(qi, torch.int32).reshape(self.batch, m.num_heads, m.head_dim)
+        k = self.ctx.to_device(ki, torch.int32).reshape(self.batch, m.num_kv_heads, m.head_dim)
+        v = self.ctx.to_device(vi, torch.int32).reshape(self.batch, m.num_kv_heads, m.head_dim)
+        out = torch.empty_like(q)
+        st = _lib.Stats() if stats else None
+        _lib.check(self.ctx.lib.insitu_step(self.cache.handle, ptr(q), ptr(k), ptr(v), ptr(out),
+                                            _lib.MODES[self.softmax],
+                                            ctypes.byref(st) if st is not None else None))
+        self._keep = (q, k, v)
+        self.last_stats = AttentionStats.from_c(st) if st is not None else None
+        return out.reshape(self.batch, m.num_heads * m.head_dim)
+
+    def forward_seam(self, qi, ki, vi) -> np.ndarray:
+        """batch == 1: (tokens, heads, d) wire tensors, one decode step per token.
+
+        Returns (tokens, num_heads * d) int64, the `out` tap of kernel.py:353.
+        """
+        qi, ki, vi = (np.asarray(a) for a in (qi, ki, vi))
+        if self.batch != 1:
+            raise ValueError("forward_seam drives a batch-1 block")
+        outs = [self.step(qi[t][None], ki[t][None], vi[t][None]).cpu().numpy()
+                for t in range(qi.shape[0])]
+        return np.concatenate(outs, axis=0).astype(np.int64)
+
+    def reset(self) -> None:
+        """kernel.py:454-456: a new sequence; tables survive."""
+        self.cache.reset()

@@ -1,0 +1,587 @@
+// The C ABI (include/insitu.h): contexts, caches, validation and launches.
+//
+// Validation mirrors the reference's raise sites: config.py:45-61 (head_dim a
+// power of two, GQA divisibility), config.py:178-207 (code widths, whole
+// bytes), quantize.py:150-156 (threshold_frac >= qk_frac), base.py:67-73
+// (capacity), ddr_layout.py:126-146 (beat-friendly planes).
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "insitu_internal.h"
+
+using namespace insitu;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string &msg) {
+    g_last_error = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what) {
+    return fail(INSITU_EHIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr, what)                        \
+    do {                                           \
+        hipError_t e_ = (expr);                    \
+        if (e_ != hipSuccess) return hip_fail(e_, what); \
+    } while (0)
+
+__global__ void zero_u64(unsigned long long *p, int n) {
+    int i = threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
+bool format_supported(const insitu_format &f, std::string &why) {
+    char buf[256];
+    if (f.head_dim != 64 && f.head_dim != 128) {
+        snprintf(buf, sizeof buf, "head_dim=%d: the HIP kernels support 64 and 128", f.head_dim);
+        why = buf;
+        return false;
+    }
+    if (f.key_bits < 1 || f.key_bits > 8 || f.value_bits < 1 || f.value_bits > 8) {
+        snprintf(buf, sizeof buf, "key_bits=%d value_bits=%d outside 1..8 (config.py:179-181)",
+                 f.key_bits, f.value_bits);
+        why = buf;
+        return false;
+    }
+    if (f.norm_bits != 16) {
+        why = "norm_bits must be 16 (the row stores two int16 norms)";
+        return false;
+    }
+    if (f.norm_frac < 1 || f.norm_frac > 15) {
+        why = "norm_frac must be in 1..15: centroid_frac + norm_frac must reach qk_frac "
+              "(quantize.py:150-156)";
+        return false;
+    }
+    if (f.qk_frac != QK_FRAC || f.qk_width != QK_WIDTH || f.centroid_frac != CENT_FRAC ||
+        f.acc_frac != ACC_FRAC || f.acc_width != ACC_WIDTH || f.score_width != SCORE_WIDTH ||
+        f.prob_frac != PROB_FRAC || f.exp_lut_bits != LUT_BITS) {
+        why = "only the reference FixedFormat (Q8.16/Q1.15/acc Q16 32b/score 48b/prob Q15/8-bit LUT) "
+              "is implemented";
+        return false;
+    }
+    if (f.rot_rounds < 0 || f.rot_rounds > 2) {
+        why = "rot_rounds must be 0, 1 or 2";
+        return false;
+    }
+    return true;
+}
+
+}  // namespace
+
+struct insitu_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    bool own_stream = false;
+    Tables *hook_tables = nullptr;        // exp table for the exp-LUT test hook
+    unsigned long long *hook_flags = nullptr;
+    int64_t *hook_i64 = nullptr;          // small staging for host arrays (codebooks)
+    size_t hook_i64_n = 0;
+};
+
+struct insitu_cache {
+    insitu_ctx *ctx = nullptr;
+    insitu_cache_desc desc{};
+    Geom g{};
+    Tables tabs_host{};
+    Tables *tabs = nullptr;
+    uint8_t *base = nullptr;
+    int64_t total_bytes = 0;
+    int64_t *len_dev[2] = {nullptr, nullptr};
+    int cur = 0;
+    std::vector<int64_t> len_host;
+    DevStats *stats = nullptr;
+    int32_t *wire_scratch = nullptr;      // rotated q/k/v for insitu_step
+};
+
+namespace {
+
+void fill_exp(Tables &t) {
+    for (int i = 0; i < 256; ++i)
+        t.exp_table[i] = (int32_t)std::nearbyint(std::exp2(-(double)i / 256.0) * 32768.0);
+    // attention.py:145-146: ceil(((span << shift) << acc_frac) / log2e).
+    const int64_t num = ((int64_t)LUT_SPAN << (ACC_FRAC - LUT_BITS)) << ACC_FRAC;
+    t.delta_max = (num + LOG2E_Q16 - 1) / LOG2E_Q16;
+}
+
+int ensure_hook(insitu_ctx *c, size_t n) {
+    if (c->hook_i64_n >= n) return INSITU_OK;
+    if (c->hook_i64) hipFree(c->hook_i64);
+    c->hook_i64 = nullptr;
+    HIP_TRY(hipMalloc(&c->hook_i64, n * sizeof(int64_t)), "hipMalloc");
+    c->hook_i64_n = n;
+    return INSITU_OK;
+}
+
+int copy_stats(insitu_cache *c, insitu_stats *out) {
+    if (!out) return INSITU_OK;
+    DevStats h{};
+    HIP_TRY(hipMemcpyAsync(&h, c->stats, sizeof h, hipMemcpyDeviceToHost, c->ctx->stream),
+            "stats copy");
+    HIP_TRY(hipStreamSynchronize(c->ctx->stream), "stream sync");
+    out->n_tokens = (int64_t)h.n_tokens;
+    out->rescale_events = (int64_t)h.rescale_events;
+    out->score_overflows = (int64_t)h.score_overflows;
+    out->acc_overflows = (int64_t)h.acc_overflows;
+    out->max_abs_score = (int64_t)h.max_abs_score;
+    out->max_abs_acc = (int64_t)h.max_abs_acc;
+    out->range_errors = (int64_t)h.range_errors;
+    out->serial_fallbacks = (int64_t)h.serial_fallbacks;
+    if (h.fault) return fail(INSITU_EFAULT, "a kernel raised its internal fault flag");
+    return INSITU_OK;
+}
+
+int zero_stats(insitu_cache *c) {
+    hipLaunchKernelGGL(zero_u64, dim3(1), dim3(64), 0, c->ctx->stream,
+                       (unsigned long long *)c->stats, (int)(sizeof(DevStats) / 8));
+    HIP_TRY(hipGetLastError(), "zero stats");
+    return INSITU_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *insitu_last_error(void) { return g_last_error.c_str(); }
+
+int insitu_ctx_create(int32_t device, void *hip_stream, insitu_ctx **out) {
+    if (!out) return fail(INSITU_EINVAL, "out is NULL");
+    *out = nullptr;
+    int n = 0;
+    HIP_TRY(hipGetDeviceCount(&n), "hipGetDeviceCount");
+    if (device < 0 || device >= n) return fail(INSITU_EINVAL, "no such device");
+    HIP_TRY(hipSetDevice(device), "hipSetDevice");
+    auto *c = new insitu_ctx();
+    c->device = device;
+    // NULL is the device's default stream (what torch uses unless told
+    // otherwise), so library kernels and the caller's copies stay ordered.
+    c->stream = (hipStream_t)hip_stream;
+    Tables t{};
+    fill_exp(t);
+    hipError_t e = hipMalloc(&c->hook_tables, sizeof(Tables));
+    if (e == hipSuccess) e = hipMemcpy(c->hook_tables, &t, sizeof(Tables), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMalloc(&c->hook_flags, 64);
+    if (e != hipSuccess) {
+        insitu_ctx_destroy(c);
+        return hip_fail(e, "ctx tables");
+    }
+    *out = c;
+    return INSITU_OK;
+}
+
+int insitu_ctx_destroy(insitu_ctx *c) {
+    if (!c) return INSITU_OK;
+    hipSetDevice(c->device);
+    if (c->stream) hipStreamSynchronize(c->stream);
+    if (c->hook_tables) hipFree(c->hook_tables);
+    if (c->hook_flags) hipFree(c->hook_flags);
+    if (c->hook_i64) hipFree(c->hook_i64);
+    if (c->own_stream && c->stream) hipStreamDestroy(c->stream);
+    delete c;
+    return INSITU_OK;
+}
+
+int insitu_ctx_sync(insitu_ctx *c) {
+    if (!c) return fail(INSITU_EINVAL, "ctx is NULL");
+    HIP_TRY(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    return INSITU_OK;
+}
+
+void *insitu_ctx_stream(insitu_ctx *c) { return c ? (void *)c->stream : nullptr; }
+
+int insitu_rotate(insitu_ctx *c, const int32_t *x, int32_t *y, int64_t n_vec,
+                  const insitu_format *fmt) {
+    if (!c || !fmt || (!x && n_vec) || (!y && n_vec)) return fail(INSITU_EINVAL, "null argument");
+    const int d = fmt->head_dim;
+    if (d < 16 || d > 128 || (d & (d - 1)))
+        return fail(INSITU_EINVAL, "rotate supports power-of-two d in 16..128 (rotate.py:146-147)");
+    if (fmt->rot_rounds < 0 || fmt->rot_rounds > 2) return fail(INSITU_EINVAL, "rot_rounds 0..2");
+    if (n_vec < 0 || n_vec > 0x7fffffff) return fail(INSITU_EBADLEN, "n_vec out of range");
+    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    HIP_TRY(launch_rotate(c->stream, x, y, n_vec, d, fmt->rot_rounds, fmt->rot_signs,
+                          c->hook_flags),
+            "rotate launch");
+    return INSITU_OK;
+}
+
+int insitu_encode(insitu_ctx *c, const int32_t *x, int64_t n_vec, const insitu_format *fmt,
+                  const int64_t *bounds_host, int32_t bits, int32_t *norm, uint8_t *codes) {
+    if (!c || !fmt || !bounds_host) return fail(INSITU_EINVAL, "null argument");
+    std::string why;
+    if (!format_supported(*fmt, why)) return fail(INSITU_EINVAL, why);
+    if (bits < 1 || bits > 8) return fail(INSITU_EINVAL, "bits outside 1..8");
+    if (n_vec < 0 || n_vec > 0x7fffffff) return fail(INSITU_EBADLEN, "n_vec out of range");
+    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    const int nb = (1 << bits) - 1;
+    int rc = ensure_hook(c, 256);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(c->hook_i64, bounds_host, nb * sizeof(int64_t), hipMemcpyHostToDevice,
+                           c->stream),
+            "bounds upload");
+    HIP_TRY(launch_encode(c->stream, x, n_vec, fmt->head_dim, fmt->norm_frac, c->hook_i64, nb, norm,
+                          codes),
+            "encode launch");
+    HIP_TRY(hipStreamSynchronize(c->stream), "sync");   // the staging buffer is reused
+    return INSITU_OK;
+}
+
+int insitu_qtab(insitu_ctx *c, const int32_t *q, int32_t n_heads, int32_t d,
+                const int64_t *centroids_host, int32_t n_c, int64_t *table) {
+    if (!c || !centroids_host) return fail(INSITU_EINVAL, "null argument");
+    if (n_c < 1 || n_c > 256 || n_heads < 0 || d < 1) return fail(INSITU_EBADLEN, "bad shape");
+    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    int rc = ensure_hook(c, 256);
+    if (rc) return rc;
+    HIP_TRY(hipMemcpyAsync(c->hook_i64, centroids_host, n_c * sizeof(int64_t),
+                           hipMemcpyHostToDevice, c->stream),
+            "centroid upload");
+    HIP_TRY(launch_qtab(c->stream, q, n_heads, d, c->hook_i64, n_c, table), "qtab launch");
+    HIP_TRY(hipStreamSynchronize(c->stream), "sync");
+    return INSITU_OK;
+}
+
+int insitu_exp_lut(insitu_ctx *c, const int64_t *delta, int64_t n, int32_t *p) {
+    if (!c) return fail(INSITU_EINVAL, "null argument");
+    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    HIP_TRY(launch_exp_lut(c->stream, c->hook_tables, delta, n, p), "exp launch");
+    return INSITU_OK;
+}
+
+int insitu_finalize(insitu_ctx *c, const int64_t *acc, const int64_t *l, int32_t rows, int32_t d,
+                    int64_t *out, int64_t *recip, int32_t *shift) {
+    if (!c) return fail(INSITU_EINVAL, "null argument");
+    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    HIP_TRY(launch_finalize(c->stream, acc, l, rows, d, out, recip, shift), "finalize launch");
+    return INSITU_OK;
+}
+
+int insitu_cache_create(insitu_ctx *c, const insitu_cache_desc *desc, insitu_cache **out) {
+    if (!c || !desc || !out) return fail(INSITU_EINVAL, "null argument");
+    *out = nullptr;
+    std::string why;
+    if (!format_supported(desc->fmt, why)) return fail(INSITU_EINVAL, why);
+    const insitu_format &f = desc->fmt;
+    if (desc->n_kv_heads < 1 || desc->n_q_heads < 1 || desc->n_q_heads % desc->n_kv_heads)
+        return fail(INSITU_EINVAL, "num_heads must be a multiple of num_kv_heads (config.py:49-53)");
+    if (desc->n_q_heads / desc->n_kv_heads > MAX_G)
+        return fail(INSITU_EINVAL, "more than 8 query heads per KV head is not supported");
+    if (desc->batch < 1 || desc->capacity < 1) return fail(INSITU_EINVAL, "batch and capacity >= 1");
+    if (!desc->key_centroids_host || !desc->key_bounds_host || !desc->value_centroids_host ||
+        !desc->value_bounds_host)
+        return fail(INSITU_EINVAL, "codebooks are required");
+    const int nk = 1 << f.key_bits, nv = 1 << f.value_bits;
+    for (int i = 1; i < nk; ++i)
+        if (desc->key_centroids_host[i] <= desc->key_centroids_host[i - 1])
+            return fail(INSITU_EINVAL, "key centroids must be strictly ascending (codebook.py:55-58)");
+    for (int i = 1; i < nv; ++i)
+        if (desc->value_centroids_host[i] <= desc->value_centroids_host[i - 1])
+            return fail(INSITU_EINVAL, "value centroids must be strictly ascending");
+    for (int i = 0; i < nk; ++i)
+        if (std::llabs(desc->key_centroids_host[i]) >= (1ll << 20))
+            return fail(INSITU_ERANGE, "a key centroid does not fit 20 bits (hw/vectors.py:314)");
+    for (int i = 0; i < nv; ++i)
+        if (std::llabs(desc->value_centroids_host[i]) >= (1ll << 20))
+            return fail(INSITU_ERANGE, "a value centroid does not fit 20 bits");
+
+    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    auto *k = new insitu_cache();
+    k->ctx = c;
+    k->desc = *desc;
+    k->desc.key_centroids_host = k->desc.key_bounds_host = nullptr;
+    k->desc.value_centroids_host = k->desc.value_bounds_host = nullptr;
+
+    Geom &g = k->g;
+    g.d = f.head_dim;
+    g.kb = f.key_bits;
+    g.vb = f.value_bits;
+    g.norm_frac = f.norm_frac;
+    g.n_kv = desc->n_kv_heads;
+    g.n_q = desc->n_q_heads;
+    g.G = g.n_q / g.n_kv;
+    g.batch = desc->batch;
+    g.capacity = desc->capacity;
+    g.key_bytes = g.d * g.kb / 8;
+    g.value_bytes = g.d * g.vb / 8;
+    g.row_bytes = g.key_bytes + g.value_bytes + 4;
+    // ddr_layout.py:110-124 + 148-163: fields first, then 16-byte beats.
+    const int fields[3][2] = {{0, g.key_bytes},
+                              {g.key_bytes, g.key_bytes + g.value_bytes},
+                              {g.key_bytes + g.value_bytes, g.row_bytes}};
+    g.n_planes = 0;
+    int maxw = 0;
+    for (auto &fl : fields) {
+        for (int a = fl[0]; a < fl[1];) {
+            int bnd = a + 16 < fl[1] ? a + 16 : fl[1];
+            if (g.n_planes >= MAX_PLANES) {
+                delete k;
+                return fail(INSITU_EINVAL, "row needs more than 16 planes");
+            }
+            g.plane_lo[g.n_planes] = a;
+            g.plane_w[g.n_planes] = bnd - a;
+            if (16 % (bnd - a)) {
+                delete k;
+                return fail(INSITU_EINVAL, "plane width does not divide the 16-byte beat "
+                                           "(ddr_layout.py:140-146)");
+            }
+            maxw = maxw > bnd - a ? maxw : bnd - a;
+            ++g.n_planes;
+            a = bnd;
+        }
+    }
+    g.span = (desc->capacity * maxw + 4095) / 4096 * 4096;   // ddr_layout.py:195-196
+    g.head_stride = g.n_planes * g.span;
+    g.seq_stride = g.n_kv * g.head_stride;
+    k->total_bytes = g.seq_stride * g.batch;
+
+    Tables &t = k->tabs_host;
+    fill_exp(t);
+    for (int i = 0; i < nk; ++i) t.kc[i] = desc->key_centroids_host[i];
+    for (int i = 0; i + 1 < nk; ++i) t.kbnd[i] = desc->key_bounds_host[i];
+    for (int i = 0; i < nv; ++i) t.vc[i] = desc->value_centroids_host[i];
+    for (int i = 0; i + 1 < nv; ++i) t.vbnd[i] = desc->value_bounds_host[i];
+
+    hipError_t e = hipMalloc(&k->base, k->total_bytes);
+    if (e == hipSuccess) e = hipMemsetAsync(k->base, 0, k->total_bytes, c->stream);
+    if (e == hipSuccess) e = hipMalloc(&k->tabs, sizeof(Tables));
+    if (e == hipSuccess)
+        e = hipMemcpyAsync(k->tabs, &t, sizeof(Tables), hipMemcpyHostToDevice, c->stream);
+    for (int i = 0; i < 2 && e == hipSuccess; ++i) {
+        e = hipMalloc(&k->len_dev[i], sizeof(int64_t) * g.batch);
+        if (e == hipSuccess) e = hipMemsetAsync(k->len_dev[i], 0, sizeof(int64_t) * g.batch, c->stream);
+    }
+    if (e == hipSuccess) e = hipMalloc(&k->stats, sizeof(DevStats));
+    if (e == hipSuccess) e = hipMemsetAsync(k->stats, 0, sizeof(DevStats), c->stream);
+    if (e == hipSuccess)
+        e = hipMalloc(&k->wire_scratch,
+                      sizeof(int32_t) * (size_t)g.batch * (g.n_q + 2 * g.n_kv) * g.d);
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) {
+        insitu_cache_destroy(k);
+        return e == hipErrorOutOfMemory ? fail(INSITU_ENOMEM, "cache allocation")
+                                        : hip_fail(e, "cache allocation");
+    }
+    g.base = k->base;
+    k->len_host.assign(g.batch, 0);
+    *out = k;
+    return INSITU_OK;
+}
+
+int insitu_cache_destroy(insitu_cache *k) {
+    if (!k) return INSITU_OK;
+    hipSetDevice(k->ctx->device);
+    hipStreamSynchronize(k->ctx->stream);
+    if (k->base) hipFree(k->base);
+    if (k->tabs) hipFree(k->tabs);
+    for (auto *p : k->len_dev)
+        if (p) hipFree(p);
+    if (k->stats) hipFree(k->stats);
+    if (k->wire_scratch) hipFree(k->wire_scratch);
+    delete k;
+    return INSITU_OK;
+}
+
+int insitu_cache_reset(insitu_cache *k) {
+    if (!k) return fail(INSITU_EINVAL, "cache is NULL");
+    HIP_TRY(hipSetDevice(k->ctx->device), "hipSetDevice");
+    for (auto *p : k->len_dev)
+        HIP_TRY(hipMemsetAsync(p, 0, sizeof(int64_t) * k->g.batch, k->ctx->stream), "reset");
+    HIP_TRY(hipStreamSynchronize(k->ctx->stream), "sync");
+    k->len_host.assign(k->g.batch, 0);
+    return INSITU_OK;
+}
+
+int insitu_cache_length(const insitu_cache *k, int32_t seq, int64_t *len) {
+    if (!k || !len) return fail(INSITU_EINVAL, "null argument");
+    if (seq < 0 || seq >= k->g.batch) return fail(INSITU_EINVAL, "no such sequence");
+    *len = k->len_host[seq];
+    return INSITU_OK;
+}
+
+int insitu_cache_set_length(insitu_cache *k, int32_t seq, int64_t len) {
+    if (!k) return fail(INSITU_EINVAL, "cache is NULL");
+    if (seq < 0 || seq >= k->g.batch) return fail(INSITU_EINVAL, "no such sequence");
+    if (len < 0 || len > k->g.capacity) return fail(INSITU_ECAPACITY, "length beyond capacity");
+    HIP_TRY(hipSetDevice(k->ctx->device), "hipSetDevice");
+    k->len_host[seq] = len;
+    HIP_TRY(hipMemcpyAsync(k->len_dev[k->cur] + seq, &k->len_host[seq], sizeof(int64_t),
+                           hipMemcpyHostToDevice, k->ctx->stream),
+            "length upload");
+    HIP_TRY(hipStreamSynchronize(k->ctx->stream), "sync");
+    return INSITU_OK;
+}
+
+int insitu_cache_layout(const insitu_cache *k, insitu_layout *o) {
+    if (!k || !o) return fail(INSITU_EINVAL, "null argument");
+    std::memset(o, 0, sizeof *o);
+    o->row_bytes = k->g.row_bytes;
+    o->n_planes = k->g.n_planes;
+    for (int p = 0; p < k->g.n_planes; ++p) {
+        o->plane_lo[p] = k->g.plane_lo[p];
+        o->plane_width[p] = k->g.plane_w[p];
+    }
+    o->plane_span = k->g.span;
+    o->head_stride = k->g.head_stride;
+    o->seq_stride = k->g.seq_stride;
+    o->total_bytes = k->total_bytes;
+    o->device_base = (uint64_t)(uintptr_t)k->base;
+    return INSITU_OK;
+}
+
+static int append_impl(insitu_cache *k, int seq_lo, int seq_hi, const int32_t *kr,
+                       const int32_t *vr, int32_t n_tok) {
+    if (!k || !kr || !vr) return fail(INSITU_EINVAL, "null argument");
+    if (n_tok < 0) return fail(INSITU_EBADLEN, "n_tok < 0");
+    if (n_tok == 0) return INSITU_OK;
+    for (int b = seq_lo; b < seq_hi; ++b)
+        if (k->len_host[b] + n_tok > k->g.capacity) {
+            char buf[200];
+            snprintf(buf, sizeof buf,
+                     "cache holds %lld of %lld tokens; cannot append %d (base.py:67-73)",
+                     (long long)k->len_host[b], (long long)k->g.capacity, n_tok);
+            return fail(INSITU_ECAPACITY, buf);
+        }
+    HIP_TRY(hipSetDevice(k->ctx->device), "hipSetDevice");
+    HIP_TRY(launch_append(k->ctx->stream, k->g, k->tabs, kr, vr, n_tok, seq_lo, seq_hi,
+                          k->len_dev[k->cur], k->len_dev[k->cur ^ 1], k->stats),
+            "append launch");
+    k->cur ^= 1;
+    for (int b = seq_lo; b < seq_hi; ++b) k->len_host[b] += n_tok;
+    return INSITU_OK;
+}
+
+int insitu_append(insitu_cache *k, const int32_t *kr, const int32_t *vr, int32_t n_tok) {
+    if (!k) return fail(INSITU_EINVAL, "cache is NULL");
+    return append_impl(k, 0, k->g.batch, kr, vr, n_tok);
+}
+
+int insitu_append_seq(insitu_cache *k, int32_t seq, const int32_t *kr, const int32_t *vr,
+                      int32_t n_tok) {
+    if (!k) return fail(INSITU_EINVAL, "cache is NULL");
+    if (seq < 0 || seq >= k->g.batch) return fail(INSITU_EINVAL, "no such sequence");
+    return append_impl(k, seq, seq + 1, kr, vr, n_tok);
+}
+
+static int attend_impl(insitu_cache *k, const int32_t *q, int32_t *out, int32_t mode) {
+    const int64_t *len = k->len_dev[k->cur];
+    HIP_TRY(launch_attend_serial(k->ctx->stream, k->g, k->tabs, q, out, len,
+                                 mode == INSITU_TWO_PASS ? 1 : 0, k->stats),
+            "attend launch");
+    return INSITU_OK;
+}
+
+int insitu_attend(insitu_cache *k, const int32_t *q, int32_t *out, int32_t mode,
+                  insitu_stats *stats) {
+    if (!k || !q || !out) return fail(INSITU_EINVAL, "null argument");
+    if (mode < INSITU_SEQUENTIAL || mode > INSITU_SERIAL) return fail(INSITU_EINVAL, "unknown mode");
+    HIP_TRY(hipSetDevice(k->ctx->device), "hipSetDevice");
+    int rc = zero_stats(k);
+    if (rc) return rc;
+    rc = attend_impl(k, q, out, mode);
+    if (rc) return rc;
+    return copy_stats(k, stats);
+}
+
+int insitu_step(insitu_cache *k, const int32_t *q, const int32_t *kw, const int32_t *vw,
+                int32_t *out, int32_t mode, insitu_stats *stats) {
+    if (!k || !q || !kw || !vw || !out) return fail(INSITU_EINVAL, "null argument");
+    if (mode < INSITU_SEQUENTIAL || mode > INSITU_SERIAL) return fail(INSITU_EINVAL, "unknown mode");
+    const Geom &g = k->g;
+    int32_t *qr = k->wire_scratch;
+    int32_t *kr = qr + (size_t)g.batch * g.n_q * g.d;
+    int32_t *vr = kr + (size_t)g.batch * g.n_kv * g.d;
+    HIP_TRY(hipSetDevice(k->ctx->device), "hipSetDevice");
+    int rc = zero_stats(k);
+    if (rc) return rc;
+    // kernel.py:271-276: k, v and q are all rotated; then append; then attend.
+    HIP_TRY(launch_rotate(k->ctx->stream, kw, kr, (int64_t)g.batch * g.n_kv, g.d,
+                          k->desc.fmt.rot_rounds, k->desc.fmt.rot_signs, &k->stats->range_errors),
+            "rotate k");
+    HIP_TRY(launch_rotate(k->ctx->stream, vw, vr, (int64_t)g.batch * g.n_kv, g.d,
+                          k->desc.fmt.rot_rounds, k->desc.fmt.rot_signs, &k->stats->range_errors),
+            "rotate v");
+    HIP_TRY(launch_rotate(k->ctx->stream, q, qr, (int64_t)g.batch * g.n_q, g.d,
+                          k->desc.fmt.rot_rounds, k->desc.fmt.rot_signs, &k->stats->range_errors),
+            "rotate q");
+    rc = append_impl(k, 0, g.batch, kr, vr, 1);
+    if (rc) return rc;
+    rc = attend_impl(k, qr, out, mode);
+    if (rc) return rc;
+    return copy_stats(k, stats);
+}
+
+int insitu_read_rows(insitu_cache *k, int32_t seq, int32_t head, int64_t t0, int64_t n,
+                     uint8_t *rows) {
+    if (!k || (!rows && n)) return fail(INSITU_EINVAL, "null argument");
+    const Geom &g = k->g;
+    if (seq < 0 || seq >= g.batch || head < 0 || head >= g.n_kv)
+        return fail(INSITU_EINVAL, "no such sequence/head");
+    if (t0 < 0 || n < 0 || t0 + n > g.capacity) return fail(INSITU_EBADLEN, "rows outside capacity");
+    if (n == 0) return INSITU_OK;
+    HIP_TRY(hipSetDevice(k->ctx->device), "hipSetDevice");
+    std::vector<uint8_t> stage((size_t)n * 16);
+    for (int p = 0; p < g.n_planes; ++p) {
+        const int w = g.plane_w[p];
+        const uint8_t *src = g.base + seq * g.seq_stride + head * g.head_stride + p * g.span + t0 * w;
+        HIP_TRY(hipMemcpyAsync(stage.data(), src, (size_t)n * w, hipMemcpyDeviceToHost, k->ctx->stream),
+                "row read");
+        HIP_TRY(hipStreamSynchronize(k->ctx->stream), "sync");
+        for (int64_t t = 0; t < n; ++t)
+            std::memcpy(rows + t * g.row_bytes + g.plane_lo[p], stage.data() + t * w, w);
+    }
+    return INSITU_OK;
+}
+
+int insitu_load_rows(insitu_cache *k, int32_t seq, int32_t head, int64_t t0, int64_t n,
+                     const uint8_t *rows) {
+    if (!k || (!rows && n)) return fail(INSITU_EINVAL, "null argument");
+    const Geom &g = k->g;
+    if (seq < 0 || seq >= g.batch || head < 0 || head >= g.n_kv)
+        return fail(INSITU_EINVAL, "no such sequence/head");
+    if (t0 < 0 || n < 0 || t0 + n > g.capacity) return fail(INSITU_EBADLEN, "rows outside capacity");
+    if (n == 0) return INSITU_OK;
+    HIP_TRY(hipSetDevice(k->ctx->device), "hipSetDevice");
+    std::vector<uint8_t> stage((size_t)n * 16);
+    for (int p = 0; p < g.n_planes; ++p) {
+        const int w = g.plane_w[p];
+        for (int64_t t = 0; t < n; ++t)
+            std::memcpy(stage.data() + t * w, rows + t * g.row_bytes + g.plane_lo[p], w);
+        uint8_t *dst = g.base + seq * g.seq_stride + head * g.head_stride + p * g.span + t0 * w;
+        HIP_TRY(hipMemcpyAsync(dst, stage.data(), (size_t)n * w, hipMemcpyHostToDevice, k->ctx->stream),
+                "row load");
+        HIP_TRY(hipStreamSynchronize(k->ctx->stream), "sync");
+    }
+    return INSITU_OK;
+}
+
+int insitu_read_image(insitu_cache *k, int32_t seq, uint8_t *img, int64_t nbytes) {
+    if (!k || !img) return fail(INSITU_EINVAL, "null argument");
+    if (seq < 0 || seq >= k->g.batch) return fail(INSITU_EINVAL, "no such sequence");
+    if (nbytes != k->g.seq_stride) return fail(INSITU_EBADLEN, "image size must be seq_stride");
+    HIP_TRY(hipSetDevice(k->ctx->device), "hipSetDevice");
+    HIP_TRY(hipMemcpyAsync(img, k->g.base + seq * k->g.seq_stride, nbytes, hipMemcpyDeviceToHost,
+                           k->ctx->stream),
+            "image read");
+    HIP_TRY(hipStreamSynchronize(k->ctx->stream), "sync");
+    return INSITU_OK;
+}
+
+int insitu_load_image(insitu_cache *k, int32_t seq, const uint8_t *img, int64_t nbytes) {
+    if (!k || !img) return fail(INSITU_EINVAL, "null argument");
+    if (seq < 0 || seq >= k->g.batch) return fail(INSITU_EINVAL, "no such sequence");
+    if (nbytes != k->g.seq_stride) return fail(INSITU_EBADLEN, "image size must be seq_stride");
+    HIP_TRY(hipSetDevice(k->ctx->device), "hipSetDevice");
+    HIP_TRY(hipMemcpyAsync(k->g.base + seq * k->g.seq_stride, img, nbytes, hipMemcpyHostToDevice,
+                           k->ctx->stream),
+            "image load");
+    HIP_TRY(hipStreamSynchronize(k->ctx->stream), "sync");
+    return INSITU_OK;
+}
+
+}  // extern "C"

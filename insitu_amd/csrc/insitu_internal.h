@@ -1,0 +1,172 @@
+// Internal definitions shared by the HIP translation units of libinsitu_hip.
+//
+// Fixed-point constants follow config.py:214-254 of the reference
+// (FixedFormat defaults). The kernels are written for that format; the
+// cache constructor rejects any other one with INSITU_EINVAL rather than
+// computing something subtly different.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/insitu.h"
+
+namespace insitu {
+
+constexpr int QK_FRAC = 16;       // Q8.16 seam values
+constexpr int QK_WIDTH = 24;
+constexpr int CENT_FRAC = 15;     // Q1.15 centroids
+constexpr int ACC_FRAC = 16;
+constexpr int ACC_WIDTH = 32;
+constexpr int SCORE_WIDTH = 48;
+constexpr int PROB_FRAC = 15;
+constexpr int LUT_BITS = 8;
+constexpr int MAX_INT_PART = PROB_FRAC + 1;                      // attention.py:113
+constexpr int LUT_SPAN = (MAX_INT_PART + 1) << LUT_BITS;         // 4352, attention.py:129
+constexpr int64_t LOG2E_Q16 = 94548;                             // round(log2(e) * 2^16)
+constexpr int64_t SCORE_LO = -(int64_t(1) << (SCORE_WIDTH - 1));
+constexpr int64_t SCORE_HI = (int64_t(1) << (SCORE_WIDTH - 1)) - 1;
+constexpr int64_t ACC_LO = -(int64_t(1) << (ACC_WIDTH - 1));
+constexpr int64_t ACC_HI = (int64_t(1) << (ACC_WIDTH - 1)) - 1;
+constexpr int MAX_PLANES = 16;
+constexpr int MAX_D = 128;
+constexpr int MAX_G = 8;          // query heads per KV head handled by one block
+constexpr int64_t Q_ROT_LIMIT = int64_t(1) << 27;  // |q_rot| bound that keeps scores exact
+
+// Plane geometry of a cache: hw/ddr_layout.py:148-214, one region per sequence.
+struct Geom {
+    uint8_t *base;
+    int64_t seq_stride, head_stride, span, capacity;
+    int32_t n_planes;
+    int32_t plane_lo[MAX_PLANES];
+    int32_t plane_w[MAX_PLANES];
+    int32_t row_bytes, key_bytes, value_bytes;   // norms follow the value field, 4 B
+    int32_t d, kb, vb, norm_frac;
+    int32_t n_kv, n_q, G, batch;
+};
+
+// Device-resident constants of a cache: codebooks and the exp table.
+struct Tables {
+    int64_t kc[256];     // key centroids, Q1.15
+    int64_t kbnd[256];   // key boundaries
+    int64_t vc[256];
+    int64_t vbnd[256];
+    int32_t exp_table[256];   // rint(2^(-i/256) * 2^15), attention.py:106-108
+    int64_t delta_max;        // attention.py:145-146
+};
+
+// Device statistics; merged with atomics (AttentionStats.merge semantics).
+struct DevStats {
+    unsigned long long n_tokens;          // max
+    unsigned long long rescale_events;    // sum
+    unsigned long long score_overflows;   // sum
+    unsigned long long acc_overflows;     // sum
+    unsigned long long max_abs_score;     // max
+    unsigned long long max_abs_acc;       // max
+    unsigned long long range_errors;      // sum
+    unsigned long long serial_fallbacks;  // sum
+    unsigned long long fault;             // nonzero = internal error
+};
+
+// ---------------------------------------------------------------------------
+// device helpers
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ int64_t wmul(int64_t a, int64_t b) {
+    return (int64_t)((uint64_t)a * (uint64_t)b);
+}
+__device__ __forceinline__ int64_t wadd(int64_t a, int64_t b) {
+    return (int64_t)((uint64_t)a + (uint64_t)b);
+}
+
+// ExpLut.__call__ (attention.py:153-159) for delta >= 0: the flat index is
+// floor(min(delta, delta_max) * log2e / 2^24); past the table it is zero.
+__device__ __forceinline__ int32_t exp_lut(int64_t delta, const int32_t *table, int64_t delta_max) {
+    int64_t d = delta < delta_max ? delta : delta_max;
+    uint64_t u = ((uint64_t)d * (uint64_t)LOG2E_Q16) >> (ACC_FRAC + ACC_FRAC - LUT_BITS);
+    if (u >= (uint64_t)LUT_SPAN) return 0;
+    return table[u & 255] >> (int)(u >> LUT_BITS);
+}
+
+// reciprocal + _finalize for one row (attention.py:177-250, 873-880).
+struct Recip {
+    int64_t r;
+    int32_t shift;
+};
+__device__ __forceinline__ Recip reciprocal(int64_t l) {
+    int64_t s = 0;
+    if (l >= 2) {
+        s = 63 - __clzll((unsigned long long)l);
+        if (s > 47) s = 47;
+    }
+    int64_t k = s - 31;
+    int64_t ln = k >= 0 ? (l >> k) : (int64_t)((uint64_t)l << (-k));
+    Recip out;
+    out.r = l > 0 ? (int64_t)(((uint64_t)1 << 62) / (uint64_t)(ln > 1 ? ln : 1)) : 0;
+    out.shift = (int32_t)(62 - PROB_FRAC + k);
+    return out;
+}
+
+__device__ __forceinline__ uint8_t *plane_ptr(const Geom &g, int b, int h, int p) {
+    return g.base + (int64_t)b * g.seq_stride + (int64_t)h * g.head_stride + (int64_t)p * g.span;
+}
+
+// Code of channel c in an LSB-first bitstream of `bits`-wide codes (quantize.py:271-283).
+__device__ __forceinline__ int code_at(const uint8_t *field, int c, int bits) {
+    int o = c * bits;
+    int j = o >> 3, sh = o & 7;
+    uint32_t v = field[j];
+    if (sh + bits > 8) v |= (uint32_t)field[j + 1] << 8;
+    return (int)((v >> sh) & ((1u << bits) - 1u));
+}
+
+__device__ __forceinline__ int64_t sext16(uint32_t v) {
+    return (int64_t)(int16_t)(uint16_t)(v & 0xFFFFu);
+}
+
+// Wave-wide (64-lane) int64 sum, wrapping.
+__device__ __forceinline__ int64_t wave_sum64(int64_t v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = wadd(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+__device__ __forceinline__ int64_t wave_max64(int64_t v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        int64_t w = __shfl_xor(v, o, 64);
+        v = w > v ? w : v;
+    }
+    return v;
+}
+
+__device__ __forceinline__ void stat_max(unsigned long long *p, int64_t v) {
+    atomicMax(p, (unsigned long long)(v < 0 ? -v : v));
+}
+
+}  // namespace insitu
+
+// Host-side internal API between translation units.
+namespace insitu {
+
+struct LaunchErr {
+    hipError_t e;
+};
+
+hipError_t launch_rotate(hipStream_t s, const int32_t *x, int32_t *y, int64_t n_vec, int d,
+                         int rounds, const uint64_t (*signs)[2], unsigned long long *range_err);
+hipError_t launch_encode(hipStream_t s, const int32_t *x, int64_t n_vec, int d, int norm_frac,
+                         const int64_t *bounds_dev, int n_bounds, int32_t *norm, uint8_t *codes);
+hipError_t launch_qtab(hipStream_t s, const int32_t *q, int n_heads, int d, const int64_t *c_dev,
+                       int n_c, int64_t *table);
+hipError_t launch_exp_lut(hipStream_t s, const Tables *t, const int64_t *delta, int64_t n,
+                          int32_t *p);
+hipError_t launch_finalize(hipStream_t s, const int64_t *acc, const int64_t *l, int rows, int d,
+                           int64_t *out, int64_t *recip, int32_t *shift);
+hipError_t launch_append(hipStream_t s, const Geom &g, const Tables *t, const int32_t *k,
+                         const int32_t *v, int n_tok, int seq_lo, int seq_hi, const int64_t *len_in,
+                         int64_t *len_out, DevStats *st);
+hipError_t launch_attend_serial(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
+                                int32_t *out, const int64_t *len, int two_pass, DevStats *st);
+
+}  // namespace insitu

@@ -1,0 +1,365 @@
+// The write path: rotation, norm + threshold encode, row packing and the
+// plane-layout append; plus the small test hooks (qtab, exp LUT, finalize).
+//
+// rotate   ops/rotate.py:170-197   one wave per vector, lane = channel; the
+//                                  FWHT butterflies are cross-lane xor shuffles
+// encode   ops/quantize.py:164-196 wave reduction for sum(x^2), exact isqrt,
+//                                  half-even requantize, strict '>' compares
+// append   cache/compressed.py:64-86 + quantize.py:237-252 + hw/ddr_layout.py:198-214
+#include "insitu_internal.h"
+
+namespace insitu {
+
+// ---------------------------------------------------------------------------
+// rotation
+// ---------------------------------------------------------------------------
+
+// Up to two channels per lane (d <= 128): channel lane and lane + 64.
+template <int CPL>
+__device__ void fwht_wave(int64_t (&x)[CPL], int d) {
+    const int lane = threadIdx.x & 63;
+    const int hmax = d < 64 ? d : 64;
+    for (int h = 1; h < hmax; h <<= 1) {
+#pragma unroll
+        for (int k = 0; k < CPL; ++k) {
+            int64_t other = __shfl_xor(x[k], h, 64);
+            x[k] = (lane & h) ? (other - x[k]) : (x[k] + other);
+        }
+    }
+    if (CPL == 2 && d == 128) {
+        int64_t a = x[0], b = x[CPL - 1];
+        x[0] = a + b;
+        x[CPL - 1] = a - b;
+    }
+}
+
+__device__ __forceinline__ int64_t rot_scale(int64_t v, int d) {
+    // 1/sqrt(d): exact shift for even powers of two, else Q15 multiply (rotate.py:190-191).
+    switch (d) {
+        case 16: return v >> 2;
+        case 64: return v >> 3;
+        case 256: return v >> 4;
+        case 32: return (v * 5793) >> 15;
+        case 128: return (v * 2896) >> 15;
+        default: return v;
+    }
+}
+
+template <int CPL>
+__global__ void __launch_bounds__(64) rotate_kernel(const int32_t *__restrict__ x, int32_t *y,
+                                                    int64_t n_vec, int d, int rounds,
+                                                    uint64_t s0a, uint64_t s0b, uint64_t s1a,
+                                                    uint64_t s1b, unsigned long long *range_err) {
+    const int64_t vec = blockIdx.x;
+    if (vec >= n_vec) return;
+    const int lane = threadIdx.x;
+    int64_t v[CPL];
+    const bool live0 = lane < d;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+        int ch = lane + 64 * k;
+        v[k] = (ch < d) ? (int64_t)x[vec * d + ch] : 0;
+    }
+    for (int r = 0; r < rounds; ++r) {
+        uint64_t wa = r == 0 ? s0a : s1a, wb = r == 0 ? s0b : s1b;
+#pragma unroll
+        for (int k = 0; k < CPL; ++k) {
+            int ch = lane + 64 * k;
+            uint64_t w = ch < 64 ? wa : wb;
+            if ((w >> (ch & 63)) & 1) v[k] = -v[k];
+        }
+        fwht_wave<CPL>(v, d);
+#pragma unroll
+        for (int k = 0; k < CPL; ++k) v[k] = rot_scale(v[k], d);
+    }
+    (void)live0;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+        int ch = lane + 64 * k;
+        if (ch < d) {
+            if (v[k] < INT32_MIN || v[k] > INT32_MAX) atomicAdd(range_err, 1ull);
+            y[vec * d + ch] = (int32_t)v[k];
+        }
+    }
+}
+
+hipError_t launch_rotate(hipStream_t s, const int32_t *x, int32_t *y, int64_t n_vec, int d,
+                         int rounds, const uint64_t (*signs)[2], unsigned long long *range_err) {
+    if (n_vec <= 0) return hipSuccess;
+    if (rounds > 2) return hipErrorInvalidValue;  // the kernel carries two sign diagonals
+    uint64_t s0a = rounds > 0 ? signs[0][0] : 0, s0b = rounds > 0 ? signs[0][1] : 0;
+    uint64_t s1a = rounds > 1 ? signs[1][0] : 0, s1b = rounds > 1 ? signs[1][1] : 0;
+    dim3 grid((unsigned)n_vec), block(64);
+    if (d <= 64)
+        hipLaunchKernelGGL(rotate_kernel<1>, grid, block, 0, s, x, y, n_vec, d, rounds, s0a, s0b,
+                           s1a, s1b, range_err);
+    else
+        hipLaunchKernelGGL(rotate_kernel<2>, grid, block, 0, s, x, y, n_vec, d, rounds, s0a, s0b,
+                           s1a, s1b, range_err);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// norm + encode
+// ---------------------------------------------------------------------------
+
+// isqrt (quantize.py:42-60): float seed, then corrected to r^2 <= a < (r+1)^2.
+__device__ __forceinline__ int64_t isqrt64(int64_t a) {
+    if (a <= 0) return 0;
+    int64_t r = (int64_t)sqrt((double)a);
+    while (r > 0 && r * r > a) --r;
+    while ((r + 1) * (r + 1) <= a) ++r;
+    return r;
+}
+
+// rshift(x, n, "even") for x >= 0 (fixed.py:83-88), n >= 1.
+__device__ __forceinline__ int64_t rshift_even(int64_t a, int n) {
+    if (n <= 0) return a << (-n);
+    int64_t half = int64_t(1) << (n - 1);
+    int64_t q = (a + half) >> n;
+    if ((a & ((int64_t(1) << n) - 1)) == half) q &= ~int64_t(1);
+    return q;
+}
+
+// _norm_wire: isqrt(sum x^2 // d) in Q16, half-even into Q(norm_frac), clamp int16.
+template <int CPL>
+__device__ int64_t norm_wire(const int64_t (&x)[CPL], int d, int norm_frac) {
+    int64_t sq = 0;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) sq += x[k] * x[k];
+    sq = wave_sum64(sq);
+    int64_t mean = sq >= 0 ? sq / d : -((-sq + d - 1) / d);   // floor division
+    int64_t n = isqrt64(mean);
+    int64_t w = rshift_even(n, QK_FRAC - norm_frac);
+    if (w > 32767) w = 32767;
+    if (w < -32768) w = -32768;
+    return w;
+}
+
+// _encode_plane: #{i : (x << (norm_frac - 1)) > norm * b_i}.
+__device__ __forceinline__ int encode_one(int64_t x, int64_t norm, const int64_t *bnd, int n_b,
+                                          int norm_frac) {
+    int64_t xs = x << (CENT_FRAC + norm_frac - QK_FRAC);
+    int c = 0;
+    for (int i = 0; i < n_b; ++i) c += (xs > norm * bnd[i]) ? 1 : 0;
+    return c;
+}
+
+template <int CPL>
+__global__ void __launch_bounds__(64) encode_kernel(const int32_t *__restrict__ x, int64_t n_vec,
+                                                    int d, int norm_frac,
+                                                    const int64_t *__restrict__ bnd, int n_b,
+                                                    int32_t *norm, uint8_t *codes) {
+    __shared__ int64_t sb[256];
+    const int lane = threadIdx.x;
+    for (int i = lane; i < n_b; i += 64) sb[i] = bnd[i];
+    __syncthreads();
+    const int64_t vec = blockIdx.x;
+    if (vec >= n_vec) return;
+    int64_t v[CPL];
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+        int ch = lane + 64 * k;
+        v[k] = ch < d ? (int64_t)x[vec * d + ch] : 0;
+    }
+    int64_t w = norm_wire<CPL>(v, d, norm_frac);
+    if (lane == 0) norm[vec] = (int32_t)w;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+        int ch = lane + 64 * k;
+        if (ch < d) codes[vec * d + ch] = (uint8_t)encode_one(v[k], w, sb, n_b, norm_frac);
+    }
+}
+
+hipError_t launch_encode(hipStream_t s, const int32_t *x, int64_t n_vec, int d, int norm_frac,
+                         const int64_t *bounds_dev, int n_bounds, int32_t *norm, uint8_t *codes) {
+    if (n_vec <= 0) return hipSuccess;
+    dim3 grid((unsigned)n_vec), block(64);
+    if (d <= 64)
+        hipLaunchKernelGGL(encode_kernel<1>, grid, block, 0, s, x, n_vec, d, norm_frac, bounds_dev,
+                           n_bounds, norm, codes);
+    else
+        hipLaunchKernelGGL(encode_kernel<2>, grid, block, 0, s, x, n_vec, d, norm_frac, bounds_dev,
+                           n_bounds, norm, codes);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// append: one wave per (sequence, token, kv head) -> one packed row
+// ---------------------------------------------------------------------------
+
+template <int CPL>
+__global__ void __launch_bounds__(64) append_kernel(Geom g, const Tables *__restrict__ tabs,
+                                                    const int32_t *__restrict__ k,
+                                                    const int32_t *__restrict__ v, int n_tok,
+                                                    int seq_lo, const int64_t *__restrict__ len_in,
+                                                    int64_t *len_out, int seq_hi,
+                                                    DevStats *st) {
+    __shared__ uint8_t codes[2][MAX_D];
+    __shared__ uint32_t row[80];
+    const int lane = threadIdx.x;
+    const int h = blockIdx.x % g.n_kv;
+    const int t = (blockIdx.x / g.n_kv) % n_tok;
+    const int b = seq_lo + blockIdx.x / (g.n_kv * n_tok);
+    const int d = g.d;
+
+    // The length bookkeeping rides on block 0: len_out = len_in + n_tok for the
+    // sequences this call appends to, len_in elsewhere (double-buffered so no
+    // block can observe a half-updated length).
+    if (blockIdx.x == 0) {
+        for (int i = lane; i < g.batch; i += 64)
+            len_out[i] = len_in[i] + ((i >= seq_lo && i < seq_hi) ? n_tok : 0);
+    }
+
+    const int64_t pos = len_in[b] + t;
+    if (pos >= g.capacity) {     // the host checks capacity first; this only guards memory
+        if (lane == 0) atomicAdd(&st->fault, 1ull);
+        return;
+    }
+    const int64_t src = (((int64_t)(b - seq_lo) * n_tok + t) * g.n_kv + h) * d;
+    int64_t nk, nv;
+    {
+        int64_t x[CPL];
+#pragma unroll
+        for (int q = 0; q < CPL; ++q) {
+            int ch = lane + 64 * q;
+            x[q] = ch < d ? (int64_t)k[src + ch] : 0;
+        }
+        nk = norm_wire<CPL>(x, d, g.norm_frac);
+#pragma unroll
+        for (int q = 0; q < CPL; ++q) {
+            int ch = lane + 64 * q;
+            if (ch < d) codes[0][ch] = (uint8_t)encode_one(x[q], nk, tabs->kbnd, (1 << g.kb) - 1,
+                                                           g.norm_frac);
+        }
+    }
+    {
+        int64_t x[CPL];
+#pragma unroll
+        for (int q = 0; q < CPL; ++q) {
+            int ch = lane + 64 * q;
+            x[q] = ch < d ? (int64_t)v[src + ch] : 0;
+        }
+        nv = norm_wire<CPL>(x, d, g.norm_frac);
+#pragma unroll
+        for (int q = 0; q < CPL; ++q) {
+            int ch = lane + 64 * q;
+            if (ch < d) codes[1][ch] = (uint8_t)encode_one(x[q], nv, tabs->vbnd, (1 << g.vb) - 1,
+                                                           g.norm_frac);
+        }
+    }
+    __syncthreads();
+
+    // Pack: dword w of the row holds row bits [32w, 32w + 32). The key field
+    // is d*kb bits, the value field d*vb bits, then k_norm | v_norm << 16.
+    const int kwords = g.key_bytes / 4, vwords = g.value_bytes / 4;
+    const int nwords = g.row_bytes / 4;
+    if (lane < nwords) {
+        uint32_t word = 0;
+        if (lane < kwords + vwords) {
+            const int field = lane < kwords ? 0 : 1;
+            const int bits = field == 0 ? g.kb : g.vb;
+            const int w = field == 0 ? lane : lane - kwords;
+            const int bit0 = 32 * w;
+            const int c_first = bit0 / bits;
+            const int c_last = (bit0 + 31) / bits;
+            for (int c = c_first; c <= c_last && c < d; ++c) {
+                int64_t off = (int64_t)c * bits - bit0;   // may be negative for a straddling code
+                uint64_t cv = codes[field][c];
+                uint64_t placed = off >= 0 ? (cv << off) : (cv >> (-off));
+                word |= (uint32_t)(placed & 0xFFFFFFFFull);
+            }
+        } else {
+            word = (uint32_t)(nk & 0xFFFF) | ((uint32_t)(nv & 0xFFFF) << 16);
+        }
+        row[lane] = word;
+    }
+    __syncthreads();
+    // Scatter into the planes: row byte 4*lane lies in exactly one plane,
+    // because every plane boundary is a field boundary and fields are whole dwords.
+    if (lane < nwords) {
+        const int byte = 4 * lane;
+        int p = 0;
+        while (p + 1 < g.n_planes && byte >= g.plane_lo[p + 1]) ++p;
+        uint8_t *dst = plane_ptr(g, b, h, p) + pos * g.plane_w[p] + (byte - g.plane_lo[p]);
+        *(uint32_t *)dst = row[lane];
+    }
+}
+
+hipError_t launch_append(hipStream_t s, const Geom &g, const Tables *t, const int32_t *k,
+                         const int32_t *v, int n_tok, int seq_lo, int seq_hi, const int64_t *len_in,
+                         int64_t *len_out, DevStats *st) {
+    const int64_t blocks = (int64_t)(seq_hi - seq_lo) * n_tok * g.n_kv;
+    if (blocks <= 0) return hipSuccess;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    dim3 grid((unsigned)blocks), block(64);
+    if (g.d <= 64)
+        hipLaunchKernelGGL(append_kernel<1>, grid, block, 0, s, g, t, k, v, n_tok, seq_lo, len_in,
+                           len_out, seq_hi, st);
+    else
+        hipLaunchKernelGGL(append_kernel<2>, grid, block, 0, s, g, t, k, v, n_tok, seq_lo, len_in,
+                           len_out, seq_hi, st);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// test hooks
+// ---------------------------------------------------------------------------
+
+__global__ void qtab_kernel(const int32_t *__restrict__ q, int n_heads, int d,
+                            const int64_t *__restrict__ c, int n_c, int64_t *table) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t total = (int64_t)n_heads * d * n_c;
+    if (i >= total) return;
+    const int ci = (int)(i % n_c);
+    const int64_t hc = i / n_c;
+    table[i] = (int64_t)q[hc] * c[ci];
+}
+
+hipError_t launch_qtab(hipStream_t s, const int32_t *q, int n_heads, int d, const int64_t *c_dev,
+                       int n_c, int64_t *table) {
+    const int64_t total = (int64_t)n_heads * d * n_c;
+    if (total <= 0) return hipSuccess;
+    hipLaunchKernelGGL(qtab_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, q,
+                       n_heads, d, c_dev, n_c, table);
+    return hipGetLastError();
+}
+
+__global__ void exp_lut_kernel(const Tables *__restrict__ t, const int64_t *__restrict__ delta,
+                               int64_t n, int32_t *p) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int64_t dl = delta[i];
+    p[i] = dl < 0 ? -1 : exp_lut(dl, t->exp_table, t->delta_max);
+}
+
+hipError_t launch_exp_lut(hipStream_t s, const Tables *t, const int64_t *delta, int64_t n,
+                          int32_t *p) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(exp_lut_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, t,
+                       delta, n, p);
+    return hipGetLastError();
+}
+
+__global__ void finalize_kernel(const int64_t *__restrict__ acc, const int64_t *__restrict__ l,
+                                int rows, int d, int64_t *out, int64_t *recip, int32_t *shift) {
+    const int r = blockIdx.x;
+    if (r >= rows) return;
+    Recip rc = reciprocal(l[r]);
+    if (threadIdx.x == 0) {
+        if (recip) recip[r] = rc.r;
+        if (shift) shift[r] = rc.shift;
+    }
+    for (int j = threadIdx.x; j < d; j += blockDim.x)
+        out[(int64_t)r * d + j] = wmul(acc[(int64_t)r * d + j], rc.r) >> rc.shift;
+}
+
+hipError_t launch_finalize(hipStream_t s, const int64_t *acc, const int64_t *l, int rows, int d,
+                           int64_t *out, int64_t *recip, int32_t *shift) {
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(finalize_kernel, dim3(rows), dim3(64), 0, s, acc, l, rows, d, out, recip,
+                       shift);
+    return hipGetLastError();
+}
+
+}  // namespace insitu

@@ -1,0 +1,274 @@
+"""GPU parity: every stage of the HIP path against the oracle and the reference's goldens.
+
+All calls go through libinsitu_hip.so (the C ABI). Bit-exact is the bar for
+every integer stage. Sizes are chosen so the oracle finishes in seconds.
+"""
+
+import numpy as np
+import pytest
+
+from oracle import hexio as hx
+from oracle import native
+from oracle.attention import attend_online, attend_two_pass
+from oracle.layout import DdrLayout
+from oracle.quantize import Cache, Format, encode, pack, unpack
+from oracle.rotate import rotate, signs_from_seed
+
+pytestmark = pytest.mark.gpu
+
+FMT = Format()
+
+
+def _cache(ctx, capacity, *, d=64, kb=4, vb=2, batch=1, n_kv=8, n_q=32):
+    from insitu_amd import QuantConfig
+    from insitu_amd.cache import CompressedCache
+    return CompressedCache(n_kv, d, capacity, QuantConfig(key_bits=kb, value_bits=vb),
+                           batch=batch, n_q_heads=n_q, ctx=ctx)
+
+
+@pytest.fixture(scope="module")
+def fixture_cache(ctx):
+    rows = np.stack([hx.bytes_rows(f"cache_rows_h{h}.hex") for h in range(8)], axis=1)
+    c = _cache(ctx, 65)
+    for h in range(8):
+        c.load_rows(rows[:, h], h)
+    c.set_length(65)
+    return c, rows
+
+
+# -- the write path -----------------------------------------------------------
+
+def test_rotation_random_vectors_and_wire(ctx):
+    from insitu_amd.rotate import Rotation
+    rot = Rotation.from_seed(64, 0, 1)
+    assert rot.sign_words()[0][0] == 0x81191FF5899001F8
+    rin = hx.lanes("rot_random_in.hex", 24, 64)
+    got = rot.apply(rin, ctx).cpu().numpy()
+    np.testing.assert_array_equal(got, hx.lanes("rot_random_out.hex", 24, 64))
+    for n in "qkv":
+        got = rot.apply(hx.lanes(f"wire_{n}.hex", 24, 64), ctx).cpu().numpy()
+        np.testing.assert_array_equal(got, hx.lanes(f"rot_{n}.hex", 24, 64))
+
+
+@pytest.mark.parametrize("d,rounds,seed", [(128, 1, 0), (64, 2, 3), (128, 2, 5), (64, 0, 0)])
+def test_rotation_other_shapes_against_oracle(ctx, d, rounds, seed):
+    from insitu_amd.rotate import Rotation
+    rng = np.random.default_rng(d + rounds)
+    x = rng.integers(-(1 << 23), 1 << 23, size=(300, d))
+    rot = Rotation.from_seed(d, seed, rounds)
+    np.testing.assert_array_equal(rot.apply(x, ctx).cpu().numpy(),
+                                  rotate(x, signs_from_seed(d, seed, rounds)))
+
+
+def test_encoder_norms_and_codes_including_ties(ctx):
+    from insitu_amd import ops
+    x = hx.lanes("enc_in.hex", 24, 64)
+    _, kb, _, vb = FMT.codebooks()
+    for bits, bnd, name in ((4, kb, "key"), (2, vb, "value")):
+        norm, codes = ops.encode(x, bnd, bits, ctx=ctx)
+        np.testing.assert_array_equal(norm, hx.scalars("enc_norm.hex", 16))
+        np.testing.assert_array_equal(codes, hx.lanes(f"enc_idx_{name}.hex", 8, 64, signed=False))
+
+
+def test_qtab(ctx):
+    from insitu_amd import ops
+    rq = hx.lanes("rot_q.hex", 24, 64)
+    got = ops.qtab(rq, FMT.codebooks()[0], ctx)
+    np.testing.assert_array_equal(got.reshape(32, -1), hx.lanes("qtab_table.hex", 43, 64 * 16))
+
+
+def test_exp_lut_every_reachable_output(ctx):
+    from insitu_amd import ops
+    d = hx.scalars("exp_in.hex", 48)
+    np.testing.assert_array_equal(ops.exp_lut(d, ctx), hx.scalars("exp_out.hex", 16, signed=False))
+    with pytest.raises(ValueError):
+        ops.exp_lut(np.array([-1]), ctx)
+
+
+def test_finalize_goldens(ctx):
+    from insitu_amd import ops
+    fa, fl = hx.lanes("fin_acc.hex", 32, 64), hx.scalars("fin_l.hex", 48)
+    out, r, sh = ops.finalize(fa, fl, ctx)
+    np.testing.assert_array_equal(r, hx.scalars("fin_recip.hex", 32, signed=False))
+    np.testing.assert_array_equal(sh, hx.scalars("fin_shift.hex", 8, signed=False))
+    np.testing.assert_array_equal(out, hx.lanes("fin_out.hex", 48, 64))
+
+
+def test_append_writes_kv_rows(ctx):
+    c = _cache(ctx, 4)
+    rk, rv = hx.lanes("rot_k.hex", 24, 64), hx.lanes("rot_v.hex", 24, 64)
+    c.append_rotated(rk[None], rv[None])
+    assert c.length == 1
+    np.testing.assert_array_equal(c.buf[0], hx.bytes_rows("kv_rows.hex"))
+
+
+@pytest.mark.parametrize("d,kb,vb", [(64, 4, 2), (128, 3, 3), (64, 1, 8), (128, 5, 2)])
+def test_append_matches_oracle_encode_pack(ctx, d, kb, vb):
+    f = Format(d=d, key_bits=kb, value_bits=vb)
+    rng = np.random.default_rng(kb * 10 + vb)
+    n = 37
+    k = rng.integers(-(1 << 23), 1 << 23, size=(n, 8, d))
+    v = rng.integers(-(1 << 23), 1 << 23, size=(n, 8, d))
+    k[3, 2] = 0                                   # zero vector: norm 0, all-equal codes
+    c = _cache(ctx, 64, d=d, kb=kb, vb=vb)
+    c.append_rotated(k[:20], v[:20])
+    c.append_rotated(k[20:], v[20:])
+    assert c.length == n
+    np.testing.assert_array_equal(c.buf, pack(encode(k, v, f), f))
+    with pytest.raises(ValueError):
+        c.append_rotated(k, v)                     # 37 + 37 > 64 (base.py:67-73)
+    assert c.length == n
+
+
+def test_device_plane_image_is_the_ddr_image(fixture_cache):
+    c, rows = fixture_cache
+    lay = DdrLayout.for_format(FMT, 8, 65)
+    assert {k: v for k, v in c.layout().items() if k in lay.describe()} == lay.describe()
+    np.testing.assert_array_equal(c.image(), hx.bytes_rows("ddr_image.hex").reshape(-1))
+    np.testing.assert_array_equal(c.buf, rows)
+
+
+# -- attention ------------------------------------------------------------------
+
+@pytest.mark.parametrize("mode", ["online", "serial", "split"])
+def test_out_online_golden(fixture_cache, mode):
+    from insitu_amd.attention import CompressedAttention
+    c, _ = fixture_cache
+    q = hx.lanes("rot_q.hex", 24, 64)
+    out, st = CompressedAttention(c).attend(q[None], mode)
+    np.testing.assert_array_equal(out.cpu().numpy().reshape(-1),
+                                  hx.lanes("out.online.hex", 24, 2048)[0])
+    assert st.n_tokens == 65 and st.acc_overflows == 0 and st.score_overflows == 0
+
+
+def test_out_two_pass_golden(fixture_cache):
+    from insitu_amd.attention import CompressedAttention
+    c, _ = fixture_cache
+    q = hx.lanes("rot_q.hex", 24, 64)
+    out, st = CompressedAttention(c).attend(q[None], "two_pass")
+    np.testing.assert_array_equal(out.cpu().numpy().reshape(-1), hx.lanes("out.hex", 24, 2048)[0])
+    assert st.rescale_events == 0
+
+
+def test_stress_query_group0_matches_oracle_stats(fixture_cache):
+    from insitu_amd.attention import CompressedAttention
+    c, rows = fixture_cache
+    q2 = hx.lanes("sm2_q.hex", 24, 64)
+    got, st = CompressedAttention(c).attend_online(q2, 0)
+    want, wst = attend_online(q2, unpack(rows[:, 0], FMT), FMT)
+    np.testing.assert_array_equal(got, want)
+
+
+def _random_cache_inputs(rng, T, d=64, n_kv=8, scale=1 << 20):
+    k = rng.integers(-scale, scale, size=(T, n_kv, d))
+    v = rng.integers(-scale, scale, size=(T, n_kv, d))
+    return k, v
+
+
+@pytest.mark.parametrize("mode", ["online", "two_pass", "split"])
+@pytest.mark.parametrize("T", [1, 2, 63, 64, 65, 700, 3000])
+def test_attend_random_contexts_against_native_oracle(ctx, mode, T):
+    from insitu_amd.attention import CompressedAttention
+    rng = np.random.default_rng(T)
+    k, v = _random_cache_inputs(rng, T)
+    c = _cache(ctx, T + 5)
+    c.append_rotated(k, v)
+    q = rng.integers(-(1 << 22), 1 << 22, size=(32, 64))
+    out, st = CompressedAttention(c).attend(q[None], mode)
+    host = Cache(8, T, FMT)
+    host.append_rotated(k, v)
+    fn = native.attend_two_pass if mode == "two_pass" else native.attend_online
+    want = np.concatenate([fn(q[4 * h:4 * h + 4], host.view(h), FMT)[0] for h in range(8)])
+    np.testing.assert_array_equal(out.cpu().numpy()[0], want)
+
+
+def test_acc_clamp_path_is_exact(ctx):
+    """Huge value norms drive the int32 accumulator into its clamp; the online path clamps
+    per token (attention.py:502-503), two-pass once at the end (:443-444)."""
+    from insitu_amd.attention import CompressedAttention
+    rng = np.random.default_rng(11)
+    T = 1000
+    k = rng.integers(-(1 << 16), 1 << 16, size=(T, 8, 64))          # flat attention
+    v = rng.integers(-(1 << 23), 1 << 23, size=(T, 8, 64))
+    v[:, :, :] = np.abs(v[:, :, :])                                 # same-sign channels pile up
+    c = _cache(ctx, T)
+    c.append_rotated(k, v)
+    q = rng.integers(-(1 << 10), 1 << 10, size=(32, 64))
+    host = Cache(8, T, FMT)
+    host.append_rotated(k, v)
+    for mode, fn in (("online", native.attend_online), ("two_pass", native.attend_two_pass)):
+        out, st = CompressedAttention(c).attend(q[None], mode)
+        want, sts = [], []
+        for h in range(8):
+            o, s = fn(q[4 * h:4 * h + 4], host.view(h), FMT)
+            want.append(o)
+            sts.append(s)
+        np.testing.assert_array_equal(out.cpu().numpy()[0], np.concatenate(want))
+        assert st.acc_overflows == sum(s.acc_overflows for s in sts)
+        assert st.acc_overflows > 0, "the case must actually reach the clamp"
+        assert st.rescale_events == sum(s.rescale_events for s in sts)
+        assert st.max_abs_acc == max(s.max_abs_acc for s in sts)
+        assert st.max_abs_score == max(s.max_abs_score for s in sts)
+
+
+def test_d128_3b3b_against_native_oracle(ctx):
+    from insitu_amd.attention import CompressedAttention
+    f = Format(d=128, key_bits=3, value_bits=3)
+    rng = np.random.default_rng(12)
+    T = 500
+    k, v = _random_cache_inputs(rng, T, d=128)
+    c = _cache(ctx, T, d=128, kb=3, vb=3)
+    c.append_rotated(k, v)
+    q = rng.integers(-(1 << 22), 1 << 22, size=(32, 128))
+    host = Cache(8, T, f)
+    host.append_rotated(k, v)
+    for mode, fn in (("online", native.attend_online), ("two_pass", native.attend_two_pass)):
+        out, _ = CompressedAttention(c).attend(q[None], mode)
+        want = np.concatenate([fn(q[4 * h:4 * h + 4], host.view(h), f)[0] for h in range(8)])
+        np.testing.assert_array_equal(out.cpu().numpy()[0], want)
+
+
+def test_batched_ragged_sequences(ctx):
+    from insitu_amd.attention import CompressedAttention
+    rng = np.random.default_rng(13)
+    lens = [1, 130, 64, 257]
+    c = _cache(ctx, 300, batch=len(lens))
+    hosts = []
+    for b, T in enumerate(lens):
+        k, v = _random_cache_inputs(rng, T)
+        c.append_rotated(k, v, seq=b)
+        h = Cache(8, T, FMT)
+        h.append_rotated(k, v)
+        hosts.append(h)
+    assert c.lengths() == lens
+    q = rng.integers(-(1 << 22), 1 << 22, size=(len(lens), 32, 64))
+    out, _ = CompressedAttention(c).attend(q, "online")
+    out = out.cpu().numpy()
+    for b, h in enumerate(hosts):
+        want = np.concatenate([native.attend_online(q[b, 4 * g:4 * g + 4], h.view(g), FMT)[0]
+                               for g in range(8)])
+        np.testing.assert_array_equal(out[b], want)
+
+
+# -- the seam: sequential decode from an empty cache ------------------------------
+
+def test_sequential_decode_from_empty_matches_the_oracle_every_step(ctx):
+    """Config-1 shape at reduced length: every step appends then attends (kernel.py:253-353)."""
+    from insitu_amd import ModelConfig, QuantConfig
+    from insitu_amd.block import AttentionBlock
+    from insitu_amd.workload import Workload
+    steps = 48
+    wl = Workload(seed=0)
+    qi, ki, vi = wl.steps(steps)
+    blk = AttentionBlock(ModelConfig.llama32_1b(), QuantConfig(key_bits=4, value_bits=2),
+                         capacity=steps, ctx=ctx)
+    sg = signs_from_seed(64, 0, 1)
+    host = Cache(8, steps, FMT)
+    for t in range(steps):
+        out = blk.step(qi[:, t], ki[:, t], vi[:, t]).cpu().numpy()[0]
+        qr, kr, vr = rotate(qi[0, t], sg), rotate(ki[0, t], sg), rotate(vi[0, t], sg)
+        host.append_rotated(kr[None], vr[None])
+        want = np.concatenate([attend_online(qr[4 * h:4 * h + 4], host.view(h), FMT)[0]
+                               for h in range(8)]).reshape(-1)
+        np.testing.assert_array_equal(out, want, err_msg=f"step {t}")
+    np.testing.assert_array_equal(blk.cache.buf, host.buf[:steps])

@@ -1,0 +1,116 @@
+"""Host-side logic of the product, and the C ABI's surface, without a GPU."""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from oracle import hexio as hx
+from oracle.codebook import gaussian
+from oracle.quantize import CompressedKV, Format, pack
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_product_codebooks_match_the_goldens_and_the_oracle():
+    from insitu_amd.codebook import Codebook
+    np.testing.assert_array_equal(Codebook.gaussian(4).centroids, hx.scalars("cb_centroids_key.hex", 20))
+    np.testing.assert_array_equal(Codebook.gaussian(4).boundaries, hx.scalars("enc_bounds_key.hex", 20))
+    np.testing.assert_array_equal(Codebook.gaussian(2).centroids, hx.scalars("cb_centroids_value.hex", 20))
+    np.testing.assert_array_equal(Codebook.gaussian(2).boundaries, hx.scalars("enc_bounds_value.hex", 20))
+    for bits in range(1, 9):
+        c, b = gaussian(bits)
+        np.testing.assert_array_equal(Codebook.gaussian(bits).centroids, c)
+        np.testing.assert_array_equal(Codebook.gaussian(bits).boundaries, b)
+    u = Codebook.uniform(3)
+    assert np.all(np.diff(u.centroids) > 0)
+    with pytest.raises(ValueError):
+        Codebook.build("nope", 2)
+
+
+def test_product_rotation_signs():
+    from insitu_amd.rotate import Rotation
+    assert Rotation.from_seed(64, 0).sign_words() == [(0x81191FF5899001F8, 0)]
+    r = Rotation.from_seed(128, 0)
+    w0, w1 = r.sign_words()[0]
+    for i in range(128):
+        bit = ((w0 if i < 64 else w1) >> (i % 64)) & 1
+        assert bit == int(r.signs[0, i] < 0)
+    with pytest.raises(ValueError):
+        Rotation.from_seed(48, 0)
+
+
+def test_product_unpack_rows_matches_the_oracle_format():
+    from insitu_amd.cache import unpack_rows
+    rows = hx.bytes_rows("cache_rows_h3.hex")
+    kv = unpack_rows(rows, 64, 4, 2)
+    back = pack(CompressedKV(kv.k_idx, kv.k_norm, kv.v_idx, kv.v_norm), Format())
+    np.testing.assert_array_equal(back, rows)
+    rng = np.random.default_rng(0)
+    f = Format(d=128, key_bits=3, value_bits=3)
+    kv = CompressedKV(rng.integers(0, 8, (5, 128)).astype(np.uint8), np.array([1, -1, 7, -32768, 32767]),
+                      rng.integers(0, 8, (5, 128)).astype(np.uint8), np.array([0, 2, -3, 4, 5]))
+    got = unpack_rows(pack(kv, f), 128, 3, 3)
+    np.testing.assert_array_equal(got.k_idx, kv.k_idx)
+    np.testing.assert_array_equal(got.v_norm, kv.v_norm)
+
+
+def test_config_validation_mirrors_the_reference():
+    from insitu_amd.config import FixedFormat, ModelConfig, QuantConfig
+    assert QuantConfig().key_bits == 3                  # the reference's default (config.py:141)
+    assert QuantConfig(key_bits=4).bytes_per_token(64) == 52
+    assert QuantConfig(key_bits=3, value_bits=3).bytes_per_token(128) == 100
+    with pytest.raises(ValueError):
+        QuantConfig(key_bits=9)
+    with pytest.raises(ValueError):
+        QuantConfig(norm_frac=16)
+    with pytest.raises(ValueError):
+        ModelConfig(hidden_size=2048, num_heads=32, num_kv_heads=7, head_dim=64)
+    with pytest.raises(ValueError):
+        ModelConfig(hidden_size=2048, num_heads=32, num_kv_heads=8, head_dim=48)
+    assert ModelConfig.llama32_1b().kv_groups == 4
+    f = FixedFormat()
+    assert f.score_shift_for(QuantConfig()) == 24 and f.acc_shift_for(QuantConfig()) == 23
+
+
+def test_workload_generator_is_deterministic_and_in_range():
+    from insitu_amd.workload import Workload, to_fixed
+    a = Workload(seed=0).steps(3)
+    b = Workload(seed=0).steps(3)
+    for x, y in zip(a, b):
+        np.testing.assert_array_equal(x, y)
+    q, k, v = a
+    assert q.shape == (1, 3, 32, 64) and k.shape == (1, 3, 8, 64)
+    assert np.abs(q).max() < (1 << 23)
+    np.testing.assert_array_equal(to_fixed([0.5 / 65536, 1.5 / 65536, 1e6, -1e6]),
+                                  [0, 2, (1 << 23) - 1, -(1 << 23)])
+    w = Workload(seed=1, head_dim=128, outlier_mode="percent")
+    assert w.q_scale.shape == (32, 128) and set(np.unique(w.q_scale)) <= {1.0, 16.0}
+
+
+def test_library_exports_every_declared_symbol():
+    """The C ABI loads and exports exactly what include/insitu.h declares (no GPU call)."""
+    from insitu_amd import _lib
+    hdr = open(os.path.join(ROOT, "include", "insitu.h")).read()
+    declared = set(re.findall(r"\b(insitu_[a-z_]+)\s*\(", hdr))
+    assert declared == set(_lib.EXPORTS), declared ^ set(_lib.EXPORTS)
+    if not os.path.exists(_lib.LIB_PATH):
+        from insitu_amd.build import build
+        build()
+    lib = ctypes.CDLL(_lib.LIB_PATH)
+    for name in sorted(declared):
+        assert hasattr(lib, name), name
+    loaded = _lib.load()
+    assert loaded.insitu_last_error() is not None
+
+
+def test_product_never_imports_the_oracle():
+    pkg = os.path.join(ROOT, "insitu_amd")
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".h", ".cpp")):
+                text = open(os.path.join(dirpath, f)).read()
+                assert not re.search(r"^\s*(from|import)\s+oracle\b", text, re.M), f
+                assert "liboracle" not in text, f
