@@ -1,0 +1,226 @@
+"""Benchmark: compressed-KV scan GB/s (% HBM peak) + us/decode-step at ctx 32k, 1 GPU.
+
+Workload: one Llama-3.2-1B-shape layer (32 query heads,
+8 KV heads, d=64, 4-bit keys / 2-bit values), batch 1. Each cache is filled by
+32,767 GPU appends of seeded synthetic q/k/v (insitu_amd/workload.py), then
+every timed step is one decode step from the wire: rotate q/k/v, append the
+token's compressed k/v row, attend over the whole cache (ctx 32,768 at the
+first step), Q16 out. The scan bytes are the compressed-cache bytes the
+attend reads: sum over KV heads of ctx * 52 B.
+
+Defeating the 256 MB Infinity Cache: R >= 20 caches of ~17 MB each (more than
+256 MB in total) are filled identically and the steps rotate through them, so
+consecutive steps never re-read a cache that is still resident.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode online]
+    python bench.py --copy-calibration      # a plain copy kernel of known size
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, published
+CTX = 32768
+N_Q, N_KV, D = 32, 8, 64
+ROW = 52
+
+
+def _args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=40)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--mode", default="online", choices=["online", "two_pass", "split", "serial"])
+    ap.add_argument("--caches", type=int, default=20)
+    ap.add_argument("--ctx", type=int, default=CTX)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true")
+    return ap.parse_args()
+
+
+def copy_calibration() -> None:
+    """A plain device copy of known size, for scaling FETCH_SIZE/WRITE_SIZE counters."""
+    import torch
+    n = 256 << 20
+    a = torch.empty(n, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(5):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_per_dispatch": n, "dispatches": 5}))
+
+
+def cpu_baseline(cache, q_rot_all, out_gpu, budget_s: float = 20.0):
+    """The oracle's numpy attend_online on this step's cache, KV group by KV group.
+
+    A bounded sample: as many KV groups as fit `budget_s` (at least one). Also
+    checks the GPU output of the same groups bit-for-bit.
+    """
+    from oracle.attention import attend_online
+    from oracle.quantize import Format
+    fmt = Format()
+    rows_t = 0.0
+    done = 0
+    t_all = 0.0
+    for h in range(N_KV):
+        kv = cache.view(h)
+        q = q_rot_all[4 * h:4 * h + 4]
+        t0 = time.perf_counter()
+        want, _ = attend_online(q, kv, fmt)
+        dt = time.perf_counter() - t0
+        if not np.array_equal(want, out_gpu[4 * h:4 * h + 4]):
+            raise AssertionError(f"bench step disagrees with the oracle on KV group {h}")
+        t_all += dt
+        rows_t += kv.k_idx.shape[0]
+        done += 1
+        if t_all > budget_s:
+            break
+    gbs = rows_t * ROW / t_all / 1e9
+    return {"value": round(gbs, 6), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"oracle numpy attend_online (per-token loop) on {done} of {N_KV} KV groups "
+                      f"of the last timed step's cache ({int(rows_t)} rows, {t_all:.1f} s); "
+                      f"affinity {len(os.sched_getaffinity(0))} cores, numpy single-threaded loop",
+            "s_per_decode_step_extrapolated": round(t_all / done * N_KV, 3)}
+
+
+def main() -> int:
+    a = _args()
+    if a.copy_calibration:
+        copy_calibration()
+        return 0
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path "
+              f"(asked for --gpus {a.gpus}); run with --gpus 1", file=sys.stderr)
+        return 2
+    import torch
+
+    from insitu_amd import ModelConfig, QuantConfig
+    from insitu_amd.attention import CompressedAttention
+    from insitu_amd.cache import CompressedCache
+    from insitu_amd.rotate import Rotation
+    from insitu_amd.runtime import default_context
+    from insitu_amd.workload import Workload
+
+    ctx = default_context(0)
+    quant = QuantConfig(key_bits=4, value_bits=2)
+    model = ModelConfig.llama32_1b()
+    rot = Rotation.for_quant(quant, D)
+    n_steps_total = a.warmup + a.steps
+    per_cache = (n_steps_total + a.caches - 1) // a.caches
+    capacity = a.ctx + per_cache
+
+    # Prefill data: ctx-1 tokens of seeded wire k/v, rotated and appended on the GPU.
+    wl = Workload(seed=0)
+    _, k, v = wl.steps(a.ctx - 1)
+    kr = rot.apply(k[0], ctx)
+    vr = rot.apply(v[0], ctx)
+    qs, ks, vs = wl.steps(n_steps_total)      # the decode tokens
+    del k, v
+    caches = []
+    for _ in range(a.caches):
+        c = CompressedCache(N_KV, D, capacity, quant, batch=1, n_q_heads=N_Q, ctx=ctx)
+        c.append_rotated(kr, vr)
+        caches.append(c)
+    attn = [CompressedAttention(c) for c in caches]
+    qs_d = ctx.to_device(qs[0], torch.int32)
+    ks_d = ctx.to_device(ks[0], torch.int32)
+    vs_d = ctx.to_device(vs[0], torch.int32)
+    torch.cuda.synchronize()
+    total_mb = sum(c.layout()["device_total_bytes"] for c in caches) / 2 ** 20
+
+    outs = [torch.empty((1, N_Q, D), dtype=torch.int32, device=ctx.torch_device)
+            for _ in range(n_steps_total)]
+    q_rot_keep = []
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(n_steps_total)]
+    lib = ctx.lib
+    from insitu_amd import _lib
+    from insitu_amd.runtime import ptr
+    mode = _lib.MODES[a.mode]
+    qr_buf = torch.empty((n_steps_total, N_Q, D), dtype=torch.int32, device=ctx.torch_device)
+    kr_buf = torch.empty((n_steps_total, N_KV, D), dtype=torch.int32, device=ctx.torch_device)
+    vr_buf = torch.empty((n_steps_total, N_KV, D), dtype=torch.int32, device=ctx.torch_device)
+    import ctypes
+    fmt = caches[0].format
+    scan_bytes = []
+
+    def step(i):
+        c = caches[i % a.caches]
+        # rotate (kernel.py:271-276), append (:282-284), attend (:337-345)
+        _lib.check(lib.insitu_rotate(ctx.handle, ptr(ks_d[i]), ptr(kr_buf[i]), N_KV, ctypes.byref(fmt)))
+        _lib.check(lib.insitu_rotate(ctx.handle, ptr(vs_d[i]), ptr(vr_buf[i]), N_KV, ctypes.byref(fmt)))
+        _lib.check(lib.insitu_rotate(ctx.handle, ptr(qs_d[i]), ptr(qr_buf[i]), N_Q, ctypes.byref(fmt)))
+        _lib.check(lib.insitu_append_seq(c.handle, 0, ptr(kr_buf[i]), ptr(vr_buf[i]), 1))
+        ev[i][0].record()
+        _lib.check(lib.insitu_attend(c.handle, ptr(qr_buf[i]), ptr(outs[i]), mode, None))
+        ev[i][1].record()
+        scan_bytes.append(N_KV * ROW * (a.ctx + i // a.caches))
+
+    for i in range(a.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(a.warmup, n_steps_total):
+        step(i)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    timed = range(a.warmup, n_steps_total)
+    attend_ms = np.array([ev[i][0].elapsed_time(ev[i][1]) for i in timed])
+    bytes_timed = np.array([scan_bytes[i] for i in timed], dtype=np.float64)
+    kernel_gbs = float(bytes_timed.sum() / (attend_ms.sum() / 1e3) / 1e9)
+    whole_gbs = float(bytes_timed.sum() / wall / 1e9)
+    per_launch_bytes = float(bytes_timed.mean())
+
+    # Correctness of the timed work: the last step against the oracle (and the CPU baseline).
+    last = n_steps_total - 1
+    out_last = outs[last].cpu().numpy()[0].astype(np.int64)
+    cache_last = caches[last % a.caches]
+    cpu = None
+    if not a.no_cpu_baseline:
+        cpu = cpu_baseline(cache_last, qr_buf[last].cpu().numpy().astype(np.int64), out_last)
+
+    res = {
+        "metric": "compressed-KV scan GB/s (% HBM peak) + us/decode-step at ctx 32k, 1 GPU",
+        "value": round(whole_gbs, 3),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(wall / a.steps * 1e3, 4),
+        "us_per_decode_step": round(wall / a.steps * 1e6, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int64",
+        "data": "synthetic (seeded N(0,1) q/k/v with 4 outlier channels x8 per head, Q8.16)",
+        "config": {"workload": "C2: Llama-3.2-1B-shape single layer, batch 1, ctx 32768, "
+                               "4b K / 2b V, decode step = rotate + append + attend",
+                   "mode": a.mode, "ctx_first_step": a.ctx, "rotating_caches": a.caches,
+                   "rotating_mb": round(total_mb, 1), "kv_heads": N_KV, "q_heads": N_Q,
+                   "head_dim": D, "row_bytes": ROW},
+        "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 3), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(kernel_gbs / HBM_PEAK_GBS, 5),
+                     "traffic": None, "kernel": "attend (all kernels of insitu_attend)",
+                     "algorithmic_bytes_per_launch": per_launch_bytes,
+                     "avg_attend_us": round(float(attend_ms.mean()) * 1e3, 3),
+                     "cycles_per_row_gpu_wide_2p4ghz": round(
+                         float(attend_ms.mean()) * 1e-3 * 2.4e9 / (per_launch_bytes / ROW), 4)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

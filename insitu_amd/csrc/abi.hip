@@ -99,6 +99,8 @@ struct insitu_cache {
     std::vector<int64_t> len_host;
     DevStats *stats = nullptr;
     int32_t *wire_scratch = nullptr;      // rotated q/k/v for insitu_step
+    void *chunk_scratch = nullptr;        // run sums and counters of the chunked attend
+    int64_t max_chunks = 0, pool = 0;
 };
 
 namespace {
@@ -361,6 +363,13 @@ int insitu_cache_create(insitu_ctx *c, const insitu_cache_desc *desc, insitu_cac
     if (e == hipSuccess)
         e = hipMalloc(&k->wire_scratch,
                       sizeof(int32_t) * (size_t)g.batch * (g.n_q + 2 * g.n_kv) * g.d);
+    if (e == hipSuccess && chunked_supported(g)) {
+        k->max_chunks = chunked_max_chunks(desc->capacity);
+        k->pool = k->max_chunks * 2 + 64;
+        const size_t nb = chunked_scratch_bytes(g, k->max_chunks, k->pool);
+        e = hipMalloc(&k->chunk_scratch, nb);
+        if (e == hipSuccess) e = hipMemsetAsync(k->chunk_scratch, 0, nb, c->stream);
+    }
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) {
         insitu_cache_destroy(k);
@@ -383,6 +392,7 @@ int insitu_cache_destroy(insitu_cache *k) {
         if (p) hipFree(p);
     if (k->stats) hipFree(k->stats);
     if (k->wire_scratch) hipFree(k->wire_scratch);
+    if (k->chunk_scratch) hipFree(k->chunk_scratch);
     delete k;
     return INSITU_OK;
 }
@@ -470,8 +480,14 @@ int insitu_append_seq(insitu_cache *k, int32_t seq, const int32_t *kr, const int
 
 static int attend_impl(insitu_cache *k, const int32_t *q, int32_t *out, int32_t mode) {
     const int64_t *len = k->len_dev[k->cur];
-    HIP_TRY(launch_attend_serial(k->ctx->stream, k->g, k->tabs, q, out, len,
-                                 mode == INSITU_TWO_PASS ? 1 : 0, k->stats),
+    const int two_pass = mode == INSITU_TWO_PASS ? 1 : 0;
+    if (mode != INSITU_SERIAL && k->chunk_scratch) {
+        HIP_TRY(launch_attend_chunked(k->ctx->stream, k->g, k->tabs, q, out, len, k->chunk_scratch,
+                                      k->max_chunks, k->pool, two_pass, k->stats),
+                "chunked attend launch");
+        return INSITU_OK;
+    }
+    HIP_TRY(launch_attend_serial(k->ctx->stream, k->g, k->tabs, q, out, len, two_pass, k->stats),
             "attend launch");
     return INSITU_OK;
 }

@@ -206,6 +206,8 @@ def test_acc_clamp_path_is_exact(ctx):
         np.testing.assert_array_equal(out.cpu().numpy()[0], np.concatenate(want))
         assert st.acc_overflows == sum(s.acc_overflows for s in sts)
         assert st.acc_overflows > 0, "the case must actually reach the clamp"
+        if mode == "online":
+            assert st.serial_fallbacks > 0, "the accumulator bound must have sent heads to the serial path"
         assert st.rescale_events == sum(s.rescale_events for s in sts)
         assert st.max_abs_acc == max(s.max_abs_acc for s in sts)
         assert st.max_abs_score == max(s.max_abs_score for s in sts)
@@ -272,3 +274,139 @@ def test_sequential_decode_from_empty_matches_the_oracle_every_step(ctx):
                                for h in range(8)]).reshape(-1)
         np.testing.assert_array_equal(out, want, err_msg=f"step {t}")
     np.testing.assert_array_equal(blk.cache.buf, host.buf[:steps])
+
+
+# -- the chunked kernels: their own edge cases --------------------------------------
+
+def _host_reference(k, v, q, f=FMT, two_pass=False):
+    T = k.shape[0]
+    host = Cache(8, T, f)
+    host.append_rotated(k, v)
+    fn = native.attend_two_pass if two_pass else native.attend_online
+    outs, sts = [], []
+    for h in range(8):
+        o, s = fn(q[4 * h:4 * h + 4], host.view(h), f)
+        outs.append(o)
+        sts.append(s)
+    return np.concatenate(outs), sts
+
+
+def test_chunked_equals_serial_and_counts_the_same_events(ctx):
+    from insitu_amd.attention import CompressedAttention
+    rng = np.random.default_rng(21)
+    T = 2600
+    k, v = _random_cache_inputs(rng, T)
+    c = _cache(ctx, T)
+    c.append_rotated(k, v)
+    q = rng.integers(-(1 << 22), 1 << 22, size=(32, 64))
+    a = CompressedAttention(c)
+    o1, s1 = a.attend(q[None], "online")
+    o2, s2 = a.attend(q[None], "serial")
+    np.testing.assert_array_equal(o1.cpu().numpy(), o2.cpu().numpy())
+    want, sts = _host_reference(k, v, q)
+    np.testing.assert_array_equal(o1.cpu().numpy()[0], want)
+    for st in (s1, s2):
+        assert st.rescale_events == sum(s.rescale_events for s in sts)
+        assert st.score_overflows == sum(s.score_overflows for s in sts)
+        assert st.max_abs_score == max(s.max_abs_score for s in sts)
+        assert st.max_abs_acc == max(s.max_abs_acc for s in sts)
+        assert st.n_tokens == T and st.acc_overflows == 0
+    assert s1.serial_fallbacks == 0
+
+
+def test_rising_scores_exhaust_the_run_pool_and_fall_back_exactly(ctx):
+    """Every token a new maximum: thousands of rescale events; the run pool overflows and
+    the affected heads are recomputed serially (still bit-exact)."""
+    from insitu_amd.attention import CompressedAttention
+    T = 1500
+    rng = np.random.default_rng(22)
+    base = rng.integers(-(1 << 20), 1 << 20, size=(1, 8, 64))
+    grow = (np.arange(1, T + 1)[:, None, None] * 2000)
+    k = np.clip(base + grow * np.sign(base), -(1 << 23), (1 << 23) - 1)
+    v = rng.integers(-(1 << 20), 1 << 20, size=(T, 8, 64))
+    c = _cache(ctx, T)
+    c.append_rotated(k, v)
+    # q aligned with the key direction so scores grow with the norm
+    qv = np.sign(base[0]).repeat(4, axis=0) * (1 << 18)
+    out, st = CompressedAttention(c).attend(qv[None], "online")
+    want, sts = _host_reference(k, v, qv)
+    np.testing.assert_array_equal(out.cpu().numpy()[0], want)
+    assert st.rescale_events == sum(s.rescale_events for s in sts) > 500
+
+
+def test_out_of_range_query_falls_back_exactly(ctx):
+    from insitu_amd.attention import CompressedAttention
+    rng = np.random.default_rng(23)
+    T = 700
+    k, v = _random_cache_inputs(rng, T)
+    c = _cache(ctx, T)
+    c.append_rotated(k, v)
+    q = rng.integers(-(1 << 22), 1 << 22, size=(32, 64))
+    q[4:8] = rng.integers(1 << 29, 1 << 30, size=(4, 64)) * rng.choice([-1, 1], size=(4, 64))
+    out, st = CompressedAttention(c).attend(q[None], "online")
+    want, _ = _host_reference(k, v, q)
+    np.testing.assert_array_equal(out.cpu().numpy()[0], want)
+    assert st.serial_fallbacks == 4 and st.range_errors > 0
+
+
+@pytest.mark.parametrize("mode", ["online", "two_pass"])
+def test_full_c2_context_against_native_oracle(ctx, mode):
+    """ctx 32,768 (BASELINE config 2 size) on the workload's own distribution."""
+    from insitu_amd.attention import CompressedAttention
+    from insitu_amd.rotate import Rotation
+    from insitu_amd.workload import Workload
+    T = 32768
+    q, k, v = Workload(seed=0).steps(T)
+    sg = signs_from_seed(64, 0, 1)
+    kr, vr = rotate(k[0], sg), rotate(v[0], sg)
+    qr = rotate(q[0, -1], sg)
+    c = _cache(ctx, T)
+    c.append_rotated(kr, vr)
+    out, st = CompressedAttention(c).attend(qr[None], mode)
+    want, sts = _host_reference(kr, vr, qr, two_pass=(mode == "two_pass"))
+    np.testing.assert_array_equal(out.cpu().numpy()[0], want)
+    assert st.serial_fallbacks == 0
+    assert st.rescale_events == sum(s.rescale_events for s in sts)
+
+
+def test_ragged_batch_multi_chunk(ctx):
+    from insitu_amd.attention import CompressedAttention
+    rng = np.random.default_rng(24)
+    lens = [1500, 1, 513, 512, 0, 2049]
+    c = _cache(ctx, 2100, batch=len(lens))
+    data = []
+    for b, T in enumerate(lens):
+        k, v = _random_cache_inputs(rng, max(T, 1))
+        if T:
+            c.append_rotated(k[:T], v[:T], seq=b)
+        data.append((k[:T], v[:T]))
+    q = rng.integers(-(1 << 22), 1 << 22, size=(len(lens), 32, 64))
+    for mode in ("online", "two_pass"):
+        out, _ = CompressedAttention(c).attend(q, mode)
+        out = out.cpu().numpy()
+        for b, (k, v) in enumerate(data):
+            if k.shape[0] == 0:
+                assert not out[b].any()
+                continue
+            want, _ = _host_reference(k, v, q[b], two_pass=(mode == "two_pass"))
+            np.testing.assert_array_equal(out[b], want, err_msg=f"{mode} seq {b}")
+
+
+def test_repeated_calls_reuse_the_counters(ctx):
+    """The chunk-completion and run-pool counters are reset by each call's last workgroup."""
+    from insitu_amd.attention import CompressedAttention
+    rng = np.random.default_rng(25)
+    T = 1300
+    k, v = _random_cache_inputs(rng, T)
+    c = _cache(ctx, T + 10)
+    c.append_rotated(k[:1000], v[:1000])
+    a = CompressedAttention(c)
+    q = rng.integers(-(1 << 22), 1 << 22, size=(32, 64))
+    first, _ = a.attend(q[None], "online")
+    for _ in range(5):
+        again, _ = a.attend(q[None], "online")
+        np.testing.assert_array_equal(again.cpu().numpy(), first.cpu().numpy())
+    c.append_rotated(k[1000:], v[1000:])
+    out, _ = a.attend(q[None], "online")
+    want, _ = _host_reference(k, v, q)
+    np.testing.assert_array_equal(out.cpu().numpy()[0], want)
