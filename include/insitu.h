@@ -146,7 +146,8 @@ int insitu_append_seq(insitu_cache *cache, int32_t seq, const int32_t *k_rot_dev
 
 /* attend_online / attend_two_pass over every sequence's cache (kernel.py:337-345,
  * attention.py:429-513). q_rot_dev int32 (batch, n_q_heads, d) rotated;
- * out_dev int32 (batch, n_q_heads, d) Q16. stats_host may be NULL (no sync). */
+ * out_dev int32 (batch, n_q_heads, d) Q16. stats_host may be NULL: then nothing
+ * synchronises and no statistics are gathered. */
 int insitu_attend(insitu_cache *cache, const int32_t *q_rot_dev, int32_t *out_dev, int32_t mode,
                   insitu_stats *stats_host);
 

@@ -365,7 +365,7 @@ int insitu_cache_create(insitu_ctx *c, const insitu_cache_desc *desc, insitu_cac
                       sizeof(int32_t) * (size_t)g.batch * (g.n_q + 2 * g.n_kv) * g.d);
     if (e == hipSuccess && chunked_supported(g)) {
         k->max_chunks = chunked_max_chunks(desc->capacity);
-        k->pool = k->max_chunks * 2 + 64;
+        k->pool = chunked_pool_slots(k->max_chunks);
         const size_t nb = chunked_scratch_bytes(g, k->max_chunks, k->pool);
         e = hipMalloc(&k->chunk_scratch, nb);
         if (e == hipSuccess) e = hipMemsetAsync(k->chunk_scratch, 0, nb, c->stream);
@@ -497,7 +497,9 @@ int insitu_attend(insitu_cache *k, const int32_t *q, int32_t *out, int32_t mode,
     if (!k || !q || !out) return fail(INSITU_EINVAL, "null argument");
     if (mode < INSITU_SEQUENTIAL || mode > INSITU_SERIAL) return fail(INSITU_EINVAL, "unknown mode");
     HIP_TRY(hipSetDevice(k->ctx->device), "hipSetDevice");
-    int rc = zero_stats(k);
+    // Statistics are only gathered (and the device counters only cleared) when
+    // the caller asks for them; without them the call never synchronises.
+    int rc = stats ? zero_stats(k) : INSITU_OK;
     if (rc) return rc;
     rc = attend_impl(k, q, out, mode);
     if (rc) return rc;
@@ -513,7 +515,7 @@ int insitu_step(insitu_cache *k, const int32_t *q, const int32_t *kw, const int3
     int32_t *kr = qr + (size_t)g.batch * g.n_q * g.d;
     int32_t *vr = kr + (size_t)g.batch * g.n_kv * g.d;
     HIP_TRY(hipSetDevice(k->ctx->device), "hipSetDevice");
-    int rc = zero_stats(k);
+    int rc = stats ? zero_stats(k) : INSITU_OK;
     if (rc) return rc;
     // kernel.py:271-276: k, v and q are all rotated; then append; then attend.
     HIP_TRY(launch_rotate(k->ctx->stream, kw, kr, (int64_t)g.batch * g.n_kv, g.d,

@@ -1,63 +1,103 @@
 // The chunked attend: attend_online / attend_two_pass (ops/attention.py:429-513)
-// over a context split into 512-token chunks, bit-exact with the sequential
+// over a context split into 1,024-token chunks, bit-exact with the sequential
 // reference.
 //
 // Why it can be exact. In the online softmax the running maximum m_t is the
-// prefix maximum of the scores, so a chunk can reproduce the reference's
-// arithmetic token for token once it knows the maximum of everything before
-// it (M_in): the tokens where s_t > m_{t-1} are the rescale events, the factor
-// there is LUT(s_t - m_{t-1}), and every other token contributes
-// floor(v_norm * p * c_v[code] / 2^23) with p = LUT(m_t - s_t) -- plain
-// integers. Between two events these terms only add, so a chunk hands over,
-// per query head, one integer segment sum (and the sum of p) per event-free
-// run plus the factor that opens each run. Replaying
+// prefix maximum of the scores, so a chunk reproduces the reference's
+// arithmetic token for token once it knows the maximum of everything before it
+// (M_in): the tokens with s_t > m_{t-1} are the rescale events, the factor
+// there is LUT(s_t - m_{t-1}), and every other token contributes the integer
+// floor(v_norm * p * c_v[code] / 2^23) with p = LUT(m_t - s_t). Between two
+// events these terms only add, so a chunk hands over, per query head, one
+// integer sum (and the sum of p) per event-free run, plus the factor opening
+// each run. Replaying
 //     acc = floor(acc * f / 2^15) + S,   l = floor(l * f / 2^15) + L
 // over the runs in order is exactly the reference recurrence, provided the
 // per-token int32 clamp of acc (attention.py:502-503) never fires; that is
-// proven per run from a bound on |acc| plus the sum of |term| bounds, and a
-// head whose bound fails is recomputed on the serial path.
+// proven per run from a bound on |acc| plus the sum of per-term bounds, and a
+// head whose bound fails is recomputed on the serial path (serial_head.h).
 //
-// Kernels (one workgroup of 256 threads per (chunk, sequence, KV head)):
-//   chunk_max    exact scores of the chunk for the G=4 query heads sharing the
-//                KV head (lane = token), chunk maxima -> cmax
-//   chunk_accum  the same scores again, M_in from cmax, an in-chunk prefix-max
-//                scan (events, p), run sums per head (wave = head, lane =
-//                channel) into a per-(sequence, head) pool; the last workgroup
-//                of a (sequence, KV head) replays the runs, finalizes and
-//                writes the Q16 output.
-// Scores: sum_ch q[ch] * c[code_ch] in fp64 FMA (every partial sum is an
-// integer below 2^51, so it is exact), then the int64 norm multiply and >>24
-// as the reference does.
+// Sequential (online) mode is one kernel. Workgroups are numbered chunk-major
+// (all chunk-0 workgroups, then all chunk-1 ...), score their chunk (lane =
+// token, G = 4 query heads per KV head), publish the chunk maximum, and read
+// the maxima of their predecessors with a decoupled look-back. A workgroup
+// only waits for workgroups with smaller numbers, which the dispatcher has
+// already placed and which publish their maximum before they wait on anyone.
+// The wait is bounded all the same: a workgroup that gives up marks its
+// (sequence, KV head) for the serial path instead of hanging. The look-back
+// words carry the value they publish, so they are read with relaxed atomics
+// and no cache maintenance. Two-pass mode needs the maximum of the whole
+// context, so it runs a chunk-max kernel first and the same chunk kernel second.
+//
+// The last workgroup of each (sequence, KV head) replays the runs, one thread
+// per (query head, channel): it walks the chunks in order with the run sums
+// loaded ahead of the walk, finalizes and writes Q16.
+// Scores: sum_ch q[ch] * c[code_ch] in fp64 FMA -- every partial sum is an
+// integer below 2^51, so it is exact -- then the int64 norm multiply and >>24
+// of the reference.
 #include "serial_head.h"
 
 namespace insitu {
 
 constexpr int CT = 256;              // threads per workgroup
-constexpr int TPT = 2;               // tokens per thread in the score phase
+constexpr int TPT = 4;               // tokens per thread in the score phase
 constexpr int CHUNK = CT * TPT;      // tokens per workgroup
 constexpr int GF = 4;                // query heads per KV head on this path
-constexpr int FLAG_POOL = 1;         // segment pool exhausted
-constexpr int EV_BIT = 0x10000;      // event marker beside the 16-bit factor
+constexpr int VB_MAX = 3;            // widest value code staged in LDS
+constexpr int HMAX = 512;            // chunks per (sequence, KV head) the replay stages in LDS
+constexpr int SLOTS0 = 64;           // run slots of chunk 0 (it sees most rescale events)
+constexpr int SLOTS = 8;             // run slots of every later chunk
+constexpr int PF = 32;               // run sums the replay loads ahead of its walk
+constexpr int SPAD = CHUNK + CHUNK / 4;   // score row with one pad slot per 4 tokens
+static_assert(TPT == 4, "the padded score layout assumes four tokens per thread");
+constexpr int FLAG_POOL = 1;         // run pool exhausted
+constexpr int FLAG_WIDE = 2;         // a run sum bound reached 2^31
+constexpr unsigned long long ST_AGG = 1ull << 62, ST_INC = 2ull << 62;
+constexpr unsigned long long ST_VAL = (1ull << 62) - 1;
+constexpr int SPIN_LIMIT = 1 << 20;
 constexpr double MAGIC = 6755399441055744.0;   // 1.5 * 2^52
 constexpr int64_t MAGIC_BITS = 0x4338000000000000LL;
 constexpr double DOT_LIMIT = 2251799813685248.0;  // 2^51
 
+// What a chunk publishes, per query head: w0 = n_seg | flags << 16 | score
+// overflows << 32, w1 = max |score| (both per chunk, all heads). Run slots
+// hold L, B and the opening factor f. Everything published between
+// workgroups goes through relaxed agent-scope atomics, which are coherent
+// across the XCDs without writing back or invalidating whole L2 caches.
 struct ChunkHdr {
-    int32_t n_seg, flags, pool_off, pad;
+    uint64_t w0, w1;
 };
 struct SegMeta {
-    int64_t L, B;
-    int32_t f, pad0;
-    int64_t pad1;
+    int64_t L, B, f, pad;
 };
 
+__device__ __forceinline__ void pub64(void *p, uint64_t v) {
+    __hip_atomic_store((uint64_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void pub32(void *p, uint32_t v) {
+    __hip_atomic_store((uint32_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t get64(const void *p) {
+    return __hip_atomic_load((uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t get32(const void *p) {
+    return __hip_atomic_load((uint32_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until this thread's stores (the relaxed atomics above) have completed.
+__device__ __forceinline__ void stores_done() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0x0F70);          // vmcnt(0)
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 struct Chunked {
-    int64_t *cmax;          // [chain][max_chunks][GF]
-    ChunkHdr *hdr;          // [chain][max_chunks][GF]
-    SegMeta *meta;          // [chain][GF][pool]
-    int64_t *segS;          // [chain][GF][pool][d]
-    unsigned int *done;     // [chain]
-    unsigned int *pool_ctr; // [chain][GF]
+    int64_t *cmax;                 // [chain][max_chunks][GF]   (two-pass)
+    unsigned long long *status;    // [chain][max_chunks][GF]   look-back words
+    ChunkHdr *hdr;                 // [chain][max_chunks][GF]
+    SegMeta *meta;                 // [chain][GF][pool]
+    int32_t *segS;                 // [chain][GF][pool][d]
+    unsigned int *done;            // [chain]
+    unsigned int *chain_fb;        // [chain]  nonzero: recompute this chain serially
     int32_t max_chunks, pool;
 };
 
@@ -67,92 +107,196 @@ struct KF {
     static constexpr int KWORDS = KBYTES / 4;
     static constexpr int NFULL = KBYTES / 16;
     static constexpr int HALF = (KBYTES % 16) / 8;
+    static constexpr int KPLANES = NFULL + HALF;
     static constexpr int CPL = D / 64;
     static constexpr uint32_t MASK = (1u << KB) - 1u;
-    static constexpr int RS = ((D * KB / 8 + D * 4 / 8 + 4) + 3) / 4 * 4;   // widest row with VB <= 4
+    static constexpr int VW = D * VB_MAX / 32;                 // value words staged per token
+    static constexpr int RS = ((D * KB / 8 + D * VB_MAX / 8 + 4) + 3) / 4 * 4;
 };
 
 __device__ __forceinline__ int64_t dbl_to_i64(double x) {
-    // x is an integer with |x| < 2^51: adding 1.5 * 2^52 puts it in the low mantissa bits.
+    // x is an integer with |x| <= 2^51: adding 1.5 * 2^52 puts it in the low mantissa bits.
     return (int64_t)__double_as_longlong(x + MAGIC) - MAGIC_BITS;
 }
 
-// Exact scores of one token for the GF heads (attention.py:333-359).
-template <int D, int KB>
-__device__ __forceinline__ void token_scores(const uint8_t *__restrict__ hb, int64_t span,
-                                             int norm_plane, int64_t t, const double (*qf)[GF],
-                                             const double *kcf, int score_shift, int64_t (&s)[GF],
-                                             uint32_t &normw) {
-    using K = KF<D, KB>;
-    uint32_t w[K::KWORDS + 1];
-#pragma unroll
-    for (int p = 0; p < K::NFULL; ++p) {
-        const uint4 v = *(const uint4 *)(hb + p * span + t * 16);
-        w[4 * p] = v.x;
-        w[4 * p + 1] = v.y;
-        w[4 * p + 2] = v.z;
-        w[4 * p + 3] = v.w;
-    }
-    if (K::HALF) {
-        const uint2 v = *(const uint2 *)(hb + K::NFULL * span + t * 8);
-        w[4 * K::NFULL] = v.x;
-        w[4 * K::NFULL + 1] = v.y;
-    }
-    w[K::KWORDS] = 0;
-    normw = *(const uint32_t *)(hb + norm_plane * span + t * 4);
-    double acc[GF];
-#pragma unroll
-    for (int h = 0; h < GF; ++h) acc[h] = 0.0;
-#pragma unroll
-    for (int c = 0; c < D; ++c) {
-        const int o = c * KB;
-        const int wi = o >> 5, sh = o & 31;
-        uint32_t code;
-        if (sh + KB <= 32)
-            code = (w[wi] >> sh) & K::MASK;
-        else
-            code = __builtin_amdgcn_alignbit(w[wi + 1], w[wi], sh) & K::MASK;
-        const double cent = kcf[code];
-#pragma unroll
-        for (int h = 0; h < GF; ++h) acc[h] = fma(qf[c][h], cent, acc[h]);
-    }
-    const int64_t kn = sext16(normw);
-#pragma unroll
-    for (int h = 0; h < GF; ++h) s[h] = wmul(dbl_to_i64(acc[h]), kn) >> score_shift;
+__device__ __forceinline__ unsigned long long st_pack(unsigned long long flag, int64_t v) {
+    return flag | (unsigned long long)(v - SCORE_LO);
+}
+__device__ __forceinline__ int64_t st_val(unsigned long long w) {
+    return (int64_t)(w & ST_VAL) + SCORE_LO;
 }
 
+template <int D, int KB>
+struct ChunkLds {
+    struct Phase {
+        int64_t s[GF][SPAD];       // token tl at tl + tl / 4: conflict-free for both phases
+        uint16_t p[GF][CHUNK];
+        uint16_t f[GF][CHUNK];
+        uint32_t evbits[GF][CHUNK / 32];
+        uint32_t vw[CHUNK][KF<D, KB>::VW];
+        int16_t vn[CHUNK];
+    };
+    struct Replay {
+        ChunkHdr hdr[GF][HMAX];
+    };
+    union {
+        Phase ph;
+        Replay rp;
+        SerialLds<KF<D, KB>::RS> fb[GF];
+    } u;
+    double qf[D][GF];
+    double kcf[16];
+    int64_t kc[16];
+    int64_t vc[16];
+    int32_t expt[256];
+    int64_t min_[GF];
+    int64_t wt[CT / 64][GF];
+    int64_t red[CT / 64][GF];
+    int qok;
+    int last;
+    int lb_fail;
+    unsigned long long ovf, mabs;
+};
+
+// Run slots of a chunk: chunk 0 owns [0, SLOTS0), chunk c > 0 owns SLOTS after it.
+__device__ __forceinline__ int slot_base(int chunk) { return chunk == 0 ? 0 : SLOTS0 + (chunk - 1) * SLOTS; }
+__device__ __forceinline__ int slot_count(int chunk) { return chunk == 0 ? SLOTS0 : SLOTS; }
+
 // Shared prologue: q (fp64) and the key centroids (fp64) into LDS; checks that
-// every head's score stays an exact fp64 integer (|dot| < 2^51).
+// every head's score stays an exact fp64 integer (|dot| < 2^51). Chunk 0 also
+// counts rotated queries beyond the +-2^27 the 24-bit seam can produce.
 template <int D>
 __device__ __forceinline__ bool load_q(const Geom &g, const Tables *__restrict__ tabs,
-                                       const int32_t *__restrict__ q, int b, int kvh,
-                                       double (*qf)[GF], double *kcf, int *qok) {
+                                       const int32_t *__restrict__ q, int b, int kvh, bool count,
+                                       double (*qf)[GF], double *kcf, int *qok, DevStats *st) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int nk = 1 << g.kb;
     if (tid < nk) kcf[tid] = (double)tabs->kc[tid];
     if (tid == 0) *qok = 1;
     __syncthreads();
-    // wave wv handles head wv
-    const int32_t *qrow = q + ((int64_t)b * g.n_q + kvh * GF + wv) * D;
+    const int32_t *qrow = q + ((int64_t)b * g.n_q + kvh * GF + wv) * D;   // wave wv: head wv
     double l1 = 0.0;
+    int64_t bad = 0;
 #pragma unroll
     for (int k = 0; k < D / 64; ++k) {
         const int c = lane + 64 * k;
         const int32_t v = qrow[c];
         qf[c][wv] = (double)v;
         l1 += fabs((double)v);
+        bad += ((int64_t)v >= Q_ROT_LIMIT || (int64_t)v <= -Q_ROT_LIMIT) ? 1 : 0;
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) l1 += __shfl_xor(l1, o, 64);
+    bad = wave_sum64(bad);
     if (lane == 0) {
         double cmax = 0.0;
         for (int i = 0; i < nk; ++i) cmax = fmax(cmax, fabs(kcf[i]));
-        // l1 and cmax are exact in fp64 (below 2^53); the product bounds |dot|.
         if (!(l1 * cmax < DOT_LIMIT)) atomicAnd(qok, 0);
+        if (count && bad) atomicAdd(&st->range_errors, (unsigned long long)bad);
     }
     __syncthreads();
     return *qok != 0;
 }
+
+// Scores of this thread's TPT tokens (t = t0 + j*CT + tid) for the GF heads.
+// Every channel's q is read once and used for all TPT tokens.
+// The key codes and norm words of this thread's TPT tokens (t = t0 + j*CT + tid).
+template <int D, int KB>
+__device__ __forceinline__ void load_keys(const Geom &g, const uint8_t *__restrict__ hb, int64_t t0,
+                                          int64_t T, uint32_t (&w)[TPT][KF<D, KB>::KWORDS + 1],
+                                          uint32_t (&normw)[TPT]) {
+    using K = KF<D, KB>;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < TPT; ++j) {
+        const int64_t t = t0 + j * CT + tid;
+        const int64_t tc = t < T ? t : 0;            // past the end: read token 0, unused
+#pragma unroll
+        for (int p = 0; p < K::NFULL; ++p) {
+            const uint4 v = *(const uint4 *)(hb + p * g.span + tc * 16);
+            w[j][4 * p] = v.x;
+            w[j][4 * p + 1] = v.y;
+            w[j][4 * p + 2] = v.z;
+            w[j][4 * p + 3] = v.w;
+        }
+        if (K::HALF) {
+            const uint2 v = *(const uint2 *)(hb + K::NFULL * g.span + tc * 8);
+            w[j][4 * K::NFULL] = v.x;
+            w[j][4 * K::NFULL + 1] = v.y;
+        }
+        w[j][K::KWORDS] = 0;
+        normw[j] = *(const uint32_t *)(hb + (g.n_planes - 1) * g.span + tc * 4);
+    }
+}
+
+// Exact scores of those tokens for the GF heads (attention.py:333-359). Every
+// channel's q is read once and used for all TPT tokens.
+template <int D, int KB>
+__device__ __forceinline__ void score_keys(const uint32_t (&w)[TPT][KF<D, KB>::KWORDS + 1],
+                                           const uint32_t (&normw)[TPT], const double (*qf)[GF],
+                                           const double *kcf, int score_shift,
+                                           int64_t (&s)[TPT][GF]) {
+    using K = KF<D, KB>;
+    double acc[TPT][GF];
+#pragma unroll
+    for (int j = 0; j < TPT; ++j)
+#pragma unroll
+        for (int h = 0; h < GF; ++h) acc[j][h] = 0.0;
+    const char *kb8 = (const char *)kcf;
+    // Every index below is a compile-time constant once the loops unroll, so the
+    // code words stay in registers. The centroid of code x sits at byte 8x of kcf.
+#pragma unroll
+    for (int wd = 0; wd < K::KWORDS; ++wd) {
+        uint32_t m0[TPT], m1[TPT];
+        if (KB == 4) {
+            // bytes of m0 hold 8 * (even nibbles), bytes of m1 hold 8 * (odd nibbles)
+#pragma unroll
+            for (int j = 0; j < TPT; ++j) {
+                m0[j] = (w[j][wd] << 3) & 0x78787878u;
+                m1[j] = (w[j][wd] >> 1) & 0x78787878u;
+            }
+        }
+#pragma unroll
+        for (int c = (32 * wd + KB - 1) / KB; c < D && c * KB < 32 * (wd + 1); ++c) {
+            const int o = c * KB;
+            const int sh = o & 31;
+            double qv[GF];
+#pragma unroll
+            for (int h = 0; h < GF; ++h) qv[h] = qf[c][h];
+#pragma unroll
+            for (int j = 0; j < TPT; ++j) {
+                uint32_t off;
+                if (KB == 4) {
+                    const int nib = sh >> 2;
+                    off = ((nib & 1 ? m1[j] : m0[j]) >> (8 * (nib >> 1))) & 0x78u;
+                } else if (sh + KB <= 32) {
+                    off = ((w[j][wd] >> sh) & K::MASK) << 3;
+                } else {
+                    off = (__builtin_amdgcn_alignbit(w[j][wd + 1], w[j][wd], sh) & K::MASK) << 3;
+                }
+                const double cent = *(const double *)(kb8 + off);
+#pragma unroll
+                for (int h = 0; h < GF; ++h) acc[j][h] = fma(qv[h], cent, acc[j][h]);
+            }
+        }
+        // Pin the accumulators at every word so the compiler cannot turn the loop
+        // nest inside out (load every centroid first, FMA at the end), which spills.
+#pragma unroll
+        for (int j = 0; j < TPT; ++j)
+#pragma unroll
+            for (int h = 0; h < GF; ++h) asm volatile("" : "+v"(acc[j][h]));
+    }
+#pragma unroll
+    for (int j = 0; j < TPT; ++j) {
+        const int64_t kn = sext16(normw[j]);
+#pragma unroll
+        for (int h = 0; h < GF; ++h) s[j][h] = wmul(dbl_to_i64(acc[j][h]), kn) >> score_shift;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// two-pass pre-pass: the maximum score of every chunk, and the score statistics
+// ---------------------------------------------------------------------------
 
 template <int D, int KB>
 __global__ void __launch_bounds__(CT) chunk_max_kernel(Geom g, const Tables *__restrict__ tabs,
@@ -171,45 +315,32 @@ __global__ void __launch_bounds__(CT) chunk_max_kernel(Geom g, const Tables *__r
     if (chunk >= nch) return;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     if (tid == 0) ovf_s = mabs_s = 0;
-    const bool ok = load_q<D>(g, tabs, q, b, kvh, qf, kcf, &qok);
-    if (chunk == 0) {
-        // The seam promises 24-bit lanes; a rotated query beyond +-2^27 is flagged
-        // (the arithmetic stays exact: such heads go to the serial path).
-        const int32_t *qrow = q + ((int64_t)b * g.n_q + kvh * GF + wv) * D;
-        unsigned long long bad = 0;
-        for (int c = lane; c < D; c += 64) {
-            const int64_t v = qrow[c];
-            bad += (v >= Q_ROT_LIMIT || v <= -Q_ROT_LIMIT) ? 1 : 0;
-        }
-        bad = (unsigned long long)wave_sum64((int64_t)bad);
-        if (lane == 0 && bad) atomicAdd(&st->range_errors, bad);
-    }
-    const uint8_t *hb = plane_ptr(g, b, kvh, 0);
-    const int score_shift = CENT_FRAC + g.norm_frac;
+    const bool ok = load_q<D>(g, tabs, q, b, kvh, chunk == 0, qf, kcf, &qok, st);
     int64_t mx[GF];
 #pragma unroll
     for (int h = 0; h < GF; ++h) mx[h] = SCORE_LO;
     unsigned long long ovf = 0;
     int64_t mabs = 0;
     if (ok) {
+        int64_t s[TPT][GF];
+        uint32_t nw[TPT];
+        uint32_t kw[TPT][KF<D, KB>::KWORDS + 1];
+        const int64_t t0 = (int64_t)chunk * CHUNK;
+        load_keys<D, KB>(g, plane_ptr(g, b, kvh, 0), t0, T, kw, nw);
+        score_keys<D, KB>(kw, nw, qf, kcf, CENT_FRAC + g.norm_frac, s);
 #pragma unroll
         for (int j = 0; j < TPT; ++j) {
-            const int64_t t = (int64_t)chunk * CHUNK + j * CT + tid;
-            if (t < T) {
-                int64_t s[GF];
-                uint32_t nw;
-                token_scores<D, KB>(hb, g.span, g.n_planes - 1, t, qf, kcf, score_shift, s, nw);
+            if (t0 + j * CT + tid >= T) continue;
 #pragma unroll
-                for (int h = 0; h < GF; ++h) {
-                    int64_t v = s[h];
-                    if (v < SCORE_LO || v > SCORE_HI) {
-                        ++ovf;
-                        v = v < SCORE_LO ? SCORE_LO : SCORE_HI;
-                    }
-                    const int64_t a = v < 0 ? -v : v;
-                    mabs = a > mabs ? a : mabs;
-                    mx[h] = v > mx[h] ? v : mx[h];
+            for (int h = 0; h < GF; ++h) {
+                int64_t v = s[j][h];
+                if (v < SCORE_LO || v > SCORE_HI) {
+                    ++ovf;
+                    v = v < SCORE_LO ? SCORE_LO : SCORE_HI;
                 }
+                const int64_t a = v < 0 ? -v : v;
+                mabs = a > mabs ? a : mabs;
+                mx[h] = v > mx[h] ? v : mx[h];
             }
         }
     }
@@ -221,7 +352,7 @@ __global__ void __launch_bounds__(CT) chunk_max_kernel(Geom g, const Tables *__r
     ovf = (unsigned long long)wave_sum64((int64_t)ovf);
     mabs = wave_max64(mabs);
     if (lane == 0) {
-        atomicAdd(&ovf_s, ovf);
+        if (ovf) atomicAdd(&ovf_s, ovf);
         atomicMax(&mabs_s, (unsigned long long)mabs);
     }
     __syncthreads();
@@ -230,407 +361,596 @@ __global__ void __launch_bounds__(CT) chunk_max_kernel(Geom g, const Tables *__r
         for (int w = 1; w < CT / 64; ++w) m = red[w][tid] > m ? red[w][tid] : m;
         ck.cmax[((int64_t)chain * ck.max_chunks + chunk) * GF + tid] = m;
     }
-    if (tid == 0 && ok) {
-        if (ovf_s) atomicAdd(&st->score_overflows, ovf_s);
-        atomicMax(&st->max_abs_score, mabs_s);
-    }
 }
 
-template <int D, int KB>
-struct AccumLds {
-    struct Phase {
-        int64_t s[GF][CHUNK];
-        int32_t p[GF][CHUNK];
-        int32_t ev[GF][CHUNK];
-        uint32_t vw[CHUNK][D * 4 / 32];
-        int32_t vn[CHUNK];
-    };
-    union {
-        Phase ph;
-        SerialLds<KF<D, KB>::RS> fb[GF];
-    } u;
-    double qf[D][GF];
-    double kcf[16];
-    int64_t kc[16];
-    int64_t vc[16];
-    int32_t expt[256];
-    int64_t min_[GF];
-    int64_t wt[CT / 64][GF];
-    int qok;
-    int last;
-};
+// ---------------------------------------------------------------------------
+// the chunk kernel
+// ---------------------------------------------------------------------------
 
-template <int D, int KB>
-__global__ void __launch_bounds__(CT) chunk_accum_kernel(Geom g, const Tables *__restrict__ tabs,
-                                                         const int32_t *__restrict__ q, int32_t *out,
-                                                         const int64_t *__restrict__ len,
-                                                         Chunked ck, int two_pass, DevStats *st) {
+template <int D, int KB, bool SEQ>
+__global__ void __launch_bounds__(CT) chunk_kernel(Geom g, const Tables *__restrict__ tabs,
+                                                   const int32_t *__restrict__ q, int32_t *out,
+                                                   const int64_t *__restrict__ len, Chunked ck,
+                                                   DevStats *st) {
     using K = KF<D, KB>;
     constexpr int CPL = K::CPL;
-    __shared__ AccumLds<D, KB> S;
-    const int chunk = blockIdx.x, chain = blockIdx.y;
+    __shared__ ChunkLds<D, KB> S;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int n_chains = g.batch * g.n_kv;
+
+    // Sequential mode numbers workgroups chunk-major, so every predecessor of
+    // a chunk has a smaller workgroup number.
+    int chunk, chain;
+    if (SEQ) {
+        chunk = (int)(blockIdx.x / (unsigned)n_chains);
+        chain = (int)(blockIdx.x % (unsigned)n_chains);
+    } else {
+        chunk = blockIdx.x;
+        chain = blockIdx.y;
+    }
     const int b = chain / g.n_kv, kvh = chain % g.n_kv;
     const int64_t T = len[b];
     const int64_t nch = T > 0 ? (T + CHUNK - 1) / CHUNK : 1;
-    if (chunk >= nch) return;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const bool has_work = chunk < nch;
     const int nv = 1 << g.vb;
-    const int vwords = g.value_bytes / 4;
     const int acc_shift = CENT_FRAC + g.norm_frac + PROB_FRAC - ACC_FRAC;
     const int score_shift = CENT_FRAC + g.norm_frac;
-
-    if (tid < 16) S.kc[tid] = tid < (1 << g.kb) ? tabs->kc[tid] : 0;
-    if (tid < 16) S.vc[tid] = tid < nv ? tabs->vc[tid] : 0;
-    S.expt[tid] = tabs->exp_table[tid];
-    const bool ok = load_q<D>(g, tabs, q, b, kvh, S.qf, S.kcf, &S.qok);
-    const uint8_t *hb = plane_ptr(g, b, kvh, 0);
     const int64_t t0 = (int64_t)chunk * CHUNK;
 
-    // -- phase 1: scores (lane = token) and the value codes of the chunk ------
-    if (ok) {
+    if (has_work) {
+        // Issue this chunk's key and value loads first; they land while the
+        // query and the tables are staged below.
+        const uint8_t *hb = plane_ptr(g, b, kvh, 0);
+        uint32_t kw[TPT][K::KWORDS + 1];
+        uint32_t nw[TPT];
+        load_keys<D, KB>(g, hb, t0, T, kw, nw);
+        const int vwords = g.value_bytes / 4;
+        uint32_t vreg[TPT][K::VW];
 #pragma unroll
         for (int j = 0; j < TPT; ++j) {
-            const int tl = j * CT + tid;
-            const int64_t t = t0 + tl;
-            int64_t s[GF];
-            uint32_t nw = 0;
-            if (t < T) {
-                token_scores<D, KB>(hb, g.span, g.n_planes - 1, t, S.qf, S.kcf, score_shift, s, nw);
+            const int64_t t = t0 + j * CT + tid;
+            const int64_t tc = t < T ? t : 0;
+            int wi = 0;
 #pragma unroll
-                for (int h = 0; h < GF; ++h)
-                    s[h] = s[h] < SCORE_LO ? SCORE_LO : (s[h] > SCORE_HI ? SCORE_HI : s[h]);
-                // value codes: they follow the key field; their planes are 16 or 8 bytes wide
-                const int vp0 = K::NFULL + K::HALF;
-                int wi = 0;
-                for (int p = vp0; wi < vwords; ++p) {
-                    const int wdt = g.plane_w[p];
-                    const uint32_t *src = (const uint32_t *)(hb + p * g.span + t * wdt);
-                    for (int i = 0; i < wdt / 4; ++i) S.u.ph.vw[tl][wi++] = src[i];
-                }
-            } else {
+            for (int p = K::KPLANES; p < K::KPLANES + (K::VW + 3) / 4; ++p) {
+                if (wi >= vwords) break;
+                const int wdt = g.plane_w[p];
+                const uint32_t *src = (const uint32_t *)(hb + p * g.span + tc * wdt);
 #pragma unroll
-                for (int h = 0; h < GF; ++h) s[h] = SCORE_LO;
+                for (int i = 0; i < 4; ++i)
+                    if (i < wdt / 4 && wi < K::VW) vreg[j][wi++] = src[i];
             }
-            S.u.ph.vn[tl] = (int32_t)sext16(nw >> 16);
-#pragma unroll
-            for (int h = 0; h < GF; ++h) S.u.ph.s[h][tl] = s[h];
         }
-    }
-    // -- phase 2: the maximum of everything before this chunk (or of all, two-pass)
-    {
-        const int64_t lim = two_pass ? nch : chunk;
-        int64_t m = SCORE_LO;
-        for (int64_t c = lane; c < lim; c += 64) {
-            const int64_t v = ck.cmax[((int64_t)chain * ck.max_chunks + c) * GF + wv];
-            m = v > m ? v : m;
+        if (tid < 16) S.kc[tid] = tid < (1 << g.kb) ? tabs->kc[tid] : 0;
+        if (tid < 16) S.vc[tid] = tid < nv ? tabs->vc[tid] : 0;
+        S.expt[tid] = tabs->exp_table[tid];
+        if (tid == 0) {
+            S.ovf = S.mabs = 0;
+            S.lb_fail = 0;
         }
-        m = wave_max64(m);
-        if (lane == 0) S.min_[wv] = m;
-    }
-    __syncthreads();
+        const bool ok = load_q<D>(g, tabs, q, b, kvh, SEQ && chunk == 0, S.qf, S.kcf, &S.qok, st);
 
-    // -- phase 3: events and p per token (thread owns TPT consecutive tokens) ---
-    if (ok) {
-        int64_t sv[GF][TPT];
-        int64_t run[GF];
+        // -- phase 1: scores (lane = token), value codes into LDS ------------------
+        int64_t mx[GF];
 #pragma unroll
-        for (int h = 0; h < GF; ++h) {
-            run[h] = SCORE_LO;
+        for (int h = 0; h < GF; ++h) mx[h] = SCORE_LO;
+        if (ok) {
+            int64_t s[TPT][GF];
+            score_keys<D, KB>(kw, nw, S.qf, S.kcf, score_shift, s);
+            unsigned long long ovf = 0;
+            int64_t mabs = 0;
 #pragma unroll
             for (int j = 0; j < TPT; ++j) {
-                sv[h][j] = S.u.ph.s[h][tid * TPT + j];
-                run[h] = sv[h][j] > run[h] ? sv[h][j] : run[h];
+                const int tl = j * CT + tid;
+                const int64_t t = t0 + tl;
+                if (t < T) {
+#pragma unroll
+                    for (int h = 0; h < GF; ++h) {
+                        int64_t v = s[j][h];
+                        if (v < SCORE_LO || v > SCORE_HI) {
+                            ++ovf;
+                            v = v < SCORE_LO ? SCORE_LO : SCORE_HI;
+                        }
+                        const int64_t a = v < 0 ? -v : v;
+                        mabs = a > mabs ? a : mabs;
+                        mx[h] = v > mx[h] ? v : mx[h];
+                        S.u.ph.s[h][tl + (tl >> 2)] = v;
+                    }
+#pragma unroll
+                    for (int i = 0; i < K::VW; ++i)
+                        if (i < vwords) S.u.ph.vw[tl][i] = vreg[j][i];
+                } else {
+#pragma unroll
+                    for (int h = 0; h < GF; ++h) S.u.ph.s[h][tl + (tl >> 2)] = SCORE_LO;
+                }
+                S.u.ph.vn[tl] = (int16_t)(nw[j] >> 16);
+            }
+            ovf = (unsigned long long)wave_sum64((int64_t)ovf);
+            mabs = wave_max64(mabs);
+            if (lane == 0) {
+                if (ovf) atomicAdd(&S.ovf, ovf);
+                atomicMax(&S.mabs, (unsigned long long)mabs);
             }
         }
-        int64_t excl[GF];
-        if (!two_pass) {
+#pragma unroll
+        for (int h = 0; h < GF; ++h) {
+            const int64_t m = wave_max64(mx[h]);
+            if (lane == 0) S.red[wv][h] = m;
+        }
+        __syncthreads();
+
+        // -- phase 2: the maximum before this chunk (sequential) or of all chunks --
+        if (SEQ) {
+            const int h = wv;
+            int64_t local = S.red[0][h];
+            for (int w = 1; w < CT / 64; ++w) local = S.red[w][h] > local ? S.red[w][h] : local;
+            unsigned long long *my = ck.status + ((int64_t)chain * ck.max_chunks + chunk) * GF + h;
+            int64_t run = SCORE_LO;
+            bool fail = false;
+            if (chunk == 0) {
+                if (lane == 0)
+                    __hip_atomic_store(my, st_pack(ST_INC, local), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                if (lane == 0)
+                    __hip_atomic_store(my, st_pack(ST_AGG, local), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                int64_t base = chunk - 1;       // the predecessor lane 0 reads
+                int spins = 0;
+                for (;;) {
+                    const int64_t pc = base - lane;
+                    unsigned long long flag = ST_INC;
+                    int64_t val = SCORE_LO;
+                    if (pc >= 0) {
+                        const unsigned long long w = __hip_atomic_load(
+                            ck.status + ((int64_t)chain * ck.max_chunks + pc) * GF + h,
+                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        flag = w & ~ST_VAL;
+                        val = st_val(w);
+                    }
+                    const unsigned long long inc = __ballot(flag == ST_INC);
+                    const int nearest = inc ? __ffsll((long long)inc) - 1 : 64;
+                    const unsigned long long wait = __ballot(flag == 0 && lane <= nearest);
+                    if (wait) {
+                        if (++spins > SPIN_LIMIT) {
+                            fail = true;
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(2);
+                        continue;
+                    }
+                    const int64_t v = wave_max64(lane <= nearest ? val : SCORE_LO);
+                    run = v > run ? v : run;
+                    if (nearest < 64) break;
+                    base -= 64;
+                }
+                const int64_t incl = run > local ? run : local;
+                if (lane == 0)
+                    __hip_atomic_store(my, st_pack(ST_INC, incl), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            }
+            if (lane == 0) {
+                S.min_[h] = run;
+                if (fail) S.lb_fail = 1;
+            }
+        } else {
+            int64_t m = SCORE_LO;
+            for (int64_t c = lane; c < nch; c += 64) {
+                const int64_t v = ck.cmax[((int64_t)chain * ck.max_chunks + c) * GF + wv];
+                m = v > m ? v : m;
+            }
+            m = wave_max64(m);
+            if (lane == 0) S.min_[wv] = m;
+        }
+        __syncthreads();
+        if (SEQ && S.lb_fail && tid == 0) atomicOr(&ck.chain_fb[chain], 1u);
+
+        // -- phase 3: events and p per token (thread owns TPT consecutive tokens) ---
+        if (ok) {
+            int64_t sv[GF][TPT];
+            int64_t excl[GF];
 #pragma unroll
             for (int h = 0; h < GF; ++h) {
-                int64_t v = run[h];
+                int64_t run = SCORE_LO;
 #pragma unroll
-                for (int o = 1; o < 64; o <<= 1) {
-                    const int64_t u = __shfl_up(v, o, 64);
-                    if (lane >= o) v = u > v ? u : v;
+                for (int j = 0; j < TPT; ++j) {
+                    sv[h][j] = S.u.ph.s[h][tid * (TPT + 1) + j];
+                    run = sv[h][j] > run ? sv[h][j] : run;
                 }
-                if (lane == 63) S.wt[wv][h] = v;
-                const int64_t u = __shfl_up(v, 1, 64);
-                excl[h] = lane > 0 ? u : SCORE_LO;
+                excl[h] = SCORE_LO;
+                if (SEQ) {
+                    int64_t v = run;
+#pragma unroll
+                    for (int o = 1; o < 64; o <<= 1) {
+                        const int64_t u = __shfl_up(v, o, 64);
+                        if (lane >= o) v = u > v ? u : v;
+                    }
+                    if (lane == 63) S.wt[wv][h] = v;
+                    const int64_t u = __shfl_up(v, 1, 64);
+                    excl[h] = lane > 0 ? u : SCORE_LO;
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int h = 0; h < GF; ++h) {
+                uint32_t bits = 0;
+                if (!SEQ) {
+                    const int64_t M = S.min_[h];
+#pragma unroll
+                    for (int j = 0; j < TPT; ++j) {
+                        const int tl = tid * TPT + j;
+                        S.u.ph.p[h][tl] = t0 + tl < T
+                            ? (uint16_t)exp_lut(M - sv[h][j], S.expt, tabs->delta_max) : (uint16_t)0;
+                    }
+                } else {
+                    int64_t prev = S.min_[h];
+                    for (int w = 0; w < wv; ++w) prev = S.wt[w][h] > prev ? S.wt[w][h] : prev;
+                    prev = excl[h] > prev ? excl[h] : prev;
+#pragma unroll
+                    for (int j = 0; j < TPT; ++j) {
+                        const int tl = tid * TPT + j;
+                        uint32_t p = 0, f = 0;
+                        if (t0 + tl < T) {
+                            const int64_t sj = sv[h][j];
+                            if (sj > prev) {
+                                f = (uint32_t)exp_lut(sj - prev, S.expt, tabs->delta_max);
+                                bits |= 1u << j;
+                                prev = sj;
+                            }
+                            p = (uint32_t)exp_lut(prev - sj, S.expt, tabs->delta_max);
+                        }
+                        S.u.ph.p[h][tl] = (uint16_t)p;     // p <= 32768 fits 16 bits unsigned
+                        S.u.ph.f[h][tl] = (uint16_t)f;
+                    }
+                }
+                // gather the event bits of 8 threads (32 consecutive tokens) into one word
+                uint32_t word = bits << ((tid & 7) * TPT);
+#pragma unroll
+                for (int o = 1; o < 8; o <<= 1) word |= __shfl_xor(word, o, 64);
+                if ((tid & 7) == 0) S.u.ph.evbits[h][tid >> 3] = word;
             }
         }
         __syncthreads();
-#pragma unroll
-        for (int h = 0; h < GF; ++h) {
-            if (two_pass) {
-                const int64_t M = S.min_[h];
-#pragma unroll
-                for (int j = 0; j < TPT; ++j) {
-                    const int tl = tid * TPT + j;
-                    const bool valid = t0 + tl < T;
-                    S.u.ph.p[h][tl] = valid ? exp_lut(M - sv[h][j], S.expt, tabs->delta_max) : 0;
-                    S.u.ph.ev[h][tl] = 0;
-                }
-            } else {
-                int64_t prev = S.min_[h];
-                for (int w = 0; w < wv; ++w) prev = S.wt[w][h] > prev ? S.wt[w][h] : prev;
-                prev = excl[h] > prev ? excl[h] : prev;
-#pragma unroll
-                for (int j = 0; j < TPT; ++j) {
-                    const int tl = tid * TPT + j;
-                    int32_t p = 0, ev = 0;
-                    if (t0 + tl < T) {
-                        const int64_t sj = sv[h][j];
-                        if (sj > prev) {
-                            ev = EV_BIT | exp_lut(sj - prev, S.expt, tabs->delta_max);
-                            prev = sj;
-                        }
-                        p = exp_lut(prev - sj, S.expt, tabs->delta_max);
-                    }
-                    S.u.ph.p[h][tl] = p;
-                    S.u.ph.ev[h][tl] = ev;
-                }
-            }
-        }
-    }
-    __syncthreads();
 
-    // -- phase 4: run sums, wave = head, lane = channel ------------------------
-    if (ok) {
-        const int h = wv;
-        int n_ev = 0;
-        for (int blk = 0; blk < CHUNK / 64; ++blk)
-            n_ev += __popcll(__ballot(S.u.ph.ev[h][blk * 64 + lane] != 0));
-        const int n_seg = n_ev + 1;
-        int off = 0, flags = 0;
-        if (lane == 0) off = (int)atomicAdd(&ck.pool_ctr[chain * GF + h], (unsigned)n_seg);
-        off = __shfl(off, 0, 64);
-        if (off + n_seg > ck.pool) flags |= FLAG_POOL;
-        if (!flags) {
-            // lane -> channel(s): code position in the value words is fixed per lane
-            int wi[CPL], sh[CPL];
+        // -- phase 4: run sums, wave = head, lane = channel ------------------------
+        if (ok) {
+            const int h = wv;
+            int64_t n_ev = 0;
+            for (int i = lane; i < CHUNK / 32; i += 64) n_ev += __popc(S.u.ph.evbits[h][i]);
+            n_ev = wave_sum64(n_ev);
+            const int n_seg = (int)n_ev + 1;
+            const int off = slot_base(chunk);
+            int flags = 0;
+            if (n_seg > slot_count(chunk)) flags |= FLAG_POOL;
+            if (!flags) {
+                int wi[CPL], sh[CPL];
 #pragma unroll
-            for (int k = 0; k < CPL; ++k) {
-                const int bit = (lane + 64 * k) * g.vb;
-                wi[k] = bit >> 5;
-                sh[k] = bit & 31;
-            }
-            const uint32_t vmask = (1u << g.vb) - 1u;
-            const int64_t vcmax = [&] {
-                int64_t m = 0;
+                for (int k = 0; k < CPL; ++k) {
+                    const int bit = (lane + 64 * k) * g.vb;
+                    wi[k] = bit >> 5;
+                    sh[k] = bit & 31;
+                }
+                const uint32_t vmask = (1u << g.vb) - 1u;
+                int64_t vcmax = 0;
                 for (int i = 0; i < nv; ++i) {
                     const int64_t a = S.vc[i] < 0 ? -S.vc[i] : S.vc[i];
-                    m = a > m ? a : m;
+                    vcmax = a > vcmax ? a : vcmax;
                 }
-                return m;
-            }();
-            SegMeta *meta = ck.meta + ((int64_t)chain * GF + h) * ck.pool;
-            int64_t *segS = ck.segS + ((int64_t)chain * GF + h) * ck.pool * D;
-            int seg = 0;
-            int32_t segf = 0;
-            int64_t Ssum[CPL];
+                SegMeta *meta = ck.meta + ((int64_t)chain * GF + h) * ck.pool;
+                int32_t *segS = ck.segS + ((int64_t)chain * GF + h) * ck.pool * D;
+                int seg = 0;
+                int32_t segf = 0;
+                int64_t Ssum[CPL];
 #pragma unroll
-            for (int k = 0; k < CPL; ++k) Ssum[k] = 0;
-            int64_t L = 0, B = 0;
-            for (int blk = 0; blk < CHUNK / 64; ++blk) {
-                const int32_t pv = S.u.ph.p[h][blk * 64 + lane];
-                const int32_t evv = S.u.ph.ev[h][blk * 64 + lane];
-                unsigned long long mask = __ballot(pv != 0);
-                while (mask) {
-                    const int i = __ffsll((long long)mask) - 1;
-                    mask &= mask - 1;
-                    const int tl = blk * 64 + i;
-                    const int32_t p = __shfl(pv, i, 64);
-                    const int32_t e = __shfl(evv, i, 64);
-                    if (e) {
-                        // close the run that the event ends
-                        if (lane == 0) {
-                            meta[off + seg].L = L;
-                            meta[off + seg].B = B;
-                            meta[off + seg].f = segf;
+                for (int k = 0; k < CPL; ++k) Ssum[k] = 0;
+                int64_t L = 0, B = 0;
+                auto close_run = [&]() {
+                    // The pool holds int32 run sums; |S| <= B, so a bound at or past
+                    // 2^31 sends the head to the serial path.
+                    if (B > ACC_HI) flags |= FLAG_WIDE;
+                    if (lane == 0) {
+                        pub64(&meta[off + seg].L, (uint64_t)L);
+                        pub64(&meta[off + seg].B, (uint64_t)B);
+                        pub64(&meta[off + seg].f, (uint64_t)(int64_t)segf);
+                    }
+#pragma unroll
+                    for (int k = 0; k < CPL; ++k)
+                        pub32(&segS[(int64_t)(off + seg) * D + lane + 64 * k], (uint32_t)(int32_t)Ssum[k]);
+                };
+                for (int blk = 0; blk < CHUNK / 64; ++blk) {
+                    const int tl0 = blk * 64;
+                    const uint32_t pv = S.u.ph.p[h][tl0 + lane];
+                    const unsigned long long evmask =
+                        (unsigned long long)S.u.ph.evbits[h][blk * 2] |
+                        ((unsigned long long)S.u.ph.evbits[h][blk * 2 + 1] << 32);
+                    unsigned long long mask = __ballot(pv != 0) | evmask;
+                    while (mask) {
+                        const int i = __ffsll((long long)mask) - 1;
+                        mask &= mask - 1;
+                        const int tl = tl0 + i;
+                        const int32_t p = (int32_t)__shfl(pv, i, 64);
+                        if ((evmask >> i) & 1ull) {
+                            close_run();
+                            ++seg;
+                            segf = S.u.ph.f[h][tl];
+#pragma unroll
+                            for (int k = 0; k < CPL; ++k) Ssum[k] = 0;
+                            L = 0;
+                            B = 0;
                         }
+                        const int32_t w = (int32_t)S.u.ph.vn[tl] * p;        // |w| <= 2^30
 #pragma unroll
-                        for (int k = 0; k < CPL; ++k) segS[(int64_t)(off + seg) * D + lane + 64 * k] = Ssum[k];
-                        ++seg;
-                        segf = e & 0xFFFF;
-#pragma unroll
-                        for (int k = 0; k < CPL; ++k) Ssum[k] = 0;
-                        L = 0;
-                        B = 0;
+                        for (int k = 0; k < CPL; ++k) {
+                            const uint32_t lo = S.u.ph.vw[tl][wi[k]];
+                            uint32_t code;
+                            if (sh[k] + g.vb <= 32)
+                                code = (lo >> sh[k]) & vmask;
+                            else
+                                code = __builtin_amdgcn_alignbit(S.u.ph.vw[tl][wi[k] + 1], lo, sh[k]) & vmask;
+                            Ssum[k] += ((int64_t)w * S.vc[code]) >> acc_shift;
+                        }
+                        L += p;
+                        const int64_t aw = w < 0 ? -(int64_t)w : (int64_t)w;
+                        B += ((aw * vcmax) >> acc_shift) + 1;
                     }
-                    const int32_t w = S.u.ph.vn[tl] * p;          // |w| <= 2^30
-#pragma unroll
-                    for (int k = 0; k < CPL; ++k) {
-                        const uint32_t lo = S.u.ph.vw[tl][wi[k]];
-                        uint32_t code;
-                        if (sh[k] + g.vb <= 32)
-                            code = (lo >> sh[k]) & vmask;
-                        else
-                            code = __builtin_amdgcn_alignbit(S.u.ph.vw[tl][wi[k] + 1], lo, sh[k]) & vmask;
-                        Ssum[k] += ((int64_t)w * S.vc[code]) >> acc_shift;
-                    }
-                    L += p;
-                    const int64_t aw = w < 0 ? -(int64_t)w : (int64_t)w;
-                    B += ((aw * vcmax) >> acc_shift) + 1;
                 }
+                close_run();
             }
             if (lane == 0) {
-                meta[off + seg].L = L;
-                meta[off + seg].B = B;
-                meta[off + seg].f = segf;
+                ChunkHdr *hp = &ck.hdr[((int64_t)chain * ck.max_chunks + chunk) * GF + h];
+                pub64(&hp->w0, (uint64_t)(uint32_t)n_seg | ((uint64_t)(uint32_t)flags << 16) |
+                                   ((uint64_t)S.ovf << 32));
+                pub64(&hp->w1, S.mabs);
             }
-#pragma unroll
-            for (int k = 0; k < CPL; ++k) segS[(int64_t)(off + seg) * D + lane + 64 * k] = Ssum[k];
+        } else if (tid < GF) {
+            // q failed its range check: the chain goes to the serial path, which counts its own
+            ChunkHdr *hp = &ck.hdr[((int64_t)chain * ck.max_chunks + chunk) * GF + tid];
+            pub64(&hp->w0, 1);
+            pub64(&hp->w1, 0);
         }
-        if (lane == 0) {
-            ChunkHdr hd;
-            hd.n_seg = n_seg;
-            hd.flags = flags;
-            hd.pool_off = off;
-            hd.pad = 0;
-            ck.hdr[((int64_t)chain * ck.max_chunks + chunk) * GF + h] = hd;
+
+        // -- phase 5: the last workgroup of this (sequence, KV head) replays -------
+        stores_done();
+        __syncthreads();
+        if (tid == 0) {
+            const unsigned prior = __hip_atomic_fetch_add(&ck.done[chain], 1u, __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_AGENT);
+            S.last = prior == (unsigned)(nch - 1);
         }
-    }
-
-    // -- phase 5: the last workgroup of this (sequence, KV head) combines ------
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const unsigned prior = atomicAdd(&ck.done[chain], 1u);
-        S.last = prior == (unsigned)(nch - 1);
-    }
-    __syncthreads();
-    if (!S.last) return;
-    __threadfence();
-
-    const int h = wv;
-    const int qh = kvh * GF + h;
-    int32_t *orow = out + ((int64_t)b * g.n_q + qh) * D;
-    bool fb = !ok;
-    int64_t acc[CPL];
-#pragma unroll
-    for (int k = 0; k < CPL; ++k) acc[k] = 0;
-    int64_t l = 0, R = 0;
-    unsigned long long events = 0;
-    if (!fb) {
-        for (int64_t c = 0; c < nch && !fb; ++c) {
-            const ChunkHdr hd = ck.hdr[((int64_t)chain * ck.max_chunks + c) * GF + h];
-            if (hd.flags) {
-                fb = true;
-                break;
+        __syncthreads();
+        if (S.last) {
+            const bool chain_fb = !ok || nch > HMAX ||
+                                  __hip_atomic_load(&ck.chain_fb[chain], __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT) != 0;
+            if (nch <= HMAX) {
+                for (int i = tid; i < nch * GF; i += CT) {
+                    const int c = i / GF, hh = i % GF;
+                    const ChunkHdr *hp = &ck.hdr[((int64_t)chain * ck.max_chunks + c) * GF + hh];
+                    S.u.rp.hdr[hh][c].w0 = get64(&hp->w0);
+                    S.u.rp.hdr[hh][c].w1 = get64(&hp->w1);
+                }
             }
-            const SegMeta *meta = ck.meta + ((int64_t)chain * GF + h) * ck.pool + hd.pool_off;
-            const int64_t *segS = ck.segS + (((int64_t)chain * GF + h) * ck.pool + hd.pool_off) * D;
-            for (int j = 0; j < hd.n_seg; ++j) {
-                const SegMeta m = meta[j];
-                if (!two_pass) {
-                    if (j > 0) {
+            __syncthreads();
+            if (wv == 0 && nch <= HMAX) {
+                // score statistics of the whole chain, from the chunk headers
+                int64_t ovf = 0, mabs = 0;
+                for (int c = lane; c < nch; c += 64) {
+                    ovf += (int64_t)(S.u.rp.hdr[0][c].w0 >> 32);
+                    const int64_t m = (int64_t)S.u.rp.hdr[0][c].w1;
+                    mabs = m > mabs ? m : mabs;
+                }
+                ovf = wave_sum64(ovf);
+                mabs = wave_max64(mabs);
+                if (lane == 0) {
+                    S.ovf = (unsigned long long)ovf;
+                    S.mabs = (unsigned long long)mabs;
+                }
+            }
+            // One thread per (query head h = wave, channel = lane [+64]): walk the
+            // chunks in order; the run sums of the next PF chunks are loaded first.
+            const int h = wv;
+            int64_t acc[CPL];
 #pragma unroll
-                        for (int k = 0; k < CPL; ++k) acc[k] = wmul(acc[k], m.f) >> PROB_FRAC;
-                        l = wmul(l, m.f) >> PROB_FRAC;
-                        R = (wmul(R, m.f) >> PROB_FRAC) + 1;
-                        ++events;
+            for (int k = 0; k < CPL; ++k) acc[k] = 0;
+            int64_t l = 0, R = 0;
+            unsigned long long events = 0;
+            bool fb = chain_fb;
+            if (!fb) {
+                const SegMeta *meta = ck.meta + ((int64_t)chain * GF + h) * ck.pool;
+                const int32_t *segS = ck.segS + ((int64_t)chain * GF + h) * ck.pool * D;
+                for (int c0 = 0; c0 < nch && !fb; c0 += PF) {
+                    int32_t pre[PF][CPL];
+                    int64_t preL[PF], preB[PF];
+#pragma unroll
+                    for (int i = 0; i < PF; ++i) {
+                        const int c = c0 + i < nch ? c0 + i : 0;
+                        const int slot = slot_base(c);
+#pragma unroll
+                        for (int k = 0; k < CPL; ++k)
+                            pre[i][k] = (int32_t)get32(&segS[(int64_t)slot * D + lane + 64 * k]);
+                        preL[i] = (int64_t)get64(&meta[slot].L);
+                        preB[i] = (int64_t)get64(&meta[slot].B);
                     }
-                    R += m.B;
-                    if (R > ACC_HI) {
-                        fb = true;
-                        break;
+#pragma unroll
+                    for (int i = 0; i < PF; ++i) {
+                        const int c = c0 + i;
+                        if (c >= nch || fb) break;
+                        const uint64_t w0 = S.u.rp.hdr[h][c].w0;
+                        const int n_seg = (int)(w0 & 0xFFFF), hflags = (int)((w0 >> 16) & 0xFFFF);
+                        if (hflags) {
+                            fb = true;
+                            break;
+                        }
+                        for (int j = 0; j < n_seg; ++j) {
+                            int32_t sv[CPL];
+                            int64_t L, B;
+                            if (j == 0) {
+#pragma unroll
+                                for (int k = 0; k < CPL; ++k) sv[k] = pre[i][k];
+                                L = preL[i];
+                                B = preB[i];
+                            } else {
+                                const int slot = slot_base(c) + j;
+#pragma unroll
+                                for (int k = 0; k < CPL; ++k)
+                                    sv[k] = (int32_t)get32(&segS[(int64_t)slot * D + lane + 64 * k]);
+                                L = (int64_t)get64(&meta[slot].L);
+                                B = (int64_t)get64(&meta[slot].B);
+                                if (SEQ) {
+                                    const int64_t f = (int64_t)get64(&meta[slot].f);
+#pragma unroll
+                                    for (int k = 0; k < CPL; ++k) acc[k] = wmul(acc[k], f) >> PROB_FRAC;
+                                    l = wmul(l, f) >> PROB_FRAC;
+                                    R = (wmul(R, f) >> PROB_FRAC) + 1;
+                                    ++events;
+                                }
+                            }
+                            R += B;
+                            if (SEQ && R > ACC_HI) {
+                                fb = true;
+                                break;
+                            }
+#pragma unroll
+                            for (int k = 0; k < CPL; ++k) acc[k] += sv[k];
+                            l += L;
+                        }
                     }
                 }
+            }
+            __syncthreads();   // the replay buffers are dead; the serial path reuses the LDS
+            const int qh = kvh * GF + h;
+            int32_t *orow = out + ((int64_t)b * g.n_q + qh) * D;
+            if (fb) {
+                // Score statistics were counted already unless q failed its range check.
+                serial_head<CPL, K::RS>(g, tabs, S.kc, S.vc, q + ((int64_t)b * g.n_q + qh) * D, b,
+                                        kvh, T, SEQ ? 0 : 1, !ok, S.u.fb[h], orow, st);
+                if (lane == 0) atomicAdd(&st->serial_fallbacks, 1ull);
+            } else {
+                unsigned long long aovf = 0;
+                if (!SEQ) {
 #pragma unroll
-                for (int k = 0; k < CPL; ++k) acc[k] += segS[(int64_t)j * D + lane + 64 * k];
-                l += m.L;
+                    for (int k = 0; k < CPL; ++k)
+                        if (acc[k] < ACC_LO || acc[k] > ACC_HI) {
+                            ++aovf;
+                            acc[k] = acc[k] < ACC_LO ? ACC_LO : ACC_HI;
+                        }
+                }
+                const Recip rc = reciprocal(l);
+                int64_t amax = 0;
+#pragma unroll
+                for (int k = 0; k < CPL; ++k) {
+                    orow[lane + 64 * k] = (int32_t)(wmul(acc[k], rc.r) >> rc.shift);
+                    const int64_t a = acc[k] < 0 ? -acc[k] : acc[k];
+                    amax = a > amax ? a : amax;
+                }
+                amax = wave_max64(amax);
+                aovf = (unsigned long long)wave_sum64((int64_t)aovf);
+                if (lane == 0) {
+                    S.wt[h][0] = (int64_t)events;
+                    S.wt[h][1] = amax;
+                    S.wt[h][2] = (int64_t)aovf;
+                }
+            }
+            if (lane == 0) S.wt[h][3] = fb ? 1 : 0;
+            __syncthreads();
+            if (tid == 0) {
+                // one set of statistics atomics per (sequence, KV head)
+                int64_t ev = 0, am = 0, ao = 0;
+                bool any = false;
+                for (int hh = 0; hh < GF; ++hh) {
+                    if (S.wt[hh][3]) continue;     // the serial path counted that head itself
+                    any = true;
+                    ev += S.wt[hh][0];
+                    am = S.wt[hh][1] > am ? S.wt[hh][1] : am;
+                    ao += S.wt[hh][2];
+                }
+                if (any) {
+                    atomicMax(&st->n_tokens, (unsigned long long)T);
+                    if (ev) atomicAdd(&st->rescale_events, (unsigned long long)ev);
+                    atomicMax(&st->max_abs_acc, (unsigned long long)am);
+                    if (ao) atomicAdd(&st->acc_overflows, (unsigned long long)ao);
+                }
+                if (ok) {
+                    if (S.ovf) atomicAdd(&st->score_overflows, S.ovf);
+                    atomicMax(&st->max_abs_score, S.mabs);
+                }
+            }
+            // Reset this chain's completion counter and look-back words for the
+            // next call: every other workgroup of the chain has finished with them.
+            for (int64_t i = tid; i < nch * GF; i += CT)
+                ck.status[(int64_t)chain * ck.max_chunks * GF + i] = 0;
+            if (tid == 0) {
+                ck.done[chain] = 0;
+                ck.chain_fb[chain] = 0;
             }
         }
     }
-    __syncthreads();   // the phase buffers are dead from here; the fallback reuses them
-    if (fb) {
-        // Score statistics were counted by chunk_max unless q failed its range check.
-        serial_head<CPL, K::RS>(g, tabs, S.kc, S.vc, q + ((int64_t)b * g.n_q + qh) * D, b, kvh, T,
-                                two_pass, !ok, S.u.fb[h], orow, st);
-        if (lane == 0) atomicAdd(&st->serial_fallbacks, 1ull);
-    } else {
-        unsigned long long aovf = 0;
-        if (two_pass) {
-#pragma unroll
-            for (int k = 0; k < CPL; ++k)
-                if (acc[k] < ACC_LO || acc[k] > ACC_HI) {
-                    ++aovf;
-                    acc[k] = acc[k] < ACC_LO ? ACC_LO : ACC_HI;
-                }
-        }
-        const Recip rc = reciprocal(l);
-        int64_t amax = 0;
-#pragma unroll
-        for (int k = 0; k < CPL; ++k) {
-            orow[lane + 64 * k] = (int32_t)(wmul(acc[k], rc.r) >> rc.shift);
-            const int64_t a = acc[k] < 0 ? -acc[k] : acc[k];
-            amax = a > amax ? a : amax;
-        }
-        amax = wave_max64(amax);
-        aovf = (unsigned long long)wave_sum64((int64_t)aovf);
-        if (lane == 0) {
-            atomicMax(&st->n_tokens, (unsigned long long)T);
-            atomicAdd(&st->rescale_events, events);
-            atomicMax(&st->max_abs_acc, (unsigned long long)amax);
-            if (aovf) atomicAdd(&st->acc_overflows, aovf);
-        }
-    }
-    // reset the counters for the next call (every other workgroup of this chain is done)
-    if (lane == 0) ck.pool_ctr[chain * GF + h] = 0;
-    if (tid == 0) ck.done[chain] = 0;
 }
 
 template <int D, int KB>
 static hipError_t launch_fast(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
                               int32_t *out, const int64_t *len, const Chunked &ck, int two_pass,
                               DevStats *st) {
-    dim3 grid((unsigned)ck.max_chunks, (unsigned)(g.batch * g.n_kv)), block(CT);
-    hipLaunchKernelGGL((chunk_max_kernel<D, KB>), grid, block, 0, s, g, t, q, len, ck, st);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((chunk_accum_kernel<D, KB>), grid, block, 0, s, g, t, q, out, len, ck,
-                       two_pass, st);
+    const unsigned chains = (unsigned)(g.batch * g.n_kv);
+    if (two_pass) {
+        dim3 grid((unsigned)ck.max_chunks, chains), block(CT);
+        hipLaunchKernelGGL((chunk_max_kernel<D, KB>), grid, block, 0, s, g, t, q, len, ck, st);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        hipLaunchKernelGGL((chunk_kernel<D, KB, false>), grid, block, 0, s, g, t, q, out, len, ck, st);
+        return hipGetLastError();
+    }
+    dim3 grid((unsigned)ck.max_chunks * chains), block(CT);
+    hipLaunchKernelGGL((chunk_kernel<D, KB, true>), grid, block, 0, s, g, t, q, out, len, ck, st);
     return hipGetLastError();
 }
 
 bool chunked_supported(const Geom &g) {
     return g.G == GF && (g.d == 64 || g.d == 128) && g.kb >= 2 && g.kb <= 4 && g.vb >= 1 &&
-           g.vb <= 4;
+           g.vb <= VB_MAX;
 }
 
 int64_t chunked_max_chunks(int64_t capacity) { return (capacity + CHUNK - 1) / CHUNK; }
 
-size_t chunked_scratch_bytes(const Geom &g, int64_t max_chunks, int64_t pool) {
+int64_t chunked_pool_slots(int64_t max_chunks) { return SLOTS0 + (max_chunks - 1) * SLOTS; }
+
+static void carve(const Geom &g, int64_t max_chunks, int64_t pool, uint8_t *p, Chunked *ck,
+                  size_t *total) {
     const int64_t chains = (int64_t)g.batch * g.n_kv;
+    size_t o = 0;
+    auto take = [&](size_t n) {
+        const size_t at = o;
+        o += (n + 255) / 256 * 256;
+        return p ? p + at : nullptr;
+    };
+    Chunked c{};
+    c.cmax = (int64_t *)take(chains * max_chunks * GF * sizeof(int64_t));
+    c.status = (unsigned long long *)take(chains * max_chunks * GF * sizeof(unsigned long long));
+    c.hdr = (ChunkHdr *)take(chains * max_chunks * GF * sizeof(ChunkHdr));
+    c.meta = (SegMeta *)take(chains * GF * pool * sizeof(SegMeta));
+    c.segS = (int32_t *)take(chains * GF * pool * g.d * sizeof(int32_t));
+    c.done = (unsigned int *)take(chains * sizeof(unsigned int));
+    c.chain_fb = (unsigned int *)take(chains * sizeof(unsigned int));
+    c.max_chunks = (int32_t)max_chunks;
+    c.pool = (int32_t)pool;
+    if (ck) *ck = c;
+    if (total) *total = o;
+}
+
+size_t chunked_scratch_bytes(const Geom &g, int64_t max_chunks, int64_t pool) {
     size_t n = 0;
-    n += chains * max_chunks * GF * sizeof(int64_t);
-    n += chains * max_chunks * GF * sizeof(ChunkHdr);
-    n += chains * GF * pool * sizeof(SegMeta);
-    n += chains * GF * pool * g.d * sizeof(int64_t);
-    n += chains * sizeof(unsigned int);
-    n += chains * GF * sizeof(unsigned int);
-    return n + 1024;
+    carve(g, max_chunks, pool, nullptr, nullptr, &n);
+    return n;
 }
 
 hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
                                  int32_t *out, const int64_t *len, void *scratch, int64_t max_chunks,
                                  int64_t pool, int two_pass, DevStats *st) {
     const int64_t chains = (int64_t)g.batch * g.n_kv;
-    uint8_t *p = (uint8_t *)scratch;
+    if (max_chunks > 65535 || chains > 65535 || max_chunks * chains > 0x7fffffff)
+        return hipErrorInvalidValue;
     Chunked ck;
-    ck.cmax = (int64_t *)p;
-    p += chains * max_chunks * GF * sizeof(int64_t);
-    ck.hdr = (ChunkHdr *)p;
-    p += chains * max_chunks * GF * sizeof(ChunkHdr);
-    ck.meta = (SegMeta *)p;
-    p += chains * GF * pool * sizeof(SegMeta);
-    ck.segS = (int64_t *)p;
-    p += chains * GF * pool * g.d * sizeof(int64_t);
-    ck.done = (unsigned int *)p;
-    p += chains * sizeof(unsigned int);
-    ck.pool_ctr = (unsigned int *)p;
-    ck.max_chunks = (int32_t)max_chunks;
-    ck.pool = (int32_t)pool;
-    if (max_chunks > 65535 || chains > 65535) return hipErrorInvalidValue;
+    carve(g, max_chunks, pool, (uint8_t *)scratch, &ck, nullptr);
 #define INSITU_FAST(DD, KK)                                                          \
     if (g.d == DD && g.kb == KK)                                                     \
         return launch_fast<DD, KK>(s, g, t, q, out, len, ck, two_pass, st);

@@ -168,6 +168,7 @@ hipError_t launch_append(hipStream_t s, const Geom &g, const Tables *t, const in
                          int64_t *len_out, DevStats *st);
 bool chunked_supported(const Geom &g);
 int64_t chunked_max_chunks(int64_t capacity);
+int64_t chunked_pool_slots(int64_t max_chunks);
 size_t chunked_scratch_bytes(const Geom &g, int64_t max_chunks, int64_t pool);
 hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
                                  int32_t *out, const int64_t *len, void *scratch, int64_t max_chunks,
