@@ -30,12 +30,15 @@
 // context, so it runs a chunk-max kernel first and the same chunk kernel second.
 //
 // The last workgroup of each (sequence, KV head) replays the runs, one thread
-// per (query head, channel): it walks the chunks in order with the run sums
-// loaded ahead of the walk, finalizes and writes Q16.
+// per (query head, channel). It reads every chunk's header in one batch of
+// loads, lists the chain's runs in order in LDS, loads their sums 64 runs at a
+// time (one round trip for a typical context, whose rescale events are few),
+// walks them, finalizes and writes Q16.
 // Scores: sum_ch q[ch] * c[code_ch] in fp64 FMA -- every partial sum is an
 // integer below 2^51, so it is exact -- then the int64 norm multiply and >>24
 // of the reference.
 #include "serial_head.h"
+#include "wave.h"
 
 namespace insitu {
 
@@ -44,12 +47,11 @@ constexpr int TPT = 4;               // tokens per thread in the score phase
 constexpr int CHUNK = CT * TPT;      // tokens per workgroup
 constexpr int GF = 4;                // query heads per KV head on this path
 constexpr int VB_MAX = 3;            // widest value code staged in LDS
-constexpr int HMAX = 512;            // chunks per (sequence, KV head) the replay stages in LDS
+constexpr int HMAX = 512;            // chunks per (sequence, KV head) on the chunked path
+constexpr int NSEG = 2048;           // runs per (sequence, KV head, query head) the replay lists
 constexpr int SLOTS0 = 64;           // run slots of chunk 0 (it sees most rescale events)
 constexpr int SLOTS = 8;             // run slots of every later chunk
-constexpr int PF = 32;               // run sums the replay loads ahead of its walk
-constexpr int SPAD = CHUNK + CHUNK / 4;   // score row with one pad slot per 4 tokens
-static_assert(TPT == 4, "the padded score layout assumes four tokens per thread");
+constexpr uint16_t RUN_EVENT = 0x8000;
 constexpr int FLAG_POOL = 1;         // run pool exhausted
 constexpr int FLAG_WIDE = 2;         // a run sum bound reached 2^31
 constexpr unsigned long long ST_AGG = 1ull << 62, ST_INC = 2ull << 62;
@@ -60,15 +62,17 @@ constexpr int64_t MAGIC_BITS = 0x4338000000000000LL;
 constexpr double DOT_LIMIT = 2251799813685248.0;  // 2^51
 
 // What a chunk publishes, per query head: w0 = n_seg | flags << 16 | score
-// overflows << 32, w1 = max |score| (both per chunk, all heads). Run slots
-// hold L, B and the opening factor f. Everything published between
-// workgroups goes through relaxed agent-scope atomics, which are coherent
-// across the XCDs without writing back or invalidating whole L2 caches.
+// overflows << 32, w1 = max |score| (both per chunk, all heads). A run slot
+// holds lf = L | f << 32 (L = sum of p < 2^26, f = the factor opening the run,
+// <= 2^15) and b = B, the bound on |run sum| (< 2^31 unless FLAG_WIDE is set).
+// Everything published between workgroups goes through relaxed agent-scope
+// atomics, which are coherent across the XCDs without writing back or
+// invalidating whole L2 caches.
 struct ChunkHdr {
     uint64_t w0, w1;
 };
 struct SegMeta {
-    int64_t L, B, f, pad;
+    uint64_t lf, b;
 };
 
 __device__ __forceinline__ void pub64(void *p, uint64_t v) {
@@ -126,18 +130,23 @@ __device__ __forceinline__ int64_t st_val(unsigned long long w) {
     return (int64_t)(w & ST_VAL) + SCORE_LO;
 }
 
+// An active token of a chunk (p != 0, or a rescale event) for one head:
+// token index | event << 10 | value << 11, the value being p, or the factor f
+// at an event (where p is LUT(0), the same for every event).
+static_assert(CHUNK <= 1024, "ActRec holds a 10-bit token index");
+__device__ __forceinline__ uint32_t act_rec(int tl, bool ev, uint32_t val) {
+    return (uint32_t)tl | (ev ? 1u << 10 : 0u) | (val << 11);
+}
+
 template <int D, int KB>
 struct ChunkLds {
     struct Phase {
-        int64_t s[GF][SPAD];       // token tl at tl + tl / 4: conflict-free for both phases
-        uint16_t p[GF][CHUNK];
-        uint16_t f[GF][CHUNK];
-        uint32_t evbits[GF][CHUNK / 32];
+        uint32_t rec[GF][CHUNK];   // each head's active tokens in order (ActRec)
         uint32_t vw[CHUNK][KF<D, KB>::VW];
         int16_t vn[CHUNK];
     };
     struct Replay {
-        ChunkHdr hdr[GF][HMAX];
+        uint16_t slot[GF][NSEG];   // the runs in order: slot | RUN_EVENT when a rescale opens it
     };
     union {
         Phase ph;
@@ -148,8 +157,13 @@ struct ChunkLds {
     double kcf[16];
     int64_t kc[16];
     int64_t vc[16];
+    int32_t vc32[16];
+    int64_t vcmax;
     int32_t expt[256];
-    int64_t min_[GF];
+    int32_t cntw[CT / 64][GF];     // active tokens per wave and head
+    int32_t evw[CT / 64][GF];      // rescale events per wave and head
+    int64_t min_[GF];              // the maximum before this chunk (two-pass: of all chunks)
+    int64_t lmax[GF];              // this chunk's own maximum
     int64_t wt[CT / 64][GF];
     int64_t red[CT / 64][GF];
     int qok;
@@ -161,6 +175,7 @@ struct ChunkLds {
 // Run slots of a chunk: chunk 0 owns [0, SLOTS0), chunk c > 0 owns SLOTS after it.
 __device__ __forceinline__ int slot_base(int chunk) { return chunk == 0 ? 0 : SLOTS0 + (chunk - 1) * SLOTS; }
 __device__ __forceinline__ int slot_count(int chunk) { return chunk == 0 ? SLOTS0 : SLOTS; }
+static_assert(SLOTS0 + (HMAX - 1) * SLOTS < RUN_EVENT, "run slots of the chunked path fit 15 bits");
 
 // Shared prologue: q (fp64) and the key centroids (fp64) into LDS; checks that
 // every head's score stays an exact fp64 integer (|dot| < 2^51). Chunk 0 also
@@ -175,32 +190,30 @@ __device__ __forceinline__ bool load_q(const Geom &g, const Tables *__restrict__
     if (tid == 0) *qok = 1;
     __syncthreads();
     const int32_t *qrow = q + ((int64_t)b * g.n_q + kvh * GF + wv) * D;   // wave wv: head wv
-    double l1 = 0.0;
+    int64_t l1 = 0;
     int64_t bad = 0;
 #pragma unroll
     for (int k = 0; k < D / 64; ++k) {
         const int c = lane + 64 * k;
         const int32_t v = qrow[c];
         qf[c][wv] = (double)v;
-        l1 += fabs((double)v);
+        l1 += v < 0 ? -(int64_t)v : (int64_t)v;
         bad += ((int64_t)v >= Q_ROT_LIMIT || (int64_t)v <= -Q_ROT_LIMIT) ? 1 : 0;
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) l1 += __shfl_xor(l1, o, 64);
-    bad = wave_sum64(bad);
+    l1 = wave_sum_i64(l1);                  // < 2^38: exact as a double below
+    bad = wave_sum_i64(bad);
     if (lane == 0) {
         double cmax = 0.0;
         for (int i = 0; i < nk; ++i) cmax = fmax(cmax, fabs(kcf[i]));
-        if (!(l1 * cmax < DOT_LIMIT)) atomicAnd(qok, 0);
+        if (!((double)l1 * cmax < DOT_LIMIT)) atomicAnd(qok, 0);
         if (count && bad) atomicAdd(&st->range_errors, (unsigned long long)bad);
     }
     __syncthreads();
     return *qok != 0;
 }
 
-// Scores of this thread's TPT tokens (t = t0 + j*CT + tid) for the GF heads.
-// Every channel's q is read once and used for all TPT tokens.
-// The key codes and norm words of this thread's TPT tokens (t = t0 + j*CT + tid).
+// The key codes and norm words of this thread's TPT consecutive tokens
+// (t = t0 + TPT * tid + j): a wave reads one contiguous span of each plane.
 template <int D, int KB>
 __device__ __forceinline__ void load_keys(const Geom &g, const uint8_t *__restrict__ hb, int64_t t0,
                                           int64_t T, uint32_t (&w)[TPT][KF<D, KB>::KWORDS + 1],
@@ -209,7 +222,7 @@ __device__ __forceinline__ void load_keys(const Geom &g, const uint8_t *__restri
     const int tid = threadIdx.x;
 #pragma unroll
     for (int j = 0; j < TPT; ++j) {
-        const int64_t t = t0 + j * CT + tid;
+        const int64_t t = t0 + tid * TPT + j;
         const int64_t tc = t < T ? t : 0;            // past the end: read token 0, unused
 #pragma unroll
         for (int p = 0; p < K::NFULL; ++p) {
@@ -330,7 +343,7 @@ __global__ void __launch_bounds__(CT) chunk_max_kernel(Geom g, const Tables *__r
         score_keys<D, KB>(kw, nw, qf, kcf, CENT_FRAC + g.norm_frac, s);
 #pragma unroll
         for (int j = 0; j < TPT; ++j) {
-            if (t0 + j * CT + tid >= T) continue;
+            if (t0 + tid * TPT + j >= T) continue;
 #pragma unroll
             for (int h = 0; h < GF; ++h) {
                 int64_t v = s[j][h];
@@ -346,11 +359,11 @@ __global__ void __launch_bounds__(CT) chunk_max_kernel(Geom g, const Tables *__r
     }
 #pragma unroll
     for (int h = 0; h < GF; ++h) {
-        const int64_t m = wave_max64(mx[h]);
+        const int64_t m = wave_max_i64(mx[h]);
         if (lane == 0) red[wv][h] = m;
     }
-    ovf = (unsigned long long)wave_sum64((int64_t)ovf);
-    mabs = wave_max64(mabs);
+    ovf = (unsigned long long)wave_sum_i64((int64_t)ovf);
+    mabs = wave_max_i64(mabs);
     if (lane == 0) {
         if (ovf) atomicAdd(&ovf_s, ovf);
         atomicMax(&mabs_s, (unsigned long long)mabs);
@@ -368,14 +381,15 @@ __global__ void __launch_bounds__(CT) chunk_max_kernel(Geom g, const Tables *__r
 // ---------------------------------------------------------------------------
 
 template <int D, int KB, bool SEQ>
-__global__ void __launch_bounds__(CT) chunk_kernel(Geom g, const Tables *__restrict__ tabs,
+__global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__restrict__ tabs,
                                                    const int32_t *__restrict__ q, int32_t *out,
                                                    const int64_t *__restrict__ len, Chunked ck,
                                                    DevStats *st) {
     using K = KF<D, KB>;
     constexpr int CPL = K::CPL;
     __shared__ ChunkLds<D, KB> S;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);      // wave index, scalar
     const int n_chains = g.batch * g.n_kv;
 
     // Sequential mode numbers workgroups chunk-major, so every predecessor of
@@ -408,21 +422,33 @@ __global__ void __launch_bounds__(CT) chunk_kernel(Geom g, const Tables *__restr
         uint32_t vreg[TPT][K::VW];
 #pragma unroll
         for (int j = 0; j < TPT; ++j) {
-            const int64_t t = t0 + j * CT + tid;
+            const int64_t t = t0 + tid * TPT + j;
             const int64_t tc = t < T ? t : 0;
-            int wi = 0;
+            // The value field is split into 16-byte planes (the last one narrower),
+            // so value word 4 * p + i sits in word i of value plane p.
 #pragma unroll
-            for (int p = K::KPLANES; p < K::KPLANES + (K::VW + 3) / 4; ++p) {
-                if (wi >= vwords) break;
-                const int wdt = g.plane_w[p];
-                const uint32_t *src = (const uint32_t *)(hb + p * g.span + tc * wdt);
+            for (int p = 0; p < (K::VW + 3) / 4; ++p) {
+                const int wdt = g.plane_w[K::KPLANES + p];
+                const uint32_t *src = (const uint32_t *)(hb + (K::KPLANES + p) * g.span + tc * wdt);
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    if (i < wdt / 4 && wi < K::VW) vreg[j][wi++] = src[i];
+                    if (4 * p + i < K::VW) vreg[j][4 * p + i] = 4 * p + i < vwords ? src[i] : 0u;
             }
         }
         if (tid < 16) S.kc[tid] = tid < (1 << g.kb) ? tabs->kc[tid] : 0;
-        if (tid < 16) S.vc[tid] = tid < nv ? tabs->vc[tid] : 0;
+        if (tid < 16) {
+            const int64_t c = tid < nv ? tabs->vc[tid] : 0;
+            S.vc[tid] = c;
+            S.vc32[tid] = (int32_t)c;                 // |centroid| < 2^18 (Q1.15)
+        }
+        if (tid == 0) {
+            int64_t m = 0;
+            for (int i = 0; i < nv; ++i) {
+                const int64_t a = tabs->vc[i] < 0 ? -tabs->vc[i] : tabs->vc[i];
+                m = a > m ? a : m;
+            }
+            S.vcmax = m;
+        }
         S.expt[tid] = tabs->exp_table[tid];
         if (tid == 0) {
             S.ovf = S.mabs = 0;
@@ -430,8 +456,10 @@ __global__ void __launch_bounds__(CT) chunk_kernel(Geom g, const Tables *__restr
         }
         const bool ok = load_q<D>(g, tabs, q, b, kvh, SEQ && chunk == 0, S.qf, S.kcf, &S.qok, st);
 
-        // -- phase 1: scores (lane = token), value codes into LDS ------------------
+        // -- phase 1: scores of the thread's TPT consecutive tokens, which stay in
+        // registers for the scan; value codes into LDS ----------------------------
         int64_t mx[GF];
+        int64_t sv[GF][TPT];      // clamped scores, SCORE_LO past the end
 #pragma unroll
         for (int h = 0; h < GF; ++h) mx[h] = SCORE_LO;
         if (ok) {
@@ -441,7 +469,7 @@ __global__ void __launch_bounds__(CT) chunk_kernel(Geom g, const Tables *__restr
             int64_t mabs = 0;
 #pragma unroll
             for (int j = 0; j < TPT; ++j) {
-                const int tl = j * CT + tid;
+                const int tl = tid * TPT + j;
                 const int64_t t = t0 + tl;
                 if (t < T) {
 #pragma unroll
@@ -454,19 +482,19 @@ __global__ void __launch_bounds__(CT) chunk_kernel(Geom g, const Tables *__restr
                         const int64_t a = v < 0 ? -v : v;
                         mabs = a > mabs ? a : mabs;
                         mx[h] = v > mx[h] ? v : mx[h];
-                        S.u.ph.s[h][tl + (tl >> 2)] = v;
+                        sv[h][j] = v;
                     }
 #pragma unroll
                     for (int i = 0; i < K::VW; ++i)
                         if (i < vwords) S.u.ph.vw[tl][i] = vreg[j][i];
                 } else {
 #pragma unroll
-                    for (int h = 0; h < GF; ++h) S.u.ph.s[h][tl + (tl >> 2)] = SCORE_LO;
+                    for (int h = 0; h < GF; ++h) sv[h][j] = SCORE_LO;
                 }
                 S.u.ph.vn[tl] = (int16_t)(nw[j] >> 16);
             }
-            ovf = (unsigned long long)wave_sum64((int64_t)ovf);
-            mabs = wave_max64(mabs);
+            ovf = (unsigned long long)wave_sum_i64((int64_t)ovf);
+            mabs = wave_max_i64(mabs);
             if (lane == 0) {
                 if (ovf) atomicAdd(&S.ovf, ovf);
                 atomicMax(&S.mabs, (unsigned long long)mabs);
@@ -474,7 +502,7 @@ __global__ void __launch_bounds__(CT) chunk_kernel(Geom g, const Tables *__restr
         }
 #pragma unroll
         for (int h = 0; h < GF; ++h) {
-            const int64_t m = wave_max64(mx[h]);
+            const int64_t m = wave_max_i64(mx[h]);
             if (lane == 0) S.red[wv][h] = m;
         }
         __syncthreads();
@@ -519,7 +547,7 @@ __global__ void __launch_bounds__(CT) chunk_kernel(Geom g, const Tables *__restr
                         __builtin_amdgcn_s_sleep(2);
                         continue;
                     }
-                    const int64_t v = wave_max64(lane <= nearest ? val : SCORE_LO);
+                    const int64_t v = wave_max_i64(lane <= nearest ? val : SCORE_LO);
                     run = v > run ? v : run;
                     if (nearest < 64) break;
                     base -= 64;
@@ -531,6 +559,7 @@ __global__ void __launch_bounds__(CT) chunk_kernel(Geom g, const Tables *__restr
             }
             if (lane == 0) {
                 S.min_[h] = run;
+                S.lmax[h] = local;
                 if (fail) S.lb_fail = 1;
             }
         } else {
@@ -539,159 +568,192 @@ __global__ void __launch_bounds__(CT) chunk_kernel(Geom g, const Tables *__restr
                 const int64_t v = ck.cmax[((int64_t)chain * ck.max_chunks + c) * GF + wv];
                 m = v > m ? v : m;
             }
-            m = wave_max64(m);
+            m = wave_max_i64(m);
             if (lane == 0) S.min_[wv] = m;
         }
         __syncthreads();
         if (SEQ && S.lb_fail && tid == 0) atomicOr(&ck.chain_fb[chain], 1u);
 
-        // -- phase 3: events and p per token (thread owns TPT consecutive tokens) ---
+        // -- phase 3: events, p, and each head's active tokens listed in order ----
+        // (the thread owns TPT consecutive tokens). Two exact shortcuts: a head
+        // whose chunk maximum does not exceed the maximum before the chunk has no
+        // rescale event, so it needs no scan; and a token at or below
+        // prev - delta_max has p = 0 for every later prev too (prev only grows),
+        // so a wave whose tokens are all that far down does no LUT work.
         if (ok) {
-            int64_t sv[GF][TPT];
+            const int64_t dm = tabs->delta_max;
+            bool evh[GF];
             int64_t excl[GF];
+            bool any_ev = false;
 #pragma unroll
             for (int h = 0; h < GF; ++h) {
-                int64_t run = SCORE_LO;
+                evh[h] = SEQ && uni64(S.lmax[h]) > uni64(S.min_[h]);
+                any_ev = any_ev || evh[h];
+                excl[h] = SCORE_LO;
+                if (evh[h]) {
+                    int64_t run = SCORE_LO;
+#pragma unroll
+                    for (int j = 0; j < TPT; ++j) run = sv[h][j] > run ? sv[h][j] : run;
+                    const int64_t v = wave_scan64<OpMax64>(run, SCORE_LO);
+                    if (lane == 63) S.wt[wv][h] = v;
+                    excl[h] = wave_shr1_64(v, SCORE_LO);
+                }
+            }
+            if (any_ev) __syncthreads();
+            uint32_t rec[GF][TPT];
+            uint32_t act[GF];
+            uint32_t pos[GF];
+#pragma unroll
+            for (int h = 0; h < GF; ++h) {
+                int64_t prev = uni64(S.min_[h]);
+                if (evh[h]) {
+                    for (int w = 0; w < wv; ++w) prev = S.wt[w][h] > prev ? S.wt[w][h] : prev;
+                    prev = excl[h] > prev ? excl[h] : prev;
+                }
+                act[h] = 0;
+                pos[h] = 0;
+                bool live = false;
 #pragma unroll
                 for (int j = 0; j < TPT; ++j) {
-                    sv[h][j] = S.u.ph.s[h][tid * (TPT + 1) + j];
-                    run = sv[h][j] > run ? sv[h][j] : run;
+                    rec[h][j] = 0;
+                    live = live || (t0 + tid * TPT + j < T && sv[h][j] > prev - dm);
                 }
-                excl[h] = SCORE_LO;
-                if (SEQ) {
-                    int64_t v = run;
+                int32_t tot = 0, evt = 0;
+                if (__ballot(live)) {
+                    // Branch-free per token: an event records f = LUT(s - prev)
+                    // (its own p is LUT(0)), any other token p = LUT(prev - s).
+                    uint32_t nev = 0;
 #pragma unroll
-                    for (int o = 1; o < 64; o <<= 1) {
-                        const int64_t u = __shfl_up(v, o, 64);
-                        if (lane >= o) v = u > v ? u : v;
+                    for (int j = 0; j < TPT; ++j) {
+                        const int tl = tid * TPT + j;
+                        const bool in = t0 + tl < T;
+                        const int64_t sj = sv[h][j];
+                        const bool ev = evh[h] && in && sj > prev;
+                        const uint32_t val = (uint32_t)exp_lut(ev ? sj - prev : prev - sj, S.expt, dm);
+                        prev = ev ? sj : prev;
+                        rec[h][j] = act_rec(tl, ev, val);          // val <= 2^15 fits the field
+                        act[h] |= (in && (ev || val != 0)) ? 1u << j : 0u;
+                        nev += ev ? 1u : 0u;
                     }
-                    if (lane == 63) S.wt[wv][h] = v;
-                    const int64_t u = __shfl_up(v, 1, 64);
-                    excl[h] = lane > 0 ? u : SCORE_LO;
+                    const uint32_t c = (uint32_t)__popc(act[h]);
+                    const uint32_t incl = wave_scan_add32(c);
+                    pos[h] = incl - c;
+                    tot = __builtin_amdgcn_readlane((int)incl, 63);
+                    if (evh[h]) evt = __builtin_amdgcn_readlane((int)wave_scan_add32(nev), 63);
+                }
+                if (lane == 0) {
+                    S.cntw[wv][h] = tot;
+                    S.evw[wv][h] = evt;
                 }
             }
             __syncthreads();
 #pragma unroll
             for (int h = 0; h < GF; ++h) {
-                uint32_t bits = 0;
-                if (!SEQ) {
-                    const int64_t M = S.min_[h];
+                if (!act[h]) continue;
+                uint32_t at = pos[h];
+                for (int w = 0; w < wv; ++w) at += (uint32_t)S.cntw[w][h];
 #pragma unroll
-                    for (int j = 0; j < TPT; ++j) {
-                        const int tl = tid * TPT + j;
-                        S.u.ph.p[h][tl] = t0 + tl < T
-                            ? (uint16_t)exp_lut(M - sv[h][j], S.expt, tabs->delta_max) : (uint16_t)0;
-                    }
-                } else {
-                    int64_t prev = S.min_[h];
-                    for (int w = 0; w < wv; ++w) prev = S.wt[w][h] > prev ? S.wt[w][h] : prev;
-                    prev = excl[h] > prev ? excl[h] : prev;
-#pragma unroll
-                    for (int j = 0; j < TPT; ++j) {
-                        const int tl = tid * TPT + j;
-                        uint32_t p = 0, f = 0;
-                        if (t0 + tl < T) {
-                            const int64_t sj = sv[h][j];
-                            if (sj > prev) {
-                                f = (uint32_t)exp_lut(sj - prev, S.expt, tabs->delta_max);
-                                bits |= 1u << j;
-                                prev = sj;
-                            }
-                            p = (uint32_t)exp_lut(prev - sj, S.expt, tabs->delta_max);
-                        }
-                        S.u.ph.p[h][tl] = (uint16_t)p;     // p <= 32768 fits 16 bits unsigned
-                        S.u.ph.f[h][tl] = (uint16_t)f;
-                    }
-                }
-                // gather the event bits of 8 threads (32 consecutive tokens) into one word
-                uint32_t word = bits << ((tid & 7) * TPT);
-#pragma unroll
-                for (int o = 1; o < 8; o <<= 1) word |= __shfl_xor(word, o, 64);
-                if ((tid & 7) == 0) S.u.ph.evbits[h][tid >> 3] = word;
+                for (int j = 0; j < TPT; ++j)
+                    if ((act[h] >> j) & 1u) S.u.ph.rec[h][at++] = rec[h][j];
             }
         }
         __syncthreads();
 
-        // -- phase 4: run sums, wave = head, lane = channel ------------------------
+        // -- phase 4: run sums over the active list, wave = head, lane = channel --
         if (ok) {
             const int h = wv;
-            int64_t n_ev = 0;
-            for (int i = lane; i < CHUNK / 32; i += 64) n_ev += __popc(S.u.ph.evbits[h][i]);
-            n_ev = wave_sum64(n_ev);
-            const int n_seg = (int)n_ev + 1;
+            int n_act = 0, n_ev = 0;
+#pragma unroll
+            for (int w = 0; w < CT / 64; ++w) {
+                n_act += S.cntw[w][h];
+                n_ev += S.evw[w][h];
+            }
+            n_act = uni32(n_act);
+            n_ev = uni32(n_ev);
+            const int n_seg = n_ev + 1;
             const int off = slot_base(chunk);
             int flags = 0;
             if (n_seg > slot_count(chunk)) flags |= FLAG_POOL;
             if (!flags) {
-                int wi[CPL], sh[CPL];
+                int wi[CPL], wi1[CPL], sh[CPL];
 #pragma unroll
                 for (int k = 0; k < CPL; ++k) {
                     const int bit = (lane + 64 * k) * g.vb;
                     wi[k] = bit >> 5;
+                    wi1[k] = wi[k] + 1 < K::VW ? wi[k] + 1 : wi[k];
                     sh[k] = bit & 31;
                 }
                 const uint32_t vmask = (1u << g.vb) - 1u;
-                int64_t vcmax = 0;
-                for (int i = 0; i < nv; ++i) {
-                    const int64_t a = S.vc[i] < 0 ? -S.vc[i] : S.vc[i];
-                    vcmax = a > vcmax ? a : vcmax;
-                }
+                const uint64_t vcmax = (uint64_t)uni64(S.vcmax);
+                const int32_t pev = uni32(S.expt[0]);       // p of an event token: LUT(0)
                 SegMeta *meta = ck.meta + ((int64_t)chain * GF + h) * ck.pool;
                 int32_t *segS = ck.segS + ((int64_t)chain * GF + h) * ck.pool * D;
                 int seg = 0;
                 int32_t segf = 0;
-                int64_t Ssum[CPL];
+                // |run sum| <= B < 2^31 unless FLAG_WIDE, so int32 sums are exact
+                // whenever they are used.
+                int32_t Ssum[CPL];
 #pragma unroll
                 for (int k = 0; k < CPL; ++k) Ssum[k] = 0;
                 int64_t L = 0, B = 0;
                 auto close_run = [&]() {
-                    // The pool holds int32 run sums; |S| <= B, so a bound at or past
-                    // 2^31 sends the head to the serial path.
                     if (B > ACC_HI) flags |= FLAG_WIDE;
                     if (lane == 0) {
-                        pub64(&meta[off + seg].L, (uint64_t)L);
-                        pub64(&meta[off + seg].B, (uint64_t)B);
-                        pub64(&meta[off + seg].f, (uint64_t)(int64_t)segf);
+                        pub64(&meta[off + seg].lf, (uint64_t)L | ((uint64_t)(uint32_t)segf << 32));
+                        pub64(&meta[off + seg].b, (uint64_t)B);
                     }
 #pragma unroll
                     for (int k = 0; k < CPL; ++k)
-                        pub32(&segS[(int64_t)(off + seg) * D + lane + 64 * k], (uint32_t)(int32_t)Ssum[k]);
+                        pub32(&segS[(int64_t)(off + seg) * D + lane + 64 * k], (uint32_t)Ssum[k]);
                 };
-                for (int blk = 0; blk < CHUNK / 64; ++blk) {
-                    const int tl0 = blk * 64;
-                    const uint32_t pv = S.u.ph.p[h][tl0 + lane];
-                    const unsigned long long evmask =
-                        (unsigned long long)S.u.ph.evbits[h][blk * 2] |
-                        ((unsigned long long)S.u.ph.evbits[h][blk * 2 + 1] << 32);
-                    unsigned long long mask = __ballot(pv != 0) | evmask;
-                    while (mask) {
-                        const int i = __ffsll((long long)mask) - 1;
-                        mask &= mask - 1;
-                        const int tl = tl0 + i;
-                        const int32_t p = (int32_t)__shfl(pv, i, 64);
-                        if ((evmask >> i) & 1ull) {
-                            close_run();
-                            ++seg;
-                            segf = S.u.ph.f[h][tl];
+                for (int a0 = 0; a0 < n_act; a0 += 64) {
+                    // lane i decodes list entry a0 + i; the walk reads them back with readlane
+                    const int e = a0 + lane;
+                    const uint32_t r = e < n_act ? S.u.ph.rec[h][e] : 0u;
+                    const int tl_i = (int)(r & 1023u);
+                    const int ev_i = (int)((r >> 10) & 1u);
+                    const int val_i = (int)(r >> 11);
+                    const int32_t p_i = ev_i ? pev : val_i;
+                    const int32_t w_i = (int32_t)S.u.ph.vn[tl_i] * p_i;       // |w| <= 2^30
+                    const uint64_t aw = (uint64_t)(w_i < 0 ? -(int64_t)w_i : (int64_t)w_i);
+                    const int32_t bw_i = (int32_t)((aw * vcmax) >> acc_shift) + 1;
+                    const int cnt = n_act - a0 < 64 ? n_act - a0 : 64;
+                    for (int j0 = 0; j0 < cnt; j0 += 8) {
+                        // the centroids of the next 8 entries first (independent LDS reads)
+                        int32_t cv[8][CPL];
 #pragma unroll
-                            for (int k = 0; k < CPL; ++k) Ssum[k] = 0;
-                            L = 0;
-                            B = 0;
-                        }
-                        const int32_t w = (int32_t)S.u.ph.vn[tl] * p;        // |w| <= 2^30
+                        for (int jj = 0; jj < 8; ++jj) {
+                            const int tl = __builtin_amdgcn_readlane(tl_i, j0 + jj);
 #pragma unroll
-                        for (int k = 0; k < CPL; ++k) {
-                            const uint32_t lo = S.u.ph.vw[tl][wi[k]];
-                            uint32_t code;
-                            if (sh[k] + g.vb <= 32)
-                                code = (lo >> sh[k]) & vmask;
-                            else
-                                code = __builtin_amdgcn_alignbit(S.u.ph.vw[tl][wi[k] + 1], lo, sh[k]) & vmask;
-                            Ssum[k] += ((int64_t)w * S.vc[code]) >> acc_shift;
+                            for (int k = 0; k < CPL; ++k) {
+                                // both words, unconditionally: a 3-bit code may cross into
+                                // the next one (the last word never has a code crossing out)
+                                const uint32_t lo = S.u.ph.vw[tl][wi[k]];
+                                const uint32_t hi = S.u.ph.vw[tl][wi1[k]];
+                                cv[jj][k] = S.vc32[__builtin_amdgcn_alignbit(hi, lo, sh[k]) & vmask];
+                            }
                         }
-                        L += p;
-                        const int64_t aw = w < 0 ? -(int64_t)w : (int64_t)w;
-                        B += ((aw * vcmax) >> acc_shift) + 1;
+#pragma unroll
+                        for (int jj = 0; jj < 8; ++jj) {
+                            const int j = j0 + jj;
+                            if (j < cnt) {
+                                if (__builtin_amdgcn_readlane(ev_i, j)) {
+                                    close_run();
+                                    ++seg;
+                                    segf = __builtin_amdgcn_readlane(val_i, j);
+#pragma unroll
+                                    for (int k = 0; k < CPL; ++k) Ssum[k] = 0;
+                                    L = 0;
+                                    B = 0;
+                                }
+                                const int32_t w = __builtin_amdgcn_readlane(w_i, j);
+#pragma unroll
+                                for (int k = 0; k < CPL; ++k)
+                                    Ssum[k] += (int32_t)(((int64_t)w * cv[jj][k]) >> acc_shift);
+                                L += __builtin_amdgcn_readlane(p_i, j);
+                                B += __builtin_amdgcn_readlane(bw_i, j);
+                            }
+                        }
                     }
                 }
                 close_run();
@@ -722,32 +784,10 @@ __global__ void __launch_bounds__(CT) chunk_kernel(Geom g, const Tables *__restr
             const bool chain_fb = !ok || nch > HMAX ||
                                   __hip_atomic_load(&ck.chain_fb[chain], __ATOMIC_RELAXED,
                                                     __HIP_MEMORY_SCOPE_AGENT) != 0;
-            if (nch <= HMAX) {
-                for (int i = tid; i < nch * GF; i += CT) {
-                    const int c = i / GF, hh = i % GF;
-                    const ChunkHdr *hp = &ck.hdr[((int64_t)chain * ck.max_chunks + c) * GF + hh];
-                    S.u.rp.hdr[hh][c].w0 = get64(&hp->w0);
-                    S.u.rp.hdr[hh][c].w1 = get64(&hp->w1);
-                }
-            }
-            __syncthreads();
-            if (wv == 0 && nch <= HMAX) {
-                // score statistics of the whole chain, from the chunk headers
-                int64_t ovf = 0, mabs = 0;
-                for (int c = lane; c < nch; c += 64) {
-                    ovf += (int64_t)(S.u.rp.hdr[0][c].w0 >> 32);
-                    const int64_t m = (int64_t)S.u.rp.hdr[0][c].w1;
-                    mabs = m > mabs ? m : mabs;
-                }
-                ovf = wave_sum64(ovf);
-                mabs = wave_max64(mabs);
-                if (lane == 0) {
-                    S.ovf = (unsigned long long)ovf;
-                    S.mabs = (unsigned long long)mabs;
-                }
-            }
-            // One thread per (query head h = wave, channel = lane [+64]): walk the
-            // chunks in order; the run sums of the next PF chunks are loaded first.
+            // The chunk headers give the score statistics of the whole chain
+            // (when q passed its range check) and the run counts.
+            const bool hdr_stats = ok && nch <= HMAX;
+            // Wave h replays query head h, lane = channel.
             const int h = wv;
             int64_t acc[CPL];
 #pragma unroll
@@ -755,63 +795,100 @@ __global__ void __launch_bounds__(CT) chunk_kernel(Geom g, const Tables *__restr
             int64_t l = 0, R = 0;
             unsigned long long events = 0;
             bool fb = chain_fb;
+            int total = 0;
+            if (nch <= HMAX) {
+                // One load per lane and 64 chunks, then a scan of the run counts
+                // lists the runs of head h in order, by slot, in LDS.
+                constexpr int HPL = HMAX / 64;
+                uint64_t w0[HPL], w1[HPL];
+#pragma unroll
+                for (int i = 0; i < HPL; ++i) {
+                    const int c = lane + 64 * i;
+                    w0[i] = 0;
+                    w1[i] = 0;
+                    if (c < nch) {
+                        const ChunkHdr *hp = &ck.hdr[((int64_t)chain * ck.max_chunks + c) * GF + h];
+                        w0[i] = get64(&hp->w0);
+                        if (h == 0) w1[i] = get64(&hp->w1);
+                    }
+                }
+                int flags = 0;
+                int64_t ovf = 0, mabs = 0;
+                uint16_t *sl = S.u.rp.slot[h];
+#pragma unroll
+                for (int i = 0; i < HPL; ++i) {
+                    if (64 * i >= nch) break;
+                    const int c = lane + 64 * i;
+                    const int n = (int)(w0[i] & 0xFFFF);       // 0 past the last chunk
+                    flags |= (int)((w0[i] >> 16) & 0xFFFF);
+                    ovf += (int64_t)(w0[i] >> 32);
+                    mabs = (int64_t)w1[i] > mabs ? (int64_t)w1[i] : mabs;
+                    const int incl = (int)wave_scan_add32((uint32_t)n);
+                    const int start = total + incl - n;
+                    total += __builtin_amdgcn_readlane(incl, 63);
+                    if (!fb)
+                        for (int j = 0; j < n && start + j < NSEG; ++j)
+                            sl[start + j] = (uint16_t)((slot_base(c) + j) | (j ? RUN_EVENT : 0));
+                }
+                total = __builtin_amdgcn_readfirstlane(total);    // wave-uniform
+                if (__ballot(flags != 0) || total > NSEG) fb = true;
+                if (h == 0) {
+                    ovf = wave_sum_i64(ovf);
+                    mabs = wave_max_i64(mabs);
+                    if (lane == 0) {
+                        S.ovf = (unsigned long long)ovf;
+                        S.mabs = (unsigned long long)mabs;
+                    }
+                }
+            }
             if (!fb) {
+                // The walk, SB runs at a time: lane i < SB loads run i's L, f and B
+                // (read back with readlane), every lane its channels' run sums.
+                constexpr int SB = 64 / CPL;
                 const SegMeta *meta = ck.meta + ((int64_t)chain * GF + h) * ck.pool;
                 const int32_t *segS = ck.segS + ((int64_t)chain * GF + h) * ck.pool * D;
-                for (int c0 = 0; c0 < nch && !fb; c0 += PF) {
-                    int32_t pre[PF][CPL];
-                    int64_t preL[PF], preB[PF];
+                const uint16_t *sl = S.u.rp.slot[h];
+                wave_sync();
+                for (int g0 = 0; g0 < total && !fb; g0 += SB) {
+                    // Lane i holds run g0 + i's list entry; every lane reads the entries
+                    // back with readlane, so the run-sum loads issue back to back.
+                    const bool mine = lane < SB && g0 + lane < total;
+                    const uint32_t ent = mine ? sl[g0 + lane] : 0u;
+                    int32_t sv[SB][CPL];
 #pragma unroll
-                    for (int i = 0; i < PF; ++i) {
-                        const int c = c0 + i < nch ? c0 + i : 0;
-                        const int slot = slot_base(c);
+                    for (int i = 0; i < SB; ++i) {
+                        const int si = __builtin_amdgcn_readlane((int)ent, i) & (RUN_EVENT - 1);
+                        // unconditional (slot 0 past the end): no branch between the loads
 #pragma unroll
                         for (int k = 0; k < CPL; ++k)
-                            pre[i][k] = (int32_t)get32(&segS[(int64_t)slot * D + lane + 64 * k]);
-                        preL[i] = (int64_t)get64(&meta[slot].L);
-                        preB[i] = (int64_t)get64(&meta[slot].B);
+                            sv[i][k] = (int32_t)get32(&segS[(int64_t)si * D + lane + 64 * k]);
                     }
+                    uint64_t mlf = 0, mb = 0;
+                    if (mine) {
+                        const int si = (int)(ent & (RUN_EVENT - 1));
+                        mlf = get64(&meta[si].lf);
+                        mb = get64(&meta[si].b);
+                    }
+                    // Past a failed bound the values are garbage, unused: the head
+                    // goes to the serial path. No early exit, so the loop unrolls
+                    // and sv stays in registers.
 #pragma unroll
-                    for (int i = 0; i < PF; ++i) {
-                        const int c = c0 + i;
-                        if (c >= nch || fb) break;
-                        const uint64_t w0 = S.u.rp.hdr[h][c].w0;
-                        const int n_seg = (int)(w0 & 0xFFFF), hflags = (int)((w0 >> 16) & 0xFFFF);
-                        if (hflags) {
-                            fb = true;
-                            break;
-                        }
-                        for (int j = 0; j < n_seg; ++j) {
-                            int32_t sv[CPL];
-                            int64_t L, B;
-                            if (j == 0) {
+                    for (int i = 0; i < SB; ++i) {
+                        if (g0 + i < total) {
+                            const int64_t L = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)mlf, i);
+                            const int64_t f = (uint32_t)__builtin_amdgcn_readlane((int)(mlf >> 32), i);
+                            const int64_t B = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)mb, i);
+                            if (SEQ && (__builtin_amdgcn_readlane((int)ent, i) & RUN_EVENT)) {
 #pragma unroll
-                                for (int k = 0; k < CPL; ++k) sv[k] = pre[i][k];
-                                L = preL[i];
-                                B = preB[i];
-                            } else {
-                                const int slot = slot_base(c) + j;
-#pragma unroll
-                                for (int k = 0; k < CPL; ++k)
-                                    sv[k] = (int32_t)get32(&segS[(int64_t)slot * D + lane + 64 * k]);
-                                L = (int64_t)get64(&meta[slot].L);
-                                B = (int64_t)get64(&meta[slot].B);
-                                if (SEQ) {
-                                    const int64_t f = (int64_t)get64(&meta[slot].f);
-#pragma unroll
-                                    for (int k = 0; k < CPL; ++k) acc[k] = wmul(acc[k], f) >> PROB_FRAC;
-                                    l = wmul(l, f) >> PROB_FRAC;
-                                    R = (wmul(R, f) >> PROB_FRAC) + 1;
-                                    ++events;
-                                }
+                                for (int k = 0; k < CPL; ++k) acc[k] = wmul(acc[k], f) >> PROB_FRAC;
+                                l = wmul(l, f) >> PROB_FRAC;
+                                R = (wmul(R, f) >> PROB_FRAC) + 1;
+                                ++events;
                             }
                             R += B;
-                            if (SEQ && R > ACC_HI) {
-                                fb = true;
-                                break;
-                            }
+                            if (SEQ && R > ACC_HI) fb = true;
 #pragma unroll
-                            for (int k = 0; k < CPL; ++k) acc[k] += sv[k];
+                            for (int k = 0; k < CPL; ++k) acc[k] += sv[i][k];
                             l += L;
                         }
                     }
@@ -821,9 +898,9 @@ __global__ void __launch_bounds__(CT) chunk_kernel(Geom g, const Tables *__restr
             const int qh = kvh * GF + h;
             int32_t *orow = out + ((int64_t)b * g.n_q + qh) * D;
             if (fb) {
-                // Score statistics were counted already unless q failed its range check.
+                // The serial path counts score statistics only when the headers did not.
                 serial_head<CPL, K::RS>(g, tabs, S.kc, S.vc, q + ((int64_t)b * g.n_q + qh) * D, b,
-                                        kvh, T, SEQ ? 0 : 1, !ok, S.u.fb[h], orow, st);
+                                        kvh, T, SEQ ? 0 : 1, !hdr_stats, S.u.fb[h], orow, st);
                 if (lane == 0) atomicAdd(&st->serial_fallbacks, 1ull);
             } else {
                 unsigned long long aovf = 0;
@@ -843,8 +920,8 @@ __global__ void __launch_bounds__(CT) chunk_kernel(Geom g, const Tables *__restr
                     const int64_t a = acc[k] < 0 ? -acc[k] : acc[k];
                     amax = a > amax ? a : amax;
                 }
-                amax = wave_max64(amax);
-                aovf = (unsigned long long)wave_sum64((int64_t)aovf);
+                amax = wave_max_i64(amax);
+                aovf = (unsigned long long)wave_sum_i64((int64_t)aovf);
                 if (lane == 0) {
                     S.wt[h][0] = (int64_t)events;
                     S.wt[h][1] = amax;
@@ -870,7 +947,7 @@ __global__ void __launch_bounds__(CT) chunk_kernel(Geom g, const Tables *__restr
                     atomicMax(&st->max_abs_acc, (unsigned long long)am);
                     if (ao) atomicAdd(&st->acc_overflows, (unsigned long long)ao);
                 }
-                if (ok) {
+                if (hdr_stats) {
                     if (S.ovf) atomicAdd(&st->score_overflows, S.ovf);
                     atomicMax(&st->max_abs_score, S.mabs);
                 }

@@ -81,11 +81,15 @@ __device__ __forceinline__ int64_t wadd(int64_t a, int64_t b) {
 
 // ExpLut.__call__ (attention.py:153-159) for delta >= 0: the flat index is
 // floor(min(delta, delta_max) * log2e / 2^24); past the table it is zero.
+// delta_max < 2^20, so after the clamp the product fits a 32x32->64 multiply.
+// Branch-free: the table read is unconditional (index & 255 is always in
+// range) and a select zeroes the past-the-table case, so the compiler can
+// batch the LDS reads of several calls.
 __device__ __forceinline__ int32_t exp_lut(int64_t delta, const int32_t *table, int64_t delta_max) {
-    int64_t d = delta < delta_max ? delta : delta_max;
-    uint64_t u = ((uint64_t)d * (uint64_t)LOG2E_Q16) >> (ACC_FRAC + ACC_FRAC - LUT_BITS);
-    if (u >= (uint64_t)LUT_SPAN) return 0;
-    return table[u & 255] >> (int)(u >> LUT_BITS);
+    const uint32_t d = (uint32_t)(delta < delta_max ? delta : delta_max);
+    const uint32_t u = (uint32_t)(((uint64_t)d * (uint64_t)LOG2E_Q16) >> (ACC_FRAC + ACC_FRAC - LUT_BITS));
+    const int32_t v = table[u & 255] >> (u >> LUT_BITS);
+    return u < (uint32_t)LUT_SPAN ? v : 0;
 }
 
 // reciprocal + _finalize for one row (attention.py:177-250, 873-880).
@@ -102,7 +106,18 @@ __device__ __forceinline__ Recip reciprocal(int64_t l) {
     int64_t k = s - 31;
     int64_t ln = k >= 0 ? (l >> k) : (int64_t)((uint64_t)l << (-k));
     Recip out;
-    out.r = l > 0 ? (int64_t)(((uint64_t)1 << 62) / (uint64_t)(ln > 1 ? ln : 1)) : 0;
+    out.r = 0;
+    if (l > 0) {
+        // floor(2^62 / ln) without a 64-bit integer division. ln lies in
+        // [2^31, 2^48): it is exact in fp64 and the quotient is at most 2^31, so
+        // the correctly rounded fp64 quotient truncates to the floor or to one
+        // more (when the true quotient sits just below an integer); the integer
+        // check r * ln <= 2^62 (no overflow: r * ln <= 2^62 + ln) settles it.
+        const uint64_t n = (uint64_t)ln;
+        uint64_t r = (uint64_t)(4611686018427387904.0 / (double)n);
+        if (r * n > ((uint64_t)1 << 62)) --r;
+        out.r = (int64_t)r;
+    }
     out.shift = (int32_t)(62 - PROB_FRAC + k);
     return out;
 }

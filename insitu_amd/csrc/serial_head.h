@@ -10,6 +10,7 @@
 #pragma once
 
 #include "insitu_internal.h"
+#include "wave.h"
 
 namespace insitu {
 
@@ -93,7 +94,7 @@ __device__ void serial_head(const Geom &g, const Tables *__restrict__ tabs,
                 s_mine = s;
             }
             for (int j = 0; j < n; ++j) {
-                const int64_t sj = __shfl(s_mine, j, 64);
+                const int64_t sj = readlane64(s_mine, j);
                 int64_t p;
                 if (!two_pass) {
                     if (sj > m) {
@@ -152,10 +153,10 @@ __device__ void serial_head(const Geom &g, const Tables *__restrict__ tabs,
             amax = a > amax ? a : amax;
         }
     }
-    amax = wave_max64(amax);
-    max_abs_s = wave_max64(max_abs_s);
-    sovf = (unsigned long long)wave_sum64((int64_t)sovf);
-    aovf = (unsigned long long)wave_sum64((int64_t)aovf);
+    amax = wave_max_i64(amax);
+    max_abs_s = wave_max_i64(max_abs_s);
+    sovf = (unsigned long long)wave_sum_i64((int64_t)sovf);
+    aovf = (unsigned long long)wave_sum_i64((int64_t)aovf);
     if (lane == 0) {
         atomicMax(&st->n_tokens, (unsigned long long)T);
         atomicAdd(&st->rescale_events, events);

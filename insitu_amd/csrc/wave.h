@@ -1,0 +1,107 @@
+// Wave-wide (64-lane) reductions and scans built on DPP row operations and
+// readlane, so that no step goes through the LDS permute unit (ds_bpermute)
+// and its round-trip latency. CDNA waves are 64 lanes in four rows of 16.
+//
+// The reductions return a wave-uniform value; the scans are inclusive in lane
+// order. All of them expect every lane of the wave to be active.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace insitu {
+
+// DPP controls (GCN3/CDNA encoding).
+constexpr int DPP_QUAD_1032 = 0xB1;     // quad_perm [1,0,3,2]: lane ^ 1
+constexpr int DPP_QUAD_2301 = 0x4E;     // quad_perm [2,3,0,1]: lane ^ 2
+constexpr int DPP_ROW_SHR1 = 0x111;
+constexpr int DPP_ROW_SHR2 = 0x112;
+constexpr int DPP_ROW_SHR4 = 0x114;
+constexpr int DPP_ROW_SHR8 = 0x118;
+constexpr int DPP_ROW_MIRROR = 0x140;        // lane i <-> 15 - i within a row
+constexpr int DPP_ROW_HALF_MIRROR = 0x141;   // lane i <-> 7 - i within 8 lanes
+constexpr int DPP_ROW_BCAST15 = 0x142;       // lane 15 of each row -> the next row
+constexpr int DPP_ROW_BCAST31 = 0x143;       // lane 31 -> rows 2 and 3
+constexpr int DPP_WAVE_SHR1 = 0x138;         // lane i <- lane i - 1 across the wave
+
+// v from the lane selected by CTRL; lanes without a source (or outside ROWS)
+// get `fill`.
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ uint32_t dpp32(uint32_t fill, uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)fill, (int)v, CTRL, ROWS, 0xF, false);
+}
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ int64_t dpp64(int64_t fill, int64_t v) {
+    const uint32_t lo = dpp32<CTRL, ROWS>((uint32_t)fill, (uint32_t)v);
+    const uint32_t hi = dpp32<CTRL, ROWS>((uint32_t)((uint64_t)fill >> 32), (uint32_t)((uint64_t)v >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ int64_t readlane64(int64_t v, int lane) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), lane);
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// A value every lane holds the same copy of (read from LDS, say), made
+// wave-uniform for the compiler so that it lives in SGPRs and drives scalar
+// branches.
+__device__ __forceinline__ int32_t uni32(int32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ int64_t uni64(int64_t v) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)((uint64_t)v >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+struct OpMax64 {
+    __device__ static int64_t f(int64_t a, int64_t b) { return a > b ? a : b; }
+};
+struct OpAdd64 {
+    __device__ static int64_t f(int64_t a, int64_t b) { return (int64_t)((uint64_t)a + (uint64_t)b); }
+};
+
+// Reduction of every lane's value, wave-uniform. Within each row the four DPP
+// steps leave every lane with the row's result; readlane combines the rows.
+template <class OP>
+__device__ __forceinline__ int64_t wave_reduce64(int64_t v) {
+    v = OP::f(v, dpp64<DPP_QUAD_1032>(v, v));
+    v = OP::f(v, dpp64<DPP_QUAD_2301>(v, v));
+    v = OP::f(v, dpp64<DPP_ROW_HALF_MIRROR>(v, v));
+    v = OP::f(v, dpp64<DPP_ROW_MIRROR>(v, v));
+    const int64_t r0 = readlane64(v, 0), r1 = readlane64(v, 16);
+    const int64_t r2 = readlane64(v, 32), r3 = readlane64(v, 48);
+    return OP::f(OP::f(r0, r1), OP::f(r2, r3));
+}
+
+__device__ __forceinline__ int64_t wave_max_i64(int64_t v) { return wave_reduce64<OpMax64>(v); }
+__device__ __forceinline__ int64_t wave_sum_i64(int64_t v) { return wave_reduce64<OpAdd64>(v); }
+
+// Inclusive scan in lane order; `id` is the operation's identity.
+template <class OP>
+__device__ __forceinline__ int64_t wave_scan64(int64_t v, int64_t id) {
+    v = OP::f(v, dpp64<DPP_ROW_SHR1>(id, v));
+    v = OP::f(v, dpp64<DPP_ROW_SHR2>(id, v));
+    v = OP::f(v, dpp64<DPP_ROW_SHR4>(id, v));
+    v = OP::f(v, dpp64<DPP_ROW_SHR8>(id, v));
+    v = OP::f(v, dpp64<DPP_ROW_BCAST15, 0xA>(id, v));
+    v = OP::f(v, dpp64<DPP_ROW_BCAST31, 0xC>(id, v));
+    return v;
+}
+
+// The value of the previous lane (lane 0 gets `id`).
+__device__ __forceinline__ int64_t wave_shr1_64(int64_t v, int64_t id) {
+    return dpp64<DPP_WAVE_SHR1>(id, v);
+}
+
+// 32-bit inclusive prefix sum in lane order.
+__device__ __forceinline__ uint32_t wave_scan_add32(uint32_t v) {
+    v += dpp32<DPP_ROW_SHR1>(0u, v);
+    v += dpp32<DPP_ROW_SHR2>(0u, v);
+    v += dpp32<DPP_ROW_SHR4>(0u, v);
+    v += dpp32<DPP_ROW_SHR8>(0u, v);
+    v += dpp32<DPP_ROW_BCAST15, 0xA>(0u, v);
+    v += dpp32<DPP_ROW_BCAST31, 0xC>(0u, v);
+    return v;
+}
+
+}  // namespace insitu

@@ -94,6 +94,27 @@ def test_finalize_goldens(ctx):
     np.testing.assert_array_equal(out, hx.lanes("fin_out.hex", 48, 64))
 
 
+def test_finalize_reciprocal_edges(ctx):
+    """l across its whole 48-bit range, powers of two and their neighbours, and
+    denominators whose 2^62 / l_n quotient sits just below an integer."""
+    from insitu_amd import ops
+    from oracle.attention import finalize, reciprocal
+    fmt = Format()
+    rng = np.random.default_rng(7)
+    edges = [1, 2, 3, (1 << 31) - 1, 1 << 31, (1 << 31) + 1, (1 << 32) - 1, 1 << 32,
+             (1 << 47) - 1, 1 << 47, (1 << 48) - 1]
+    pows = [x for b in range(1, 48) for x in ((1 << b) - 1, 1 << b, (1 << b) + 1)]
+    ln = rng.integers(1 << 31, 1 << 32, size=4000, dtype=np.int64)
+    near = ((1 << 62) // ((1 << 62) // ln + 1)) + 1     # quotient just below an integer
+    ls = np.concatenate([edges, pows, rng.integers(1, 1 << 48, size=2000), near]).astype(np.int64)
+    acc = rng.integers(-(1 << 31), 1 << 31, size=(ls.size, 8)).astype(np.int64)
+    out, r, sh = ops.finalize(acc, ls, ctx)
+    want_r, want_sh = reciprocal(ls, fmt)
+    np.testing.assert_array_equal(r, want_r)
+    np.testing.assert_array_equal(sh, want_sh)
+    np.testing.assert_array_equal(out, finalize(acc, ls, fmt))
+
+
 def test_append_writes_kv_rows(ctx):
     c = _cache(ctx, 4)
     rk, rv = hx.lanes("rot_k.hex", 24, 64), hx.lanes("rot_v.hex", 24, 64)

@@ -114,3 +114,23 @@ def test_product_never_imports_the_oracle():
                 text = open(os.path.join(dirpath, f)).read()
                 assert not re.search(r"^\s*(from|import)\s+oracle\b", text, re.M), f
                 assert "liboracle" not in text, f
+
+
+def test_fp64_quotient_method_of_the_device_reciprocal():
+    """The kernels compute floor(2^62 / n), n in [2^31, 2^48), as the correctly
+    rounded fp64 quotient truncated, minus one when r * n > 2^62. Checked here
+    against exact integer division, numpy's float64 division being IEEE like the
+    GPU's, on random n and on n whose quotient sits just below an integer."""
+    rng = np.random.default_rng(11)
+    n = np.concatenate([
+        rng.integers(1 << 31, 1 << 32, size=200_000),
+        rng.integers(1 << 32, 1 << 48, size=200_000),
+        [1 << 31, (1 << 32) - 1, (1 << 47) + 1, (1 << 48) - 1],
+    ]).astype(np.uint64)
+    q = (np.uint64(1) << np.uint64(62)) // n
+    near = (np.uint64(1) << np.uint64(62)) // (q + np.uint64(1)) + np.uint64(1)
+    n = np.concatenate([n, near[(near >= (1 << 31)) & (near < (1 << 48))]])
+    exact = (np.uint64(1) << np.uint64(62)) // n
+    r = (4611686018427387904.0 / n.astype(np.float64)).astype(np.uint64)
+    r = np.where(r * n > (np.uint64(1) << np.uint64(62)), r - np.uint64(1), r)
+    np.testing.assert_array_equal(r, exact)
