@@ -48,6 +48,21 @@ def _args():
     return ap.parse_args()
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "chunk_kernel_c2_traffic.json")
+
+
+def measured_traffic(mode: str, ctx: int):
+    """HBM bytes per attend launch from the committed FETCH_SIZE/WRITE_SIZE passes.
+
+    Those passes profile the sequential attend at ctx 32,768; any other mode or
+    context has no measurement, and the field is null.
+    """
+    if mode != "online" or ctx != CTX or not os.path.exists(TRAFFIC_FILE):
+        return None
+    with open(TRAFFIC_FILE) as f:
+        return json.load(f).get("traffic_bytes")
+
+
 def copy_calibration() -> None:
     """A plain device copy of known size, for scaling FETCH_SIZE/WRITE_SIZE counters."""
     import torch
@@ -211,7 +226,8 @@ def main() -> int:
                    "head_dim": D, "row_bytes": ROW},
         "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 3), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(kernel_gbs / HBM_PEAK_GBS, 5),
-                     "traffic": None, "kernel": "attend (all kernels of insitu_attend)",
+                     "traffic": measured_traffic(a.mode, a.ctx),
+                     "kernel": "chunk_kernel (the one launch of insitu_attend; two-pass mode adds chunk_max_kernel)",
                      "algorithmic_bytes_per_launch": per_launch_bytes,
                      "avg_attend_us": round(float(attend_ms.mean()) * 1e3, 3),
                      "cycles_per_row_gpu_wide_2p4ghz": round(

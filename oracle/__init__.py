@@ -31,5 +31,6 @@ How each part is pinned (so a plausible mistake fails a check):
   attention.attend_two_pass   tb/vectors out.hex
   attention.reciprocal/final  tb/vectors fin_*
   c/oracle.c                  equal to the numpy functions above on seeded
-                              cases (tests/test_oracle_c.py)
+                              cases (tests/test_oracle_numerics.py,
+                              test_native_oracle_equals_numpy_oracle)
 """
