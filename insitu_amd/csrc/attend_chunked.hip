@@ -37,13 +37,15 @@
 // Scores: sum_ch q[ch] * c[code_ch] in fp64 FMA -- every partial sum is an
 // integer below 2^51, so it is exact -- then the int64 norm multiply and >>24
 // of the reference.
+#include <type_traits>
+
 #include "serial_head.h"
 #include "wave.h"
 
 namespace insitu {
 
-constexpr int CT = 256;              // threads per workgroup
-constexpr int TPT = 4;               // tokens per thread in the score phase
+constexpr int CT = 512;              // threads per workgroup: 8 waves, 2 per SIMD
+constexpr int TPT = 2;               // tokens per thread in the score phase
 constexpr int CHUNK = CT * TPT;      // tokens per workgroup
 constexpr int GF = 4;                // query heads per KV head on this path
 constexpr int VB_MAX = 3;            // widest value code staged in LDS
@@ -102,6 +104,7 @@ struct Chunked {
     int32_t *segS;                 // [chain][GF][pool][d]
     unsigned int *done;            // [chain]
     unsigned int *chain_fb;        // [chain]  nonzero: recompute this chain serially
+    double *qd;                    // [chain][D][GF]  the chain's query rows in fp64
     int32_t max_chunks, pool;
 };
 
@@ -153,7 +156,6 @@ struct ChunkLds {
         Replay rp;
         SerialLds<KF<D, KB>::RS> fb[GF];
     } u;
-    double qf[D][GF];
     double kcf[16];
     int64_t kc[16];
     int64_t vc[16];
@@ -177,40 +179,81 @@ __device__ __forceinline__ int slot_base(int chunk) { return chunk == 0 ? 0 : SL
 __device__ __forceinline__ int slot_count(int chunk) { return chunk == 0 ? SLOTS0 : SLOTS; }
 static_assert(SLOTS0 + (HMAX - 1) * SLOTS < RUN_EVENT, "run slots of the chunked path fit 15 bits");
 
-// Shared prologue: q (fp64) and the key centroids (fp64) into LDS; checks that
-// every head's score stays an exact fp64 integer (|dot| < 2^51). Chunk 0 also
-// counts rotated queries beyond the +-2^27 the 24-bit seam can produce.
+// Shared prologue: the key centroids (fp64) into LDS, and the KV group's GF
+// query rows in fp64, channel-major ([c][h]), into the chain's slot of global
+// scratch, from where the score loop reads them back with scalar loads (as
+// scalar FMA operands; see qgroup). Every workgroup of a chain writes the same
+// values to the same slot, so their stores may overlap harmlessly; each reads
+// the slot only after its own stores have completed. The scalar cache cannot
+// hold an older copy: it is invalidated at the start of every dispatch and the
+// slot is not read before this point.
+//
+// Also checks that every score of the group stays an exact fp64 integer:
+// |dot| <= ||q||_1 * max|c| < 2^51. With `count`, queries beyond the +-2^27
+// the 24-bit seam can produce are counted as range errors (once per call).
 template <int D>
 __device__ __forceinline__ bool load_q(const Geom &g, const Tables *__restrict__ tabs,
                                        const int32_t *__restrict__ q, int b, int kvh, bool count,
-                                       double (*qf)[GF], double *kcf, int *qok, DevStats *st) {
+                                       double *qslot, double *kcf, int *qok, DevStats *st) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int nk = 1 << g.kb;
     if (tid < nk) kcf[tid] = (double)tabs->kc[tid];
     if (tid == 0) *qok = 1;
     __syncthreads();
-    const int32_t *qrow = q + ((int64_t)b * g.n_q + kvh * GF + wv) * D;   // wave wv: head wv
-    int64_t l1 = 0;
-    int64_t bad = 0;
+    if (wv < GF) {
+        const int32_t *qrow = q + ((int64_t)b * g.n_q + kvh * GF + wv) * D;   // wave wv: head wv
+        int64_t l1 = 0, bad = 0;
 #pragma unroll
-    for (int k = 0; k < D / 64; ++k) {
-        const int c = lane + 64 * k;
-        const int32_t v = qrow[c];
-        qf[c][wv] = (double)v;
-        l1 += v < 0 ? -(int64_t)v : (int64_t)v;
-        bad += ((int64_t)v >= Q_ROT_LIMIT || (int64_t)v <= -Q_ROT_LIMIT) ? 1 : 0;
+        for (int k = 0; k < D / 64; ++k) {
+            const int c = lane + 64 * k;
+            const int32_t v = qrow[c];
+            qslot[c * GF + wv] = (double)v;
+            l1 += v < 0 ? -(int64_t)v : (int64_t)v;
+            bad += ((int64_t)v >= Q_ROT_LIMIT || (int64_t)v <= -Q_ROT_LIMIT) ? 1 : 0;
+        }
+        l1 = wave_sum_i64(l1);                  // < 2^38: exact as a double below
+        bad = wave_sum_i64(bad);
+        if (lane == 0) {
+            double cmax = 0.0;
+            for (int i = 0; i < nk; ++i) cmax = fmax(cmax, fabs(kcf[i]));
+            if (!((double)l1 * cmax < DOT_LIMIT)) atomicAnd(qok, 0);
+            if (count && bad) atomicAdd(&st->range_errors, (unsigned long long)bad);
+        }
     }
-    l1 = wave_sum_i64(l1);                  // < 2^38: exact as a double below
-    bad = wave_sum_i64(bad);
-    if (lane == 0) {
-        double cmax = 0.0;
-        for (int i = 0; i < nk; ++i) cmax = fmax(cmax, fabs(kcf[i]));
-        if (!((double)l1 * cmax < DOT_LIMIT)) atomicAnd(qok, 0);
-        if (count && bad) atomicAdd(&st->range_errors, (unsigned long long)bad);
-    }
+    __builtin_amdgcn_s_waitcnt(0);          // this thread's slot stores have completed
     __syncthreads();
     return *qok != 0;
 }
+
+// The 8 x GF query values of channel group grp (256 bytes of the slot) into
+// SGPRs: four 64-byte scalar loads and a wait. Inline assembly because the
+// compiler only emits scalar loads for memory the kernel never writes.
+struct QGroup {
+    double v[8][GF];
+};
+__device__ __forceinline__ QGroup qgroup(const double *qslot, int grp) {
+    typedef unsigned int u32x16 __attribute__((ext_vector_type(16)));
+    u32x16 r[4];
+    const double *base = qslot + 8 * GF * grp;
+    asm volatile(
+        "s_load_dwordx16 %0, %4, 0x0\n\t"
+        "s_load_dwordx16 %1, %4, 0x40\n\t"
+        "s_load_dwordx16 %2, %4, 0x80\n\t"
+        "s_load_dwordx16 %3, %4, 0xc0\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=s"(r[0]), "=s"(r[1]), "=s"(r[2]), "=s"(r[3])
+        : "s"(base)
+        : "memory");
+    QGroup out;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+            out.v[2 * k + e / GF][e % GF] =
+                __builtin_bit_cast(double, ((uint64_t)r[k][2 * e + 1] << 32) | r[k][2 * e]);
+    return out;
+}
+static_assert(GF == 4, "qgroup reads 8 channels x 4 heads per group");
 
 // The key codes and norm words of this thread's TPT consecutive tokens
 // (t = t0 + TPT * tid + j): a wave reads one contiguous span of each plane.
@@ -242,11 +285,17 @@ __device__ __forceinline__ void load_keys(const Geom &g, const uint8_t *__restri
     }
 }
 
-// Exact scores of those tokens for the GF heads (attention.py:333-359). Every
-// channel's q is read once and used for all TPT tokens.
+// Exact scores of those tokens for the GF heads (attention.py:333-359), in
+// groups of 8 channels. Per group the TPT x 8 centroid reads are issued as one
+// LDS batch (and the 8 x GF query values as scalar loads), then the FMAs
+// run channel by channel over all TPT x GF accumulators, so an accumulator is
+// reused only every TPT * GF FMAs. The 8 codes of a group sit in one 32-bit
+// window of the key bitstream (8 * KB <= 32 bits), cut out with alignbit.
+// qslot: the chain's fp64 query rows ([c][h]), read with scalar loads so the
+// query values feed the FMAs as scalar operands.
 template <int D, int KB>
 __device__ __forceinline__ void score_keys(const uint32_t (&w)[TPT][KF<D, KB>::KWORDS + 1],
-                                           const uint32_t (&normw)[TPT], const double (*qf)[GF],
+                                           const uint32_t (&normw)[TPT], const double *qslot,
                                            const double *kcf, int score_shift,
                                            int64_t (&s)[TPT][GF]) {
     using K = KF<D, KB>;
@@ -255,45 +304,25 @@ __device__ __forceinline__ void score_keys(const uint32_t (&w)[TPT][KF<D, KB>::K
     for (int j = 0; j < TPT; ++j)
 #pragma unroll
         for (int h = 0; h < GF; ++h) acc[j][h] = 0.0;
-    const char *kb8 = (const char *)kcf;
-    // Every index below is a compile-time constant once the loops unroll, so the
-    // code words stay in registers. The centroid of code x sits at byte 8x of kcf.
 #pragma unroll
-    for (int wd = 0; wd < K::KWORDS; ++wd) {
-        uint32_t m0[TPT], m1[TPT];
-        if (KB == 4) {
-            // bytes of m0 hold 8 * (even nibbles), bytes of m1 hold 8 * (odd nibbles)
+    for (int grp = 0; grp < D / 8; ++grp) {
+        const int bo = 8 * KB * grp, wi = bo >> 5, sh = bo & 31;
+        double cv[TPT][8];
 #pragma unroll
-            for (int j = 0; j < TPT; ++j) {
-                m0[j] = (w[j][wd] << 3) & 0x78787878u;
-                m1[j] = (w[j][wd] >> 1) & 0x78787878u;
-            }
+        for (int j = 0; j < TPT; ++j) {
+            const uint32_t win = sh == 0 ? w[j][wi] : __builtin_amdgcn_alignbit(w[j][wi + 1], w[j][wi], sh);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) cv[j][i] = kcf[(win >> (i * KB)) & K::MASK];
         }
+        const QGroup qv = qgroup(qslot, grp);
 #pragma unroll
-        for (int c = (32 * wd + KB - 1) / KB; c < D && c * KB < 32 * (wd + 1); ++c) {
-            const int o = c * KB;
-            const int sh = o & 31;
-            double qv[GF];
+        for (int i = 0; i < 8; ++i)
 #pragma unroll
-            for (int h = 0; h < GF; ++h) qv[h] = qf[c][h];
+            for (int j = 0; j < TPT; ++j)
 #pragma unroll
-            for (int j = 0; j < TPT; ++j) {
-                uint32_t off;
-                if (KB == 4) {
-                    const int nib = sh >> 2;
-                    off = ((nib & 1 ? m1[j] : m0[j]) >> (8 * (nib >> 1))) & 0x78u;
-                } else if (sh + KB <= 32) {
-                    off = ((w[j][wd] >> sh) & K::MASK) << 3;
-                } else {
-                    off = (__builtin_amdgcn_alignbit(w[j][wd + 1], w[j][wd], sh) & K::MASK) << 3;
-                }
-                const double cent = *(const double *)(kb8 + off);
-#pragma unroll
-                for (int h = 0; h < GF; ++h) acc[j][h] = fma(qv[h], cent, acc[j][h]);
-            }
-        }
-        // Pin the accumulators at every word so the compiler cannot turn the loop
-        // nest inside out (load every centroid first, FMA at the end), which spills.
+                for (int h = 0; h < GF; ++h) acc[j][h] = fma(qv.v[i][h], cv[j][i], acc[j][h]);
+        // Pin the accumulators at every group so the compiler cannot turn the
+        // loop nest inside out (load every centroid first, FMA at the end).
 #pragma unroll
         for (int j = 0; j < TPT; ++j)
 #pragma unroll
@@ -316,7 +345,6 @@ __global__ void __launch_bounds__(CT) chunk_max_kernel(Geom g, const Tables *__r
                                                        const int32_t *__restrict__ q,
                                                        const int64_t *__restrict__ len,
                                                        Chunked ck, DevStats *st) {
-    __shared__ double qf[D][GF];
     __shared__ double kcf[16];
     __shared__ int qok;
     __shared__ int64_t red[CT / 64][GF];
@@ -328,7 +356,8 @@ __global__ void __launch_bounds__(CT) chunk_max_kernel(Geom g, const Tables *__r
     if (chunk >= nch) return;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     if (tid == 0) ovf_s = mabs_s = 0;
-    const bool ok = load_q<D>(g, tabs, q, b, kvh, chunk == 0, qf, kcf, &qok, st);
+    double *qslot = ck.qd + (int64_t)chain * D * GF;
+    const bool ok = load_q<D>(g, tabs, q, b, kvh, chunk == 0, qslot, kcf, &qok, st);
     int64_t mx[GF];
 #pragma unroll
     for (int h = 0; h < GF; ++h) mx[h] = SCORE_LO;
@@ -340,7 +369,7 @@ __global__ void __launch_bounds__(CT) chunk_max_kernel(Geom g, const Tables *__r
         uint32_t kw[TPT][KF<D, KB>::KWORDS + 1];
         const int64_t t0 = (int64_t)chunk * CHUNK;
         load_keys<D, KB>(g, plane_ptr(g, b, kvh, 0), t0, T, kw, nw);
-        score_keys<D, KB>(kw, nw, qf, kcf, CENT_FRAC + g.norm_frac, s);
+        score_keys<D, KB>(kw, nw, qslot, kcf, CENT_FRAC + g.norm_frac, s);
 #pragma unroll
         for (int j = 0; j < TPT; ++j) {
             if (t0 + tid * TPT + j >= T) continue;
@@ -449,12 +478,13 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             }
             S.vcmax = m;
         }
-        S.expt[tid] = tabs->exp_table[tid];
+        if (tid < 256) S.expt[tid] = tabs->exp_table[tid];
         if (tid == 0) {
             S.ovf = S.mabs = 0;
             S.lb_fail = 0;
         }
-        const bool ok = load_q<D>(g, tabs, q, b, kvh, SEQ && chunk == 0, S.qf, S.kcf, &S.qok, st);
+        double *qslot = ck.qd + (int64_t)chain * D * GF;
+        const bool ok = load_q<D>(g, tabs, q, b, kvh, SEQ && chunk == 0, qslot, S.kcf, &S.qok, st);
 
         // -- phase 1: scores of the thread's TPT consecutive tokens, which stay in
         // registers for the scan; value codes into LDS ----------------------------
@@ -464,7 +494,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
         for (int h = 0; h < GF; ++h) mx[h] = SCORE_LO;
         if (ok) {
             int64_t s[TPT][GF];
-            score_keys<D, KB>(kw, nw, S.qf, S.kcf, score_shift, s);
+            score_keys<D, KB>(kw, nw, qslot, S.kcf, score_shift, s);
             unsigned long long ovf = 0;
             int64_t mabs = 0;
 #pragma unroll
@@ -508,7 +538,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
         __syncthreads();
 
         // -- phase 2: the maximum before this chunk (sequential) or of all chunks --
-        if (SEQ) {
+        if (SEQ && wv < GF) {
             const int h = wv;
             int64_t local = S.red[0][h];
             for (int w = 1; w < CT / 64; ++w) local = S.red[w][h] > local ? S.red[w][h] : local;
@@ -562,7 +592,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                 S.lmax[h] = local;
                 if (fail) S.lb_fail = 1;
             }
-        } else {
+        } else if (!SEQ && wv < GF) {
             int64_t m = SCORE_LO;
             for (int64_t c = lane; c < nch; c += 64) {
                 const int64_t v = ck.cmax[((int64_t)chain * ck.max_chunks + c) * GF + wv];
@@ -660,7 +690,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
         __syncthreads();
 
         // -- phase 4: run sums over the active list, wave = head, lane = channel --
-        if (ok) {
+        if (ok && wv < GF) {
             const int h = wv;
             int n_act = 0, n_ev = 0;
 #pragma unroll
@@ -764,7 +794,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                                    ((uint64_t)S.ovf << 32));
                 pub64(&hp->w1, S.mabs);
             }
-        } else if (tid < GF) {
+        } else if (!ok && tid < GF) {
             // q failed its range check: the chain goes to the serial path, which counts its own
             ChunkHdr *hp = &ck.hdr[((int64_t)chain * ck.max_chunks + chunk) * GF + tid];
             pub64(&hp->w0, 1);
@@ -787,8 +817,10 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             // The chunk headers give the score statistics of the whole chain
             // (when q passed its range check) and the run counts.
             const bool hdr_stats = ok && nch <= HMAX;
-            // Wave h replays query head h, lane = channel.
-            const int h = wv;
+            // Wave h < GF replays query head h, lane = channel; the other waves
+            // only take part in the barriers and the reset.
+            const bool hw = wv < GF;
+            const int h = hw ? wv : 0;
             int64_t acc[CPL];
 #pragma unroll
             for (int k = 0; k < CPL; ++k) acc[k] = 0;
@@ -796,7 +828,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             unsigned long long events = 0;
             bool fb = chain_fb;
             int total = 0;
-            if (nch <= HMAX) {
+            if (hw && nch <= HMAX) {
                 // One load per lane and 64 chunks, then a scan of the run counts
                 // lists the runs of head h in order, by slot, in LDS.
                 constexpr int HPL = HMAX / 64;
@@ -841,27 +873,39 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     }
                 }
             }
-            if (!fb) {
-                // The walk, SB runs at a time: lane i < SB loads run i's L, f and B
-                // (read back with readlane), every lane its channels' run sums.
+            if (hw && !fb) {
+                // The walk, SB runs at a time. Lane i < SB holds run i's list entry
+                // and loads its L, f and B; every lane loads its channels' run sums
+                // (the slot ids read back with readlane, the base address scalar).
+                // Within a stretch of runs without an event acc, l and R only add,
+                // and R only grows, so per run the walk does one add per channel;
+                // l and R are brought up to date from lane prefix sums at each
+                // event (before its rescale) and at the end of the batch, and R is
+                // checked there: a run-by-run check could not fail anywhere else.
+                // acc stays in 32 bits in sequential mode: |acc| <= R <= 2^31 - 1
+                // whenever the result is used (past a failed check the head goes to
+                // the serial path); two-pass sums need 64.
+                using AccT = typename std::conditional<SEQ, int32_t, int64_t>::type;
                 constexpr int SB = 64 / CPL;
                 const SegMeta *meta = ck.meta + ((int64_t)chain * GF + h) * ck.pool;
                 const int32_t *segS = ck.segS + ((int64_t)chain * GF + h) * ck.pool * D;
                 const uint16_t *sl = S.u.rp.slot[h];
+                AccT aw[CPL];
+#pragma unroll
+                for (int k = 0; k < CPL; ++k) aw[k] = 0;
                 wave_sync();
                 for (int g0 = 0; g0 < total && !fb; g0 += SB) {
-                    // Lane i holds run g0 + i's list entry; every lane reads the entries
-                    // back with readlane, so the run-sum loads issue back to back.
-                    const bool mine = lane < SB && g0 + lane < total;
+                    const int nb = total - g0 < SB ? total - g0 : SB;     // uniform
+                    const bool mine = lane < nb;
                     const uint32_t ent = mine ? sl[g0 + lane] : 0u;
                     int32_t sv[SB][CPL];
 #pragma unroll
                     for (int i = 0; i < SB; ++i) {
+                        // unconditional (slot 0 past the batch): no branch between the loads
                         const int si = __builtin_amdgcn_readlane((int)ent, i) & (RUN_EVENT - 1);
-                        // unconditional (slot 0 past the end): no branch between the loads
+                        const int32_t *row = segS + (int64_t)si * D;
 #pragma unroll
-                        for (int k = 0; k < CPL; ++k)
-                            sv[i][k] = (int32_t)get32(&segS[(int64_t)si * D + lane + 64 * k]);
+                        for (int k = 0; k < CPL; ++k) sv[i][k] = (int32_t)get32(row + lane + 64 * k);
                     }
                     uint64_t mlf = 0, mb = 0;
                     if (mine) {
@@ -869,35 +913,48 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                         mlf = get64(&meta[si].lf);
                         mb = get64(&meta[si].b);
                     }
-                    // Past a failed bound the values are garbage, unused: the head
-                    // goes to the serial path. No early exit, so the loop unrolls
-                    // and sv stays in registers.
+                    const uint64_t evm = SEQ ? __ballot(mine && (ent & RUN_EVENT)) : 0ull;
+                    // inclusive prefix sums of L and B over the batch's runs
+                    const int64_t PL = wave_scan64<OpAdd64>(mine ? (int64_t)(uint32_t)mlf : 0, 0);
+                    const int64_t PB = wave_scan64<OpAdd64>(mine ? (int64_t)(uint32_t)mb : 0, 0);
+                    int64_t done_L = 0, done_B = 0;     // prefix sums already added to l, R
 #pragma unroll
                     for (int i = 0; i < SB; ++i) {
-                        if (g0 + i < total) {
-                            const int64_t L = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)mlf, i);
-                            const int64_t f = (uint32_t)__builtin_amdgcn_readlane((int)(mlf >> 32), i);
-                            const int64_t B = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)mb, i);
-                            if (SEQ && (__builtin_amdgcn_readlane((int)ent, i) & RUN_EVENT)) {
+                        if (i < nb) {
+                            if (SEQ && ((evm >> i) & 1ull)) {
+                                const int64_t pl = i ? readlane64(PL, i - 1) : 0;
+                                const int64_t pb = i ? readlane64(PB, i - 1) : 0;
+                                l += pl - done_L;
+                                R += pb - done_B;
+                                done_L = pl;
+                                done_B = pb;
+                                if (R > ACC_HI) fb = true;
+                                const int64_t f =
+                                    (uint32_t)__builtin_amdgcn_readlane((int)(mlf >> 32), i);
 #pragma unroll
-                                for (int k = 0; k < CPL; ++k) acc[k] = wmul(acc[k], f) >> PROB_FRAC;
+                                for (int k = 0; k < CPL; ++k)
+                                    aw[k] = (AccT)(((int64_t)aw[k] * f) >> PROB_FRAC);
                                 l = wmul(l, f) >> PROB_FRAC;
                                 R = (wmul(R, f) >> PROB_FRAC) + 1;
                                 ++events;
                             }
-                            R += B;
-                            if (SEQ && R > ACC_HI) fb = true;
 #pragma unroll
-                            for (int k = 0; k < CPL; ++k) acc[k] += sv[i][k];
-                            l += L;
+                            for (int k = 0; k < CPL; ++k) aw[k] += (AccT)sv[i][k];
                         }
                     }
+                    const int64_t pl = readlane64(PL, nb - 1), pb = readlane64(PB, nb - 1);
+                    l += pl - done_L;
+                    R += pb - done_B;
+                    if (SEQ && R > ACC_HI) fb = true;
                 }
+#pragma unroll
+                for (int k = 0; k < CPL; ++k) acc[k] = (int64_t)aw[k];
             }
             __syncthreads();   // the replay buffers are dead; the serial path reuses the LDS
             const int qh = kvh * GF + h;
             int32_t *orow = out + ((int64_t)b * g.n_q + qh) * D;
-            if (fb) {
+            if (!hw) {
+            } else if (fb) {
                 // The serial path counts score statistics only when the headers did not.
                 serial_head<CPL, K::RS>(g, tabs, S.kc, S.vc, q + ((int64_t)b * g.n_q + qh) * D, b,
                                         kvh, T, SEQ ? 0 : 1, !hdr_stats, S.u.fb[h], orow, st);
@@ -928,7 +985,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     S.wt[h][2] = (int64_t)aovf;
                 }
             }
-            if (lane == 0) S.wt[h][3] = fb ? 1 : 0;
+            if (hw && lane == 0) S.wt[h][3] = fb ? 1 : 0;
             __syncthreads();
             if (tid == 0) {
                 // one set of statistics atomics per (sequence, KV head)
@@ -1008,6 +1065,7 @@ static void carve(const Geom &g, int64_t max_chunks, int64_t pool, uint8_t *p, C
     c.segS = (int32_t *)take(chains * GF * pool * g.d * sizeof(int32_t));
     c.done = (unsigned int *)take(chains * sizeof(unsigned int));
     c.chain_fb = (unsigned int *)take(chains * sizeof(unsigned int));
+    c.qd = (double *)take(chains * g.d * GF * sizeof(double));
     c.max_chunks = (int32_t)max_chunks;
     c.pool = (int32_t)pool;
     if (ck) *ck = c;
