@@ -652,7 +652,9 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                 if (__ballot(live)) {
                     // Branch-free per token: an event records f = LUT(s - prev)
                     // (its own p is LUT(0)), any other token p = LUT(prev - s).
-                    uint32_t nev = 0;
+                    // Counts and list positions come from one ballot per token
+                    // slot: the lanes below hold the earlier tokens.
+                    uint32_t before = 0;
 #pragma unroll
                     for (int j = 0; j < TPT; ++j) {
                         const int tl = tid * TPT + j;
@@ -662,14 +664,15 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                         const uint32_t val = (uint32_t)exp_lut(ev ? sj - prev : prev - sj, S.expt, dm);
                         prev = ev ? sj : prev;
                         rec[h][j] = act_rec(tl, ev, val);          // val <= 2^15 fits the field
-                        act[h] |= (in && (ev || val != 0)) ? 1u << j : 0u;
-                        nev += ev ? 1u : 0u;
+                        const bool a = in && (ev || val != 0);
+                        act[h] |= a ? 1u << j : 0u;
+                        const uint64_t ba = __ballot(a);
+                        before += __builtin_amdgcn_mbcnt_hi((uint32_t)(ba >> 32),
+                                                            __builtin_amdgcn_mbcnt_lo((uint32_t)ba, 0u));
+                        tot += __popcll(ba);
+                        if (evh[h]) evt += __popcll(__ballot(ev));
                     }
-                    const uint32_t c = (uint32_t)__popc(act[h]);
-                    const uint32_t incl = wave_scan_add32(c);
-                    pos[h] = incl - c;
-                    tot = __builtin_amdgcn_readlane((int)incl, 63);
-                    if (evh[h]) evt = __builtin_amdgcn_readlane((int)wave_scan_add32(nev), 63);
+                    pos[h] = before;
                 }
                 if (lane == 0) {
                     S.cntw[wv][h] = tot;
@@ -894,18 +897,31 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
 #pragma unroll
                 for (int k = 0; k < CPL; ++k) aw[k] = 0;
                 wave_sync();
+                const int zslot = ck.pool - 1;        // all zero: pads a batch
                 for (int g0 = 0; g0 < total && !fb; g0 += SB) {
                     const int nb = total - g0 < SB ? total - g0 : SB;     // uniform
+                    const int nblk = (nb + 7) >> 3;                        // blocks of 8 runs
                     const bool mine = lane < nb;
-                    const uint32_t ent = mine ? sl[g0 + lane] : 0u;
+                    const uint32_t ent = mine ? (uint32_t)sl[g0 + lane] : (uint32_t)zslot;
                     int32_t sv[SB][CPL];
 #pragma unroll
-                    for (int i = 0; i < SB; ++i) {
-                        // unconditional (slot 0 past the batch): no branch between the loads
-                        const int si = __builtin_amdgcn_readlane((int)ent, i) & (RUN_EVENT - 1);
-                        const int32_t *row = segS + (int64_t)si * D;
+                    for (int blk = 0; blk < SB / 8; ++blk) {
+                        if (blk < nblk) {
+                            // no branch between the loads of a block; past the batch
+                            // they read the zero slot
 #pragma unroll
-                        for (int k = 0; k < CPL; ++k) sv[i][k] = (int32_t)get32(row + lane + 64 * k);
+                            for (int i = 8 * blk; i < 8 * blk + 8; ++i) {
+                                const int si = __builtin_amdgcn_readlane((int)ent, i) & (RUN_EVENT - 1);
+                                const int32_t *row = segS + (int64_t)(i < nb ? si : zslot) * D;
+#pragma unroll
+                                for (int k = 0; k < CPL; ++k) sv[i][k] = (int32_t)get32(row + lane + 64 * k);
+                            }
+                        } else {
+#pragma unroll
+                            for (int i = 8 * blk; i < 8 * blk + 8; ++i)
+#pragma unroll
+                                for (int k = 0; k < CPL; ++k) sv[i][k] = 0;
+                        }
                     }
                     uint64_t mlf = 0, mb = 0;
                     if (mine) {
@@ -919,27 +935,30 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     const int64_t PB = wave_scan64<OpAdd64>(mine ? (int64_t)(uint32_t)mb : 0, 0);
                     int64_t done_L = 0, done_B = 0;     // prefix sums already added to l, R
 #pragma unroll
-                    for (int i = 0; i < SB; ++i) {
-                        if (i < nb) {
-                            if (SEQ && ((evm >> i) & 1ull)) {
-                                const int64_t pl = i ? readlane64(PL, i - 1) : 0;
-                                const int64_t pb = i ? readlane64(PB, i - 1) : 0;
-                                l += pl - done_L;
-                                R += pb - done_B;
-                                done_L = pl;
-                                done_B = pb;
-                                if (R > ACC_HI) fb = true;
-                                const int64_t f =
-                                    (uint32_t)__builtin_amdgcn_readlane((int)(mlf >> 32), i);
+                    for (int blk = 0; blk < SB / 8; ++blk) {
+                        if (blk < nblk) {
 #pragma unroll
-                                for (int k = 0; k < CPL; ++k)
-                                    aw[k] = (AccT)(((int64_t)aw[k] * f) >> PROB_FRAC);
-                                l = wmul(l, f) >> PROB_FRAC;
-                                R = (wmul(R, f) >> PROB_FRAC) + 1;
-                                ++events;
+                            for (int i = 8 * blk; i < 8 * blk + 8; ++i) {
+                                if (SEQ && ((evm >> i) & 1ull)) {
+                                    const int64_t pl = i ? readlane64(PL, i - 1) : 0;
+                                    const int64_t pb = i ? readlane64(PB, i - 1) : 0;
+                                    l += pl - done_L;
+                                    R += pb - done_B;
+                                    done_L = pl;
+                                    done_B = pb;
+                                    if (R > ACC_HI) fb = true;
+                                    const int64_t f =
+                                        (uint32_t)__builtin_amdgcn_readlane((int)(mlf >> 32), i);
+#pragma unroll
+                                    for (int k = 0; k < CPL; ++k)
+                                        aw[k] = (AccT)(((int64_t)aw[k] * f) >> PROB_FRAC);
+                                    l = wmul(l, f) >> PROB_FRAC;
+                                    R = (wmul(R, f) >> PROB_FRAC) + 1;
+                                    ++events;
+                                }
+#pragma unroll
+                                for (int k = 0; k < CPL; ++k) aw[k] += (AccT)sv[i][k];
                             }
-#pragma unroll
-                            for (int k = 0; k < CPL; ++k) aw[k] += (AccT)sv[i][k];
                         }
                     }
                     const int64_t pl = readlane64(PL, nb - 1), pb = readlane64(PB, nb - 1);
@@ -1046,7 +1065,10 @@ bool chunked_supported(const Geom &g) {
 
 int64_t chunked_max_chunks(int64_t capacity) { return (capacity + CHUNK - 1) / CHUNK; }
 
-int64_t chunked_pool_slots(int64_t max_chunks) { return SLOTS0 + (max_chunks - 1) * SLOTS; }
+// The run slots of every chunk, plus one last slot that is never written (the
+// scratch is zeroed when the cache is created): the replay pads its batches
+// with it.
+int64_t chunked_pool_slots(int64_t max_chunks) { return SLOTS0 + (max_chunks - 1) * SLOTS + 1; }
 
 static void carve(const Geom &g, int64_t max_chunks, int64_t pool, uint8_t *p, Chunked *ck,
                   size_t *total) {

@@ -413,6 +413,52 @@ def test_ragged_batch_multi_chunk(ctx):
             np.testing.assert_array_equal(out[b], want, err_msg=f"{mode} seq {b}")
 
 
+def _host_reference_kv(k, v, q, n_kv, two_pass=False):
+    """Per KV group oracle outputs for any number of KV heads (4 query heads each)."""
+    T = k.shape[0]
+    host = Cache(n_kv, T, FMT)
+    host.append_rotated(k, v)
+    fn = native.attend_two_pass if two_pass else native.attend_online
+    outs, sts = [], []
+    for h in range(n_kv):
+        o, s = fn(q[4 * h:4 * h + 4], host.view(h), FMT)
+        outs.append(o)
+        sts.append(s)
+    return np.concatenate(outs), sts
+
+
+@pytest.mark.parametrize("n_kv,lens", [
+    (2, [5000, 3100, 4097]),            # 6 (sequence, KV head) chains
+    (1, [9000, 2500, 1, 7000, 4200]),   # 5 chains
+    (3, [20000]),                       # 3 chains, 20 chunks each
+])
+def test_chains_that_straddle_xcds(ctx, n_kv, lens):
+    """Workgroups are numbered chunk-major and dispatched round-robin over the 8
+    XCDs, so with a chain count that is not a multiple of 8 the chunks of one
+    chain run on different XCDs: the look-back words, run sums, headers and
+    completion counter are then exchanged across XCD L2s."""
+    from insitu_amd.attention import CompressedAttention
+    rng = np.random.default_rng(sum(lens) + n_kv)
+    c = _cache(ctx, max(lens), batch=len(lens), n_kv=n_kv, n_q=4 * n_kv)
+    data = []
+    for b, T in enumerate(lens):
+        k, v = _random_cache_inputs(rng, T, n_kv=n_kv)
+        c.append_rotated(k, v, seq=b)
+        data.append((k, v))
+    q = rng.integers(-(1 << 22), 1 << 22, size=(len(lens), 4 * n_kv, 64))
+    for mode in ("online", "two_pass"):
+        for rep in range(2):
+            out, st = CompressedAttention(c).attend(q, mode)
+            out = out.cpu().numpy()
+            events = 0
+            for b, (k, v) in enumerate(data):
+                want, sts = _host_reference_kv(k, v, q[b], n_kv, two_pass=(mode == "two_pass"))
+                np.testing.assert_array_equal(out[b], want, err_msg=f"{mode} rep {rep} seq {b}")
+                events += sum(s.rescale_events for s in sts)
+            assert st.serial_fallbacks == 0
+            assert st.rescale_events == events
+
+
 def test_repeated_calls_reuse_the_counters(ctx):
     """The chunk-completion and run-pool counters are reset by each call's last workgroup."""
     from insitu_amd.attention import CompressedAttention
