@@ -156,6 +156,7 @@ struct ChunkLds {
         Replay rp;
         SerialLds<KF<D, KB>::RS> fb[GF];
     } u;
+    double qf[D][GF];
     double kcf[16];
     int64_t kc[16];
     int64_t vc[16];
@@ -194,7 +195,7 @@ static_assert(SLOTS0 + (HMAX - 1) * SLOTS < RUN_EVENT, "run slots of the chunked
 template <int D>
 __device__ __forceinline__ bool load_q(const Geom &g, const Tables *__restrict__ tabs,
                                        const int32_t *__restrict__ q, int b, int kvh, bool count,
-                                       double *qslot, double *kcf, int *qok, DevStats *st) {
+                                       double (*qf)[GF], double *kcf, int *qok, DevStats *st) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int nk = 1 << g.kb;
     if (tid < nk) kcf[tid] = (double)tabs->kc[tid];
@@ -207,7 +208,7 @@ __device__ __forceinline__ bool load_q(const Geom &g, const Tables *__restrict__
         for (int k = 0; k < D / 64; ++k) {
             const int c = lane + 64 * k;
             const int32_t v = qrow[c];
-            qslot[c * GF + wv] = (double)v;
+            qf[c][wv] = (double)v;
             l1 += v < 0 ? -(int64_t)v : (int64_t)v;
             bad += ((int64_t)v >= Q_ROT_LIMIT || (int64_t)v <= -Q_ROT_LIMIT) ? 1 : 0;
         }
@@ -220,7 +221,6 @@ __device__ __forceinline__ bool load_q(const Geom &g, const Tables *__restrict__
             if (count && bad) atomicAdd(&st->range_errors, (unsigned long long)bad);
         }
     }
-    __builtin_amdgcn_s_waitcnt(0);          // this thread's slot stores have completed
     __syncthreads();
     return *qok != 0;
 }
@@ -263,26 +263,35 @@ __device__ __forceinline__ void load_keys(const Geom &g, const uint8_t *__restri
                                           uint32_t (&normw)[TPT]) {
     using K = KF<D, KB>;
     const int tid = threadIdx.x;
+    // Plane by plane across the thread's tokens, in the order the score loop
+    // uses them, so that it can start on the first plane while the rest land.
+    int64_t tc[TPT];
 #pragma unroll
     for (int j = 0; j < TPT; ++j) {
         const int64_t t = t0 + tid * TPT + j;
-        const int64_t tc = t < T ? t : 0;            // past the end: read token 0, unused
+        tc[j] = t < T ? t : 0;                       // past the end: read token 0, unused
+        w[j][K::KWORDS] = 0;
+    }
 #pragma unroll
-        for (int p = 0; p < K::NFULL; ++p) {
-            const uint4 v = *(const uint4 *)(hb + p * g.span + tc * 16);
+    for (int p = 0; p < K::NFULL; ++p)
+#pragma unroll
+        for (int j = 0; j < TPT; ++j) {
+            const uint4 v = *(const uint4 *)(hb + p * g.span + tc[j] * 16);
             w[j][4 * p] = v.x;
             w[j][4 * p + 1] = v.y;
             w[j][4 * p + 2] = v.z;
             w[j][4 * p + 3] = v.w;
         }
-        if (K::HALF) {
-            const uint2 v = *(const uint2 *)(hb + K::NFULL * g.span + tc * 8);
+    if (K::HALF) {
+#pragma unroll
+        for (int j = 0; j < TPT; ++j) {
+            const uint2 v = *(const uint2 *)(hb + K::NFULL * g.span + tc[j] * 8);
             w[j][4 * K::NFULL] = v.x;
             w[j][4 * K::NFULL + 1] = v.y;
         }
-        w[j][K::KWORDS] = 0;
-        normw[j] = *(const uint32_t *)(hb + (g.n_planes - 1) * g.span + tc * 4);
     }
+#pragma unroll
+    for (int j = 0; j < TPT; ++j) normw[j] = *(const uint32_t *)(hb + (g.n_planes - 1) * g.span + tc[j] * 4);
 }
 
 // Exact scores of those tokens for the GF heads (attention.py:333-359), in
@@ -295,7 +304,7 @@ __device__ __forceinline__ void load_keys(const Geom &g, const uint8_t *__restri
 // query values feed the FMAs as scalar operands.
 template <int D, int KB>
 __device__ __forceinline__ void score_keys(const uint32_t (&w)[TPT][KF<D, KB>::KWORDS + 1],
-                                           const uint32_t (&normw)[TPT], const double *qslot,
+                                           const uint32_t (&normw)[TPT], const double (*qf)[GF],
                                            const double *kcf, int score_shift,
                                            int64_t (&s)[TPT][GF]) {
     using K = KF<D, KB>;
@@ -314,7 +323,11 @@ __device__ __forceinline__ void score_keys(const uint32_t (&w)[TPT][KF<D, KB>::K
 #pragma unroll
             for (int i = 0; i < 8; ++i) cv[j][i] = kcf[(win >> (i * KB)) & K::MASK];
         }
-        const QGroup qv = qgroup(qslot, grp);
+        QGroup qv;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int h = 0; h < GF; ++h) qv.v[i][h] = qf[8 * grp + i][h];
 #pragma unroll
         for (int i = 0; i < 8; ++i)
 #pragma unroll
@@ -345,6 +358,7 @@ __global__ void __launch_bounds__(CT) chunk_max_kernel(Geom g, const Tables *__r
                                                        const int32_t *__restrict__ q,
                                                        const int64_t *__restrict__ len,
                                                        Chunked ck, DevStats *st) {
+    __shared__ double qf[D][GF];
     __shared__ double kcf[16];
     __shared__ int qok;
     __shared__ int64_t red[CT / 64][GF];
@@ -356,8 +370,7 @@ __global__ void __launch_bounds__(CT) chunk_max_kernel(Geom g, const Tables *__r
     if (chunk >= nch) return;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     if (tid == 0) ovf_s = mabs_s = 0;
-    double *qslot = ck.qd + (int64_t)chain * D * GF;
-    const bool ok = load_q<D>(g, tabs, q, b, kvh, chunk == 0, qslot, kcf, &qok, st);
+    const bool ok = load_q<D>(g, tabs, q, b, kvh, chunk == 0, qf, kcf, &qok, st);
     int64_t mx[GF];
 #pragma unroll
     for (int h = 0; h < GF; ++h) mx[h] = SCORE_LO;
@@ -369,7 +382,7 @@ __global__ void __launch_bounds__(CT) chunk_max_kernel(Geom g, const Tables *__r
         uint32_t kw[TPT][KF<D, KB>::KWORDS + 1];
         const int64_t t0 = (int64_t)chunk * CHUNK;
         load_keys<D, KB>(g, plane_ptr(g, b, kvh, 0), t0, T, kw, nw);
-        score_keys<D, KB>(kw, nw, qslot, kcf, CENT_FRAC + g.norm_frac, s);
+        score_keys<D, KB>(kw, nw, qf, kcf, CENT_FRAC + g.norm_frac, s);
 #pragma unroll
         for (int j = 0; j < TPT; ++j) {
             if (t0 + tid * TPT + j >= T) continue;
@@ -441,8 +454,21 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
     const int64_t t0 = (int64_t)chunk * CHUNK;
 
     if (has_work) {
-        // Issue this chunk's key and value loads first; they land while the
-        // query and the tables are staged below.
+        // The small loads first (the tables and the group's query rows), then this
+        // chunk's keys and values plane by plane. The counter of outstanding
+        // vector loads drains in order, so staging the small values must not
+        // wait for the chunk's data, and the score loop starts on the first key
+        // plane while the others land.
+        const int nk = 1 << g.kb;
+        const int64_t kc_t = tid < nk ? tabs->kc[tid] : 0;
+        const int64_t vc_t = tid < nv ? tabs->vc[tid] : 0;
+        const int32_t ex_t = tid < 256 ? tabs->exp_table[tid] : 0;
+        int32_t q_t[D / 64];
+        {
+            const int32_t *qrow = q + ((int64_t)b * g.n_q + kvh * GF + (wv < GF ? wv : 0)) * D;
+#pragma unroll
+            for (int k = 0; k < D / 64; ++k) q_t[k] = wv < GF ? qrow[lane + 64 * k] : 0;
+        }
         const uint8_t *hb = plane_ptr(g, b, kvh, 0);
         uint32_t kw[TPT][K::KWORDS + 1];
         uint32_t nw[TPT];
@@ -464,27 +490,47 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     if (4 * p + i < K::VW) vreg[j][4 * p + i] = 4 * p + i < vwords ? src[i] : 0u;
             }
         }
-        if (tid < 16) S.kc[tid] = tid < (1 << g.kb) ? tabs->kc[tid] : 0;
         if (tid < 16) {
-            const int64_t c = tid < nv ? tabs->vc[tid] : 0;
-            S.vc[tid] = c;
-            S.vc32[tid] = (int32_t)c;                 // |centroid| < 2^18 (Q1.15)
+            S.kc[tid] = kc_t;
+            S.kcf[tid] = (double)kc_t;
+            S.vc[tid] = vc_t;
+            S.vc32[tid] = (int32_t)vc_t;               // |centroid| < 2^18 (Q1.15)
         }
-        if (tid == 0) {
-            int64_t m = 0;
-            for (int i = 0; i < nv; ++i) {
-                const int64_t a = tabs->vc[i] < 0 ? -tabs->vc[i] : tabs->vc[i];
-                m = a > m ? a : m;
-            }
-            S.vcmax = m;
+        if (tid < 256) S.expt[tid] = ex_t;
+        if (wv == 0) {
+            const int64_t m = wave_max_i64(vc_t < 0 ? -vc_t : vc_t);
+            if (lane == 0) S.vcmax = m;
         }
-        if (tid < 256) S.expt[tid] = tabs->exp_table[tid];
         if (tid == 0) {
             S.ovf = S.mabs = 0;
             S.lb_fail = 0;
+            S.qok = 1;
         }
-        double *qslot = ck.qd + (int64_t)chain * D * GF;
-        const bool ok = load_q<D>(g, tabs, q, b, kvh, SEQ && chunk == 0, qslot, S.kcf, &S.qok, st);
+        __syncthreads();
+        // The query rows (fp64) into LDS, and the check that every score of the
+        // group stays an exact fp64 integer: |dot| <= ||q||_1 * max|c| < 2^51.
+        // Chunk 0 counts rotated queries beyond the +-2^27 the 24-bit seam can
+        // produce (once per call).
+        if (wv < GF) {
+            int64_t l1 = 0, bad = 0;
+#pragma unroll
+            for (int k = 0; k < D / 64; ++k) {
+                const int32_t v = q_t[k];
+                S.qf[lane + 64 * k][wv] = (double)v;
+                l1 += v < 0 ? -(int64_t)v : (int64_t)v;
+                bad += ((int64_t)v >= Q_ROT_LIMIT || (int64_t)v <= -Q_ROT_LIMIT) ? 1 : 0;
+            }
+            l1 = wave_sum_i64(l1);                  // < 2^38: exact as a double below
+            bad = wave_sum_i64(bad);
+            if (lane == 0) {
+                double cmax = 0.0;
+                for (int i = 0; i < nk; ++i) cmax = fmax(cmax, fabs(S.kcf[i]));
+                if (!((double)l1 * cmax < DOT_LIMIT)) atomicAnd(&S.qok, 0);
+                if (SEQ && chunk == 0 && bad) atomicAdd(&st->range_errors, (unsigned long long)bad);
+            }
+        }
+        __syncthreads();
+        const bool ok = S.qok != 0;
 
         // -- phase 1: scores of the thread's TPT consecutive tokens, which stay in
         // registers for the scan; value codes into LDS ----------------------------
@@ -494,7 +540,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
         for (int h = 0; h < GF; ++h) mx[h] = SCORE_LO;
         if (ok) {
             int64_t s[TPT][GF];
-            score_keys<D, KB>(kw, nw, qslot, S.kcf, score_shift, s);
+            score_keys<D, KB>(kw, nw, S.qf, S.kcf, score_shift, s);
             unsigned long long ovf = 0;
             int64_t mabs = 0;
 #pragma unroll
