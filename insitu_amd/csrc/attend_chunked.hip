@@ -133,18 +133,20 @@ __device__ __forceinline__ int64_t st_val(unsigned long long w) {
     return (int64_t)(w & ST_VAL) + SCORE_LO;
 }
 
-// An active token of a chunk (p != 0, or a rescale event) for one head:
-// token index | event << 10 | value << 11, the value being p, or the factor f
-// at an event (where p is LUT(0), the same for every event).
+// A candidate token of a chunk for one head (a rescale event, or a token less
+// than delta_max below the running maximum): token index | event << 10 |
+// distance << 11. The distance is s - prev at an event and prev - s otherwise,
+// clamped to delta_max (< 2^20), so that LUT(distance) is the event's factor f
+// or the token's p (an event's own p is LUT(0), the same for every event).
 static_assert(CHUNK <= 1024, "ActRec holds a 10-bit token index");
-__device__ __forceinline__ uint32_t act_rec(int tl, bool ev, uint32_t val) {
-    return (uint32_t)tl | (ev ? 1u << 10 : 0u) | (val << 11);
+__device__ __forceinline__ uint32_t act_rec(int tl, bool ev, uint32_t dist) {
+    return (uint32_t)tl | (ev ? 1u << 10 : 0u) | (dist << 11);
 }
 
 template <int D, int KB>
 struct ChunkLds {
     struct Phase {
-        uint32_t rec[GF][CHUNK];   // each head's active tokens in order (ActRec)
+        uint32_t rec[GF][CHUNK];   // each head's candidate tokens in order (act_rec)
         uint32_t vw[CHUNK][KF<D, KB>::VW];
         int16_t vn[CHUNK];
     };
@@ -163,11 +165,11 @@ struct ChunkLds {
     int32_t vc32[16];
     int64_t vcmax;
     int32_t expt[256];
-    int32_t cntw[CT / 64][GF];     // active tokens per wave and head
-    int32_t evw[CT / 64][GF];      // rescale events per wave and head
+    int32_t cntw[GF][CT / 64];     // candidate tokens per head and wave
+    int32_t evw[GF][CT / 64];      // rescale events per head and wave
     int64_t min_[GF];              // the maximum before this chunk (two-pass: of all chunks)
     int64_t lmax[GF];              // this chunk's own maximum
-    int64_t wt[CT / 64][GF];
+    int64_t wt[GF][CT / 64];       // per head, each wave's maximum score
     int64_t red[CT / 64][GF];
     int qok;
     int last;
@@ -650,12 +652,12 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
         __syncthreads();
         if (SEQ && S.lb_fail && tid == 0) atomicOr(&ck.chain_fb[chain], 1u);
 
-        // -- phase 3: events, p, and each head's active tokens listed in order ----
+        // -- phase 3: events and each head's candidate tokens listed in order ----
         // (the thread owns TPT consecutive tokens). Two exact shortcuts: a head
         // whose chunk maximum does not exceed the maximum before the chunk has no
         // rescale event, so it needs no scan; and a token at or below
         // prev - delta_max has p = 0 for every later prev too (prev only grows),
-        // so a wave whose tokens are all that far down does no LUT work.
+        // so a wave whose tokens are all that far down records nothing.
         if (ok) {
             const int64_t dm = tabs->delta_max;
             bool evh[GF];
@@ -671,7 +673,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
 #pragma unroll
                     for (int j = 0; j < TPT; ++j) run = sv[h][j] > run ? sv[h][j] : run;
                     const int64_t v = wave_scan64<OpMax64>(run, SCORE_LO);
-                    if (lane == 63) S.wt[wv][h] = v;
+                    if (lane == 63) S.wt[h][wv] = v;
                     excl[h] = wave_shr1_64(v, SCORE_LO);
                 }
             }
@@ -683,7 +685,12 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             for (int h = 0; h < GF; ++h) {
                 int64_t prev = uni64(S.min_[h]);
                 if (evh[h]) {
-                    for (int w = 0; w < wv; ++w) prev = S.wt[w][h] > prev ? S.wt[w][h] : prev;
+                    // the maxima of the waves before this one: independent reads
+#pragma unroll
+                    for (int w = 0; w < CT / 64 - 1; ++w) {
+                        const int64_t m = S.wt[h][w];
+                        prev = w < wv && m > prev ? m : prev;
+                    }
                     prev = excl[h] > prev ? excl[h] : prev;
                 }
                 act[h] = 0;
@@ -696,8 +703,12 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                 }
                 int32_t tot = 0, evt = 0;
                 if (__ballot(live)) {
-                    // Branch-free per token: an event records f = LUT(s - prev)
-                    // (its own p is LUT(0)), any other token p = LUT(prev - s).
+                    // Per token only compares: the candidates are the events and
+                    // the tokens less than delta_max below the running maximum
+                    // (the others have p = 0). A candidate records its distance
+                    // from the running maximum, clamped to delta_max; the run-sum
+                    // phase turns it into f = LUT(s - prev) at an event (whose
+                    // own p is LUT(0)) or p = LUT(prev - s), one lane per entry.
                     // Counts and list positions come from one ballot per token
                     // slot: the lanes below hold the earlier tokens.
                     uint32_t before = 0;
@@ -706,11 +717,13 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                         const int tl = tid * TPT + j;
                         const bool in = t0 + tl < T;
                         const int64_t sj = sv[h][j];
-                        const bool ev = evh[h] && in && sj > prev;
-                        const uint32_t val = (uint32_t)exp_lut(ev ? sj - prev : prev - sj, S.expt, dm);
+                        const int64_t d = prev - sj;
+                        const bool ev = evh[h] && in && d < 0;
+                        const bool a = in && d < dm;               // events included
+                        const int64_t up = -d < dm ? -d : dm;
+                        const uint32_t dd = (uint32_t)(ev ? up : d);   // <= delta_max < 2^20 when a
                         prev = ev ? sj : prev;
-                        rec[h][j] = act_rec(tl, ev, val);          // val <= 2^15 fits the field
-                        const bool a = in && (ev || val != 0);
+                        rec[h][j] = act_rec(tl, ev, dd);
                         act[h] |= a ? 1u << j : 0u;
                         const uint64_t ba = __ballot(a);
                         before += __builtin_amdgcn_mbcnt_hi((uint32_t)(ba >> 32),
@@ -721,8 +734,8 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     pos[h] = before;
                 }
                 if (lane == 0) {
-                    S.cntw[wv][h] = tot;
-                    S.evw[wv][h] = evt;
+                    S.cntw[h][wv] = tot;
+                    S.evw[h][wv] = evt;
                 }
             }
             __syncthreads();
@@ -730,7 +743,8 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             for (int h = 0; h < GF; ++h) {
                 if (!act[h]) continue;
                 uint32_t at = pos[h];
-                for (int w = 0; w < wv; ++w) at += (uint32_t)S.cntw[w][h];
+#pragma unroll
+                for (int w = 0; w < CT / 64 - 1; ++w) at += w < wv ? (uint32_t)S.cntw[h][w] : 0u;
 #pragma unroll
                 for (int j = 0; j < TPT; ++j)
                     if ((act[h] >> j) & 1u) S.u.ph.rec[h][at++] = rec[h][j];
@@ -738,14 +752,14 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
         }
         __syncthreads();
 
-        // -- phase 4: run sums over the active list, wave = head, lane = channel --
+        // -- phase 4: run sums over the candidate list, wave = head, lane = channel -
         if (ok && wv < GF) {
             const int h = wv;
             int n_act = 0, n_ev = 0;
 #pragma unroll
             for (int w = 0; w < CT / 64; ++w) {
-                n_act += S.cntw[w][h];
-                n_ev += S.evw[w][h];
+                n_act += S.cntw[h][w];
+                n_ev += S.evw[h][w];
             }
             n_act = uni32(n_act);
             n_ev = uni32(n_ev);
@@ -765,37 +779,65 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                 const uint32_t vmask = (1u << g.vb) - 1u;
                 const uint64_t vcmax = (uint64_t)uni64(S.vcmax);
                 const int32_t pev = uni32(S.expt[0]);       // p of an event token: LUT(0)
-                SegMeta *meta = ck.meta + ((int64_t)chain * GF + h) * ck.pool;
-                int32_t *segS = ck.segS + ((int64_t)chain * GF + h) * ck.pool * D;
-                int seg = 0;
-                int32_t segf = 0;
-                // |run sum| <= B < 2^31 unless FLAG_WIDE, so int32 sums are exact
-                // whenever they are used.
-                int32_t Ssum[CPL];
+                const int64_t dm = tabs->delta_max;
+                SegMeta *meta = ck.meta + ((int64_t)chain * GF + h) * ck.pool + off;
+                int32_t *segS = ck.segS + (((int64_t)chain * GF + h) * ck.pool + off) * D;
+                // P: the running sum of the terms (wrapping int32), P0 its value
+                // where the open run began; a run's sum is their difference, exact
+                // because |run sum| <= B < 2^31 unless FLAG_WIDE is set.
+                int32_t P[CPL], P0[CPL];
 #pragma unroll
-                for (int k = 0; k < CPL; ++k) Ssum[k] = 0;
-                int64_t L = 0, B = 0;
-                auto close_run = [&]() {
-                    if (B > ACC_HI) flags |= FLAG_WIDE;
-                    if (lane == 0) {
-                        pub64(&meta[off + seg].lf, (uint64_t)L | ((uint64_t)(uint32_t)segf << 32));
-                        pub64(&meta[off + seg].b, (uint64_t)B);
-                    }
-#pragma unroll
-                    for (int k = 0; k < CPL; ++k)
-                        pub32(&segS[(int64_t)(off + seg) * D + lane + 64 * k], (uint32_t)Ssum[k]);
-                };
+                for (int k = 0; k < CPL; ++k) P[k] = P0[k] = 0;
+                int seg = 0;                  // runs closed so far
+                int64_t Lc = 0, Bc = 0;       // sums of p and of the term bounds so far
+                int64_t Ls = 0, Bs = 0;       // the same where the open run began
+                int64_t fkey = 0;             // the open run's event: (entry + 1) << 16 | f
+                bool wide = false;
                 for (int a0 = 0; a0 < n_act; a0 += 64) {
-                    // lane i decodes list entry a0 + i; the walk reads them back with readlane
+                    // Lane = entry: decode entry a0 + lane. An event's p is LUT(0)
+                    // and its LUT value is the factor f opening its run; a candidate
+                    // whose p is 0 adds exactly nothing, so its bound term is 0.
                     const int e = a0 + lane;
-                    const uint32_t r = e < n_act ? S.u.ph.rec[h][e] : 0u;
+                    const bool in = e < n_act;
+                    const uint32_t r = in ? S.u.ph.rec[h][e] : 0u;
                     const int tl_i = (int)(r & 1023u);
-                    const int ev_i = (int)((r >> 10) & 1u);
-                    const int val_i = (int)(r >> 11);
-                    const int32_t p_i = ev_i ? pev : val_i;
+                    const bool ev_i = in && ((r >> 10) & 1u);
+                    const int val_i = exp_lut((int64_t)(r >> 11), S.expt, dm);
+                    const int32_t p_i = in ? (ev_i ? pev : val_i) : 0;
                     const int32_t w_i = (int32_t)S.u.ph.vn[tl_i] * p_i;       // |w| <= 2^30
                     const uint64_t aw = (uint64_t)(w_i < 0 ? -(int64_t)w_i : (int64_t)w_i);
-                    const int32_t bw_i = (int32_t)((aw * vcmax) >> acc_shift) + 1;
+                    const int64_t bw_i = w_i != 0 ? (int64_t)((aw * vcmax) >> acc_shift) + 1 : 0;
+                    const uint64_t evm = __ballot(ev_i);
+                    // L and B of every run an event of this block closes: prefix sums
+                    // over the entries, less their values where that run began (at
+                    // the previous event, or where the open run began before the
+                    // block -- prefix sums never decrease, so an exclusive max-scan
+                    // over the events finds it). f comes the same way, keyed by entry.
+                    const int64_t lp = Lc + wave_scan64<OpAdd64>(p_i, 0);
+                    const int64_t bp = Bc + wave_scan64<OpAdd64>(bw_i, 0);
+                    const int64_t lx = lp - p_i, bx = bp - bw_i;              // before the entry
+                    const int64_t key = ev_i ? (int64_t)(e + 1) << 16 | val_i : fkey;
+                    const int64_t lb = wave_shr1_64(wave_scan64<OpMax64>(ev_i ? lx : Ls, Ls), Ls);
+                    const int64_t bb = wave_shr1_64(wave_scan64<OpMax64>(ev_i ? bx : Bs, Bs), Bs);
+                    const int64_t kb = wave_shr1_64(wave_scan64<OpMax64>(key, fkey), fkey);
+                    if (ev_i) {
+                        const int ri = seg + (int)__builtin_amdgcn_mbcnt_hi(
+                                                 (uint32_t)(evm >> 32),
+                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)evm, 0u));
+                        const int64_t B = bx - bb;
+                        wide = wide || B > ACC_HI;
+                        pub64(&meta[ri].lf, (uint64_t)(lx - lb) | ((uint64_t)(kb & 0xFFFF) << 32));
+                        pub64(&meta[ri].b, (uint64_t)B);
+                    }
+                    Lc = readlane64(lp, 63);
+                    Bc = readlane64(bp, 63);
+                    if (evm) {
+                        const int le = 63 - __clzll((long long)evm);        // the block's last event
+                        Ls = readlane64(lx, le);
+                        Bs = readlane64(bx, le);
+                        fkey = readlane64(key, le);
+                    }
+                    // Lane = channel: the terms of the entries in order, 8 at a time.
                     const int cnt = n_act - a0 < 64 ? n_act - a0 : 64;
                     for (int j0 = 0; j0 < cnt; j0 += 8) {
                         // the centroids of the next 8 entries first (independent LDS reads)
@@ -816,26 +858,33 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                         for (int jj = 0; jj < 8; ++jj) {
                             const int j = j0 + jj;
                             if (j < cnt) {
-                                if (__builtin_amdgcn_readlane(ev_i, j)) {
-                                    close_run();
-                                    ++seg;
-                                    segf = __builtin_amdgcn_readlane(val_i, j);
+                                if ((evm >> j) & 1ull) {
+                                    // the event closes the open run: publish its sum
 #pragma unroll
-                                    for (int k = 0; k < CPL; ++k) Ssum[k] = 0;
-                                    L = 0;
-                                    B = 0;
+                                    for (int k = 0; k < CPL; ++k) {
+                                        pub32(&segS[(int64_t)seg * D + lane + 64 * k], (uint32_t)(P[k] - P0[k]));
+                                        P0[k] = P[k];
+                                    }
+                                    ++seg;
                                 }
                                 const int32_t w = __builtin_amdgcn_readlane(w_i, j);
 #pragma unroll
                                 for (int k = 0; k < CPL; ++k)
-                                    Ssum[k] += (int32_t)(((int64_t)w * cv[jj][k]) >> acc_shift);
-                                L += __builtin_amdgcn_readlane(p_i, j);
-                                B += __builtin_amdgcn_readlane(bw_i, j);
+                                    P[k] += (int32_t)(((int64_t)w * cv[jj][k]) >> acc_shift);
                             }
                         }
                     }
                 }
-                close_run();
+                // the open run closes at the end of the chunk
+                if (lane == 0) {
+                    pub64(&meta[seg].lf, (uint64_t)(Lc - Ls) | ((uint64_t)(fkey & 0xFFFF) << 32));
+                    pub64(&meta[seg].b, (uint64_t)(Bc - Bs));
+                }
+                wide = wide || Bc - Bs > ACC_HI;
+#pragma unroll
+                for (int k = 0; k < CPL; ++k)
+                    pub32(&segS[(int64_t)seg * D + lane + 64 * k], (uint32_t)(P[k] - P0[k]));
+                if (__ballot(wide)) flags |= FLAG_WIDE;
             }
             if (lane == 0) {
                 ChunkHdr *hp = &ck.hdr[((int64_t)chain * ck.max_chunks + chunk) * GF + h];
