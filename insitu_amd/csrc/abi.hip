@@ -101,6 +101,7 @@ struct insitu_cache {
     int32_t *wire_scratch = nullptr;      // rotated q/k/v for insitu_step
     void *chunk_scratch = nullptr;        // run sums and counters of the chunked attend
     int64_t max_chunks = 0, pool = 0;
+    uint32_t calls = 0;                   // chunked attends so far: tags this call's flags
 };
 
 namespace {
@@ -363,7 +364,7 @@ int insitu_cache_create(insitu_ctx *c, const insitu_cache_desc *desc, insitu_cac
     if (e == hipSuccess)
         e = hipMalloc(&k->wire_scratch,
                       sizeof(int32_t) * (size_t)g.batch * (g.n_q + 2 * g.n_kv) * g.d);
-    if (e == hipSuccess && chunked_supported(g)) {
+    if (e == hipSuccess && chunked_supported(g, desc->capacity)) {
         k->max_chunks = chunked_max_chunks(desc->capacity);
         k->pool = chunked_pool_slots(k->max_chunks);
         const size_t nb = chunked_scratch_bytes(g, k->max_chunks, k->pool);
@@ -483,7 +484,7 @@ static int attend_impl(insitu_cache *k, const int32_t *q, int32_t *out, int32_t 
     const int two_pass = mode == INSITU_TWO_PASS ? 1 : 0;
     if (mode != INSITU_SERIAL && k->chunk_scratch) {
         HIP_TRY(launch_attend_chunked(k->ctx->stream, k->g, k->tabs, q, out, len, k->chunk_scratch,
-                                      k->max_chunks, k->pool, two_pass, k->stats),
+                                      k->max_chunks, k->pool, k->calls++, two_pass, k->stats),
                 "chunked attend launch");
         return INSITU_OK;
     }

@@ -51,20 +51,26 @@ constexpr int GF = 4;                // query heads per KV head on this path
 constexpr int VB_MAX = 3;            // widest value code staged in LDS
 constexpr int HMAX = 512;            // chunks per (sequence, KV head) on the chunked path
 constexpr int NSEG = 2048;           // runs per (sequence, KV head, query head) the replay lists
-constexpr int SLOTS0 = 64;           // run slots of chunk 0 (it sees most rescale events)
-constexpr int SLOTS = 8;             // run slots of every later chunk
+constexpr int SLOTS = 8;             // run slots of every chunk after chunk 0 (which holds one state)
 constexpr uint16_t RUN_EVENT = 0x8000;
 constexpr int FLAG_POOL = 1;         // run pool exhausted
 constexpr int FLAG_WIDE = 2;         // a run sum bound reached 2^31
+// Look-back words: flag (bits 62-63) | call epoch (bits 48-61) | score - SCORE_LO
+// (bits 0-47). A word whose epoch is not the current call's is unpublished, so
+// the words never need resetting between calls.
 constexpr unsigned long long ST_AGG = 1ull << 62, ST_INC = 2ull << 62;
-constexpr unsigned long long ST_VAL = (1ull << 62) - 1;
+constexpr unsigned long long ST_FLAGS = 3ull << 62;
+constexpr int EPOCH_BITS = 14;
+constexpr unsigned EPOCH_MASK = (1u << EPOCH_BITS) - 1u;
 constexpr int SPIN_LIMIT = 1 << 20;
 constexpr double MAGIC = 6755399441055744.0;   // 1.5 * 2^52
 constexpr int64_t MAGIC_BITS = 0x4338000000000000LL;
 constexpr double DOT_LIMIT = 2251799813685248.0;  // 2^51
 
 // What a chunk publishes, per query head: w0 = n_seg | flags << 16 | score
-// overflows << 32, w1 = max |score| (both per chunk, all heads). A run slot
+// overflows << 24 | call epoch << 40, w1 = max |score| (the statistics are per
+// chunk, all heads). w0 is the flag the replaying workgroup polls: it goes out
+// after the head's run slots and w1 have completed. A run slot
 // holds lf = L | f << 32 (L = sum of p < 2^26, f = the factor opening the run,
 // <= 2^15) and b = B, the bound on |run sum| (< 2^31 unless FLAG_WIDE is set).
 // Everything published between workgroups goes through relaxed agent-scope
@@ -102,10 +108,10 @@ struct Chunked {
     ChunkHdr *hdr;                 // [chain][max_chunks][GF]
     SegMeta *meta;                 // [chain][GF][pool]
     int32_t *segS;                 // [chain][GF][pool][d]
-    unsigned int *done;            // [chain]
-    unsigned int *chain_fb;        // [chain]  nonzero: recompute this chain serially
-    double *qd;                    // [chain][D][GF]  the chain's query rows in fp64
+    unsigned int *done;            // [chain]  workgroups of the chain done with their runs
+    unsigned int *chain_fb;        // [chain]  the call's epoch: recompute this chain serially
     int32_t max_chunks, pool;
+    uint32_t ep;                   // this call's epoch, 1 .. 2^14 - 1
 };
 
 template <int D, int KB>
@@ -126,11 +132,14 @@ __device__ __forceinline__ int64_t dbl_to_i64(double x) {
     return (int64_t)__double_as_longlong(x + MAGIC) - MAGIC_BITS;
 }
 
-__device__ __forceinline__ unsigned long long st_pack(unsigned long long flag, int64_t v) {
-    return flag | (unsigned long long)(v - SCORE_LO);
+__device__ __forceinline__ unsigned long long st_pack(unsigned long long flag, unsigned ep, int64_t v) {
+    return flag | (unsigned long long)ep << 48 | (unsigned long long)(v - SCORE_LO);
+}
+__device__ __forceinline__ unsigned long long st_flag(unsigned long long w, unsigned ep) {
+    return ((unsigned)(w >> 48) & EPOCH_MASK) == ep ? w & ST_FLAGS : 0ull;
 }
 __device__ __forceinline__ int64_t st_val(unsigned long long w) {
-    return (int64_t)(w & ST_VAL) + SCORE_LO;
+    return (int64_t)(w & ((1ull << 48) - 1)) + SCORE_LO;
 }
 
 // A candidate token of a chunk for one head (a rescale event, or a token less
@@ -177,23 +186,15 @@ struct ChunkLds {
     unsigned long long ovf, mabs;
 };
 
-// Run slots of a chunk: chunk 0 owns [0, SLOTS0), chunk c > 0 owns SLOTS after it.
-__device__ __forceinline__ int slot_base(int chunk) { return chunk == 0 ? 0 : SLOTS0 + (chunk - 1) * SLOTS; }
-__device__ __forceinline__ int slot_count(int chunk) { return chunk == 0 ? SLOTS0 : SLOTS; }
-static_assert(SLOTS0 + (HMAX - 1) * SLOTS < RUN_EVENT, "run slots of the chunked path fit 15 bits");
+// Run slots: chunk 0 owns slot 0 (its replayed state), chunk c > 0 owns SLOTS after it.
+__device__ __forceinline__ int slot_base(int chunk) { return chunk == 0 ? 0 : 1 + (chunk - 1) * SLOTS; }
+static_assert(1 + (HMAX - 1) * SLOTS < RUN_EVENT, "run slots of the chunked path fit 15 bits");
 
-// Shared prologue: the key centroids (fp64) into LDS, and the KV group's GF
-// query rows in fp64, channel-major ([c][h]), into the chain's slot of global
-// scratch, from where the score loop reads them back with scalar loads (as
-// scalar FMA operands; see qgroup). Every workgroup of a chain writes the same
-// values to the same slot, so their stores may overlap harmlessly; each reads
-// the slot only after its own stores have completed. The scalar cache cannot
-// hold an older copy: it is invalidated at the start of every dispatch and the
-// slot is not read before this point.
-//
-// Also checks that every score of the group stays an exact fp64 integer:
-// |dot| <= ||q||_1 * max|c| < 2^51. With `count`, queries beyond the +-2^27
-// the 24-bit seam can produce are counted as range errors (once per call).
+// The two-pass pre-pass's prologue: the key centroids (fp64) and the KV
+// group's GF query rows (fp64, channel-major [c][h]) into LDS, and the check
+// that every score of the group stays an exact fp64 integer:
+// |dot| <= ||q||_1 * max|c| < 2^51. With `count`, queries beyond the +-2^27 the
+// 24-bit seam can produce are counted as range errors (once per call).
 template <int D>
 __device__ __forceinline__ bool load_q(const Geom &g, const Tables *__restrict__ tabs,
                                        const int32_t *__restrict__ q, int b, int kvh, bool count,
@@ -227,35 +228,6 @@ __device__ __forceinline__ bool load_q(const Geom &g, const Tables *__restrict__
     return *qok != 0;
 }
 
-// The 8 x GF query values of channel group grp (256 bytes of the slot) into
-// SGPRs: four 64-byte scalar loads and a wait. Inline assembly because the
-// compiler only emits scalar loads for memory the kernel never writes.
-struct QGroup {
-    double v[8][GF];
-};
-__device__ __forceinline__ QGroup qgroup(const double *qslot, int grp) {
-    typedef unsigned int u32x16 __attribute__((ext_vector_type(16)));
-    u32x16 r[4];
-    const double *base = qslot + 8 * GF * grp;
-    asm volatile(
-        "s_load_dwordx16 %0, %4, 0x0\n\t"
-        "s_load_dwordx16 %1, %4, 0x40\n\t"
-        "s_load_dwordx16 %2, %4, 0x80\n\t"
-        "s_load_dwordx16 %3, %4, 0xc0\n\t"
-        "s_waitcnt lgkmcnt(0)"
-        : "=s"(r[0]), "=s"(r[1]), "=s"(r[2]), "=s"(r[3])
-        : "s"(base)
-        : "memory");
-    QGroup out;
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-            out.v[2 * k + e / GF][e % GF] =
-                __builtin_bit_cast(double, ((uint64_t)r[k][2 * e + 1] << 32) | r[k][2 * e]);
-    return out;
-}
-static_assert(GF == 4, "qgroup reads 8 channels x 4 heads per group");
 
 // The key codes and norm words of this thread's TPT consecutive tokens
 // (t = t0 + TPT * tid + j): a wave reads one contiguous span of each plane.
@@ -298,12 +270,11 @@ __device__ __forceinline__ void load_keys(const Geom &g, const uint8_t *__restri
 
 // Exact scores of those tokens for the GF heads (attention.py:333-359), in
 // groups of 8 channels. Per group the TPT x 8 centroid reads are issued as one
-// LDS batch (and the 8 x GF query values as scalar loads), then the FMAs
-// run channel by channel over all TPT x GF accumulators, so an accumulator is
-// reused only every TPT * GF FMAs. The 8 codes of a group sit in one 32-bit
-// window of the key bitstream (8 * KB <= 32 bits), cut out with alignbit.
-// qslot: the chain's fp64 query rows ([c][h]), read with scalar loads so the
-// query values feed the FMAs as scalar operands.
+// LDS batch (the query values are LDS broadcasts, qf = [c][h] in fp64), then
+// the FMAs run channel by channel over all TPT x GF accumulators, so an
+// accumulator is reused only every TPT * GF FMAs. The 8 codes of a group sit in
+// one 32-bit window of the key bitstream (8 * KB <= 32 bits), cut out with
+// alignbit.
 template <int D, int KB>
 __device__ __forceinline__ void score_keys(const uint32_t (&w)[TPT][KF<D, KB>::KWORDS + 1],
                                            const uint32_t (&normw)[TPT], const double (*qf)[GF],
@@ -325,17 +296,17 @@ __device__ __forceinline__ void score_keys(const uint32_t (&w)[TPT][KF<D, KB>::K
 #pragma unroll
             for (int i = 0; i < 8; ++i) cv[j][i] = kcf[(win >> (i * KB)) & K::MASK];
         }
-        QGroup qv;
+        double qv[8][GF];
 #pragma unroll
         for (int i = 0; i < 8; ++i)
 #pragma unroll
-            for (int h = 0; h < GF; ++h) qv.v[i][h] = qf[8 * grp + i][h];
+            for (int h = 0; h < GF; ++h) qv[i][h] = qf[8 * grp + i][h];
 #pragma unroll
         for (int i = 0; i < 8; ++i)
 #pragma unroll
             for (int j = 0; j < TPT; ++j)
 #pragma unroll
-                for (int h = 0; h < GF; ++h) acc[j][h] = fma(qv.v[i][h], cv[j][i], acc[j][h]);
+                for (int h = 0; h < GF; ++h) acc[j][h] = fma(qv[i][h], cv[j][i], acc[j][h]);
         // Pin the accumulators at every group so the compiler cannot turn the
         // loop nest inside out (load every centroid first, FMA at the end).
 #pragma unroll
@@ -595,11 +566,11 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             bool fail = false;
             if (chunk == 0) {
                 if (lane == 0)
-                    __hip_atomic_store(my, st_pack(ST_INC, local), __ATOMIC_RELAXED,
+                    __hip_atomic_store(my, st_pack(ST_INC, ck.ep, local), __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
             } else {
                 if (lane == 0)
-                    __hip_atomic_store(my, st_pack(ST_AGG, local), __ATOMIC_RELAXED,
+                    __hip_atomic_store(my, st_pack(ST_AGG, ck.ep, local), __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
                 int64_t base = chunk - 1;       // the predecessor lane 0 reads
                 int spins = 0;
@@ -611,7 +582,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                         const unsigned long long w = __hip_atomic_load(
                             ck.status + ((int64_t)chain * ck.max_chunks + pc) * GF + h,
                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        flag = w & ~ST_VAL;
+                        flag = st_flag(w, ck.ep);
                         val = st_val(w);
                     }
                     const unsigned long long inc = __ballot(flag == ST_INC);
@@ -632,7 +603,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                 }
                 const int64_t incl = run > local ? run : local;
                 if (lane == 0)
-                    __hip_atomic_store(my, st_pack(ST_INC, incl), __ATOMIC_RELAXED,
+                    __hip_atomic_store(my, st_pack(ST_INC, ck.ep, incl), __ATOMIC_RELAXED,
                                        __HIP_MEMORY_SCOPE_AGENT);
             }
             if (lane == 0) {
@@ -650,7 +621,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             if (lane == 0) S.min_[wv] = m;
         }
         __syncthreads();
-        if (SEQ && S.lb_fail && tid == 0) atomicOr(&ck.chain_fb[chain], 1u);
+        if (SEQ && S.lb_fail && tid == 0) pub32(&ck.chain_fb[chain], ck.ep);
 
         // -- phase 3: events and each head's candidate tokens listed in order ----
         // (the thread owns TPT consecutive tokens). Two exact shortcuts: a head
@@ -753,6 +724,19 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
         __syncthreads();
 
         // -- phase 4: run sums over the candidate list, wave = head, lane = channel -
+        // Chunk 0 starts the sequence (acc = l = 0), so it replays its own runs
+        // here: acc, l and R (the bound on |acc|) after its last token stand in
+        // for all its runs. Every later chunk publishes its runs.
+        // acc stays in 32 bits in sequential mode: |acc| <= R <= 2^31 - 1
+        // whenever the result is used (past a failed check the head goes to the
+        // serial path); two-pass sums need 64.
+        using AccT = typename std::conditional<SEQ, int32_t, int64_t>::type;
+        const bool own = chunk == 0;
+        AccT acc0[CPL];
+#pragma unroll
+        for (int k = 0; k < CPL; ++k) acc0[k] = 0;
+        int64_t l0 = 0, R0 = 0;
+        int n_ev0 = 0, flags0 = 0;
         if (ok && wv < GF) {
             const int h = wv;
             int n_act = 0, n_ev = 0;
@@ -766,7 +750,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             const int n_seg = n_ev + 1;
             const int off = slot_base(chunk);
             int flags = 0;
-            if (n_seg > slot_count(chunk)) flags |= FLAG_POOL;
+            if (!own && n_seg > SLOTS) flags |= FLAG_POOL;
             if (!flags) {
                 int wi[CPL], wi1[CPL], sh[CPL];
 #pragma unroll
@@ -820,14 +804,16 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     const int64_t lb = wave_shr1_64(wave_scan64<OpMax64>(ev_i ? lx : Ls, Ls), Ls);
                     const int64_t bb = wave_shr1_64(wave_scan64<OpMax64>(ev_i ? bx : Bs, Bs), Bs);
                     const int64_t kb = wave_shr1_64(wave_scan64<OpMax64>(key, fkey), fkey);
+                    const int64_t Lr = lx - lb, Br = bx - bb;   // at an event: the run it closes
                     if (ev_i) {
-                        const int ri = seg + (int)__builtin_amdgcn_mbcnt_hi(
-                                                 (uint32_t)(evm >> 32),
-                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)evm, 0u));
-                        const int64_t B = bx - bb;
-                        wide = wide || B > ACC_HI;
-                        pub64(&meta[ri].lf, (uint64_t)(lx - lb) | ((uint64_t)(kb & 0xFFFF) << 32));
-                        pub64(&meta[ri].b, (uint64_t)B);
+                        wide = wide || Br > ACC_HI;
+                        if (!own) {
+                            const int ri = seg + (int)__builtin_amdgcn_mbcnt_hi(
+                                                     (uint32_t)(evm >> 32),
+                                                     __builtin_amdgcn_mbcnt_lo((uint32_t)evm, 0u));
+                            pub64(&meta[ri].lf, (uint64_t)Lr | ((uint64_t)(kb & 0xFFFF) << 32));
+                            pub64(&meta[ri].b, (uint64_t)Br);
+                        }
                     }
                     Lc = readlane64(lp, 63);
                     Bc = readlane64(bp, 63);
@@ -859,12 +845,24 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                             const int j = j0 + jj;
                             if (j < cnt) {
                                 if ((evm >> j) & 1ull) {
-                                    // the event closes the open run: publish its sum
+                                    // the event closes the open run
+                                    if (own) {
+                                        // acc = floor((acc + S) * f / 2^15), and l and R alike
+                                        const int64_t f = (uint32_t)__builtin_amdgcn_readlane(val_i, j);
+                                        l0 = ((l0 + readlane64(Lr, j)) * f) >> PROB_FRAC;
+                                        R0 += readlane64(Br, j);
+                                        if (R0 > ACC_HI) wide = true;
+                                        R0 = ((R0 * f) >> PROB_FRAC) + 1;
 #pragma unroll
-                                    for (int k = 0; k < CPL; ++k) {
-                                        pub32(&segS[(int64_t)seg * D + lane + 64 * k], (uint32_t)(P[k] - P0[k]));
-                                        P0[k] = P[k];
+                                        for (int k = 0; k < CPL; ++k)
+                                            acc0[k] = (AccT)(((int64_t)(AccT)(acc0[k] + (AccT)(P[k] - P0[k])) * f) >> PROB_FRAC);
+                                    } else {
+#pragma unroll
+                                        for (int k = 0; k < CPL; ++k)
+                                            pub32(&segS[(int64_t)seg * D + lane + 64 * k], (uint32_t)(P[k] - P0[k]));
                                     }
+#pragma unroll
+                                    for (int k = 0; k < CPL; ++k) P0[k] = P[k];
                                     ++seg;
                                 }
                                 const int32_t w = __builtin_amdgcn_readlane(w_i, j);
@@ -876,31 +874,49 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     }
                 }
                 // the open run closes at the end of the chunk
-                if (lane == 0) {
-                    pub64(&meta[seg].lf, (uint64_t)(Lc - Ls) | ((uint64_t)(fkey & 0xFFFF) << 32));
-                    pub64(&meta[seg].b, (uint64_t)(Bc - Bs));
-                }
                 wide = wide || Bc - Bs > ACC_HI;
+                if (own) {
 #pragma unroll
-                for (int k = 0; k < CPL; ++k)
-                    pub32(&segS[(int64_t)seg * D + lane + 64 * k], (uint32_t)(P[k] - P0[k]));
+                    for (int k = 0; k < CPL; ++k) acc0[k] += (AccT)(P[k] - P0[k]);
+                    l0 += Lc - Ls;
+                    R0 += Bc - Bs;
+                    if (SEQ && R0 > ACC_HI) wide = true;
+                } else {
+                    if (lane == 0) {
+                        pub64(&meta[seg].lf, (uint64_t)(Lc - Ls) | ((uint64_t)(fkey & 0xFFFF) << 32));
+                        pub64(&meta[seg].b, (uint64_t)(Bc - Bs));
+                    }
+#pragma unroll
+                    for (int k = 0; k < CPL; ++k)
+                        pub32(&segS[(int64_t)seg * D + lane + 64 * k], (uint32_t)(P[k] - P0[k]));
+                }
                 if (__ballot(wide)) flags |= FLAG_WIDE;
             }
-            if (lane == 0) {
+            n_ev0 = n_ev;
+            flags0 = flags;
+            if (!own) {
+                // The header: w1 goes out with the run sums, w0 once this head's
+                // stores have completed.
                 ChunkHdr *hp = &ck.hdr[((int64_t)chain * ck.max_chunks + chunk) * GF + h];
-                pub64(&hp->w0, (uint64_t)(uint32_t)n_seg | ((uint64_t)(uint32_t)flags << 16) |
-                                   ((uint64_t)S.ovf << 32));
-                pub64(&hp->w1, S.mabs);
+                if (lane == 0) pub64(&hp->w1, S.mabs);
+                stores_done();
+                if (lane == 0)
+                    pub64(&hp->w0, (uint64_t)(uint32_t)n_seg | ((uint64_t)(uint32_t)flags << 16) |
+                                       ((uint64_t)(S.ovf & 0xFFFF) << 24) | ((uint64_t)ck.ep << 40));
             }
-        } else if (!ok && tid < GF) {
+        } else if (!ok && wv < GF && !own) {
             // q failed its range check: the chain goes to the serial path, which counts its own
-            ChunkHdr *hp = &ck.hdr[((int64_t)chain * ck.max_chunks + chunk) * GF + tid];
-            pub64(&hp->w0, 1);
-            pub64(&hp->w1, 0);
+            ChunkHdr *hp = &ck.hdr[((int64_t)chain * ck.max_chunks + chunk) * GF + wv];
+            if (lane == 0) pub64(&hp->w1, 0);
+            stores_done();
+            if (lane == 0) pub64(&hp->w0, 1ull | ((uint64_t)ck.ep << 40));
         }
 
-        // -- phase 5: the last workgroup of this (sequence, KV head) replays -------
-        stores_done();
+        // -- phase 5: the last workgroup of the chain replays -----------------------
+        // Chunks 1 .. nch-1 count themselves done once their runs are out; chunk 0
+        // first, so that when it is the last (its many rescale events make it the
+        // slowest) its state never leaves the registers. Otherwise it publishes
+        // the state after counting, and the last workgroup waits for its header.
         __syncthreads();
         if (tid == 0) {
             const unsigned prior = __hip_atomic_fetch_add(&ck.done[chain], 1u, __ATOMIC_RELAXED,
@@ -908,60 +924,119 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             S.last = prior == (unsigned)(nch - 1);
         }
         __syncthreads();
-        if (S.last) {
-            const bool chain_fb = !ok || nch > HMAX ||
-                                  __hip_atomic_load(&ck.chain_fb[chain], __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT) != 0;
-            // The chunk headers give the score statistics of the whole chain
-            // (when q passed its range check) and the run counts.
-            const bool hdr_stats = ok && nch <= HMAX;
-            // Wave h < GF replays query head h, lane = channel; the other waves
-            // only take part in the barriers and the reset.
-            const bool hw = wv < GF;
-            const int h = hw ? wv : 0;
-            int64_t acc[CPL];
+        const bool last = S.last != 0;
+        if (own && !last && wv < GF) {
+            // chunk 0's state in its slot: acc (|acc| < 2^31 whenever it is used),
+            // l | events << 32, and R
+            const int h = wv;
+            const int64_t base = (int64_t)chain * GF + h;
 #pragma unroll
-            for (int k = 0; k < CPL; ++k) acc[k] = 0;
+            for (int k = 0; k < CPL; ++k) pub32(&ck.segS[base * ck.pool * D + lane + 64 * k], (uint32_t)acc0[k]);
+            ChunkHdr *hp = &ck.hdr[((int64_t)chain * ck.max_chunks) * GF + h];
+            if (lane == 0) {
+                pub64(&ck.meta[base * ck.pool].lf, (uint64_t)(uint32_t)l0 | ((uint64_t)(uint32_t)n_ev0 << 32));
+                pub64(&ck.meta[base * ck.pool].b, (uint64_t)R0);
+                pub64(&hp->w1, ok ? S.mabs : 0ull);
+            }
+            stores_done();
+            if (lane == 0)
+                pub64(&hp->w0, 1ull | ((uint64_t)(uint32_t)flags0 << 16) |
+                                   ((uint64_t)(ok ? S.ovf & 0xFFFF : 0) << 24) | ((uint64_t)ck.ep << 40));
+        }
+        if (last) {
+            const bool hw = wv < GF;              // wave h < GF replays query head h, lane = channel
+            const int h = hw ? wv : 0;
+            constexpr int HPL = HMAX / 64;
+            constexpr int SB = 64 / CPL;          // runs per batch
+            AccT aw[CPL];
+#pragma unroll
+            for (int k = 0; k < CPL; ++k) aw[k] = 0;
             int64_t l = 0, R = 0;
             unsigned long long events = 0;
-            bool fb = chain_fb;
-            int total = 0;
-            if (hw && nch <= HMAX) {
-                // One load per lane and 64 chunks, then a scan of the run counts
-                // lists the runs of head h in order, by slot, in LDS.
-                constexpr int HPL = HMAX / 64;
+            bool fb = !ok;
+            const bool hdr_stats = ok;
+            if (hw) {
+                const ChunkHdr *hdr = ck.hdr + (int64_t)chain * ck.max_chunks * GF + h;  // chunk c: hdr[c * GF]
+                const SegMeta *meta = ck.meta + ((int64_t)chain * GF + h) * ck.pool;
+                const int32_t *segS = ck.segS + ((int64_t)chain * GF + h) * ck.pool * D;
+                uint16_t *sl = S.u.rp.slot[h];
+                const int zslot = ck.pool - 1;    // never written: all zero
+                const uint32_t ep = ck.ep;
+                auto cur = [ep](uint64_t w) __attribute__((always_inline)) { return (uint32_t)(w >> 40) == ep; };
+                // Chunk 0's state: in the registers, or out of its slot once its header is up.
+                int flags = 0;
+                int64_t ovf = 0, mabs = 0;
+                if (own) {
+#pragma unroll
+                    for (int k = 0; k < CPL; ++k) aw[k] = acc0[k];
+                    l = l0;
+                    R = R0;
+                    events = (unsigned long long)n_ev0;
+                    flags = flags0;
+                    if (h == 0 && lane == 0) {
+                        ovf = (int64_t)S.ovf;
+                        mabs = (int64_t)S.mabs;
+                    }
+                } else if (!fb) {
+                    uint64_t h0 = 0;
+                    int spins = 0;
+                    for (;;) {
+                        h0 = (uint64_t)uni64((int64_t)get64(&hdr[0].w0));   // all lanes, one word
+                        if (cur(h0)) break;
+                        if (++spins > SPIN_LIMIT) {
+                            fb = true;
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(1);
+                    }
+                    if (!fb) {
+                        flags = (int)((h0 >> 16) & 0xFF);
+#pragma unroll
+                        for (int k = 0; k < CPL; ++k) aw[k] = (AccT)(int32_t)get32(segS + lane + 64 * k);
+                        const uint64_t lf = get64(&meta[0].lf);
+                        l = (int64_t)(uint32_t)lf;
+                        events = lf >> 32;
+                        R = (int64_t)get64(&meta[0].b);
+                        if (h == 0 && lane == 0) {
+                            ovf = (int64_t)((h0 >> 24) & 0xFFFF);
+                            mabs = (int64_t)get64(&hdr[0].w1);
+                        }
+                    }
+                }
+                // The runs of chunks 1 .. nch-1 in order: one header load per lane and
+                // 64 chunks, then a scan of the run counts lists them by slot in LDS.
+                int total = 0;
                 uint64_t w0[HPL], w1[HPL];
 #pragma unroll
                 for (int i = 0; i < HPL; ++i) {
-                    const int c = lane + 64 * i;
+                    const int c = 1 + lane + 64 * i;
                     w0[i] = 0;
                     w1[i] = 0;
                     if (c < nch) {
-                        const ChunkHdr *hp = &ck.hdr[((int64_t)chain * ck.max_chunks + c) * GF + h];
-                        w0[i] = get64(&hp->w0);
-                        if (h == 0) w1[i] = get64(&hp->w1);
+                        w0[i] = get64(&hdr[(int64_t)c * GF].w0);
+                        if (h == 0) w1[i] = get64(&hdr[(int64_t)c * GF].w1);
                     }
                 }
-                int flags = 0;
-                int64_t ovf = 0, mabs = 0;
-                uint16_t *sl = S.u.rp.slot[h];
 #pragma unroll
                 for (int i = 0; i < HPL; ++i) {
-                    if (64 * i >= nch) break;
-                    const int c = lane + 64 * i;
-                    const int n = (int)(w0[i] & 0xFFFF);       // 0 past the last chunk
-                    flags |= (int)((w0[i] >> 16) & 0xFFFF);
-                    ovf += (int64_t)(w0[i] >> 32);
+                    if (64 * i + 1 >= nch) break;
+                    const int c = 1 + lane + 64 * i;
+                    const bool in = c < nch;
+                    if (in && !cur(w0[i])) flags |= FLAG_POOL;     // cannot happen: it counted itself done
+                    const int n = in ? (int)(w0[i] & 0xFFFF) : 0;
+                    flags |= in ? (int)((w0[i] >> 16) & 0xFF) : 0;
+                    ovf += in ? (int64_t)((w0[i] >> 24) & 0xFFFF) : 0;
                     mabs = (int64_t)w1[i] > mabs ? (int64_t)w1[i] : mabs;
                     const int incl = (int)wave_scan_add32((uint32_t)n);
                     const int start = total + incl - n;
                     total += __builtin_amdgcn_readlane(incl, 63);
-                    if (!fb)
-                        for (int j = 0; j < n && start + j < NSEG; ++j)
-                            sl[start + j] = (uint16_t)((slot_base(c) + j) | (j ? RUN_EVENT : 0));
+                    for (int j = 0; j < n && start + j < NSEG; ++j)
+                        sl[start + j] = (uint16_t)((slot_base(c) + j) | (j ? RUN_EVENT : 0));
                 }
-                total = __builtin_amdgcn_readfirstlane(total);    // wave-uniform
+                total = uni32(total);
                 if (__ballot(flags != 0) || total > NSEG) fb = true;
+                // A chunk whose look-back timed out flagged the chain before its header.
+                if (get32(&ck.chain_fb[chain]) == ep) fb = true;
                 if (h == 0) {
                     ovf = wave_sum_i64(ovf);
                     mabs = wave_max_i64(mabs);
@@ -970,29 +1045,16 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                         S.mabs = (unsigned long long)mabs;
                     }
                 }
-            }
-            if (hw && !fb) {
+                fb = __builtin_amdgcn_readfirstlane((int)fb) != 0;
+                wave_sync();
                 // The walk, SB runs at a time. Lane i < SB holds run i's list entry
                 // and loads its L, f and B; every lane loads its channels' run sums
-                // (the slot ids read back with readlane, the base address scalar).
-                // Within a stretch of runs without an event acc, l and R only add,
-                // and R only grows, so per run the walk does one add per channel;
-                // l and R are brought up to date from lane prefix sums at each
-                // event (before its rescale) and at the end of the batch, and R is
-                // checked there: a run-by-run check could not fail anywhere else.
-                // acc stays in 32 bits in sequential mode: |acc| <= R <= 2^31 - 1
-                // whenever the result is used (past a failed check the head goes to
-                // the serial path); two-pass sums need 64.
-                using AccT = typename std::conditional<SEQ, int32_t, int64_t>::type;
-                constexpr int SB = 64 / CPL;
-                const SegMeta *meta = ck.meta + ((int64_t)chain * GF + h) * ck.pool;
-                const int32_t *segS = ck.segS + ((int64_t)chain * GF + h) * ck.pool * D;
-                const uint16_t *sl = S.u.rp.slot[h];
-                AccT aw[CPL];
-#pragma unroll
-                for (int k = 0; k < CPL; ++k) aw[k] = 0;
-                wave_sync();
-                const int zslot = ck.pool - 1;        // all zero: pads a batch
+                // (the slot ids read back with readlane). Within a stretch of runs
+                // without an event acc, l and R only add, and R only grows, so per
+                // run the walk does one add per channel; l and R are brought up to
+                // date from lane prefix sums at each event (before its rescale) and
+                // at the end of the batch, and R is checked there: a run-by-run check
+                // could not fail anywhere else.
                 for (int g0 = 0; g0 < total && !fb; g0 += SB) {
                     const int nb = total - g0 < SB ? total - g0 : SB;     // uniform
                     const int nblk = (nb + 7) >> 3;                        // blocks of 8 runs
@@ -1056,14 +1118,14 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                             }
                         }
                     }
-                    const int64_t pl = readlane64(PL, nb - 1), pb = readlane64(PB, nb - 1);
-                    l += pl - done_L;
-                    R += pb - done_B;
+                    l += readlane64(PL, nb - 1) - done_L;
+                    R += readlane64(PB, nb - 1) - done_B;
                     if (SEQ && R > ACC_HI) fb = true;
                 }
-#pragma unroll
-                for (int k = 0; k < CPL; ++k) acc[k] = (int64_t)aw[k];
             }
+            int64_t acc[CPL];
+#pragma unroll
+            for (int k = 0; k < CPL; ++k) acc[k] = (int64_t)aw[k];
             __syncthreads();   // the replay buffers are dead; the serial path reuses the LDS
             const int qh = kvh * GF + h;
             int32_t *orow = out + ((int64_t)b * g.n_q + qh) * D;
@@ -1092,7 +1154,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     amax = a > amax ? a : amax;
                 }
                 amax = wave_max_i64(amax);
-                aovf = (unsigned long long)wave_sum_i64((int64_t)aovf);
+                if (!SEQ) aovf = (unsigned long long)wave_sum_i64((int64_t)aovf);
                 if (lane == 0) {
                     S.wt[h][0] = (int64_t)events;
                     S.wt[h][1] = amax;
@@ -1122,14 +1184,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     if (S.ovf) atomicAdd(&st->score_overflows, S.ovf);
                     atomicMax(&st->max_abs_score, S.mabs);
                 }
-            }
-            // Reset this chain's completion counter and look-back words for the
-            // next call: every other workgroup of the chain has finished with them.
-            for (int64_t i = tid; i < nch * GF; i += CT)
-                ck.status[(int64_t)chain * ck.max_chunks * GF + i] = 0;
-            if (tid == 0) {
-                ck.done[chain] = 0;
-                ck.chain_fb[chain] = 0;
+                ck.done[chain] = 0;        // every other workgroup of the chain has counted itself
             }
         }
     }
@@ -1153,17 +1208,18 @@ static hipError_t launch_fast(hipStream_t s, const Geom &g, const Tables *t, con
     return hipGetLastError();
 }
 
-bool chunked_supported(const Geom &g) {
+int64_t chunked_max_chunks(int64_t capacity) { return (capacity + CHUNK - 1) / CHUNK; }
+
+bool chunked_supported(const Geom &g, int64_t capacity) {
     return g.G == GF && (g.d == 64 || g.d == 128) && g.kb >= 2 && g.kb <= 4 && g.vb >= 1 &&
-           g.vb <= VB_MAX;
+           g.vb <= VB_MAX && chunked_max_chunks(capacity) <= HMAX;
 }
 
-int64_t chunked_max_chunks(int64_t capacity) { return (capacity + CHUNK - 1) / CHUNK; }
 
 // The run slots of every chunk, plus one last slot that is never written (the
 // scratch is zeroed when the cache is created): the replay pads its batches
 // with it.
-int64_t chunked_pool_slots(int64_t max_chunks) { return SLOTS0 + (max_chunks - 1) * SLOTS + 1; }
+int64_t chunked_pool_slots(int64_t max_chunks) { return 1 + (max_chunks - 1) * SLOTS + 1; }
 
 static void carve(const Geom &g, int64_t max_chunks, int64_t pool, uint8_t *p, Chunked *ck,
                   size_t *total) {
@@ -1182,7 +1238,6 @@ static void carve(const Geom &g, int64_t max_chunks, int64_t pool, uint8_t *p, C
     c.segS = (int32_t *)take(chains * GF * pool * g.d * sizeof(int32_t));
     c.done = (unsigned int *)take(chains * sizeof(unsigned int));
     c.chain_fb = (unsigned int *)take(chains * sizeof(unsigned int));
-    c.qd = (double *)take(chains * g.d * GF * sizeof(double));
     c.max_chunks = (int32_t)max_chunks;
     c.pool = (int32_t)pool;
     if (ck) *ck = c;
@@ -1197,12 +1252,13 @@ size_t chunked_scratch_bytes(const Geom &g, int64_t max_chunks, int64_t pool) {
 
 hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
                                  int32_t *out, const int64_t *len, void *scratch, int64_t max_chunks,
-                                 int64_t pool, int two_pass, DevStats *st) {
+                                 int64_t pool, uint32_t call, int two_pass, DevStats *st) {
     const int64_t chains = (int64_t)g.batch * g.n_kv;
-    if (max_chunks > 65535 || chains > 65535 || max_chunks * chains > 0x7fffffff)
+    if (max_chunks > HMAX || chains > 65535 || max_chunks * chains > 0x7fffffff)
         return hipErrorInvalidValue;
     Chunked ck;
     carve(g, max_chunks, pool, (uint8_t *)scratch, &ck, nullptr);
+    ck.ep = call % EPOCH_MASK + 1;     // 1 .. 2^14 - 1: zeroed scratch is never current
 #define INSITU_FAST(DD, KK)                                                          \
     if (g.d == DD && g.kb == KK)                                                     \
         return launch_fast<DD, KK>(s, g, t, q, out, len, ck, two_pass, st);

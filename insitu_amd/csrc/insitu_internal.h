@@ -181,13 +181,13 @@ hipError_t launch_finalize(hipStream_t s, const int64_t *acc, const int64_t *l, 
 hipError_t launch_append(hipStream_t s, const Geom &g, const Tables *t, const int32_t *k,
                          const int32_t *v, int n_tok, int seq_lo, int seq_hi, const int64_t *len_in,
                          int64_t *len_out, DevStats *st);
-bool chunked_supported(const Geom &g);
+bool chunked_supported(const Geom &g, int64_t capacity);
 int64_t chunked_max_chunks(int64_t capacity);
 int64_t chunked_pool_slots(int64_t max_chunks);
 size_t chunked_scratch_bytes(const Geom &g, int64_t max_chunks, int64_t pool);
 hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
                                  int32_t *out, const int64_t *len, void *scratch, int64_t max_chunks,
-                                 int64_t pool, int two_pass, DevStats *st);
+                                 int64_t pool, uint32_t call, int two_pass, DevStats *st);
 hipError_t launch_attend_serial(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
                                 int32_t *out, const int64_t *len, int two_pass, DevStats *st);
 

@@ -47,11 +47,11 @@ __device__ __forceinline__ void stage_rows(const Geom &g, int b, int h, int64_t 
 // statistics are merged only when count_scores is set (the chunked kernel
 // has already counted them when it falls back here).
 template <int CPL, int RS>
-__device__ void serial_head(const Geom &g, const Tables *__restrict__ tabs,
-                            const int64_t *kc, const int64_t *vc,
-                            const int32_t *__restrict__ qrow, int b, int kvh, int64_t T,
-                            int two_pass, bool count_scores, SerialLds<RS> &L,
-                            int32_t *out_row, DevStats *st) {
+__device__ __forceinline__ void serial_head(const Geom &g, const Tables *__restrict__ tabs,
+                                            const int64_t *kc, const int64_t *vc,
+                                            const int32_t *__restrict__ qrow, int b, int kvh, int64_t T,
+                                            int two_pass, bool count_scores, SerialLds<RS> &L,
+                                            int32_t *out_row, DevStats *st) {
     const int lane = threadIdx.x & 63;
     const int d = g.d;
     const int score_shift = CENT_FRAC + g.norm_frac;                        // config.py:249-250

@@ -459,6 +459,31 @@ def test_chains_that_straddle_xcds(ctx, n_kv, lens):
             assert st.rescale_events == events
 
 
+def test_a_later_chunk_replays_from_chunk_zeros_published_state(ctx):
+    """Chunk 0 replays its own runs and keeps the result in registers when it is the
+    chain's last workgroup. Here the last chunk is much slower (1,024 tied top scores:
+    one event, then a candidate per token), so it replays instead and takes chunk 0's
+    state from memory once chunk 0's header is up."""
+    from insitu_amd.attention import CompressedAttention
+    rng = np.random.default_rng(31)
+    T = 3 * 1024
+    qg = rng.integers(-(1 << 22), 1 << 22, size=(8, 64))
+    q = np.repeat(qg, 4, axis=0)
+    k, v = _random_cache_inputs(rng, T, scale=1 << 17)
+    k[2 * 1024:] = (np.sign(qg) * (1 << 22))[None]
+    c = _cache(ctx, T)
+    c.append_rotated(k, v)
+    want, sts = _host_reference(k, v, q)
+    for mode in ("online", "two_pass"):
+        if mode == "two_pass":
+            want, sts = _host_reference(k, v, q, two_pass=True)
+        for rep in range(3):
+            out, st = CompressedAttention(c).attend(q[None], mode)
+            np.testing.assert_array_equal(out.cpu().numpy()[0], want, err_msg=f"{mode} rep {rep}")
+            assert st.serial_fallbacks == 0
+            assert st.rescale_events == sum(s.rescale_events for s in sts)
+
+
 def test_repeated_calls_reuse_the_counters(ctx):
     """The chunk-completion and run-pool counters are reset by each call's last workgroup."""
     from insitu_amd.attention import CompressedAttention
