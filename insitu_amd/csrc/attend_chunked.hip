@@ -1060,6 +1060,9 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     const int nblk = (nb + 7) >> 3;                        // blocks of 8 runs
                     const bool mine = lane < nb;
                     const uint32_t ent = mine ? (uint32_t)sl[g0 + lane] : (uint32_t)zslot;
+                    // lane i: the byte offset of run i's row (lanes past the batch: the zero slot)
+                    const uint32_t roff = (ent & (RUN_EVENT - 1)) * (uint32_t)(D * 4);
+                    const char *sbase = (const char *)segS + 4 * lane;
                     int32_t sv[SB][CPL];
 #pragma unroll
                     for (int blk = 0; blk < SB / 8; ++blk) {
@@ -1068,10 +1071,10 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                             // they read the zero slot
 #pragma unroll
                             for (int i = 8 * blk; i < 8 * blk + 8; ++i) {
-                                const int si = __builtin_amdgcn_readlane((int)ent, i) & (RUN_EVENT - 1);
-                                const int32_t *row = segS + (int64_t)(i < nb ? si : zslot) * D;
+                                const uint32_t o = (uint32_t)__builtin_amdgcn_readlane((int)roff, i);
 #pragma unroll
-                                for (int k = 0; k < CPL; ++k) sv[i][k] = (int32_t)get32(row + lane + 64 * k);
+                                for (int k = 0; k < CPL; ++k)
+                                    sv[i][k] = (int32_t)get32(sbase + o + 256 * k);
                             }
                         } else {
 #pragma unroll
