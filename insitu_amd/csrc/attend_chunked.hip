@@ -29,11 +29,15 @@
 // and no cache maintenance. Two-pass mode needs the maximum of the whole
 // context, so it runs a chunk-max kernel first and the same chunk kernel second.
 //
-// The last workgroup of each (sequence, KV head) replays the runs, one thread
-// per (query head, channel). It reads every chunk's header in one batch of
-// loads, lists the chain's runs in order in LDS, loads their sums 64 runs at a
+// Chunk 0 starts the sequence from acc = l = 0, so it replays its own runs as
+// it goes and hands over one state. The last workgroup of each (sequence, KV
+// head), elected by a completion counter, replays the rest, one thread per
+// (query head, channel): it reads the headers of chunks 1 .. n-1 in one batch
+// of loads, lists their runs in order in LDS, loads their sums 64 runs at a
 // time (one round trip for a typical context, whose rescale events are few),
-// walks them, finalizes and writes Q16.
+// walks them from chunk 0's state, finalizes and writes Q16. Chunk 0 counts
+// itself done before publishing its state, so when it is the last (it usually
+// is: it holds most rescale events) the state never leaves its registers.
 // Scores: sum_ch q[ch] * c[code_ch] in fp64 FMA -- every partial sum is an
 // integer below 2^51, so it is exact -- then the int64 norm multiply and >>24
 // of the reference.
