@@ -1162,37 +1162,20 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                 }
                 amax = wave_max_i64(amax);
                 if (!SEQ) aovf = (unsigned long long)wave_sum_i64((int64_t)aovf);
+                // each head's wave merges its own statistics (the serial path merges its own)
                 if (lane == 0) {
-                    S.wt[h][0] = (int64_t)events;
-                    S.wt[h][1] = amax;
-                    S.wt[h][2] = (int64_t)aovf;
-                }
-            }
-            if (hw && lane == 0) S.wt[h][3] = fb ? 1 : 0;
-            __syncthreads();
-            if (tid == 0) {
-                // one set of statistics atomics per (sequence, KV head)
-                int64_t ev = 0, am = 0, ao = 0;
-                bool any = false;
-                for (int hh = 0; hh < GF; ++hh) {
-                    if (S.wt[hh][3]) continue;     // the serial path counted that head itself
-                    any = true;
-                    ev += S.wt[hh][0];
-                    am = S.wt[hh][1] > am ? S.wt[hh][1] : am;
-                    ao += S.wt[hh][2];
-                }
-                if (any) {
                     atomicMax(&st->n_tokens, (unsigned long long)T);
-                    if (ev) atomicAdd(&st->rescale_events, (unsigned long long)ev);
-                    atomicMax(&st->max_abs_acc, (unsigned long long)am);
-                    if (ao) atomicAdd(&st->acc_overflows, (unsigned long long)ao);
+                    if (events) atomicAdd(&st->rescale_events, events);
+                    atomicMax(&st->max_abs_acc, (unsigned long long)amax);
+                    if (aovf) atomicAdd(&st->acc_overflows, aovf);
                 }
-                if (hdr_stats) {
-                    if (S.ovf) atomicAdd(&st->score_overflows, S.ovf);
-                    atomicMax(&st->max_abs_score, S.mabs);
-                }
-                ck.done[chain] = 0;        // every other workgroup of the chain has counted itself
             }
+            // the chain's score statistics, once (from the headers when they cover it)
+            if (hw && h == 0 && lane == 0 && hdr_stats) {
+                if (S.ovf) atomicAdd(&st->score_overflows, S.ovf);
+                atomicMax(&st->max_abs_score, S.mabs);
+            }
+            if (tid == 0) ck.done[chain] = 0;    // every workgroup of the chain has counted itself
         }
     }
 }
