@@ -107,6 +107,16 @@ int insitu_ctx_destroy(insitu_ctx *ctx);
 int insitu_ctx_sync(insitu_ctx *ctx);
 void *insitu_ctx_stream(insitu_ctx *ctx);
 
+/* Attend kernel timing: the measurement hook of the benchmark (no counterpart
+ * in the reference, whose attend is a Python loop). While enabled, every attend
+ * on the context's caches records a pair of HIP events on the context's stream
+ * around its attend kernels (two-pass mode: both of them). _read
+ * waits for the last pair and returns the summed kernel time in milliseconds
+ * and the number of attends since the previous read. Disabling drops what has
+ * not been read. */
+int insitu_ctx_timing(insitu_ctx *ctx, int32_t enable);
+int insitu_ctx_timing_read(insitu_ctx *ctx, double *total_ms, int64_t *n_attends);
+
 /* --- rotation: Rotation.apply (ops/rotate.py:170-197) -------------------- */
 /* x_dev, y_dev: int32 (n_vec, d). y may alias x. */
 int insitu_rotate(insitu_ctx *ctx, const int32_t *x_dev, int32_t *y_dev, int64_t n_vec,

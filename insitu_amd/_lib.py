@@ -22,7 +22,7 @@ STATUS_NAMES = {OK: "OK", EBADLEN: "EBADLEN", ERANGE: "ERANGE", EHIP: "EHIP",
 
 EXPORTS = (
     "insitu_ctx_create", "insitu_ctx_destroy", "insitu_ctx_sync", "insitu_ctx_stream",
-    "insitu_rotate", "insitu_encode", "insitu_qtab", "insitu_exp_lut", "insitu_finalize",
+    "insitu_ctx_timing", "insitu_ctx_timing_read", "insitu_rotate", "insitu_encode", "insitu_qtab", "insitu_exp_lut", "insitu_finalize",
     "insitu_cache_create", "insitu_cache_destroy", "insitu_cache_reset", "insitu_cache_length",
     "insitu_cache_set_length", "insitu_cache_layout", "insitu_append", "insitu_append_seq",
     "insitu_attend", "insitu_step", "insitu_read_rows", "insitu_load_rows", "insitu_read_image",
@@ -95,6 +95,8 @@ def load(path: str | None = None):
         "insitu_ctx_destroy": (i32, [vp]),
         "insitu_ctx_sync": (i32, [vp]),
         "insitu_ctx_stream": (vp, [vp]),
+        "insitu_ctx_timing": (i32, [vp, i32]),
+        "insitu_ctx_timing_read": (i32, [vp, P(ctypes.c_double), P(i64)]),
         "insitu_rotate": (i32, [vp, vp, vp, i64, P(Format)]),
         "insitu_encode": (i32, [vp, vp, i64, P(Format), P(i64), i32, vp, vp]),
         "insitu_qtab": (i32, [vp, vp, i32, i32, P(i64), i32, vp]),

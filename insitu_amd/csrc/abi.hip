@@ -84,6 +84,10 @@ struct insitu_ctx {
     unsigned long long *hook_flags = nullptr;
     int64_t *hook_i64 = nullptr;          // small staging for host arrays (codebooks)
     size_t hook_i64_n = 0;
+    // attend kernel timing (insitu_ctx_timing): event pairs, reused across reads
+    bool timing = false;
+    std::vector<hipEvent_t> ev;           // 2 per attend: start, end
+    size_t ev_used = 0;
 };
 
 struct insitu_cache {
@@ -98,7 +102,7 @@ struct insitu_cache {
     int cur = 0;
     std::vector<int64_t> len_host;
     DevStats *stats = nullptr;
-    int32_t *wire_scratch = nullptr;      // rotated q/k/v for insitu_step
+    int32_t *wire_scratch = nullptr;      // insitu_step: the rotated queries
     void *chunk_scratch = nullptr;        // run sums and counters of the chunked attend
     int64_t max_chunks = 0, pool = 0;
     uint32_t calls = 0;                   // chunked attends so far: tags this call's flags
@@ -183,6 +187,7 @@ int insitu_ctx_destroy(insitu_ctx *c) {
     if (!c) return INSITU_OK;
     hipSetDevice(c->device);
     if (c->stream) hipStreamSynchronize(c->stream);
+    for (hipEvent_t e : c->ev) hipEventDestroy(e);
     if (c->hook_tables) hipFree(c->hook_tables);
     if (c->hook_flags) hipFree(c->hook_flags);
     if (c->hook_i64) hipFree(c->hook_i64);
@@ -198,6 +203,29 @@ int insitu_ctx_sync(insitu_ctx *c) {
 }
 
 void *insitu_ctx_stream(insitu_ctx *c) { return c ? (void *)c->stream : nullptr; }
+
+int insitu_ctx_timing(insitu_ctx *c, int32_t enable) {
+    if (!c) return fail(INSITU_EINVAL, "ctx is NULL");
+    c->timing = enable != 0;
+    c->ev_used = 0;
+    return INSITU_OK;
+}
+
+int insitu_ctx_timing_read(insitu_ctx *c, double *total_ms, int64_t *n_attends) {
+    if (!c || !total_ms || !n_attends) return fail(INSITU_EINVAL, "null argument");
+    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    double sum = 0.0;
+    if (c->ev_used) HIP_TRY(hipEventSynchronize(c->ev[c->ev_used - 1]), "hipEventSynchronize");
+    for (size_t i = 0; i + 1 < c->ev_used; i += 2) {
+        float ms = 0.0f;
+        HIP_TRY(hipEventElapsedTime(&ms, c->ev[i], c->ev[i + 1]), "hipEventElapsedTime");
+        sum += ms;
+    }
+    *total_ms = sum;
+    *n_attends = (int64_t)(c->ev_used / 2);
+    c->ev_used = 0;
+    return INSITU_OK;
+}
 
 int insitu_rotate(insitu_ctx *c, const int32_t *x, int32_t *y, int64_t n_vec,
                   const insitu_format *fmt) {
@@ -479,18 +507,41 @@ int insitu_append_seq(insitu_cache *k, int32_t seq, const int32_t *kr, const int
     return append_impl(k, seq, seq + 1, kr, vr, n_tok);
 }
 
-static int attend_impl(insitu_cache *k, const int32_t *q, int32_t *out, int32_t mode) {
+// An event on the context's stream for attend timing, or nullptr when timing is off.
+static int timing_event(insitu_ctx *c, hipEvent_t *out) {
+    *out = nullptr;
+    if (!c->timing) return INSITU_OK;
+    if (c->ev_used == c->ev.size()) {
+        hipEvent_t e;
+        HIP_TRY(hipEventCreate(&e), "hipEventCreate");
+        c->ev.push_back(e);
+    }
+    *out = c->ev[c->ev_used++];
+    HIP_TRY(hipEventRecord(*out, c->stream), "hipEventRecord");
+    return INSITU_OK;
+}
+
+// q_staged: the chunked path's fp64 query staging already holds q (the fused
+// step's write kernel filled it).
+static int attend_impl(insitu_cache *k, const int32_t *q, int32_t *out, int32_t mode,
+                       bool q_staged) {
     const int64_t *len = k->len_dev[k->cur];
     const int two_pass = mode == INSITU_TWO_PASS ? 1 : 0;
+    hipEvent_t e0, e1;
     if (mode != INSITU_SERIAL && k->chunk_scratch) {
+        int rc = timing_event(k->ctx, &e0);
+        if (rc) return rc;
         HIP_TRY(launch_attend_chunked(k->ctx->stream, k->g, k->tabs, q, out, len, k->chunk_scratch,
-                                      k->max_chunks, k->pool, k->calls++, two_pass, k->stats),
+                                      k->max_chunks, k->pool, k->calls++, two_pass, q_staged,
+                                      k->stats),
                 "chunked attend launch");
-        return INSITU_OK;
+        return timing_event(k->ctx, &e1);
     }
+    int rc = timing_event(k->ctx, &e0);
+    if (rc) return rc;
     HIP_TRY(launch_attend_serial(k->ctx->stream, k->g, k->tabs, q, out, len, two_pass, k->stats),
             "attend launch");
-    return INSITU_OK;
+    return timing_event(k->ctx, &e1);
 }
 
 int insitu_attend(insitu_cache *k, const int32_t *q, int32_t *out, int32_t mode,
@@ -502,7 +553,7 @@ int insitu_attend(insitu_cache *k, const int32_t *q, int32_t *out, int32_t mode,
     // the caller asks for them; without them the call never synchronises.
     int rc = stats ? zero_stats(k) : INSITU_OK;
     if (rc) return rc;
-    rc = attend_impl(k, q, out, mode);
+    rc = attend_impl(k, q, out, mode, false);
     if (rc) return rc;
     return copy_stats(k, stats);
 }
@@ -513,24 +564,30 @@ int insitu_step(insitu_cache *k, const int32_t *q, const int32_t *kw, const int3
     if (mode < INSITU_SEQUENTIAL || mode > INSITU_SERIAL) return fail(INSITU_EINVAL, "unknown mode");
     const Geom &g = k->g;
     int32_t *qr = k->wire_scratch;
-    int32_t *kr = qr + (size_t)g.batch * g.n_q * g.d;
-    int32_t *vr = kr + (size_t)g.batch * g.n_kv * g.d;
+    for (int b = 0; b < g.batch; ++b)
+        if (k->len_host[b] + 1 > g.capacity) {
+            char buf[200];
+            snprintf(buf, sizeof buf, "cache holds %lld of %lld tokens; cannot append (base.py:67-73)",
+                     (long long)k->len_host[b], (long long)g.capacity);
+            return fail(INSITU_ECAPACITY, buf);
+        }
     HIP_TRY(hipSetDevice(k->ctx->device), "hipSetDevice");
     int rc = stats ? zero_stats(k) : INSITU_OK;
     if (rc) return rc;
-    // kernel.py:271-276: k, v and q are all rotated; then append; then attend.
-    HIP_TRY(launch_rotate(k->ctx->stream, kw, kr, (int64_t)g.batch * g.n_kv, g.d,
-                          k->desc.fmt.rot_rounds, k->desc.fmt.rot_signs, &k->stats->range_errors),
-            "rotate k");
-    HIP_TRY(launch_rotate(k->ctx->stream, vw, vr, (int64_t)g.batch * g.n_kv, g.d,
-                          k->desc.fmt.rot_rounds, k->desc.fmt.rot_signs, &k->stats->range_errors),
-            "rotate v");
-    HIP_TRY(launch_rotate(k->ctx->stream, q, qr, (int64_t)g.batch * g.n_q, g.d,
-                          k->desc.fmt.rot_rounds, k->desc.fmt.rot_signs, &k->stats->range_errors),
-            "rotate q");
-    rc = append_impl(k, 0, g.batch, kr, vr, 1);
-    if (rc) return rc;
-    rc = attend_impl(k, qr, out, mode);
+    // kernel.py:271-284: k, v and q are all rotated, the k/v row appended (the
+    // token attends to itself), in one kernel that also stages the rotated
+    // queries for the chunked attend; then the attend (:337-345).
+    const bool chunked = mode != INSITU_SERIAL && k->chunk_scratch;
+    double *qd = nullptr;
+    int32_t *qok = nullptr;
+    if (chunked) chunked_query_area(g, k->max_chunks, k->pool, k->chunk_scratch, &qd, &qok);
+    HIP_TRY(launch_step_write(k->ctx->stream, g, k->tabs, q, kw, vw, k->desc.fmt.rot_rounds,
+                              k->desc.fmt.rot_signs, qr, qd, qok, k->len_dev[k->cur],
+                              k->len_dev[k->cur ^ 1], k->stats),
+            "step write launch");
+    k->cur ^= 1;
+    for (int b = 0; b < g.batch; ++b) k->len_host[b] += 1;
+    rc = attend_impl(k, qr, out, mode, chunked);
     if (rc) return rc;
     return copy_stats(k, stats);
 }

@@ -43,6 +43,7 @@
 // of the reference.
 #include <type_traits>
 
+#include "query.h"
 #include "serial_head.h"
 #include "wave.h"
 
@@ -51,7 +52,6 @@ namespace insitu {
 constexpr int CT = 512;              // threads per workgroup: 8 waves, 2 per SIMD
 constexpr int TPT = 2;               // tokens per thread in the score phase
 constexpr int CHUNK = CT * TPT;      // tokens per workgroup
-constexpr int GF = 4;                // query heads per KV head on this path
 constexpr int VB_MAX = 3;            // widest value code staged in LDS
 constexpr int HMAX = 512;            // chunks per (sequence, KV head) on the chunked path
 constexpr int NSEG = 2048;           // runs per (sequence, KV head, query head) the replay lists
@@ -69,7 +69,6 @@ constexpr unsigned EPOCH_MASK = (1u << EPOCH_BITS) - 1u;
 constexpr int SPIN_LIMIT = 1 << 20;
 constexpr double MAGIC = 6755399441055744.0;   // 1.5 * 2^52
 constexpr int64_t MAGIC_BITS = 0x4338000000000000LL;
-constexpr double DOT_LIMIT = 2251799813685248.0;  // 2^51
 
 // What a chunk publishes, per query head: w0 = n_seg | flags << 16 | score
 // overflows << 24 | call epoch << 40, w1 = max |score| (the statistics are per
@@ -114,6 +113,8 @@ struct Chunked {
     int32_t *segS;                 // [chain][GF][pool][d]
     unsigned int *done;            // [chain]  workgroups of the chain done with their runs
     unsigned int *chain_fb;        // [chain]  the call's epoch: recompute this chain serially
+    double *qd;                    // [chain][d][GF]  the group's query rows in fp64 (query.h)
+    int32_t *qok;                  // [chain]  nonzero: every score of the group is exact in fp64
     int32_t max_chunks, pool;
     uint32_t ep;                   // this call's epoch, 1 .. 2^14 - 1
 };
@@ -171,7 +172,7 @@ struct ChunkLds {
         Replay rp;
         SerialLds<KF<D, KB>::RS> fb[GF];
     } u;
-    double qf[D][GF];
+    double qf[D * GF];             // the group's query rows [c][h] (unless staged)
     double kcf[16];
     int64_t kc[16];
     int64_t vc[16];
@@ -193,45 +194,6 @@ struct ChunkLds {
 // Run slots: chunk 0 owns slot 0 (its replayed state), chunk c > 0 owns SLOTS after it.
 __device__ __forceinline__ int slot_base(int chunk) { return chunk == 0 ? 0 : 1 + (chunk - 1) * SLOTS; }
 static_assert(1 + (HMAX - 1) * SLOTS < RUN_EVENT, "run slots of the chunked path fit 15 bits");
-
-// The two-pass pre-pass's prologue: the key centroids (fp64) and the KV
-// group's GF query rows (fp64, channel-major [c][h]) into LDS, and the check
-// that every score of the group stays an exact fp64 integer:
-// |dot| <= ||q||_1 * max|c| < 2^51. With `count`, queries beyond the +-2^27 the
-// 24-bit seam can produce are counted as range errors (once per call).
-template <int D>
-__device__ __forceinline__ bool load_q(const Geom &g, const Tables *__restrict__ tabs,
-                                       const int32_t *__restrict__ q, int b, int kvh, bool count,
-                                       double (*qf)[GF], double *kcf, int *qok, DevStats *st) {
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int nk = 1 << g.kb;
-    if (tid < nk) kcf[tid] = (double)tabs->kc[tid];
-    if (tid == 0) *qok = 1;
-    __syncthreads();
-    if (wv < GF) {
-        const int32_t *qrow = q + ((int64_t)b * g.n_q + kvh * GF + wv) * D;   // wave wv: head wv
-        int64_t l1 = 0, bad = 0;
-#pragma unroll
-        for (int k = 0; k < D / 64; ++k) {
-            const int c = lane + 64 * k;
-            const int32_t v = qrow[c];
-            qf[c][wv] = (double)v;
-            l1 += v < 0 ? -(int64_t)v : (int64_t)v;
-            bad += ((int64_t)v >= Q_ROT_LIMIT || (int64_t)v <= -Q_ROT_LIMIT) ? 1 : 0;
-        }
-        l1 = wave_sum_i64(l1);                  // < 2^38: exact as a double below
-        bad = wave_sum_i64(bad);
-        if (lane == 0) {
-            double cmax = 0.0;
-            for (int i = 0; i < nk; ++i) cmax = fmax(cmax, fabs(kcf[i]));
-            if (!((double)l1 * cmax < DOT_LIMIT)) atomicAnd(qok, 0);
-            if (count && bad) atomicAdd(&st->range_errors, (unsigned long long)bad);
-        }
-    }
-    __syncthreads();
-    return *qok != 0;
-}
-
 
 // The key codes and norm words of this thread's TPT consecutive tokens
 // (t = t0 + TPT * tid + j): a wave reads one contiguous span of each plane.
@@ -274,14 +236,16 @@ __device__ __forceinline__ void load_keys(const Geom &g, const uint8_t *__restri
 
 // Exact scores of those tokens for the GF heads (attention.py:333-359), in
 // groups of 8 channels. Per group the TPT x 8 centroid reads are issued as one
-// LDS batch (the query values are LDS broadcasts, qf = [c][h] in fp64), then
-// the FMAs run channel by channel over all TPT x GF accumulators, so an
-// accumulator is reused only every TPT * GF FMAs. The 8 codes of a group sit in
+// LDS batch, then the FMAs run channel by channel over all TPT x GF
+// accumulators, so an accumulator is reused only every TPT * GF FMAs. The
+// query values are the chain's staged fp64 rows qc = [c][h]: the address is
+// wave-uniform and the memory read-only in this kernel, so they arrive by
+// scalar loads and enter the FMAs as scalar operands. The 8 codes of a group sit in
 // one 32-bit window of the key bitstream (8 * KB <= 32 bits), cut out with
 // alignbit.
 template <int D, int KB>
 __device__ __forceinline__ void score_keys(const uint32_t (&w)[TPT][KF<D, KB>::KWORDS + 1],
-                                           const uint32_t (&normw)[TPT], const double (*qf)[GF],
+                                           const uint32_t (&normw)[TPT], const double *__restrict__ qc,
                                            const double *kcf, int score_shift,
                                            int64_t (&s)[TPT][GF]) {
     using K = KF<D, KB>;
@@ -304,7 +268,7 @@ __device__ __forceinline__ void score_keys(const uint32_t (&w)[TPT][KF<D, KB>::K
 #pragma unroll
         for (int i = 0; i < 8; ++i)
 #pragma unroll
-            for (int h = 0; h < GF; ++h) qv[i][h] = qf[8 * grp + i][h];
+            for (int h = 0; h < GF; ++h) qv[i][h] = qc[(8 * grp + i) * GF + h];
 #pragma unroll
         for (int i = 0; i < 8; ++i)
 #pragma unroll
@@ -330,14 +294,18 @@ __device__ __forceinline__ void score_keys(const uint32_t (&w)[TPT][KF<D, KB>::K
 // two-pass pre-pass: the maximum score of every chunk, and the score statistics
 // ---------------------------------------------------------------------------
 
-template <int D, int KB>
+// QS: the query rows are staged (query.h). Otherwise every workgroup stages
+// its group's rows from the caller's int32 rows into LDS, and chunk 0's
+// workgroup also fills the staging for the chunk kernel that follows.
+template <int D, int KB, bool QS>
 __global__ void __launch_bounds__(CT) chunk_max_kernel(Geom g, const Tables *__restrict__ tabs,
                                                        const int32_t *__restrict__ q,
+                                                       double *qd, int32_t *qok,
                                                        const int64_t *__restrict__ len,
                                                        Chunked ck, DevStats *st) {
-    __shared__ double qf[D][GF];
     __shared__ double kcf[16];
-    __shared__ int qok;
+    __shared__ double qf[QS ? 1 : D * GF];
+    __shared__ int qok_s;
     __shared__ int64_t red[CT / 64][GF];
     __shared__ unsigned long long ovf_s, mabs_s;
     const int chunk = blockIdx.x, chain = blockIdx.y;
@@ -346,8 +314,42 @@ __global__ void __launch_bounds__(CT) chunk_max_kernel(Geom g, const Tables *__r
     const int64_t nch = T > 0 ? (T + CHUNK - 1) / CHUNK : 1;
     if (chunk >= nch) return;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    // the query rows (unless staged) and the chunk's keys first, then the
+    // centroid table while they land
+    int32_t q_t[D / 64];
+    if (!QS && wv < GF) {
+        const int32_t *qrow = q + ((int64_t)b * g.n_q + kvh * GF + wv) * D;
+#pragma unroll
+        for (int k = 0; k < D / 64; ++k) q_t[k] = qrow[lane + 64 * k];
+    }
+    const int64_t t0 = (int64_t)chunk * CHUNK;
+    uint32_t nw[TPT];
+    uint32_t kw[TPT][KF<D, KB>::KWORDS + 1];
+    load_keys<D, KB>(g, plane_ptr(g, b, kvh, 0), t0, T, kw, nw);
     if (tid == 0) ovf_s = mabs_s = 0;
-    const bool ok = load_q<D>(g, tabs, q, b, kvh, chunk == 0, qf, kcf, &qok, st);
+    if (tid == 0) qok_s = 1;
+    if (tid < (1 << g.kb)) kcf[tid] = (double)tabs->kc[tid];
+    __syncthreads();
+    const double *qc = qd + (int64_t)chain * D * GF;
+    bool ok;
+    if constexpr (QS) {
+        ok = qok[chain] != 0;
+    } else {
+        if (wv < GF) {
+            double cmax = 0.0;
+            for (int i = 0; i < (1 << g.kb); ++i) cmax = fmax(cmax, fabs(kcf[i]));
+            const bool okh = stage_query_head<D / 64>(q_t, D, wv, qf, cmax,
+                                                      chunk == 0 ? &st->range_errors : nullptr);
+            if (lane == 0 && !okh) atomicAnd(&qok_s, 0);
+        }
+        __syncthreads();
+        ok = qok_s != 0;
+        qc = qf;
+        if (chunk == 0) {          // the staging the chunk kernel reads
+            for (int i = tid; i < D * GF; i += CT) qd[(int64_t)chain * D * GF + i] = qf[i];
+            if (tid == 0) qok[chain] = qok_s;
+        }
+    }
     int64_t mx[GF];
 #pragma unroll
     for (int h = 0; h < GF; ++h) mx[h] = SCORE_LO;
@@ -355,11 +357,7 @@ __global__ void __launch_bounds__(CT) chunk_max_kernel(Geom g, const Tables *__r
     int64_t mabs = 0;
     if (ok) {
         int64_t s[TPT][GF];
-        uint32_t nw[TPT];
-        uint32_t kw[TPT][KF<D, KB>::KWORDS + 1];
-        const int64_t t0 = (int64_t)chunk * CHUNK;
-        load_keys<D, KB>(g, plane_ptr(g, b, kvh, 0), t0, T, kw, nw);
-        score_keys<D, KB>(kw, nw, qf, kcf, CENT_FRAC + g.norm_frac, s);
+        score_keys<D, KB>(kw, nw, qc, kcf, CENT_FRAC + g.norm_frac, s);
 #pragma unroll
         for (int j = 0; j < TPT; ++j) {
             if (t0 + tid * TPT + j >= T) continue;
@@ -399,9 +397,14 @@ __global__ void __launch_bounds__(CT) chunk_max_kernel(Geom g, const Tables *__r
 // the chunk kernel
 // ---------------------------------------------------------------------------
 
-template <int D, int KB, bool SEQ>
+// QS: the query rows are staged (query.h) and read by scalar loads. Otherwise
+// (a standalone sequential attend, one launch) every workgroup stages its
+// group's rows from the caller's int32 rows into LDS.
+template <int D, int KB, bool SEQ, bool QS>
 __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__restrict__ tabs,
-                                                   const int32_t *__restrict__ q, int32_t *out,
+                                                   const int32_t *__restrict__ q,
+                                                   const double *__restrict__ qd,
+                                                   const int32_t *__restrict__ qok, int32_t *out,
                                                    const int64_t *__restrict__ len, Chunked ck,
                                                    DevStats *st) {
     using K = KF<D, KB>;
@@ -431,20 +434,21 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
     const int64_t t0 = (int64_t)chunk * CHUNK;
 
     if (has_work) {
-        // The small loads first (the tables and the group's query rows), then this
-        // chunk's keys and values plane by plane. The counter of outstanding
-        // vector loads drains in order, so staging the small values must not
-        // wait for the chunk's data, and the score loop starts on the first key
-        // plane while the others land.
+        // The small loads first (the tables, and the query rows unless they are
+        // staged), then this chunk's keys and values plane by plane. The counter
+        // of outstanding vector loads drains in order, so staging the small
+        // values must not wait for the chunk's data, and the score loop starts
+        // on the first key plane while the others land. Staged query rows come
+        // by scalar loads, which do not wait on that counter.
         const int nk = 1 << g.kb;
         const int64_t kc_t = tid < nk ? tabs->kc[tid] : 0;
         const int64_t vc_t = tid < nv ? tabs->vc[tid] : 0;
         const int32_t ex_t = tid < 256 ? tabs->exp_table[tid] : 0;
         int32_t q_t[D / 64];
-        {
-            const int32_t *qrow = q + ((int64_t)b * g.n_q + kvh * GF + (wv < GF ? wv : 0)) * D;
+        if (!QS && wv < GF) {
+            const int32_t *qrow = q + ((int64_t)b * g.n_q + kvh * GF + wv) * D;
 #pragma unroll
-            for (int k = 0; k < D / 64; ++k) q_t[k] = wv < GF ? qrow[lane + 64 * k] : 0;
+            for (int k = 0; k < D / 64; ++k) q_t[k] = qrow[lane + 64 * k];
         }
         const uint8_t *hb = plane_ptr(g, b, kvh, 0);
         uint32_t kw[TPT][K::KWORDS + 1];
@@ -484,30 +488,24 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             S.qok = 1;
         }
         __syncthreads();
-        // The query rows (fp64) into LDS, and the check that every score of the
-        // group stays an exact fp64 integer: |dot| <= ||q||_1 * max|c| < 2^51.
-        // Chunk 0 counts rotated queries beyond the +-2^27 the 24-bit seam can
-        // produce (once per call).
-        if (wv < GF) {
-            int64_t l1 = 0, bad = 0;
-#pragma unroll
-            for (int k = 0; k < D / 64; ++k) {
-                const int32_t v = q_t[k];
-                S.qf[lane + 64 * k][wv] = (double)v;
-                l1 += v < 0 ? -(int64_t)v : (int64_t)v;
-                bad += ((int64_t)v >= Q_ROT_LIMIT || (int64_t)v <= -Q_ROT_LIMIT) ? 1 : 0;
-            }
-            l1 = wave_sum_i64(l1);                  // < 2^38: exact as a double below
-            bad = wave_sum_i64(bad);
-            if (lane == 0) {
+        // Whether every score of the group stays an exact fp64 integer (query.h).
+        const double *qc = qd + (int64_t)chain * D * GF;
+        bool ok;
+        if constexpr (QS) {
+            ok = qok[chain] != 0;
+        } else {
+            // Chunk 0 counts the range errors of the rotated queries, once per call.
+            if (wv < GF) {
                 double cmax = 0.0;
                 for (int i = 0; i < nk; ++i) cmax = fmax(cmax, fabs(S.kcf[i]));
-                if (!((double)l1 * cmax < DOT_LIMIT)) atomicAnd(&S.qok, 0);
-                if (SEQ && chunk == 0 && bad) atomicAdd(&st->range_errors, (unsigned long long)bad);
+                const bool okh = stage_query_head<D / 64>(q_t, D, wv, S.qf, cmax,
+                                                          chunk == 0 ? &st->range_errors : nullptr);
+                if (lane == 0 && !okh) atomicAnd(&S.qok, 0);
             }
+            __syncthreads();
+            ok = S.qok != 0;
+            qc = S.qf;
         }
-        __syncthreads();
-        const bool ok = S.qok != 0;
 
         // -- phase 1: scores of the thread's TPT consecutive tokens, which stay in
         // registers for the scan; value codes into LDS ----------------------------
@@ -517,7 +515,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
         for (int h = 0; h < GF; ++h) mx[h] = SCORE_LO;
         if (ok) {
             int64_t s[TPT][GF];
-            score_keys<D, KB>(kw, nw, S.qf, S.kcf, score_shift, s);
+            score_keys<D, KB>(kw, nw, qc, S.kcf, score_shift, s);
             unsigned long long ovf = 0;
             int64_t mabs = 0;
 #pragma unroll
@@ -1183,18 +1181,30 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
 template <int D, int KB>
 static hipError_t launch_fast(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
                               int32_t *out, const int64_t *len, const Chunked &ck, int two_pass,
-                              DevStats *st) {
+                              bool q_staged, DevStats *st) {
     const unsigned chains = (unsigned)(g.batch * g.n_kv);
     if (two_pass) {
+        // the chunk-max kernel stages the query rows for the chunk kernel when the caller has not
         dim3 grid((unsigned)ck.max_chunks, chains), block(CT);
-        hipLaunchKernelGGL((chunk_max_kernel<D, KB>), grid, block, 0, s, g, t, q, len, ck, st);
+        if (q_staged)
+            hipLaunchKernelGGL((chunk_max_kernel<D, KB, true>), grid, block, 0, s, g, t, q, ck.qd, ck.qok,
+                               len, ck, st);
+        else
+            hipLaunchKernelGGL((chunk_max_kernel<D, KB, false>), grid, block, 0, s, g, t, q, ck.qd,
+                               ck.qok, len, ck, st);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL((chunk_kernel<D, KB, false>), grid, block, 0, s, g, t, q, out, len, ck, st);
+        hipLaunchKernelGGL((chunk_kernel<D, KB, false, true>), grid, block, 0, s, g, t, q, ck.qd, ck.qok,
+                           out, len, ck, st);
         return hipGetLastError();
     }
     dim3 grid((unsigned)ck.max_chunks * chains), block(CT);
-    hipLaunchKernelGGL((chunk_kernel<D, KB, true>), grid, block, 0, s, g, t, q, out, len, ck, st);
+    if (q_staged)
+        hipLaunchKernelGGL((chunk_kernel<D, KB, true, true>), grid, block, 0, s, g, t, q, ck.qd, ck.qok,
+                           out, len, ck, st);
+    else
+        hipLaunchKernelGGL((chunk_kernel<D, KB, true, false>), grid, block, 0, s, g, t, q, ck.qd, ck.qok,
+                           out, len, ck, st);
     return hipGetLastError();
 }
 
@@ -1228,6 +1238,8 @@ static void carve(const Geom &g, int64_t max_chunks, int64_t pool, uint8_t *p, C
     c.segS = (int32_t *)take(chains * GF * pool * g.d * sizeof(int32_t));
     c.done = (unsigned int *)take(chains * sizeof(unsigned int));
     c.chain_fb = (unsigned int *)take(chains * sizeof(unsigned int));
+    c.qd = (double *)take(chains * g.d * GF * sizeof(double));
+    c.qok = (int32_t *)take(chains * sizeof(int32_t));
     c.max_chunks = (int32_t)max_chunks;
     c.pool = (int32_t)pool;
     if (ck) *ck = c;
@@ -1240,9 +1252,18 @@ size_t chunked_scratch_bytes(const Geom &g, int64_t max_chunks, int64_t pool) {
     return n;
 }
 
+void chunked_query_area(const Geom &g, int64_t max_chunks, int64_t pool, void *scratch,
+                        double **qd, int32_t **qok) {
+    Chunked ck;
+    carve(g, max_chunks, pool, (uint8_t *)scratch, &ck, nullptr);
+    *qd = ck.qd;
+    *qok = ck.qok;
+}
+
 hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
                                  int32_t *out, const int64_t *len, void *scratch, int64_t max_chunks,
-                                 int64_t pool, uint32_t call, int two_pass, DevStats *st) {
+                                 int64_t pool, uint32_t call, int two_pass, bool q_staged,
+                                 DevStats *st) {
     const int64_t chains = (int64_t)g.batch * g.n_kv;
     if (max_chunks > HMAX || chains > 65535 || max_chunks * chains > 0x7fffffff)
         return hipErrorInvalidValue;
@@ -1251,7 +1272,7 @@ hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, 
     ck.ep = call % EPOCH_MASK + 1;     // 1 .. 2^14 - 1: zeroed scratch is never current
 #define INSITU_FAST(DD, KK)                                                          \
     if (g.d == DD && g.kb == KK)                                                     \
-        return launch_fast<DD, KK>(s, g, t, q, out, len, ck, two_pass, st);
+        return launch_fast<DD, KK>(s, g, t, q, out, len, ck, two_pass, q_staged, st);
     INSITU_FAST(64, 2)
     INSITU_FAST(64, 3)
     INSITU_FAST(64, 4)

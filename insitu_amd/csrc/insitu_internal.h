@@ -185,9 +185,19 @@ bool chunked_supported(const Geom &g, int64_t capacity);
 int64_t chunked_max_chunks(int64_t capacity);
 int64_t chunked_pool_slots(int64_t max_chunks);
 size_t chunked_scratch_bytes(const Geom &g, int64_t max_chunks, int64_t pool);
+// The fp64 query staging in the chunked attend's scratch (query.h): the fused
+// step's write kernel fills it, and the attend is then launched with
+// q_staged; otherwise the attend stages the caller's rotated int32 rows itself.
+void chunked_query_area(const Geom &g, int64_t max_chunks, int64_t pool, void *scratch,
+                        double **qd, int32_t **qok);
 hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
                                  int32_t *out, const int64_t *len, void *scratch, int64_t max_chunks,
-                                 int64_t pool, uint32_t call, int two_pass, DevStats *st);
+                                 int64_t pool, uint32_t call, int two_pass, bool q_staged,
+                                 DevStats *st);
+hipError_t launch_step_write(hipStream_t s, const Geom &g, const Tables *t, const int32_t *qw,
+                             const int32_t *kw, const int32_t *vw, int rounds,
+                             const uint64_t (*signs)[2], int32_t *qr, double *qd, int32_t *qok,
+                             const int64_t *len_in, int64_t *len_out, DevStats *st);
 hipError_t launch_attend_serial(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
                                 int32_t *out, const int64_t *len, int two_pass, DevStats *st);
 

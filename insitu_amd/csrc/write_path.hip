@@ -7,6 +7,7 @@
 //                                  half-even requantize, strict '>' compares
 // append   cache/compressed.py:64-86 + quantize.py:237-252 + hw/ddr_layout.py:198-214
 #include "insitu_internal.h"
+#include "query.h"
 
 namespace insitu {
 
@@ -45,21 +46,26 @@ __device__ __forceinline__ int64_t rot_scale(int64_t v, int d) {
     }
 }
 
+// The sign diagonals of up to two rounds, one 64-bit word per 64 channels.
+struct RotSigns {
+    uint64_t s0a, s0b, s1a, s1b;
+};
+
+// One wave rotates the vector at x (d channels) into y, int32 as the cache
+// and the attend consume it; values beyond int32 are counted as range errors
+// (the RTL flags them; rotate.py:170-197 leaves them unclamped).
 template <int CPL>
-__global__ void __launch_bounds__(64) rotate_kernel(const int32_t *__restrict__ x, int32_t *y,
-                                                    int64_t n_vec, int d, int rounds,
-                                                    uint64_t s0a, uint64_t s0b, uint64_t s1a,
-                                                    uint64_t s1b, unsigned long long *range_err) {
-    const int64_t vec = blockIdx.x;
-    if (vec >= n_vec) return;
-    const int lane = threadIdx.x;
+__device__ __forceinline__ void rotate_vec(const int32_t *__restrict__ x, int d, int rounds,
+                                           const RotSigns &sg, int32_t (&y)[CPL],
+                                           unsigned long long *range_err) {
+    const int lane = threadIdx.x & 63;
     int64_t v[CPL];
-    const bool live0 = lane < d;
 #pragma unroll
     for (int k = 0; k < CPL; ++k) {
         int ch = lane + 64 * k;
-        v[k] = (ch < d) ? (int64_t)x[vec * d + ch] : 0;
+        v[k] = (ch < d) ? (int64_t)x[ch] : 0;
     }
+    const uint64_t s0a = sg.s0a, s0b = sg.s0b, s1a = sg.s1a, s1b = sg.s1b;
     for (int r = 0; r < rounds; ++r) {
         uint64_t wa = r == 0 ? s0a : s1a, wb = r == 0 ? s0b : s1b;
 #pragma unroll
@@ -72,30 +78,49 @@ __global__ void __launch_bounds__(64) rotate_kernel(const int32_t *__restrict__ 
 #pragma unroll
         for (int k = 0; k < CPL; ++k) v[k] = rot_scale(v[k], d);
     }
-    (void)live0;
 #pragma unroll
     for (int k = 0; k < CPL; ++k) {
         int ch = lane + 64 * k;
-        if (ch < d) {
-            if (v[k] < INT32_MIN || v[k] > INT32_MAX) atomicAdd(range_err, 1ull);
-            y[vec * d + ch] = (int32_t)v[k];
-        }
+        if (ch < d && (v[k] < INT32_MIN || v[k] > INT32_MAX)) atomicAdd(range_err, 1ull);
+        y[k] = (int32_t)v[k];
     }
+}
+
+template <int CPL>
+__global__ void __launch_bounds__(64) rotate_kernel(const int32_t *__restrict__ x, int32_t *y,
+                                                    int64_t n_vec, int d, int rounds, RotSigns sg,
+                                                    unsigned long long *range_err) {
+    const int64_t vec = blockIdx.x;
+    if (vec >= n_vec) return;
+    const int lane = threadIdx.x;
+    int32_t r[CPL];
+    rotate_vec<CPL>(x + vec * d, d, rounds, sg, r, range_err);
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+        int ch = lane + 64 * k;
+        if (ch < d) y[vec * d + ch] = r[k];
+    }
+}
+
+static RotSigns rot_signs(int rounds, const uint64_t (*signs)[2]) {
+    RotSigns sg;
+    sg.s0a = rounds > 0 ? signs[0][0] : 0;
+    sg.s0b = rounds > 0 ? signs[0][1] : 0;
+    sg.s1a = rounds > 1 ? signs[1][0] : 0;
+    sg.s1b = rounds > 1 ? signs[1][1] : 0;
+    return sg;
 }
 
 hipError_t launch_rotate(hipStream_t s, const int32_t *x, int32_t *y, int64_t n_vec, int d,
                          int rounds, const uint64_t (*signs)[2], unsigned long long *range_err) {
     if (n_vec <= 0) return hipSuccess;
     if (rounds > 2) return hipErrorInvalidValue;  // the kernel carries two sign diagonals
-    uint64_t s0a = rounds > 0 ? signs[0][0] : 0, s0b = rounds > 0 ? signs[0][1] : 0;
-    uint64_t s1a = rounds > 1 ? signs[1][0] : 0, s1b = rounds > 1 ? signs[1][1] : 0;
+    const RotSigns sg = rot_signs(rounds, signs);
     dim3 grid((unsigned)n_vec), block(64);
     if (d <= 64)
-        hipLaunchKernelGGL(rotate_kernel<1>, grid, block, 0, s, x, y, n_vec, d, rounds, s0a, s0b,
-                           s1a, s1b, range_err);
+        hipLaunchKernelGGL(rotate_kernel<1>, grid, block, 0, s, x, y, n_vec, d, rounds, sg, range_err);
     else
-        hipLaunchKernelGGL(rotate_kernel<2>, grid, block, 0, s, x, y, n_vec, d, rounds, s0a, s0b,
-                           s1a, s1b, range_err);
+        hipLaunchKernelGGL(rotate_kernel<2>, grid, block, 0, s, x, y, n_vec, d, rounds, sg, range_err);
     return hipGetLastError();
 }
 
@@ -188,6 +213,58 @@ hipError_t launch_encode(hipStream_t s, const int32_t *x, int64_t n_vec, int d, 
 // append: one wave per (sequence, token, kv head) -> one packed row
 // ---------------------------------------------------------------------------
 
+// One wave encodes the field x (lane = channel): the norm, and the codes into
+// codes[0 .. d).
+template <int CPL>
+__device__ __forceinline__ int64_t encode_field(const int64_t (&x)[CPL], int d, int norm_frac,
+                                                const int64_t *__restrict__ bnd, int n_b,
+                                                uint8_t *codes) {
+    const int lane = threadIdx.x & 63;
+    const int64_t n = norm_wire<CPL>(x, d, norm_frac);
+#pragma unroll
+    for (int q = 0; q < CPL; ++q) {
+        int ch = lane + 64 * q;
+        if (ch < d) codes[ch] = (uint8_t)encode_one(x[q], n, bnd, n_b, norm_frac);
+    }
+    return n;
+}
+
+// One wave packs the row of (sequence b, KV head h) at token pos from the
+// codes in LDS and stores it into the planes. Dword w of the row holds row bits
+// [32w, 32w + 32): the key field is d*kb bits, the value field d*vb bits, then
+// k_norm | v_norm << 16. Row byte 4*lane lies in exactly one plane, because
+// every plane boundary is a field boundary and fields are whole dwords.
+__device__ __forceinline__ void pack_store_row(const Geom &g, const uint8_t (*codes)[MAX_D],
+                                               int64_t nk, int64_t nv, int b, int h, int64_t pos) {
+    const int lane = threadIdx.x & 63;
+    const int d = g.d;
+    const int kwords = g.key_bytes / 4, vwords = g.value_bytes / 4;
+    const int nwords = g.row_bytes / 4;
+    if (lane >= nwords) return;
+    uint32_t word = 0;
+    if (lane < kwords + vwords) {
+        const int field = lane < kwords ? 0 : 1;
+        const int bits = field == 0 ? g.kb : g.vb;
+        const int w = field == 0 ? lane : lane - kwords;
+        const int bit0 = 32 * w;
+        const int c_first = bit0 / bits;
+        const int c_last = (bit0 + 31) / bits;
+        for (int c = c_first; c <= c_last && c < d; ++c) {
+            int64_t off = (int64_t)c * bits - bit0;   // may be negative for a straddling code
+            uint64_t cv = codes[field][c];
+            uint64_t placed = off >= 0 ? (cv << off) : (cv >> (-off));
+            word |= (uint32_t)(placed & 0xFFFFFFFFull);
+        }
+    } else {
+        word = (uint32_t)(nk & 0xFFFF) | ((uint32_t)(nv & 0xFFFF) << 16);
+    }
+    const int byte = 4 * lane;
+    int p = 0;
+    while (p + 1 < g.n_planes && byte >= g.plane_lo[p + 1]) ++p;
+    uint8_t *dst = plane_ptr(g, b, h, p) + pos * g.plane_w[p] + (byte - g.plane_lo[p]);
+    *(uint32_t *)dst = word;
+}
+
 template <int CPL>
 __global__ void __launch_bounds__(64) append_kernel(Geom g, const Tables *__restrict__ tabs,
                                                     const int32_t *__restrict__ k,
@@ -196,7 +273,6 @@ __global__ void __launch_bounds__(64) append_kernel(Geom g, const Tables *__rest
                                                     int64_t *len_out, int seq_hi,
                                                     DevStats *st) {
     __shared__ uint8_t codes[2][MAX_D];
-    __shared__ uint32_t row[80];
     const int lane = threadIdx.x;
     const int h = blockIdx.x % g.n_kv;
     const int t = (blockIdx.x / g.n_kv) % n_tok;
@@ -225,13 +301,7 @@ __global__ void __launch_bounds__(64) append_kernel(Geom g, const Tables *__rest
             int ch = lane + 64 * q;
             x[q] = ch < d ? (int64_t)k[src + ch] : 0;
         }
-        nk = norm_wire<CPL>(x, d, g.norm_frac);
-#pragma unroll
-        for (int q = 0; q < CPL; ++q) {
-            int ch = lane + 64 * q;
-            if (ch < d) codes[0][ch] = (uint8_t)encode_one(x[q], nk, tabs->kbnd, (1 << g.kb) - 1,
-                                                           g.norm_frac);
-        }
+        nk = encode_field<CPL>(x, d, g.norm_frac, tabs->kbnd, (1 << g.kb) - 1, codes[0]);
     }
     {
         int64_t x[CPL];
@@ -240,50 +310,97 @@ __global__ void __launch_bounds__(64) append_kernel(Geom g, const Tables *__rest
             int ch = lane + 64 * q;
             x[q] = ch < d ? (int64_t)v[src + ch] : 0;
         }
-        nv = norm_wire<CPL>(x, d, g.norm_frac);
-#pragma unroll
-        for (int q = 0; q < CPL; ++q) {
-            int ch = lane + 64 * q;
-            if (ch < d) codes[1][ch] = (uint8_t)encode_one(x[q], nv, tabs->vbnd, (1 << g.vb) - 1,
-                                                           g.norm_frac);
-        }
+        nv = encode_field<CPL>(x, d, g.norm_frac, tabs->vbnd, (1 << g.vb) - 1, codes[1]);
     }
     __syncthreads();
+    pack_store_row(g, codes, nk, nv, b, h, pos);
+}
 
-    // Pack: dword w of the row holds row bits [32w, 32w + 32). The key field
-    // is d*kb bits, the value field d*vb bits, then k_norm | v_norm << 16.
-    const int kwords = g.key_bytes / 4, vwords = g.value_bytes / 4;
-    const int nwords = g.row_bytes / 4;
-    if (lane < nwords) {
-        uint32_t word = 0;
-        if (lane < kwords + vwords) {
-            const int field = lane < kwords ? 0 : 1;
-            const int bits = field == 0 ? g.kb : g.vb;
-            const int w = field == 0 ? lane : lane - kwords;
-            const int bit0 = 32 * w;
-            const int c_first = bit0 / bits;
-            const int c_last = (bit0 + 31) / bits;
-            for (int c = c_first; c <= c_last && c < d; ++c) {
-                int64_t off = (int64_t)c * bits - bit0;   // may be negative for a straddling code
-                uint64_t cv = codes[field][c];
-                uint64_t placed = off >= 0 ? (cv << off) : (cv >> (-off));
-                word |= (uint32_t)(placed & 0xFFFFFFFFull);
-            }
-        } else {
-            word = (uint32_t)(nk & 0xFFFF) | ((uint32_t)(nv & 0xFFFF) << 16);
+// ---------------------------------------------------------------------------
+// the fused decode step's writes (kernel.py:271-284): rotate k, v and q,
+// encode and append every (sequence, KV head)'s row, stage the query rows
+// ---------------------------------------------------------------------------
+
+// One workgroup per (sequence b, KV head h) and 2 + G waves: wave 0 takes the
+// key, wave 1 the value, waves 2 .. 2 + G - 1 the group's query heads. The
+// rotated queries go to qr (int32); with qd, also to the chunked attend's fp64
+// staging (query.h), which needs G == GF.
+template <int CPL>
+__global__ void __launch_bounds__((2 + MAX_G) * 64) step_write_kernel(
+        Geom g, const Tables *__restrict__ tabs, const int32_t *__restrict__ qw,
+        const int32_t *__restrict__ kw, const int32_t *__restrict__ vw, int rounds, RotSigns sg,
+        int32_t *qr, double *qd, int32_t *qok, const int64_t *__restrict__ len_in, int64_t *len_out,
+        DevStats *st) {
+    __shared__ uint8_t codes[2][MAX_D];
+    __shared__ int64_t norms[2];
+    __shared__ int ok_s;
+    const int lane = threadIdx.x & 63;
+    const int wv = threadIdx.x >> 6;
+    const int chain = blockIdx.x;
+    const int b = chain / g.n_kv, h = chain % g.n_kv;
+    const int d = g.d;
+
+    if (blockIdx.x == 0 && wv == 0) {
+        for (int i = lane; i < g.batch; i += 64) len_out[i] = len_in[i] + 1;
+    }
+    if (threadIdx.x == 0) ok_s = 1;
+    const int64_t pos = len_in[b];
+    const bool room = pos < g.capacity;   // the host checks capacity first; this only guards memory
+    __syncthreads();
+    if (wv < 2) {
+        const int32_t *src = (wv == 0 ? kw : vw) + ((int64_t)b * g.n_kv + h) * d;
+        int32_t r[CPL];
+        rotate_vec<CPL>(src, d, rounds, sg, r, &st->range_errors);
+        int64_t x[CPL];
+#pragma unroll
+        for (int k = 0; k < CPL; ++k) x[k] = r[k];
+        const int64_t n = wv == 0
+            ? encode_field<CPL>(x, d, g.norm_frac, tabs->kbnd, (1 << g.kb) - 1, codes[0])
+            : encode_field<CPL>(x, d, g.norm_frac, tabs->vbnd, (1 << g.vb) - 1, codes[1]);
+        if (lane == 0) norms[wv] = n;
+    } else if (wv < 2 + g.G) {
+        const int qh = h * g.G + (wv - 2);
+        const int64_t row = ((int64_t)b * g.n_q + qh) * d;
+        int32_t r[CPL];
+        rotate_vec<CPL>(qw + row, d, rounds, sg, r, &st->range_errors);
+#pragma unroll
+        for (int k = 0; k < CPL; ++k) {
+            const int ch = lane + 64 * k;
+            if (ch < d) qr[row + ch] = r[k];
         }
-        row[lane] = word;
+        if (qd) {
+            const bool ok = stage_query_head<CPL>(r, d, wv - 2, qd + (int64_t)chain * d * GF,
+                                                  key_centroid_absmax(tabs, g.kb), &st->range_errors);
+            if (lane == 0 && !ok) atomicAnd(&ok_s, 0);
+        }
     }
     __syncthreads();
-    // Scatter into the planes: row byte 4*lane lies in exactly one plane,
-    // because every plane boundary is a field boundary and fields are whole dwords.
-    if (lane < nwords) {
-        const int byte = 4 * lane;
-        int p = 0;
-        while (p + 1 < g.n_planes && byte >= g.plane_lo[p + 1]) ++p;
-        uint8_t *dst = plane_ptr(g, b, h, p) + pos * g.plane_w[p] + (byte - g.plane_lo[p]);
-        *(uint32_t *)dst = row[lane];
+    if (wv == 0) {
+        if (room)
+            pack_store_row(g, codes, norms[0], norms[1], b, h, pos);
+        else if (lane == 0)
+            atomicAdd(&st->fault, 1ull);
     }
+    if (qd && threadIdx.x == 0) qok[chain] = ok_s;
+}
+
+hipError_t launch_step_write(hipStream_t s, const Geom &g, const Tables *t, const int32_t *qw,
+                             const int32_t *kw, const int32_t *vw, int rounds,
+                             const uint64_t (*signs)[2], int32_t *qr, double *qd, int32_t *qok,
+                             const int64_t *len_in, int64_t *len_out, DevStats *st) {
+    const int64_t blocks = (int64_t)g.batch * g.n_kv;
+    if (blocks <= 0) return hipSuccess;
+    if (rounds > 2 || g.G > MAX_G || (qd && g.G != GF) || blocks > 0x7fffffff)
+        return hipErrorInvalidValue;
+    const RotSigns sg = rot_signs(rounds, signs);
+    dim3 grid((unsigned)blocks), block((unsigned)((2 + g.G) * 64));
+    if (g.d <= 64)
+        hipLaunchKernelGGL(step_write_kernel<1>, grid, block, 0, s, g, t, qw, kw, vw, rounds, sg, qr,
+                           qd, qok, len_in, len_out, st);
+    else
+        hipLaunchKernelGGL(step_write_kernel<2>, grid, block, 0, s, g, t, qw, kw, vw, rounds, sg, qr,
+                           qd, qok, len_in, len_out, st);
+    return hipGetLastError();
 }
 
 hipError_t launch_append(hipStream_t s, const Geom &g, const Tables *t, const int32_t *k,

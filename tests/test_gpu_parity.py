@@ -502,3 +502,110 @@ def test_repeated_calls_reuse_the_counters(ctx):
     out, _ = a.attend(q[None], "online")
     want, _ = _host_reference(k, v, q)
     np.testing.assert_array_equal(out.cpu().numpy()[0], want)
+
+
+# -- the fused decode step (one write kernel, then the attend) at multi-chunk contexts --
+
+@pytest.mark.parametrize("mode", ["online", "two_pass", "serial"])
+@pytest.mark.parametrize("d,kb,vb", [(64, 4, 2), (128, 3, 3)])
+def test_fused_step_ragged_batch_multi_chunk(ctx, mode, d, kb, vb):
+    """insitu_step over a ragged batch whose caches span several chunks: every
+    sequence's output against the oracle's attend on the host-rotated query, and
+    the rows the step appended byte for byte (kernel.py:271-345)."""
+    from insitu_amd import ModelConfig, QuantConfig
+    from insitu_amd.block import AttentionBlock
+    rng = np.random.default_rng(31 + d)
+    lens, steps, batch = [2500, 1100], 2, 2
+    model = ModelConfig.llama32_1b() if d == 64 else ModelConfig(
+        hidden_size=4096, num_heads=32, num_kv_heads=8, head_dim=128)
+    f = Format(d=d, key_bits=kb, value_bits=vb)
+    blk = AttentionBlock(model, QuantConfig(key_bits=kb, value_bits=vb),
+                         capacity=max(lens) + steps, batch=batch, softmax=mode, ctx=ctx)
+    sg = signs_from_seed(d, 0, 1)
+    hosts = []
+    for b, T in enumerate(lens):
+        k, v = _random_cache_inputs(rng, T, d=d)
+        blk.cache.append_rotated(k, v, seq=b)
+        h = Cache(8, T + steps, f)
+        h.append_rotated(k, v)
+        hosts.append(h)
+    fn = native.attend_two_pass if mode == "two_pass" else native.attend_online
+    for t in range(steps):
+        qw = rng.integers(-(1 << 23), 1 << 23, size=(batch, 32, d))
+        kw = rng.integers(-(1 << 23), 1 << 23, size=(batch, 8, d))
+        vw = rng.integers(-(1 << 23), 1 << 23, size=(batch, 8, d))
+        out = blk.step(qw, kw, vw).cpu().numpy().reshape(batch, 32, d)
+        for b in range(batch):
+            qr, kr, vr = rotate(qw[b], sg), rotate(kw[b], sg), rotate(vw[b], sg)
+            hosts[b].append_rotated(kr[None], vr[None])
+            want = np.concatenate([fn(qr[4 * g:4 * g + 4], hosts[b].view(g), f)[0]
+                                   for g in range(8)])
+            np.testing.assert_array_equal(out[b], want, err_msg=f"step {t} seq {b}")
+        assert blk.last_stats.serial_fallbacks == 0 and blk.last_stats.range_errors == 0
+    for b, T in enumerate(lens):
+        for g in (0, 7):
+            np.testing.assert_array_equal(blk.cache.read_rows(g, T, steps, seq=b),
+                                          hosts[b].buf[T:T + steps, g])
+
+
+@pytest.mark.parametrize("mode", ["online", "serial"])
+def test_fused_step_counts_rotated_queries_beyond_the_seam_range(ctx, mode):
+    """A wire query of 2^30 on one channel rotates to +-2^27 on every channel,
+    beyond what the 24-bit seam can produce: each such value is one range
+    error (once per call, whichever attend runs), and the output stays exact,
+    since ||q||_1 * max|c| is still below 2^51."""
+    from insitu_amd import ModelConfig, QuantConfig
+    from insitu_amd.block import AttentionBlock
+    rng = np.random.default_rng(41)
+    T = 1500
+    blk = AttentionBlock(ModelConfig.llama32_1b(), QuantConfig(key_bits=4, value_bits=2),
+                         capacity=T + 1, softmax=mode, ctx=ctx)
+    k, v = _random_cache_inputs(rng, T)
+    blk.cache.append_rotated(k, v)
+    host = Cache(8, T + 1, FMT)
+    host.append_rotated(k, v)
+    qw = rng.integers(-(1 << 22), 1 << 22, size=(1, 32, 64))
+    qw[0, 8:12] = 0
+    qw[0, 8:12, 0] = 1 << 30
+    kw = rng.integers(-(1 << 22), 1 << 22, size=(1, 8, 64))
+    vw = rng.integers(-(1 << 22), 1 << 22, size=(1, 8, 64))
+    out = blk.step(qw, kw, vw).cpu().numpy().reshape(32, 64)
+    sg = signs_from_seed(64, 0, 1)
+    qr = rotate(qw[0], sg)
+    assert np.all(np.abs(qr[8:12]) == 1 << 27)
+    host.append_rotated(rotate(kw[0], sg)[None], rotate(vw[0], sg)[None])
+    want = np.concatenate([native.attend_online(qr[4 * g:4 * g + 4], host.view(g), FMT)[0]
+                           for g in range(8)])
+    np.testing.assert_array_equal(out, want)
+    st = blk.last_stats
+    assert st.range_errors == 4 * 64 and st.serial_fallbacks == 0
+
+
+def test_attend_timing_hook_counts_every_attend(ctx):
+    """insitu_ctx_timing: one event pair per attend, in both the standalone attend
+    and the fused step; the summed kernel time is positive and read once."""
+    import ctypes
+
+    from insitu_amd import ModelConfig, QuantConfig, _lib
+    from insitu_amd.attention import CompressedAttention
+    from insitu_amd.block import AttentionBlock
+    rng = np.random.default_rng(5)
+    blk = AttentionBlock(ModelConfig.llama32_1b(), QuantConfig(key_bits=4, value_bits=2),
+                         capacity=2100, ctx=ctx)
+    k, v = _random_cache_inputs(rng, 2048)
+    blk.cache.append_rotated(k, v)
+    lib = ctx.lib
+    ms, n = ctypes.c_double(), ctypes.c_int64()
+    _lib.check(lib.insitu_ctx_timing(ctx.handle, 1))
+    try:
+        q = rng.integers(-(1 << 22), 1 << 22, size=(1, 32, 64))
+        CompressedAttention(blk.cache).attend(q, "online", stats=False)
+        CompressedAttention(blk.cache).attend(q, "two_pass", stats=False)
+        for _ in range(3):
+            blk.step(q, k[:1], v[:1], stats=False)
+        _lib.check(lib.insitu_ctx_timing_read(ctx.handle, ctypes.byref(ms), ctypes.byref(n)))
+        assert n.value == 5 and ms.value > 0.0
+        _lib.check(lib.insitu_ctx_timing_read(ctx.handle, ctypes.byref(ms), ctypes.byref(n)))
+        assert n.value == 0 and ms.value == 0.0
+    finally:
+        _lib.check(lib.insitu_ctx_timing(ctx.handle, 0))
