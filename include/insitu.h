@@ -109,8 +109,9 @@ void *insitu_ctx_stream(insitu_ctx *ctx);
 
 /* Attend kernel timing: the measurement hook of the benchmark (no counterpart
  * in the reference, whose attend is a Python loop). While enabled, every attend
- * on the context's caches records a pair of HIP events on the context's stream
- * around its attend kernels (two-pass mode: both of them). _read
+ * on the context's caches attaches a pair of HIP events to its kernel dispatches
+ * (start of the first, end of the last; hipExtLaunchKernelGGL), which adds no
+ * packets to the stream. _read
  * waits for the last pair and returns the summed kernel time in milliseconds
  * and the number of attends since the previous read. Disabling drops what has
  * not been read. */

@@ -374,6 +374,8 @@ int insitu_cache_create(insitu_ctx *c, const insitu_cache_desc *desc, insitu_cac
     Tables &t = k->tabs_host;
     fill_exp(t);
     for (int i = 0; i < nk; ++i) t.kc[i] = desc->key_centroids_host[i];
+    t.kc_absmax = 0.0;
+    for (int i = 0; i < nk; ++i) t.kc_absmax = std::fmax(t.kc_absmax, std::fabs((double)t.kc[i]));
     for (int i = 0; i + 1 < nk; ++i) t.kbnd[i] = desc->key_bounds_host[i];
     for (int i = 0; i < nv; ++i) t.vc[i] = desc->value_centroids_host[i];
     for (int i = 0; i + 1 < nv; ++i) t.vbnd[i] = desc->value_bounds_host[i];
@@ -507,41 +509,41 @@ int insitu_append_seq(insitu_cache *k, int32_t seq, const int32_t *kr, const int
     return append_impl(k, seq, seq + 1, kr, vr, n_tok);
 }
 
-// An event on the context's stream for attend timing, or nullptr when timing is off.
-static int timing_event(insitu_ctx *c, hipEvent_t *out) {
-    *out = nullptr;
+// The start/stop events of an attend when timing is on (null events otherwise),
+// from the context's pool; the launches record them.
+static int timing_events(insitu_ctx *c, LaunchEv *ev) {
+    *ev = LaunchEv{};
     if (!c->timing) return INSITU_OK;
-    if (c->ev_used == c->ev.size()) {
+    while (c->ev.size() < c->ev_used + 2) {
         hipEvent_t e;
         HIP_TRY(hipEventCreate(&e), "hipEventCreate");
         c->ev.push_back(e);
     }
-    *out = c->ev[c->ev_used++];
-    HIP_TRY(hipEventRecord(*out, c->stream), "hipEventRecord");
+    ev->start = c->ev[c->ev_used++];
+    ev->stop = c->ev[c->ev_used++];
     return INSITU_OK;
 }
 
-// q_staged: the chunked path's fp64 query staging already holds q (the fused
-// step's write kernel filled it).
+// q_staged: the chunked path's fp64 query staging already holds q (the step's
+// write kernel filled it). step: the whole decode step in the attend launch
+// (chunked sequential mode; the lengths are those before the step).
 static int attend_impl(insitu_cache *k, const int32_t *q, int32_t *out, int32_t mode,
-                       bool q_staged) {
+                       bool q_staged, const StepIn *step = nullptr) {
     const int64_t *len = k->len_dev[k->cur];
     const int two_pass = mode == INSITU_TWO_PASS ? 1 : 0;
-    hipEvent_t e0, e1;
-    if (mode != INSITU_SERIAL && k->chunk_scratch) {
-        int rc = timing_event(k->ctx, &e0);
-        if (rc) return rc;
-        HIP_TRY(launch_attend_chunked(k->ctx->stream, k->g, k->tabs, q, out, len, k->chunk_scratch,
-                                      k->max_chunks, k->pool, k->calls++, two_pass, q_staged,
-                                      k->stats),
-                "chunked attend launch");
-        return timing_event(k->ctx, &e1);
-    }
-    int rc = timing_event(k->ctx, &e0);
+    LaunchEv ev;
+    int rc = timing_events(k->ctx, &ev);
     if (rc) return rc;
-    HIP_TRY(launch_attend_serial(k->ctx->stream, k->g, k->tabs, q, out, len, two_pass, k->stats),
+    if (mode != INSITU_SERIAL && k->chunk_scratch) {
+        HIP_TRY(launch_attend_chunked(k->ctx->stream, k->g, k->tabs, q, out, len, k->chunk_scratch,
+                                      k->max_chunks, k->pool, k->calls++, two_pass, q_staged, step,
+                                      ev, k->stats),
+                "chunked attend launch");
+        return INSITU_OK;
+    }
+    HIP_TRY(launch_attend_serial(k->ctx->stream, k->g, k->tabs, q, out, len, two_pass, ev, k->stats),
             "attend launch");
-    return timing_event(k->ctx, &e1);
+    return INSITU_OK;
 }
 
 int insitu_attend(insitu_cache *k, const int32_t *q, int32_t *out, int32_t mode,
@@ -575,9 +577,24 @@ int insitu_step(insitu_cache *k, const int32_t *q, const int32_t *kw, const int3
     int rc = stats ? zero_stats(k) : INSITU_OK;
     if (rc) return rc;
     // kernel.py:271-284: k, v and q are all rotated, the k/v row appended (the
-    // token attends to itself), in one kernel that also stages the rotated
-    // queries for the chunked attend; then the attend (:337-345).
+    // token attends to itself), then the attend (:337-345). In chunked
+    // sequential mode at d = 64 that is one launch; otherwise one write kernel
+    // (which also stages the rotated queries for a chunked attend) and the attend.
     const bool chunked = mode != INSITU_SERIAL && k->chunk_scratch;
+    if (chunked && mode != INSITU_TWO_PASS && chunked_fused_step(g)) {
+        StepIn si;
+        si.qw = q;
+        si.kw = kw;
+        si.vw = vw;
+        si.sg = rot_signs(k->desc.fmt.rot_rounds, k->desc.fmt.rot_signs);
+        si.rounds = k->desc.fmt.rot_rounds;
+        si.len_out = k->len_dev[k->cur ^ 1];
+        rc = attend_impl(k, qr, out, mode, false, &si);
+        if (rc) return rc;
+        k->cur ^= 1;
+        for (int b = 0; b < g.batch; ++b) k->len_host[b] += 1;
+        return copy_stats(k, stats);
+    }
     double *qd = nullptr;
     int32_t *qok = nullptr;
     if (chunked) chunked_query_area(g, k->max_chunks, k->pool, k->chunk_scratch, &qd, &qok);

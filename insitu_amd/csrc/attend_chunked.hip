@@ -44,6 +44,7 @@
 #include <type_traits>
 
 #include "query.h"
+#include "row_codec.h"
 #include "serial_head.h"
 #include "wave.h"
 
@@ -167,12 +168,20 @@ struct ChunkLds {
     struct Replay {
         uint16_t slot[GF][NSEG];   // the runs in order: slot | RUN_EVENT when a rescale opens it
     };
+    struct NewRow {                // the fused step's new token, before the score phase
+        int64_t bnd[2][255];       // key and value boundaries
+        uint8_t codes[2][MAX_D];
+    };
     union {
         Phase ph;
         Replay rp;
+        NewRow nr;
         SerialLds<KF<D, KB>::RS> fb[GF];
     } u;
     double qf[D * GF];             // the group's query rows [c][h] (unless staged)
+    int32_t qi[GF][D];             // the fused step: the rotated rows, for the serial path
+    uint32_t row[32];              // the fused step: the new token's packed row
+    int64_t norms[2];
     double kcf[16];
     int64_t kc[16];
     int64_t vc[16];
@@ -400,13 +409,19 @@ __global__ void __launch_bounds__(CT) chunk_max_kernel(Geom g, const Tables *__r
 // QS: the query rows are staged (query.h) and read by scalar loads. Otherwise
 // (a standalone sequential attend, one launch) every workgroup stages its
 // group's rows from the caller's int32 rows into LDS.
-template <int D, int KB, bool SEQ, bool QS>
+// STEP (with SEQ, not QS): the fused decode step (kernel.py:271-345) in one
+// launch. len holds the lengths before the step and the attend covers one
+// token more: every workgroup rotates its group's wire query rows itself, and
+// the workgroup of the chunk holding the new token rotates, encodes and packs
+// its key/value row, stores it into the planes and scores it from LDS.
+template <int D, int KB, bool SEQ, bool QS, bool STEP>
 __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__restrict__ tabs,
                                                    const int32_t *__restrict__ q,
                                                    const double *__restrict__ qd,
                                                    const int32_t *__restrict__ qok, int32_t *out,
                                                    const int64_t *__restrict__ len, Chunked ck,
-                                                   DevStats *st) {
+                                                   DevStats *st, StepIn si) {
+    static_assert(!STEP || (SEQ && !QS), "the fused step is the sequential kernel with LDS queries");
     using K = KF<D, KB>;
     constexpr int CPL = K::CPL;
     __shared__ ChunkLds<D, KB> S;
@@ -425,9 +440,11 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
         chain = blockIdx.y;
     }
     const int b = chain / g.n_kv, kvh = chain % g.n_kv;
-    const int64_t T = len[b];
+    const int64_t T = len[b] + (STEP ? 1 : 0);
     const int64_t nch = T > 0 ? (T + CHUNK - 1) / CHUNK : 1;
     const bool has_work = chunk < nch;
+    const bool new_row = STEP && chunk == nch - 1;     // this chunk holds the step's new token
+    if (STEP && chunk == 0 && kvh == 0 && tid == 0) si.len_out[b] = T;
     const int nv = 1 << g.vb;
     const int acc_shift = CENT_FRAC + g.norm_frac + PROB_FRAC - ACC_FRAC;
     const int score_shift = CENT_FRAC + g.norm_frac;
@@ -445,7 +462,13 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
         const int64_t vc_t = tid < nv ? tabs->vc[tid] : 0;
         const int32_t ex_t = tid < 256 ? tabs->exp_table[tid] : 0;
         int32_t q_t[D / 64];
-        if (!QS && wv < GF) {
+        int32_t kv_t[D / 64];          // STEP: the new token's key (wave GF) or value (GF + 1)
+        if (STEP) {
+            if (wv < GF)
+                load_vec<D / 64>(si.qw + ((int64_t)b * g.n_q + kvh * GF + wv) * D, D, q_t);
+            else if (new_row && wv < GF + 2)
+                load_vec<D / 64>((wv == GF ? si.kw : si.vw) + ((int64_t)b * g.n_kv + kvh) * D, D, kv_t);
+        } else if (!QS && wv < GF) {
             const int32_t *qrow = q + ((int64_t)b * g.n_q + kvh * GF + wv) * D;
 #pragma unroll
             for (int k = 0; k < D / 64; ++k) q_t[k] = qrow[lane + 64 * k];
@@ -487,6 +510,16 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             S.lb_fail = 0;
             S.qok = 1;
         }
+        if (STEP) {
+            // The rotations, once the small rows are in: their waits leave the
+            // chunk's own loads in flight. Chunk 0 counts the queries' range
+            // errors, the new token's chunk those of its key and value.
+            if (wv < GF)
+                rotate_loaded<D / 64>(q_t, D, si.rounds, si.sg, q_t, chunk == 0 ? &st->range_errors : nullptr);
+            else if (new_row && wv < GF + 2)
+                rotate_loaded<D / 64>(kv_t, D, si.rounds, si.sg, kv_t, &st->range_errors);
+            if (new_row) stage_bounds(tabs, g, S.u.nr.bnd);
+        }
         __syncthreads();
         // Whether every score of the group stays an exact fp64 integer (query.h).
         const double *qc = qd + (int64_t)chain * D * GF;
@@ -496,15 +529,50 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
         } else {
             // Chunk 0 counts the range errors of the rotated queries, once per call.
             if (wv < GF) {
-                double cmax = 0.0;
-                for (int i = 0; i < nk; ++i) cmax = fmax(cmax, fabs(S.kcf[i]));
-                const bool okh = stage_query_head<D / 64>(q_t, D, wv, S.qf, cmax,
+                const bool okh = stage_query_head<D / 64>(q_t, D, wv, S.qf, tabs->kc_absmax,
                                                           chunk == 0 ? &st->range_errors : nullptr);
                 if (lane == 0 && !okh) atomicAnd(&S.qok, 0);
+                if (STEP) {
+#pragma unroll
+                    for (int k = 0; k < D / 64; ++k) S.qi[wv][lane + 64 * k] = q_t[k];
+                }
+            } else if (new_row && wv < GF + 2) {
+                const int f = wv - GF;         // 0: key, 1: value
+                int64_t x[D / 64];
+#pragma unroll
+                for (int k = 0; k < D / 64; ++k) x[k] = kv_t[k];
+                const int64_t n = encode_field<D / 64>(x, D, g.norm_frac, S.u.nr.bnd[f],
+                                                       (1 << (f == 0 ? g.kb : g.vb)) - 1, S.u.nr.codes[f]);
+                if (lane == 0) S.norms[f] = n;
             }
             __syncthreads();
             ok = S.qok != 0;
             qc = S.qf;
+        }
+        if (new_row) {
+            // Pack the new row, store it into the planes (agent-coherent stores:
+            // a serial fallback elsewhere reads it), and give it to the thread
+            // that holds token T - 1 in place of what its loads found there.
+            const int nwords = g.row_bytes / 4, kwords = g.key_bytes / 4, vwords = g.value_bytes / 4;
+            if (wv == GF && lane < nwords) {
+                const uint32_t w = pack_row_word(g, S.u.nr.codes, S.norms[0], S.norms[1], lane);
+                S.row[lane] = w;
+                pub32(row_word_ptr(g, b, kvh, T - 1, lane), w);
+            }
+            __syncthreads();
+            const int tl = (int)(T - 1 - t0);
+            if (tid == tl / TPT) {
+#pragma unroll
+                for (int j = 0; j < TPT; ++j)
+                    if (j == tl % TPT) {
+#pragma unroll
+                        for (int i = 0; i < K::KWORDS; ++i) kw[j][i] = S.row[i];
+                        nw[j] = S.row[nwords - 1];
+#pragma unroll
+                        for (int i = 0; i < K::VW; ++i)
+                            if (i < vwords) vreg[j][i] = S.row[kwords + i];
+                    }
+            }
         }
 
         // -- phase 1: scores of the thread's TPT consecutive tokens, which stay in
@@ -919,6 +987,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
         // first, so that when it is the last (its many rescale events make it the
         // slowest) its state never leaves the registers. Otherwise it publishes
         // the state after counting, and the last workgroup waits for its header.
+        if (new_row && wv == GF) stores_done();   // the new row is out before this chunk counts
         __syncthreads();
         if (tid == 0) {
             const unsigned prior = __hip_atomic_fetch_add(&ck.done[chain], 1u, __ATOMIC_RELAXED,
@@ -1137,8 +1206,11 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             if (!hw) {
             } else if (fb) {
                 // The serial path counts score statistics only when the headers did not.
-                serial_head<CPL, K::RS>(g, tabs, S.kc, S.vc, q + ((int64_t)b * g.n_q + qh) * D, b,
-                                        kvh, T, SEQ ? 0 : 1, !hdr_stats, S.u.fb[h], orow, st);
+                // The fused step's new row came from another workgroup: acquire it.
+                if (STEP) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+                const int32_t *qrow = STEP ? &S.qi[h][0] : q + ((int64_t)b * g.n_q + qh) * D;
+                serial_head<CPL, K::RS>(g, tabs, S.kc, S.vc, qrow, b, kvh, T, SEQ ? 0 : 1, !hdr_stats,
+                                        S.u.fb[h], orow, st);
                 if (lane == 0) atomicAdd(&st->serial_fallbacks, 1ull);
             } else {
                 unsigned long long aovf = 0;
@@ -1178,33 +1250,78 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
     }
 }
 
+// ---------------------------------------------------------------------------
+// query staging in front of a standalone attend (d = 128)
+// ---------------------------------------------------------------------------
+
+// One workgroup per (sequence, KV head); wave h stages query head h of the
+// group (query.h).
+template <int CPL>
+__global__ void __launch_bounds__(GF * 64) qprep_kernel(Geom g, const Tables *__restrict__ tabs,
+                                                        const int32_t *__restrict__ q, double *qd,
+                                                        int32_t *qok, DevStats *st) {
+    __shared__ int ok_s;
+    const int chain = blockIdx.x, h = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int b = chain / g.n_kv, kvh = chain % g.n_kv;
+    if (threadIdx.x == 0) ok_s = 1;
+    __syncthreads();
+    int32_t v[CPL];
+    load_vec<CPL>(q + ((int64_t)b * g.n_q + kvh * GF + h) * g.d, g.d, v);
+    const bool ok = stage_query_head<CPL>(v, g.d, h, qd + (int64_t)chain * g.d * GF, tabs->kc_absmax,
+                                          &st->range_errors);
+    if (lane == 0 && !ok) atomicAnd(&ok_s, 0);
+    __syncthreads();
+    if (threadIdx.x == 0) qok[chain] = ok_s;
+}
+
+// Whether a standalone sequential attend stages its query rows first (one
+// small launch) rather than every workgroup staging them in LDS. Read as
+// scalar FMA operands they keep the d = 128 chunk kernel within 128 VGPRs, two
+// workgroups per CU, where the LDS-query kernel needs about 150; at d = 64 both
+// fit, and the extra launch would only add its dispatch.
+static bool stage_queries_first(const Geom &g) { return g.d > 64; }
+
+bool chunked_fused_step(const Geom &g) { return !stage_queries_first(g); }
+
 template <int D, int KB>
 static hipError_t launch_fast(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
                               int32_t *out, const int64_t *len, const Chunked &ck, int two_pass,
-                              bool q_staged, DevStats *st) {
+                              bool q_staged, const StepIn *step, LaunchEv ev, DevStats *st) {
     const unsigned chains = (unsigned)(g.batch * g.n_kv);
+    const StepIn si = step ? *step : StepIn{};
     if (two_pass) {
+        if (step) return hipErrorInvalidValue;
         // the chunk-max kernel stages the query rows for the chunk kernel when the caller has not
         dim3 grid((unsigned)ck.max_chunks, chains), block(CT);
         if (q_staged)
-            hipLaunchKernelGGL((chunk_max_kernel<D, KB, true>), grid, block, 0, s, g, t, q, ck.qd, ck.qok,
-                               len, ck, st);
+            hipExtLaunchKernelGGL((chunk_max_kernel<D, KB, true>), grid, block, 0, s, ev.start, nullptr,
+                                  0, g, t, q, ck.qd, ck.qok, len, ck, st);
         else
-            hipLaunchKernelGGL((chunk_max_kernel<D, KB, false>), grid, block, 0, s, g, t, q, ck.qd,
-                               ck.qok, len, ck, st);
+            hipExtLaunchKernelGGL((chunk_max_kernel<D, KB, false>), grid, block, 0, s, ev.start, nullptr,
+                                  0, g, t, q, ck.qd, ck.qok, len, ck, st);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
-        hipLaunchKernelGGL((chunk_kernel<D, KB, false, true>), grid, block, 0, s, g, t, q, ck.qd, ck.qok,
-                           out, len, ck, st);
+        hipExtLaunchKernelGGL((chunk_kernel<D, KB, false, true, false>), grid, block, 0, s, nullptr,
+                              ev.stop, 0, g, t, q, ck.qd, ck.qok, out, len, ck, st, si);
         return hipGetLastError();
     }
     dim3 grid((unsigned)ck.max_chunks * chains), block(CT);
-    if (q_staged)
-        hipLaunchKernelGGL((chunk_kernel<D, KB, true, true>), grid, block, 0, s, g, t, q, ck.qd, ck.qok,
-                           out, len, ck, st);
+    if (!step && !q_staged && stage_queries_first(g)) {
+        hipLaunchKernelGGL((qprep_kernel<D / 64>), dim3(chains), dim3(GF * 64), 0, s, g, t, q, ck.qd,
+                           ck.qok, st);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        q_staged = true;
+    }
+    if (step)
+        hipExtLaunchKernelGGL((chunk_kernel<D, KB, true, false, true>), grid, block, 0, s, ev.start,
+                              ev.stop, 0, g, t, q, ck.qd, ck.qok, out, len, ck, st, si);
+    else if (q_staged)
+        hipExtLaunchKernelGGL((chunk_kernel<D, KB, true, true, false>), grid, block, 0, s, ev.start,
+                              ev.stop, 0, g, t, q, ck.qd, ck.qok, out, len, ck, st, si);
     else
-        hipLaunchKernelGGL((chunk_kernel<D, KB, true, false>), grid, block, 0, s, g, t, q, ck.qd, ck.qok,
-                           out, len, ck, st);
+        hipExtLaunchKernelGGL((chunk_kernel<D, KB, true, false, false>), grid, block, 0, s, ev.start,
+                              ev.stop, 0, g, t, q, ck.qd, ck.qok, out, len, ck, st, si);
     return hipGetLastError();
 }
 
@@ -1263,7 +1380,7 @@ void chunked_query_area(const Geom &g, int64_t max_chunks, int64_t pool, void *s
 hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
                                  int32_t *out, const int64_t *len, void *scratch, int64_t max_chunks,
                                  int64_t pool, uint32_t call, int two_pass, bool q_staged,
-                                 DevStats *st) {
+                                 const StepIn *step, LaunchEv ev, DevStats *st) {
     const int64_t chains = (int64_t)g.batch * g.n_kv;
     if (max_chunks > HMAX || chains > 65535 || max_chunks * chains > 0x7fffffff)
         return hipErrorInvalidValue;
@@ -1272,7 +1389,7 @@ hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, 
     ck.ep = call % EPOCH_MASK + 1;     // 1 .. 2^14 - 1: zeroed scratch is never current
 #define INSITU_FAST(DD, KK)                                                          \
     if (g.d == DD && g.kb == KK)                                                     \
-        return launch_fast<DD, KK>(s, g, t, q, out, len, ck, two_pass, q_staged, st);
+        return launch_fast<DD, KK>(s, g, t, q, out, len, ck, two_pass, q_staged, step, ev, st);
     INSITU_FAST(64, 2)
     INSITU_FAST(64, 3)
     INSITU_FAST(64, 4)

@@ -33,15 +33,16 @@ __global__ void __launch_bounds__(64) attend_serial_kernel(Geom g, const Tables 
 }
 
 hipError_t launch_attend_serial(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
-                                int32_t *out, const int64_t *len, int two_pass, DevStats *st) {
+                                int32_t *out, const int64_t *len, int two_pass, LaunchEv ev,
+                                DevStats *st) {
     const int64_t blocks = (int64_t)g.batch * g.n_q;
     if (blocks <= 0) return hipSuccess;
     if (g.d <= 64)
-        hipLaunchKernelGGL(attend_serial_kernel<1>, dim3((unsigned)blocks), dim3(64), 0, s, g, t, q,
-                           out, len, two_pass, st);
+        hipExtLaunchKernelGGL(attend_serial_kernel<1>, dim3((unsigned)blocks), dim3(64), 0, s,
+                              ev.start, ev.stop, 0, g, t, q, out, len, two_pass, st);
     else
-        hipLaunchKernelGGL(attend_serial_kernel<2>, dim3((unsigned)blocks), dim3(64), 0, s, g, t, q,
-                           out, len, two_pass, st);
+        hipExtLaunchKernelGGL(attend_serial_kernel<2>, dim3((unsigned)blocks), dim3(64), 0, s,
+                              ev.start, ev.stop, 0, g, t, q, out, len, two_pass, st);
     return hipGetLastError();
 }
 

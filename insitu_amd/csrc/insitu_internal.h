@@ -6,6 +6,7 @@
 // computing something subtly different.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -53,6 +54,31 @@ struct Tables {
     int64_t vbnd[256];
     int32_t exp_table[256];   // rint(2^(-i/256) * 2^15), attention.py:106-108
     int64_t delta_max;        // attention.py:145-146
+    double kc_absmax;         // max |kc[i]|, for the exactness bound of the fp64 scores
+};
+
+// The sign diagonals of up to two rotation rounds, one 64-bit word per 64 channels.
+struct RotSigns {
+    uint64_t s0a, s0b, s1a, s1b;
+};
+
+inline RotSigns rot_signs(int rounds, const uint64_t (*signs)[2]) {
+    RotSigns sg;
+    sg.s0a = rounds > 0 ? signs[0][0] : 0;
+    sg.s0b = rounds > 0 ? signs[0][1] : 0;
+    sg.s1a = rounds > 1 ? signs[1][0] : 0;
+    sg.s1b = rounds > 1 ? signs[1][1] : 0;
+    return sg;
+}
+
+// The fused decode step's inputs to the chunked attend: the wire rows (batch,
+// heads, d) in Q8.16, the rotation, and the other half of the length double
+// buffer, which receives len + 1.
+struct StepIn {
+    const int32_t *qw, *kw, *vw;
+    RotSigns sg;
+    int32_t rounds;
+    int64_t *len_out;
 };
 
 // Device statistics; merged with atomics (AttentionStats.merge semantics).
@@ -139,26 +165,6 @@ __device__ __forceinline__ int64_t sext16(uint32_t v) {
     return (int64_t)(int16_t)(uint16_t)(v & 0xFFFFu);
 }
 
-// Wave-wide (64-lane) int64 sum, wrapping.
-__device__ __forceinline__ int64_t wave_sum64(int64_t v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v = wadd(v, __shfl_xor(v, o, 64));
-    return v;
-}
-
-__device__ __forceinline__ int64_t wave_max64(int64_t v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        int64_t w = __shfl_xor(v, o, 64);
-        v = w > v ? w : v;
-    }
-    return v;
-}
-
-__device__ __forceinline__ void stat_max(unsigned long long *p, int64_t v) {
-    atomicMax(p, (unsigned long long)(v < 0 ? -v : v));
-}
-
 }  // namespace insitu
 
 // Host-side internal API between translation units.
@@ -166,6 +172,13 @@ namespace insitu {
 
 struct LaunchErr {
     hipError_t e;
+};
+
+// The start/stop timing events of a launch sequence (null: untimed). They are
+// attached to the dispatches themselves (hipExtLaunchKernelGGL), so timing
+// adds no packets to the stream.
+struct LaunchEv {
+    hipEvent_t start = nullptr, stop = nullptr;
 };
 
 hipError_t launch_rotate(hipStream_t s, const int32_t *x, int32_t *y, int64_t n_vec, int d,
@@ -185,20 +198,26 @@ bool chunked_supported(const Geom &g, int64_t capacity);
 int64_t chunked_max_chunks(int64_t capacity);
 int64_t chunked_pool_slots(int64_t max_chunks);
 size_t chunked_scratch_bytes(const Geom &g, int64_t max_chunks, int64_t pool);
-// The fp64 query staging in the chunked attend's scratch (query.h): the fused
-// step's write kernel fills it, and the attend is then launched with
-// q_staged; otherwise the attend stages the caller's rotated int32 rows itself.
+// The fp64 query staging in the chunked attend's scratch (query.h): the step's
+// write kernel fills it, and the attend is then launched with q_staged;
+// otherwise the attend stages the caller's rotated int32 rows itself. With
+// step (sequential mode only), the attend is the whole decode step: len holds
+// the lengths before it, q is unused and the wire rows come in step.
 void chunked_query_area(const Geom &g, int64_t max_chunks, int64_t pool, void *scratch,
                         double **qd, int32_t **qok);
+// Whether insitu_step runs as one fused launch in sequential mode (the
+// register budget of the fused kernel allows it at d = 64).
+bool chunked_fused_step(const Geom &g);
 hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
                                  int32_t *out, const int64_t *len, void *scratch, int64_t max_chunks,
                                  int64_t pool, uint32_t call, int two_pass, bool q_staged,
-                                 DevStats *st);
+                                 const StepIn *step, LaunchEv ev, DevStats *st);
 hipError_t launch_step_write(hipStream_t s, const Geom &g, const Tables *t, const int32_t *qw,
                              const int32_t *kw, const int32_t *vw, int rounds,
                              const uint64_t (*signs)[2], int32_t *qr, double *qd, int32_t *qok,
                              const int64_t *len_in, int64_t *len_out, DevStats *st);
 hipError_t launch_attend_serial(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
-                                int32_t *out, const int64_t *len, int two_pass, DevStats *st);
+                                int32_t *out, const int64_t *len, int two_pass, LaunchEv ev,
+                                DevStats *st);
 
 }  // namespace insitu

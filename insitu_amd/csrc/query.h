@@ -46,11 +46,4 @@ __device__ __forceinline__ bool stage_query_head(const int32_t (&v)[CPL], int d,
     return (double)l1 * kc_absmax < DOT_LIMIT;
 }
 
-// max |c| over the 2^kb key centroids, as a double.
-__device__ __forceinline__ double key_centroid_absmax(const Tables *__restrict__ tabs, int kb) {
-    double m = 0.0;
-    for (int i = 0; i < (1 << kb); ++i) m = fmax(m, fabs((double)tabs->kc[i]));
-    return m;
-}
-
 }  // namespace insitu

@@ -1,0 +1,214 @@
+// The row codec shared by the write path and the fused decode step: the
+// randomized Hadamard rotation (ops/rotate.py:170-197, one wave per vector,
+// lane = channel, the FWHT butterflies as cross-lane xor shuffles), the norm
+// and threshold encoder (ops/quantize.py:164-196: wave reduction for sum(x^2),
+// exact isqrt, half-even requantize, strict '>' compares) and the row packing
+// into the plane layout (quantize.py:237-252, hw/ddr_layout.py:198-214).
+#pragma once
+
+#include "insitu_internal.h"
+#include "wave.h"
+
+namespace insitu {
+
+// Up to two channels per lane (d <= 128): channel lane and lane + 64.
+template <int CPL>
+__device__ __forceinline__ void fwht_wave(int64_t (&x)[CPL], int d) {
+    const int lane = threadIdx.x & 63;
+    const int hmax = d < 64 ? d : 64;
+    for (int h = 1; h < hmax; h <<= 1) {
+#pragma unroll
+        for (int k = 0; k < CPL; ++k) {
+            int64_t other = __shfl_xor(x[k], h, 64);
+            x[k] = (lane & h) ? (other - x[k]) : (x[k] + other);
+        }
+    }
+    if (CPL == 2 && d == 128) {
+        int64_t a = x[0], b = x[CPL - 1];
+        x[0] = a + b;
+        x[CPL - 1] = a - b;
+    }
+}
+
+__device__ __forceinline__ int64_t rot_scale(int64_t v, int d) {
+    // 1/sqrt(d): exact shift for even powers of two, else Q15 multiply (rotate.py:190-191).
+    switch (d) {
+        case 16: return v >> 2;
+        case 64: return v >> 3;
+        case 256: return v >> 4;
+        case 32: return (v * 5793) >> 15;
+        case 128: return (v * 2896) >> 15;
+        default: return v;
+    }
+}
+
+// One wave rotates the vector at x (d channels, lane = channel) into y, int32
+// as the cache and the attend consume it; values beyond int32 are counted as
+// range errors (the RTL flags them; rotate.py:170-197 leaves them unclamped).
+// load_vec + rotate_loaded let a kernel issue its other loads in between.
+template <int CPL>
+__device__ __forceinline__ void load_vec(const int32_t *__restrict__ x, int d, int32_t (&v)[CPL]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+        int ch = lane + 64 * k;
+        v[k] = (ch < d) ? x[ch] : 0;
+    }
+}
+
+// The rotation of a vector already in registers (see load_vec); y may alias v.
+// range_err may be null (values beyond int32 are then not counted).
+template <int CPL>
+__device__ __forceinline__ void rotate_loaded(const int32_t (&in)[CPL], int d, int rounds,
+                                              const RotSigns &sg, int32_t (&y)[CPL],
+                                              unsigned long long *range_err) {
+    const int lane = threadIdx.x & 63;
+    int64_t v[CPL];
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) v[k] = in[k];
+    for (int r = 0; r < rounds; ++r) {
+        uint64_t wa = r == 0 ? sg.s0a : sg.s1a, wb = r == 0 ? sg.s0b : sg.s1b;
+#pragma unroll
+        for (int k = 0; k < CPL; ++k) {
+            int ch = lane + 64 * k;
+            uint64_t w = ch < 64 ? wa : wb;
+            if ((w >> (ch & 63)) & 1) v[k] = -v[k];
+        }
+        fwht_wave<CPL>(v, d);
+#pragma unroll
+        for (int k = 0; k < CPL; ++k) v[k] = rot_scale(v[k], d);
+    }
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) {
+        int ch = lane + 64 * k;
+        if (range_err && ch < d && (v[k] < INT32_MIN || v[k] > INT32_MAX)) atomicAdd(range_err, 1ull);
+        y[k] = (int32_t)v[k];
+    }
+}
+
+template <int CPL>
+__device__ __forceinline__ void rotate_vec(const int32_t *__restrict__ x, int d, int rounds,
+                                           const RotSigns &sg, int32_t (&y)[CPL],
+                                           unsigned long long *range_err) {
+    int32_t v[CPL];
+    load_vec<CPL>(x, d, v);
+    rotate_loaded<CPL>(v, d, rounds, sg, y, range_err);
+}
+
+// isqrt (quantize.py:42-60): float seed, then corrected to r^2 <= a < (r+1)^2.
+__device__ __forceinline__ int64_t isqrt64(int64_t a) {
+    if (a <= 0) return 0;
+    int64_t r = (int64_t)sqrt((double)a);
+    while (r > 0 && r * r > a) --r;
+    while ((r + 1) * (r + 1) <= a) ++r;
+    return r;
+}
+
+// rshift(x, n, "even") for x >= 0 (fixed.py:83-88), n >= 1.
+__device__ __forceinline__ int64_t rshift_even(int64_t a, int n) {
+    if (n <= 0) return a << (-n);
+    int64_t half = int64_t(1) << (n - 1);
+    int64_t q = (a + half) >> n;
+    if ((a & ((int64_t(1) << n) - 1)) == half) q &= ~int64_t(1);
+    return q;
+}
+
+// _norm_wire: isqrt(sum x^2 // d) in Q16, half-even into Q(norm_frac), clamp int16.
+template <int CPL>
+__device__ __forceinline__ int64_t norm_wire(const int64_t (&x)[CPL], int d, int norm_frac) {
+    int64_t sq = 0;
+#pragma unroll
+    for (int k = 0; k < CPL; ++k) sq += x[k] * x[k];
+    sq = wave_sum_i64(sq);
+    int64_t mean = sq >= 0 ? sq / d : -((-sq + d - 1) / d);   // floor division
+    int64_t n = isqrt64(mean);
+    int64_t w = rshift_even(n, QK_FRAC - norm_frac);
+    if (w > 32767) w = 32767;
+    if (w < -32768) w = -32768;
+    return w;
+}
+
+// _encode_plane: #{i : (x << (norm_frac - 1)) > norm * b_i}.
+__device__ __forceinline__ int encode_one(int64_t x, int64_t norm, const int64_t *bnd, int n_b,
+                                          int norm_frac) {
+    int64_t xs = x << (CENT_FRAC + norm_frac - QK_FRAC);
+    int c = 0;
+    for (int i = 0; i < n_b; ++i) c += (xs > norm * bnd[i]) ? 1 : 0;
+    return c;
+}
+
+// The key and value boundaries into LDS, one per thread (the compare loops of
+// the encoder then read them without a memory round trip each). The caller
+// synchronises before the first read.
+__device__ __forceinline__ void stage_bounds(const Tables *__restrict__ tabs, const Geom &g,
+                                             int64_t (*bnd)[255]) {
+    const int nkb = (1 << g.kb) - 1, nvb = (1 << g.vb) - 1;
+    for (int i = threadIdx.x; i < nkb + nvb; i += blockDim.x) {
+        if (i < nkb)
+            bnd[0][i] = tabs->kbnd[i];
+        else
+            bnd[1][i - nkb] = tabs->vbnd[i - nkb];
+    }
+}
+
+// One wave encodes the field x (lane = channel): the norm, and the codes into
+// codes[0 .. d).
+template <int CPL>
+__device__ __forceinline__ int64_t encode_field(const int64_t (&x)[CPL], int d, int norm_frac,
+                                                const int64_t *__restrict__ bnd, int n_b,
+                                                uint8_t *codes) {
+    const int lane = threadIdx.x & 63;
+    const int64_t n = norm_wire<CPL>(x, d, norm_frac);
+#pragma unroll
+    for (int q = 0; q < CPL; ++q) {
+        int ch = lane + 64 * q;
+        if (ch < d) codes[ch] = (uint8_t)encode_one(x[q], n, bnd, n_b, norm_frac);
+    }
+    return n;
+}
+
+// Dword w (< row_bytes / 4) of a packed row from the codes in LDS and the
+// norms (quantize.py:237-252): dword w holds row bits [32w, 32w + 32); the key
+// field is d*kb bits, the value field d*vb bits, then k_norm | v_norm << 16.
+__device__ __forceinline__ uint32_t pack_row_word(const Geom &g, const uint8_t (*codes)[MAX_D],
+                                                  int64_t nk, int64_t nv, int lane) {
+    const int d = g.d;
+    const int kwords = g.key_bytes / 4, vwords = g.value_bytes / 4;
+    uint32_t word = 0;
+    if (lane < kwords + vwords) {
+        const int field = lane < kwords ? 0 : 1;
+        const int bits = field == 0 ? g.kb : g.vb;
+        const int w = field == 0 ? lane : lane - kwords;
+        const int bit0 = 32 * w;
+        const int c_first = bit0 / bits;
+        const int c_last = (bit0 + 31) / bits;
+        for (int c = c_first; c <= c_last && c < d; ++c) {
+            int64_t off = (int64_t)c * bits - bit0;   // may be negative for a straddling code
+            uint64_t cv = codes[field][c];
+            uint64_t placed = off >= 0 ? (cv << off) : (cv >> (-off));
+            word |= (uint32_t)(placed & 0xFFFFFFFFull);
+        }
+    } else {
+        word = (uint32_t)(nk & 0xFFFF) | ((uint32_t)(nv & 0xFFFF) << 16);
+    }
+    return word;
+}
+
+// Where dword w of the row of (sequence b, KV head h) at token pos lives in the
+// planes (hw/ddr_layout.py:198-214). Row byte 4w lies in exactly one plane,
+// because every plane boundary is a field boundary and fields are whole dwords.
+__device__ __forceinline__ uint32_t *row_word_ptr(const Geom &g, int b, int h, int64_t pos, int w) {
+    const int byte = 4 * w;
+    int p = 0;
+    while (p + 1 < g.n_planes && byte >= g.plane_lo[p + 1]) ++p;
+    return (uint32_t *)(plane_ptr(g, b, h, p) + pos * g.plane_w[p] + (byte - g.plane_lo[p]));
+}
+
+// One wave packs the row of (sequence b, KV head h) at token pos and stores it.
+__device__ __forceinline__ void pack_store_row(const Geom &g, const uint8_t (*codes)[MAX_D],
+                                               int64_t nk, int64_t nv, int b, int h, int64_t pos) {
+    const int lane = threadIdx.x & 63;
+    if (lane < g.row_bytes / 4) *row_word_ptr(g, b, h, pos, lane) = pack_row_word(g, codes, nk, nv, lane);
+}
+
+}  // namespace insitu

@@ -1,90 +1,17 @@
 // The write path: rotation, norm + threshold encode, row packing and the
-// plane-layout append; plus the small test hooks (qtab, exp LUT, finalize).
+// plane-layout append (the codec itself is row_codec.h); plus the small test
+// hooks (qtab, exp LUT, finalize).
 //
-// rotate   ops/rotate.py:170-197   one wave per vector, lane = channel; the
-//                                  FWHT butterflies are cross-lane xor shuffles
-// encode   ops/quantize.py:164-196 wave reduction for sum(x^2), exact isqrt,
-//                                  half-even requantize, strict '>' compares
 // append   cache/compressed.py:64-86 + quantize.py:237-252 + hw/ddr_layout.py:198-214
 #include "insitu_internal.h"
 #include "query.h"
+#include "row_codec.h"
 
 namespace insitu {
 
 // ---------------------------------------------------------------------------
 // rotation
 // ---------------------------------------------------------------------------
-
-// Up to two channels per lane (d <= 128): channel lane and lane + 64.
-template <int CPL>
-__device__ void fwht_wave(int64_t (&x)[CPL], int d) {
-    const int lane = threadIdx.x & 63;
-    const int hmax = d < 64 ? d : 64;
-    for (int h = 1; h < hmax; h <<= 1) {
-#pragma unroll
-        for (int k = 0; k < CPL; ++k) {
-            int64_t other = __shfl_xor(x[k], h, 64);
-            x[k] = (lane & h) ? (other - x[k]) : (x[k] + other);
-        }
-    }
-    if (CPL == 2 && d == 128) {
-        int64_t a = x[0], b = x[CPL - 1];
-        x[0] = a + b;
-        x[CPL - 1] = a - b;
-    }
-}
-
-__device__ __forceinline__ int64_t rot_scale(int64_t v, int d) {
-    // 1/sqrt(d): exact shift for even powers of two, else Q15 multiply (rotate.py:190-191).
-    switch (d) {
-        case 16: return v >> 2;
-        case 64: return v >> 3;
-        case 256: return v >> 4;
-        case 32: return (v * 5793) >> 15;
-        case 128: return (v * 2896) >> 15;
-        default: return v;
-    }
-}
-
-// The sign diagonals of up to two rounds, one 64-bit word per 64 channels.
-struct RotSigns {
-    uint64_t s0a, s0b, s1a, s1b;
-};
-
-// One wave rotates the vector at x (d channels) into y, int32 as the cache
-// and the attend consume it; values beyond int32 are counted as range errors
-// (the RTL flags them; rotate.py:170-197 leaves them unclamped).
-template <int CPL>
-__device__ __forceinline__ void rotate_vec(const int32_t *__restrict__ x, int d, int rounds,
-                                           const RotSigns &sg, int32_t (&y)[CPL],
-                                           unsigned long long *range_err) {
-    const int lane = threadIdx.x & 63;
-    int64_t v[CPL];
-#pragma unroll
-    for (int k = 0; k < CPL; ++k) {
-        int ch = lane + 64 * k;
-        v[k] = (ch < d) ? (int64_t)x[ch] : 0;
-    }
-    const uint64_t s0a = sg.s0a, s0b = sg.s0b, s1a = sg.s1a, s1b = sg.s1b;
-    for (int r = 0; r < rounds; ++r) {
-        uint64_t wa = r == 0 ? s0a : s1a, wb = r == 0 ? s0b : s1b;
-#pragma unroll
-        for (int k = 0; k < CPL; ++k) {
-            int ch = lane + 64 * k;
-            uint64_t w = ch < 64 ? wa : wb;
-            if ((w >> (ch & 63)) & 1) v[k] = -v[k];
-        }
-        fwht_wave<CPL>(v, d);
-#pragma unroll
-        for (int k = 0; k < CPL; ++k) v[k] = rot_scale(v[k], d);
-    }
-#pragma unroll
-    for (int k = 0; k < CPL; ++k) {
-        int ch = lane + 64 * k;
-        if (ch < d && (v[k] < INT32_MIN || v[k] > INT32_MAX)) atomicAdd(range_err, 1ull);
-        y[k] = (int32_t)v[k];
-    }
-}
 
 template <int CPL>
 __global__ void __launch_bounds__(64) rotate_kernel(const int32_t *__restrict__ x, int32_t *y,
@@ -102,14 +29,6 @@ __global__ void __launch_bounds__(64) rotate_kernel(const int32_t *__restrict__ 
     }
 }
 
-static RotSigns rot_signs(int rounds, const uint64_t (*signs)[2]) {
-    RotSigns sg;
-    sg.s0a = rounds > 0 ? signs[0][0] : 0;
-    sg.s0b = rounds > 0 ? signs[0][1] : 0;
-    sg.s1a = rounds > 1 ? signs[1][0] : 0;
-    sg.s1b = rounds > 1 ? signs[1][1] : 0;
-    return sg;
-}
 
 hipError_t launch_rotate(hipStream_t s, const int32_t *x, int32_t *y, int64_t n_vec, int d,
                          int rounds, const uint64_t (*signs)[2], unsigned long long *range_err) {
@@ -127,48 +46,6 @@ hipError_t launch_rotate(hipStream_t s, const int32_t *x, int32_t *y, int64_t n_
 // ---------------------------------------------------------------------------
 // norm + encode
 // ---------------------------------------------------------------------------
-
-// isqrt (quantize.py:42-60): float seed, then corrected to r^2 <= a < (r+1)^2.
-__device__ __forceinline__ int64_t isqrt64(int64_t a) {
-    if (a <= 0) return 0;
-    int64_t r = (int64_t)sqrt((double)a);
-    while (r > 0 && r * r > a) --r;
-    while ((r + 1) * (r + 1) <= a) ++r;
-    return r;
-}
-
-// rshift(x, n, "even") for x >= 0 (fixed.py:83-88), n >= 1.
-__device__ __forceinline__ int64_t rshift_even(int64_t a, int n) {
-    if (n <= 0) return a << (-n);
-    int64_t half = int64_t(1) << (n - 1);
-    int64_t q = (a + half) >> n;
-    if ((a & ((int64_t(1) << n) - 1)) == half) q &= ~int64_t(1);
-    return q;
-}
-
-// _norm_wire: isqrt(sum x^2 // d) in Q16, half-even into Q(norm_frac), clamp int16.
-template <int CPL>
-__device__ int64_t norm_wire(const int64_t (&x)[CPL], int d, int norm_frac) {
-    int64_t sq = 0;
-#pragma unroll
-    for (int k = 0; k < CPL; ++k) sq += x[k] * x[k];
-    sq = wave_sum64(sq);
-    int64_t mean = sq >= 0 ? sq / d : -((-sq + d - 1) / d);   // floor division
-    int64_t n = isqrt64(mean);
-    int64_t w = rshift_even(n, QK_FRAC - norm_frac);
-    if (w > 32767) w = 32767;
-    if (w < -32768) w = -32768;
-    return w;
-}
-
-// _encode_plane: #{i : (x << (norm_frac - 1)) > norm * b_i}.
-__device__ __forceinline__ int encode_one(int64_t x, int64_t norm, const int64_t *bnd, int n_b,
-                                          int norm_frac) {
-    int64_t xs = x << (CENT_FRAC + norm_frac - QK_FRAC);
-    int c = 0;
-    for (int i = 0; i < n_b; ++i) c += (xs > norm * bnd[i]) ? 1 : 0;
-    return c;
-}
 
 template <int CPL>
 __global__ void __launch_bounds__(64) encode_kernel(const int32_t *__restrict__ x, int64_t n_vec,
@@ -213,58 +90,6 @@ hipError_t launch_encode(hipStream_t s, const int32_t *x, int64_t n_vec, int d, 
 // append: one wave per (sequence, token, kv head) -> one packed row
 // ---------------------------------------------------------------------------
 
-// One wave encodes the field x (lane = channel): the norm, and the codes into
-// codes[0 .. d).
-template <int CPL>
-__device__ __forceinline__ int64_t encode_field(const int64_t (&x)[CPL], int d, int norm_frac,
-                                                const int64_t *__restrict__ bnd, int n_b,
-                                                uint8_t *codes) {
-    const int lane = threadIdx.x & 63;
-    const int64_t n = norm_wire<CPL>(x, d, norm_frac);
-#pragma unroll
-    for (int q = 0; q < CPL; ++q) {
-        int ch = lane + 64 * q;
-        if (ch < d) codes[ch] = (uint8_t)encode_one(x[q], n, bnd, n_b, norm_frac);
-    }
-    return n;
-}
-
-// One wave packs the row of (sequence b, KV head h) at token pos from the
-// codes in LDS and stores it into the planes. Dword w of the row holds row bits
-// [32w, 32w + 32): the key field is d*kb bits, the value field d*vb bits, then
-// k_norm | v_norm << 16. Row byte 4*lane lies in exactly one plane, because
-// every plane boundary is a field boundary and fields are whole dwords.
-__device__ __forceinline__ void pack_store_row(const Geom &g, const uint8_t (*codes)[MAX_D],
-                                               int64_t nk, int64_t nv, int b, int h, int64_t pos) {
-    const int lane = threadIdx.x & 63;
-    const int d = g.d;
-    const int kwords = g.key_bytes / 4, vwords = g.value_bytes / 4;
-    const int nwords = g.row_bytes / 4;
-    if (lane >= nwords) return;
-    uint32_t word = 0;
-    if (lane < kwords + vwords) {
-        const int field = lane < kwords ? 0 : 1;
-        const int bits = field == 0 ? g.kb : g.vb;
-        const int w = field == 0 ? lane : lane - kwords;
-        const int bit0 = 32 * w;
-        const int c_first = bit0 / bits;
-        const int c_last = (bit0 + 31) / bits;
-        for (int c = c_first; c <= c_last && c < d; ++c) {
-            int64_t off = (int64_t)c * bits - bit0;   // may be negative for a straddling code
-            uint64_t cv = codes[field][c];
-            uint64_t placed = off >= 0 ? (cv << off) : (cv >> (-off));
-            word |= (uint32_t)(placed & 0xFFFFFFFFull);
-        }
-    } else {
-        word = (uint32_t)(nk & 0xFFFF) | ((uint32_t)(nv & 0xFFFF) << 16);
-    }
-    const int byte = 4 * lane;
-    int p = 0;
-    while (p + 1 < g.n_planes && byte >= g.plane_lo[p + 1]) ++p;
-    uint8_t *dst = plane_ptr(g, b, h, p) + pos * g.plane_w[p] + (byte - g.plane_lo[p]);
-    *(uint32_t *)dst = word;
-}
-
 template <int CPL>
 __global__ void __launch_bounds__(64) append_kernel(Geom g, const Tables *__restrict__ tabs,
                                                     const int32_t *__restrict__ k,
@@ -273,8 +98,10 @@ __global__ void __launch_bounds__(64) append_kernel(Geom g, const Tables *__rest
                                                     int64_t *len_out, int seq_hi,
                                                     DevStats *st) {
     __shared__ uint8_t codes[2][MAX_D];
+    __shared__ int64_t bnd[2][255];
     const int lane = threadIdx.x;
     const int h = blockIdx.x % g.n_kv;
+    stage_bounds(tabs, g, bnd);
     const int t = (blockIdx.x / g.n_kv) % n_tok;
     const int b = seq_lo + blockIdx.x / (g.n_kv * n_tok);
     const int d = g.d;
@@ -293,6 +120,7 @@ __global__ void __launch_bounds__(64) append_kernel(Geom g, const Tables *__rest
         return;
     }
     const int64_t src = (((int64_t)(b - seq_lo) * n_tok + t) * g.n_kv + h) * d;
+    __syncthreads();
     int64_t nk, nv;
     {
         int64_t x[CPL];
@@ -301,7 +129,7 @@ __global__ void __launch_bounds__(64) append_kernel(Geom g, const Tables *__rest
             int ch = lane + 64 * q;
             x[q] = ch < d ? (int64_t)k[src + ch] : 0;
         }
-        nk = encode_field<CPL>(x, d, g.norm_frac, tabs->kbnd, (1 << g.kb) - 1, codes[0]);
+        nk = encode_field<CPL>(x, d, g.norm_frac, bnd[0], (1 << g.kb) - 1, codes[0]);
     }
     {
         int64_t x[CPL];
@@ -310,7 +138,7 @@ __global__ void __launch_bounds__(64) append_kernel(Geom g, const Tables *__rest
             int ch = lane + 64 * q;
             x[q] = ch < d ? (int64_t)v[src + ch] : 0;
         }
-        nv = encode_field<CPL>(x, d, g.norm_frac, tabs->vbnd, (1 << g.vb) - 1, codes[1]);
+        nv = encode_field<CPL>(x, d, g.norm_frac, bnd[1], (1 << g.vb) - 1, codes[1]);
     }
     __syncthreads();
     pack_store_row(g, codes, nk, nv, b, h, pos);
@@ -332,6 +160,7 @@ __global__ void __launch_bounds__((2 + MAX_G) * 64) step_write_kernel(
         int32_t *qr, double *qd, int32_t *qok, const int64_t *__restrict__ len_in, int64_t *len_out,
         DevStats *st) {
     __shared__ uint8_t codes[2][MAX_D];
+    __shared__ int64_t bnd[2][255];
     __shared__ int64_t norms[2];
     __shared__ int ok_s;
     const int lane = threadIdx.x & 63;
@@ -344,6 +173,7 @@ __global__ void __launch_bounds__((2 + MAX_G) * 64) step_write_kernel(
         for (int i = lane; i < g.batch; i += 64) len_out[i] = len_in[i] + 1;
     }
     if (threadIdx.x == 0) ok_s = 1;
+    stage_bounds(tabs, g, bnd);
     const int64_t pos = len_in[b];
     const bool room = pos < g.capacity;   // the host checks capacity first; this only guards memory
     __syncthreads();
@@ -355,8 +185,8 @@ __global__ void __launch_bounds__((2 + MAX_G) * 64) step_write_kernel(
 #pragma unroll
         for (int k = 0; k < CPL; ++k) x[k] = r[k];
         const int64_t n = wv == 0
-            ? encode_field<CPL>(x, d, g.norm_frac, tabs->kbnd, (1 << g.kb) - 1, codes[0])
-            : encode_field<CPL>(x, d, g.norm_frac, tabs->vbnd, (1 << g.vb) - 1, codes[1]);
+            ? encode_field<CPL>(x, d, g.norm_frac, bnd[0], (1 << g.kb) - 1, codes[0])
+            : encode_field<CPL>(x, d, g.norm_frac, bnd[1], (1 << g.vb) - 1, codes[1]);
         if (lane == 0) norms[wv] = n;
     } else if (wv < 2 + g.G) {
         const int qh = h * g.G + (wv - 2);
@@ -370,7 +200,7 @@ __global__ void __launch_bounds__((2 + MAX_G) * 64) step_write_kernel(
         }
         if (qd) {
             const bool ok = stage_query_head<CPL>(r, d, wv - 2, qd + (int64_t)chain * d * GF,
-                                                  key_centroid_absmax(tabs, g.kb), &st->range_errors);
+                                                  tabs->kc_absmax, &st->range_errors);
             if (lane == 0 && !ok) atomicAnd(&ok_s, 0);
         }
     }
