@@ -1274,14 +1274,16 @@ __global__ void __launch_bounds__(GF * 64) qprep_kernel(Geom g, const Tables *__
     if (threadIdx.x == 0) qok[chain] = ok_s;
 }
 
-// Whether a standalone sequential attend stages its query rows first (one
-// small launch) rather than every workgroup staging them in LDS. Read as
-// scalar FMA operands they keep the d = 128 chunk kernel within 128 VGPRs, two
-// workgroups per CU, where the LDS-query kernel needs about 150; at d = 64 both
-// fit, and the extra launch would only add its dispatch.
-static bool stage_queries_first(const Geom &g) { return g.d > 64; }
+// Whether a sequential attend reads staged query rows (a small launch first
+// when the caller has not staged them) rather than every workgroup staging
+// them in LDS. Read as scalar FMA operands they keep the d = 128 chunk kernel
+// within 128 VGPRs, two workgroups per CU, where the LDS-query kernel needs
+// about 150; at d = 64 both fit, and the extra launch would only add its
+// dispatch. The fused decode step is the LDS-query kernel, so it runs at d = 64.
+template <int D>
+constexpr bool stage_queries_first() { return D > 64; }
 
-bool chunked_fused_step(const Geom &g) { return !stage_queries_first(g); }
+bool chunked_fused_step(const Geom &g) { return g.d <= 64; }
 
 template <int D, int KB>
 static hipError_t launch_fast(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
@@ -1306,22 +1308,24 @@ static hipError_t launch_fast(hipStream_t s, const Geom &g, const Tables *t, con
         return hipGetLastError();
     }
     dim3 grid((unsigned)ck.max_chunks * chains), block(CT);
-    if (!step && !q_staged && stage_queries_first(g)) {
-        hipLaunchKernelGGL((qprep_kernel<D / 64>), dim3(chains), dim3(GF * 64), 0, s, g, t, q, ck.qd,
-                           ck.qok, st);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        q_staged = true;
-    }
-    if (step)
-        hipExtLaunchKernelGGL((chunk_kernel<D, KB, true, false, true>), grid, block, 0, s, ev.start,
-                              ev.stop, 0, g, t, q, ck.qd, ck.qok, out, len, ck, st, si);
-    else if (q_staged)
+    if constexpr (stage_queries_first<D>()) {
+        if (step) return hipErrorInvalidValue;
+        if (!q_staged) {
+            hipLaunchKernelGGL((qprep_kernel<D / 64>), dim3(chains), dim3(GF * 64), 0, s, g, t, q,
+                               ck.qd, ck.qok, st);
+            hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
         hipExtLaunchKernelGGL((chunk_kernel<D, KB, true, true, false>), grid, block, 0, s, ev.start,
                               ev.stop, 0, g, t, q, ck.qd, ck.qok, out, len, ck, st, si);
-    else
+    } else if (step) {
+        hipExtLaunchKernelGGL((chunk_kernel<D, KB, true, false, true>), grid, block, 0, s, ev.start,
+                              ev.stop, 0, g, t, q, ck.qd, ck.qok, out, len, ck, st, si);
+    } else {
+        // rotated int32 queries in q (staged ones as well: the write kernel also stores them there)
         hipExtLaunchKernelGGL((chunk_kernel<D, KB, true, false, false>), grid, block, 0, s, ev.start,
                               ev.stop, 0, g, t, q, ck.qd, ck.qok, out, len, ck, st, si);
+    }
     return hipGetLastError();
 }
 
