@@ -60,7 +60,6 @@ constexpr int SLOTS = 8;             // run slots of every chunk after chunk 0 (
 constexpr uint16_t RUN_EVENT = 0x8000;
 constexpr int FLAG_POOL = 1;         // run pool exhausted
 constexpr int FLAG_WIDE = 2;         // a run sum bound reached 2^31
-constexpr int FLAG_LOOKBACK = 4;     // the chunk's look-back timed out: its maximum before it is unknown
 // Look-back words: flag (bits 62-63) | call epoch (bits 48-61) | score - SCORE_LO
 // (bits 0-47). A word whose epoch is not the current call's is unpublished, so
 // the words never need resetting between calls.
@@ -72,17 +71,17 @@ constexpr int SPIN_LIMIT = 1 << 20;
 constexpr double MAGIC = 6755399441055744.0;   // 1.5 * 2^52
 constexpr int64_t MAGIC_BITS = 0x4338000000000000LL;
 
-// What a chunk publishes, per query head: w0 = n_seg | flags << 16 | call
-// epoch << 40. w0 is the flag the replaying workgroup polls: it goes out after
-// the head's run slots have completed. (Each chunk adds its score statistics to
-// the device counters itself.) A run slot
+// What a chunk publishes, per query head: w0 = n_seg | flags << 16 | score
+// overflows << 24 | call epoch << 40, w1 = max |score| (the statistics are per
+// chunk, all heads). w0 is the flag the replaying workgroup polls: it goes out
+// after the head's run slots and w1 have completed. A run slot
 // holds lf = L | f << 32 (L = sum of p < 2^26, f = the factor opening the run,
 // <= 2^15) and b = B, the bound on |run sum| (< 2^31 unless FLAG_WIDE is set).
 // Everything published between workgroups goes through relaxed agent-scope
 // atomics, which are coherent across the XCDs without writing back or
 // invalidating whole L2 caches.
 struct ChunkHdr {
-    uint64_t w0;
+    uint64_t w0, w1;
 };
 struct SegMeta {
     uint64_t lf, b;
@@ -114,6 +113,7 @@ struct Chunked {
     SegMeta *meta;                 // [chain][GF][pool]
     int32_t *segS;                 // [chain][GF][pool][d]
     unsigned int *done;            // [chain]  workgroups of the chain done with their runs
+    unsigned int *chain_fb;        // [chain]  the call's epoch: recompute this chain serially
     double *qd;                    // [chain][d][GF]  the group's query rows in fp64 (query.h)
     int32_t *qok;                  // [chain]  nonzero: every score of the group is exact in fp64
     int32_t max_chunks, pool;
@@ -691,12 +691,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             if (lane == 0) S.min_[wv] = m;
         }
         __syncthreads();
-        // The chunk's score statistics go straight to the device counters
-        // (fire and forget; the serial path counts its own when q is out of range).
-        if (ok && tid == 0) {
-            if (S.ovf) atomicAdd(&st->score_overflows, S.ovf);
-            atomicMax(&st->max_abs_score, S.mabs);
-        }
+        if (SEQ && S.lb_fail && tid == 0) pub32(&ck.chain_fb[chain], ck.ep);
 
         // -- phase 3: events and each head's candidate tokens listed in order ----
         // (the thread owns TPT consecutive tokens). Two exact shortcuts: a head
@@ -824,7 +819,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             n_ev = uni32(n_ev);
             const int n_seg = n_ev + 1;
             const int off = slot_base(chunk);
-            int flags = SEQ && S.lb_fail ? FLAG_LOOKBACK : 0;
+            int flags = 0;
             if (!own && n_seg > SLOTS) flags |= FLAG_POOL;
             if (!flags) {
                 int wi[CPL], wi1[CPL], sh[CPL];
@@ -970,16 +965,19 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             n_ev0 = n_ev;
             flags0 = flags;
             if (!own) {
-                // The header, once this head's run slots have completed.
+                // The header: w1 goes out with the run sums, w0 once this head's
+                // stores have completed.
                 ChunkHdr *hp = &ck.hdr[((int64_t)chain * ck.max_chunks + chunk) * GF + h];
+                if (lane == 0) pub64(&hp->w1, S.mabs);
                 stores_done();
                 if (lane == 0)
                     pub64(&hp->w0, (uint64_t)(uint32_t)n_seg | ((uint64_t)(uint32_t)flags << 16) |
-                                       ((uint64_t)ck.ep << 40));
+                                       ((uint64_t)(S.ovf & 0xFFFF) << 24) | ((uint64_t)ck.ep << 40));
             }
         } else if (!ok && wv < GF && !own) {
             // q failed its range check: the chain goes to the serial path, which counts its own
             ChunkHdr *hp = &ck.hdr[((int64_t)chain * ck.max_chunks + chunk) * GF + wv];
+            if (lane == 0) pub64(&hp->w1, 0);
             stores_done();
             if (lane == 0) pub64(&hp->w0, 1ull | ((uint64_t)ck.ep << 40));
         }
@@ -989,18 +987,6 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
         // first, so that when it is the last (its many rescale events make it the
         // slowest) its state never leaves the registers. Otherwise it publishes
         // the state after counting, and the last workgroup waits for its header.
-        // Chunk 0 is usually the last of its chain to finish, so its head waves
-        // read the other chunks' header words before it counts itself done: the
-        // loads overlap the counter's round trip.
-        constexpr int HPL = HMAX / 64;
-        uint64_t w0pre[HPL];
-#pragma unroll
-        for (int i = 0; i < HPL; ++i) {
-            const int c = 1 + lane + 64 * i;
-            w0pre[i] = 0;
-            if (own && wv < GF && 64 * i + 1 < nch)
-                w0pre[i] = get64(&ck.hdr[((int64_t)chain * ck.max_chunks + (c < nch ? c : 0)) * GF + wv].w0);
-        }
         if (new_row && wv == GF) stores_done();   // the new row is out before this chunk counts
         __syncthreads();
         if (tid == 0) {
@@ -1021,13 +1007,17 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             if (lane == 0) {
                 pub64(&ck.meta[base * ck.pool].lf, (uint64_t)(uint32_t)l0 | ((uint64_t)(uint32_t)n_ev0 << 32));
                 pub64(&ck.meta[base * ck.pool].b, (uint64_t)R0);
+                pub64(&hp->w1, ok ? S.mabs : 0ull);
             }
             stores_done();
-            if (lane == 0) pub64(&hp->w0, 1ull | ((uint64_t)(uint32_t)flags0 << 16) | ((uint64_t)ck.ep << 40));
+            if (lane == 0)
+                pub64(&hp->w0, 1ull | ((uint64_t)(uint32_t)flags0 << 16) |
+                                   ((uint64_t)(ok ? S.ovf & 0xFFFF : 0) << 24) | ((uint64_t)ck.ep << 40));
         }
         if (last) {
             const bool hw = wv < GF;              // wave h < GF replays query head h, lane = channel
             const int h = hw ? wv : 0;
+            constexpr int HPL = HMAX / 64;
             constexpr int SB = 64 / CPL;          // runs per batch
             AccT aw[CPL];
 #pragma unroll
@@ -1035,6 +1025,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             int64_t l = 0, R = 0;
             unsigned long long events = 0;
             bool fb = !ok;
+            const bool hdr_stats = ok;
             if (hw) {
                 const ChunkHdr *hdr = ck.hdr + (int64_t)chain * ck.max_chunks * GF + h;  // chunk c: hdr[c * GF]
                 const SegMeta *meta = ck.meta + ((int64_t)chain * GF + h) * ck.pool;
@@ -1045,6 +1036,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                 auto cur = [ep](uint64_t w) __attribute__((always_inline)) { return (uint32_t)(w >> 40) == ep; };
                 // Chunk 0's state: in the registers, or out of its slot once its header is up.
                 int flags = 0;
+                int64_t ovf = 0, mabs = 0;
                 if (own) {
 #pragma unroll
                     for (int k = 0; k < CPL; ++k) aw[k] = acc0[k];
@@ -1052,6 +1044,10 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     R = R0;
                     events = (unsigned long long)n_ev0;
                     flags = flags0;
+                    if (h == 0 && lane == 0) {
+                        ovf = (int64_t)S.ovf;
+                        mabs = (int64_t)S.mabs;
+                    }
                 } else if (!fb) {
                     uint64_t h0 = 0;
                     int spins = 0;
@@ -1072,31 +1068,24 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                         l = (int64_t)(uint32_t)lf;
                         events = lf >> 32;
                         R = (int64_t)get64(&meta[0].b);
+                        if (h == 0 && lane == 0) {
+                            ovf = (int64_t)((h0 >> 24) & 0xFFFF);
+                            mabs = (int64_t)get64(&hdr[0].w1);
+                        }
                     }
                 }
                 // The runs of chunks 1 .. nch-1 in order: one header load per lane and
                 // 64 chunks, then a scan of the run counts lists them by slot in LDS.
                 int total = 0;
-                // Chunk 0 read the words before the election; a word read too
-                // early (from an older call) is read again. Every other chunk has
-                // counted itself done, so its header is out. The loads are not
-                // branched around (lanes past the chain read chunk 0's word,
-                // unused), so that the compiler can count them precisely.
-                uint64_t w0[HPL];
+                uint64_t w0[HPL], w1[HPL];
 #pragma unroll
                 for (int i = 0; i < HPL; ++i) {
                     const int c = 1 + lane + 64 * i;
-                    w0[i] = own ? w0pre[i] : 0;
-                    if (!own && 64 * i + 1 < nch) w0[i] = get64(&hdr[(int64_t)(c < nch ? c : 0) * GF].w0);
-                }
-                bool stale = false;
-#pragma unroll
-                for (int i = 0; i < HPL; ++i) stale = stale || (1 + lane + 64 * i < nch && !cur(w0[i]));
-                if (__ballot(stale)) {
-#pragma unroll
-                    for (int i = 0; i < HPL; ++i) {
-                        const int c = 1 + lane + 64 * i;
-                        if (c < nch && !cur(w0[i])) w0[i] = get64(&hdr[(int64_t)c * GF].w0);
+                    w0[i] = 0;
+                    w1[i] = 0;
+                    if (c < nch) {
+                        w0[i] = get64(&hdr[(int64_t)c * GF].w0);
+                        if (h == 0) w1[i] = get64(&hdr[(int64_t)c * GF].w1);
                     }
                 }
 #pragma unroll
@@ -1107,6 +1096,8 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     if (in && !cur(w0[i])) flags |= FLAG_POOL;     // cannot happen: it counted itself done
                     const int n = in ? (int)(w0[i] & 0xFFFF) : 0;
                     flags |= in ? (int)((w0[i] >> 16) & 0xFF) : 0;
+                    ovf += in ? (int64_t)((w0[i] >> 24) & 0xFFFF) : 0;
+                    mabs = (int64_t)w1[i] > mabs ? (int64_t)w1[i] : mabs;
                     const int incl = (int)wave_scan_add32((uint32_t)n);
                     const int start = total + incl - n;
                     total += __builtin_amdgcn_readlane(incl, 63);
@@ -1114,8 +1105,17 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                         sl[start + j] = (uint16_t)((slot_base(c) + j) | (j ? RUN_EVENT : 0));
                 }
                 total = uni32(total);
-                // (a chunk whose look-back timed out carries FLAG_LOOKBACK)
                 if (__ballot(flags != 0) || total > NSEG) fb = true;
+                // A chunk whose look-back timed out flagged the chain before its header.
+                if (get32(&ck.chain_fb[chain]) == ep) fb = true;
+                if (h == 0) {
+                    ovf = wave_sum_i64(ovf);
+                    mabs = wave_max_i64(mabs);
+                    if (lane == 0) {
+                        S.ovf = (unsigned long long)ovf;
+                        S.mabs = (unsigned long long)mabs;
+                    }
+                }
                 fb = __builtin_amdgcn_readfirstlane((int)fb) != 0;
                 wave_sync();
                 // The walk, SB runs at a time. Lane i < SB holds run i's list entry
@@ -1205,11 +1205,11 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             int32_t *orow = out + ((int64_t)b * g.n_q + qh) * D;
             if (!hw) {
             } else if (fb) {
-                // The serial path counts score statistics only when the chunks did not.
+                // The serial path counts score statistics only when the headers did not.
                 // The fused step's new row came from another workgroup: acquire it.
                 if (STEP) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
                 const int32_t *qrow = STEP ? &S.qi[h][0] : q + ((int64_t)b * g.n_q + qh) * D;
-                serial_head<CPL, K::RS>(g, tabs, S.kc, S.vc, qrow, b, kvh, T, SEQ ? 0 : 1, !ok,
+                serial_head<CPL, K::RS>(g, tabs, S.kc, S.vc, qrow, b, kvh, T, SEQ ? 0 : 1, !hdr_stats,
                                         S.u.fb[h], orow, st);
                 if (lane == 0) atomicAdd(&st->serial_fallbacks, 1ull);
             } else {
@@ -1239,6 +1239,11 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     atomicMax(&st->max_abs_acc, (unsigned long long)amax);
                     if (aovf) atomicAdd(&st->acc_overflows, aovf);
                 }
+            }
+            // the chain's score statistics, once (from the headers when they cover it)
+            if (hw && h == 0 && lane == 0 && hdr_stats) {
+                if (S.ovf) atomicAdd(&st->score_overflows, S.ovf);
+                atomicMax(&st->max_abs_score, S.mabs);
             }
             if (tid == 0) ck.done[chain] = 0;    // every workgroup of the chain has counted itself
         }
@@ -1353,6 +1358,7 @@ static void carve(const Geom &g, int64_t max_chunks, int64_t pool, uint8_t *p, C
     c.meta = (SegMeta *)take(chains * GF * pool * sizeof(SegMeta));
     c.segS = (int32_t *)take(chains * GF * pool * g.d * sizeof(int32_t));
     c.done = (unsigned int *)take(chains * sizeof(unsigned int));
+    c.chain_fb = (unsigned int *)take(chains * sizeof(unsigned int));
     c.qd = (double *)take(chains * g.d * GF * sizeof(double));
     c.qok = (int32_t *)take(chains * sizeof(int32_t));
     c.max_chunks = (int32_t)max_chunks;
