@@ -15,10 +15,18 @@ consecutive steps never re-read a cache that is still resident.
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode online]
     python bench.py --copy-calibration      # a plain copy kernel of known size
     python bench.py --config c3|c4          # the larger configurations, attend only
+    python bench.py --config c1             # config 1 in full, every step checked
 
 C3: batch 64, one layer, per-sequence contexts uniform in
 [1024, 8192] from seed 3, one attend launch over the whole batch; 3 caches
 (more than the 256 MB Infinity Cache in total) rotate between steps.
+C1: all 16 layers of a Llama-3.2-1B-shape block, batch 1,
+4,096 sequential decode steps from an empty cache, each step one insitu_step
+(rotate, append, attend) per layer; layer l draws its q/k/v from its own
+seeded stream (seed 1000 + l, as config 0). Every step of every layer is then
+compared with the oracle's online softmax over rows 0 .. t, and every cache
+byte with the oracle's packed rows. It is a parity run with its timing, not
+the headline line.
 C4: Llama-3-8B shape (32 query heads, 8 KV heads, d=128,
 3-bit K and V), batch 16, ctx 131,072, 32 layers: one step is the 32 layers'
 attends, over a 53.7 GB resident cache. The k/v of one sequence (seeded, 1%
@@ -54,7 +62,9 @@ def _args():
     ap.add_argument("--ctx", type=int, default=CTX)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
-    ap.add_argument("--config", default="c2", choices=["c2", "c3", "c4"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4"])
+    ap.add_argument("--c1-layers", type=int, default=16)
+    ap.add_argument("--c1-steps", type=int, default=4096)
     return ap.parse_args()
 
 
@@ -231,6 +241,90 @@ def bench_scale(a) -> int:
     return 0
 
 
+def bench_c1(a) -> int:
+    """Config 1 in full: 16 layers x 4,096 decode steps from empty, every step checked."""
+    import concurrent.futures
+    import ctypes
+
+    import torch
+
+    from insitu_amd import QuantConfig, _lib
+    from insitu_amd.cache import CompressedCache
+    from insitu_amd.runtime import default_context, ptr
+    from insitu_amd.workload import Workload
+    from oracle import native
+    from oracle.quantize import Format, encode, pack
+    from oracle.rotate import rotate, signs_from_seed
+
+    L, S = a.c1_layers, a.c1_steps
+    ctx = default_context(0)
+    quant = QuantConfig(key_bits=4, value_bits=2)
+    fmt = Format()
+    wire = [Workload(seed=1000 + l).steps(S) for l in range(L)]
+    caches = [CompressedCache(N_KV, D, S, quant, batch=1, n_q_heads=N_Q, ctx=ctx) for _ in range(L)]
+    dev = [tuple(ctx.to_device(x[0], torch.int32) for x in w) for w in wire]
+    outs = torch.empty((L, S, N_Q, D), dtype=torch.int32, device=ctx.torch_device)
+    lib = ctx.lib
+    mode = _lib.MODES[a.mode]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for t in range(S):
+        for l in range(L):
+            qd, kd, vd = dev[l]
+            _lib.check(lib.insitu_step(caches[l].handle, ptr(qd[t]), ptr(kd[t]), ptr(vd[t]),
+                                       ptr(outs[l, t]), mode, None))
+        if t % 512 == 511:
+            torch.cuda.synchronize()
+            print(f"c1: {t + 1} of {S} steps on the GPU", file=sys.stderr, flush=True)
+    torch.cuda.synchronize()
+    gpu_s = time.perf_counter() - t0
+    got = outs.cpu().numpy()
+    bufs = [c.buf for c in caches]
+
+    sg = signs_from_seed(D, 0, 1)
+
+    def check(l):
+        q, k, v = (np.asarray(x[0], dtype=np.int64) for x in wire[l])
+        qr = rotate(q.reshape(-1, D), sg).reshape(S, N_Q, D)
+        kr = rotate(k.reshape(-1, D), sg).reshape(S, N_KV, D)
+        vr = rotate(v.reshape(-1, D), sg).reshape(S, N_KV, D)
+        heads = [encode(kr[:, h], vr[:, h], fmt) for h in range(N_KV)]
+        want = native.decode_steps(qr, heads, fmt)
+        bad_steps = np.nonzero((got[l] != want).reshape(S, -1).any(axis=1))[0]
+        rows = np.stack([pack(hd, fmt) for hd in heads], axis=1)
+        return l, bad_steps, bool(np.array_equal(bufs[l][:S], rows))
+
+    workers = max(1, min(16, len(os.sched_getaffinity(0))))
+    t1 = time.perf_counter()
+    with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as ex:
+        results = list(ex.map(check, range(L)))
+    cpu_s = time.perf_counter() - t1
+    mism = {l: bs[:5].tolist() for l, bs, _ in results if len(bs)}
+    cache_bad = [l for l, _, ok in results if not ok]
+    rows_scanned = N_KV * L * S * (S + 1) // 2
+    res = {
+        "metric": "config-1 parity: every decode step of every layer equal to the oracle",
+        "value": int(sum(S - len(bs) for _, bs, _ in results)),
+        "unit": "steps bit-exact",
+        "steps_total": L * S,
+        "mismatched_steps_by_layer": mism,
+        "cache_bytes_mismatched_layers": cache_bad,
+        "n_gpus": 1,
+        "higher_is_better": True,
+        "dtype": "int64",
+        "data": "synthetic (seeded N(0,1) q/k/v with 4 outlier channels x8 per head, Q8.16; seed 1000 + layer)",
+        "config": {"workload": f"C1: {L} Llama-3.2-1B-shape layers, batch 1, {S} sequential decode steps "
+                               f"from an empty cache, insitu_step per layer and step", "mode": a.mode},
+        "gpu_s": round(gpu_s, 3),
+        "us_per_layer_step": round(gpu_s / (L * S) * 1e6, 2),
+        "scan_gb": round(rows_scanned * ROW / 1e9, 3),
+        "cpu_check_s": round(cpu_s, 1),
+        "cpu_check": f"oracle/c orc_decode_steps per layer on {workers} threads",
+    }
+    print(json.dumps(res))
+    return 0 if not mism and not cache_bad else 1
+
+
 def _kv_only(wl, n):
     """k and v (1, n, Hkv, d) of the workload's distribution, without q."""
     from insitu_amd.workload import to_fixed
@@ -248,6 +342,8 @@ def main() -> int:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
               f"(asked for --gpus {a.gpus}); run with --gpus 1", file=sys.stderr)
         return 2
+    if a.config == "c1":
+        return bench_c1(a)
     if a.config != "c2":
         return bench_scale(a)
     import torch

@@ -9,6 +9,7 @@
  * uint8 per channel, norms as int64.
  */
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 typedef struct {
@@ -138,6 +139,7 @@ void orc_attend_online(const orc_fmt *f, const orc_exp *e, int32_t G, const int6
             int64_t p = orc_exp_eval(e, mg - stt);
             lg = wadd(lg, p);
             int64_t w = wmul(v_norm[t], p);
+            if (w == 0) continue;        /* every term floor(0 * c / 2^23) is 0 */
             const uint8_t *vcode = v_idx + t * d;
             for (int32_t j = 0; j < d; ++j) {
                 int64_t v = wadd(a[j], asr(wmul(w, vc[vcode[j]]), f->acc_shift));
@@ -186,4 +188,38 @@ void orc_attend_two_pass(const orc_fmt *f, const orc_exp *e, int32_t G, const in
         l[g] = lg;
     }
     orc_finalize(f, G, d, acc, l, out, 0, 0);
+}
+
+/* The config-1 check: one layer's sequential decode from an empty cache
+ * (kernel.py:271-345, the token attends to itself). Step t attends its rotated
+ * query rows q[t] (n_kv groups of G rows of d) over rows 0 .. t of each KV
+ * head, exactly as orc_attend_online. k_idx/v_idx are (n_kv, cap, d) codes,
+ * k_norm/v_norm (n_kv, cap); out is (steps, n_kv, G, d). Returns 0, or -1 when
+ * scratch cannot be allocated. */
+int orc_decode_steps(const orc_fmt *f, const orc_exp *e, int32_t n_kv, int32_t G, int64_t steps,
+                     int64_t cap, const int64_t *q, const uint8_t *k_idx, const int64_t *k_norm,
+                     const uint8_t *v_idx, const int64_t *v_norm, const int64_t *kc,
+                     const int64_t *vc, int64_t *out) {
+    const int32_t d = f->d;
+    if (steps > cap) return -1;
+    int64_t *s = (int64_t *)malloc(sizeof(int64_t) * (size_t)G * (size_t)(steps > 0 ? steps : 1));
+    int64_t *acc = (int64_t *)malloc(sizeof(int64_t) * (size_t)G * (size_t)d);
+    int64_t *l = (int64_t *)malloc(sizeof(int64_t) * (size_t)G);
+    int64_t *m = (int64_t *)malloc(sizeof(int64_t) * (size_t)G);
+    int rc = (s && acc && l && m) ? 0 : -1;
+    for (int64_t t = 0; t < steps && rc == 0; ++t) {
+        for (int32_t h = 0; h < n_kv; ++h) {
+            orc_stats st;
+            memset(&st, 0, sizeof st);
+            const int64_t qo = (t * n_kv + h) * (int64_t)G * d;
+            orc_attend_online(f, e, G, q + qo, t + 1, k_idx + (int64_t)h * cap * d, k_norm + (int64_t)h * cap,
+                              v_idx + (int64_t)h * cap * d, v_norm + (int64_t)h * cap, kc, vc, s, acc, l,
+                              m, out + qo, &st);
+        }
+    }
+    free(s);
+    free(acc);
+    free(l);
+    free(m);
+    return rc;
 }

@@ -166,3 +166,35 @@ def finalize(acc, l, fmt: Format):
     lib().orc_finalize(ctypes.byref(f), rows, d, _p(acc, _I64P), _p(l, _I64P), _p(out, _I64P),
                        _p(r, _I64P), _p(sh, _I64P))
     return out, r, sh
+
+
+def decode_steps(q_rot_steps, kv_heads, fmt: Format) -> np.ndarray:
+    """One layer's sequential decode from an empty cache, every step at once.
+
+    q_rot_steps: (steps, n_kv * G, d) rotated query rows; kv_heads: one
+    CompressedKV per KV head holding at least `steps` rows (row t is step t's
+    own token). Step t attends over rows 0 .. t (kernel.py:271-345: the token
+    attends to itself), as attend_online does. Returns (steps, n_kv * G, d).
+    """
+    q = np.ascontiguousarray(q_rot_steps, dtype=np.int64)
+    steps, rows, d = q.shape
+    n_kv = len(kv_heads)
+    G = rows // n_kv
+    cap = kv_heads[0].k_idx.shape[0]
+    ki = np.ascontiguousarray(np.stack([kv.k_idx for kv in kv_heads]), dtype=np.uint8)
+    kn = np.ascontiguousarray(np.stack([kv.k_norm for kv in kv_heads]), dtype=np.int64)
+    vi = np.ascontiguousarray(np.stack([kv.v_idx for kv in kv_heads]), dtype=np.uint8)
+    vn = np.ascontiguousarray(np.stack([kv.v_norm for kv in kv_heads]), dtype=np.int64)
+    kc, _, vc, _ = fmt.codebooks()
+    kc = np.ascontiguousarray(kc, dtype=np.int64)
+    vc = np.ascontiguousarray(vc, dtype=np.int64)
+    out = np.empty_like(q)
+    f = _fmt(fmt)
+    e = _exp(fmt)
+    rc = lib().orc_decode_steps(ctypes.byref(f), ctypes.byref(e), n_kv, G, ctypes.c_int64(steps),
+                                ctypes.c_int64(cap), _p(q, _I64P), _p(ki, _U8P), _p(kn, _I64P),
+                                _p(vi, _U8P), _p(vn, _I64P), _p(kc, _I64P), _p(vc, _I64P),
+                                _p(out, _I64P))
+    if rc:
+        raise MemoryError("orc_decode_steps: no scratch or steps > cache rows")
+    return out

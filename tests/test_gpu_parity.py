@@ -297,6 +297,74 @@ def test_sequential_decode_from_empty_matches_the_oracle_every_step(ctx):
     np.testing.assert_array_equal(blk.cache.buf, host.buf[:steps])
 
 
+def test_config0_one_decode_step_at_ctx_512(ctx):
+    """Config 0 exactly: Llama-3.2-1B shape, seed 0, 511 cached tokens, then one
+    decode step (rotate, append, attend) at context 512, against the numpy
+    per-token loop over all 8 KV groups."""
+    from insitu_amd import ModelConfig, QuantConfig
+    from insitu_amd.block import AttentionBlock
+    from insitu_amd.workload import Workload
+
+    n = 512
+    q, k, v = Workload(seed=0).steps(n)
+    blk = AttentionBlock(ModelConfig.llama32_1b(), QuantConfig(key_bits=4, value_bits=2),
+                         capacity=n, ctx=ctx)
+    sg = signs_from_seed(64, 0, 1)
+    kr, vr = rotate(k[0], sg), rotate(v[0], sg)
+    blk.cache.append_rotated(kr[:n - 1], vr[:n - 1])
+    out = blk.step(q[:, n - 1], k[:, n - 1], v[:, n - 1]).cpu().numpy()[0]
+    host = Cache(8, n, FMT)
+    host.append_rotated(kr, vr)
+    qr = rotate(q[0, n - 1], sg)
+    want = np.concatenate([attend_online(qr[4 * h:4 * h + 4], host.view(h), FMT)[0]
+                           for h in range(8)]).reshape(-1)
+    np.testing.assert_array_equal(out, want)
+    np.testing.assert_array_equal(blk.cache.buf, host.buf)
+
+
+@pytest.mark.parametrize("mode", ["online", "two_pass"])
+def test_config1_layers_from_empty_every_step_and_every_cache_byte(ctx, mode):
+    """Config 1 at reduced size: 2 layers x 1,100 decode steps from an empty cache
+    (past one 1,024-token chunk), every step of every layer against the C
+    oracle's per-token loop over rows 0 .. t, then every cache byte."""
+    import torch
+
+    from insitu_amd import _lib
+    from insitu_amd.runtime import ptr
+    from insitu_amd.workload import Workload
+
+    L, S = 2, 1100
+    wire = [Workload(seed=1000 + l).steps(S) for l in range(L)]
+    caches = [_cache(ctx, S) for _ in range(L)]
+    dev = [tuple(ctx.to_device(x[0], torch.int32) for x in w) for w in wire]
+    outs = torch.empty((L, S, 32, 64), dtype=torch.int32, device=ctx.torch_device)
+    for t in range(S):
+        for l in range(L):
+            qd, kd, vd = dev[l]
+            _lib.check(ctx.lib.insitu_step(caches[l].handle, ptr(qd[t]), ptr(kd[t]), ptr(vd[t]),
+                                           ptr(outs[l, t]), _lib.MODES[mode], None))
+    got = outs.cpu().numpy()
+    sg = signs_from_seed(64, 0, 1)
+    for l in range(L):
+        q, k, v = (np.asarray(x[0], dtype=np.int64) for x in wire[l])
+        qr = rotate(q.reshape(-1, 64), sg).reshape(S, 32, 64)
+        kr = rotate(k.reshape(-1, 64), sg).reshape(S, 8, 64)
+        vr = rotate(v.reshape(-1, 64), sg).reshape(S, 8, 64)
+        heads = [encode(kr[:, h], vr[:, h], FMT) for h in range(8)]
+        if mode == "online":
+            want = native.decode_steps(qr, heads, FMT)
+        else:   # two-pass: spot steps (the C checker walks the online order)
+            want = got[l].copy()
+            for t in (0, 1, 511, 1023, 1024, S - 1):
+                want[t] = np.concatenate([native.attend_two_pass(qr[t, 4 * h:4 * h + 4],
+                                                                 heads[h].select(slice(0, t + 1)), FMT)[0]
+                                          for h in range(8)])
+        bad = np.nonzero((got[l] != want).reshape(S, -1).any(axis=1))[0]
+        assert bad.size == 0, f"layer {l}: steps {bad[:10].tolist()} differ"
+        rows = np.stack([pack(hd, FMT) for hd in heads], axis=1)
+        np.testing.assert_array_equal(caches[l].buf, rows, err_msg=f"layer {l} cache bytes")
+
+
 # -- the chunked kernels: their own edge cases --------------------------------------
 
 def _host_reference(k, v, q, f=FMT, two_pass=False):

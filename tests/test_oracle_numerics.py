@@ -235,3 +235,17 @@ def test_native_oracle_equals_numpy_oracle():
             assert a[1] == b[1]
     d = np.arange(0, 800000, 13)
     np.testing.assert_array_equal(native.exp_lut(d, FMT), ExpLut(FMT)(d))
+
+
+def test_native_decode_steps_equal_the_per_token_loop_step_by_step():
+    """The config-1 checker: step t attends rows 0 .. t, each step as attend_online does."""
+    rng = np.random.default_rng(12)
+    steps, n_kv = 40, 2
+    heads = [_random_kv(rng, steps, FMT) for _ in range(n_kv)]
+    q = rng.integers(-(1 << 22), 1 << 22, size=(steps, 4 * n_kv, FMT.d))
+    q[5] = 0
+    got = native.decode_steps(q, heads, FMT)
+    for t in (0, 1, 5, 17, steps - 1):
+        for h in range(n_kv):
+            want, _ = attend_online(q[t, 4 * h:4 * h + 4], heads[h].select(slice(0, t + 1)), FMT)
+            np.testing.assert_array_equal(got[t, 4 * h:4 * h + 4], want, err_msg=f"step {t} head {h}")
