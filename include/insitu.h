@@ -162,6 +162,16 @@ int insitu_append_seq(insitu_cache *cache, int32_t seq, const int32_t *k_rot_dev
 int insitu_attend(insitu_cache *cache, const int32_t *q_rot_dev, int32_t *out_dev, int32_t mode,
                   insitu_stats *stats_host);
 
+/* A prefill's queries against one sequence's cache (attend_online_batch,
+ * ops/attention.py:794-871, in SEQUENTIAL mode; attend_causal_batch, :517-670, in
+ * TWO_PASS mode): query i (i < n_q) attends rows 0 .. base + i, exactly as a
+ * decode step would (the prompt's rows are appended first). q_rot_dev int32
+ * (n_q, n_q_heads, d) rotated; out_dev int32 (n_q, n_q_heads, d) Q16.
+ * EBADLEN when base + n_q exceeds the sequence's length. stats_host may be NULL. */
+int insitu_attend_causal(insitu_cache *cache, int32_t seq, int64_t base, int64_t n_q,
+                         const int32_t *q_rot_dev, int32_t *out_dev, int32_t mode,
+                         insitu_stats *stats_host);
+
 /* One decode step from the wire (CMD_STEP, host/attn_proto.py:65-72; kernel.py:256-353):
  * q/k/v_dev int32 Q8.16 (batch, heads, d) -> rotate -> append -> attend -> out_dev. */
 int insitu_step(insitu_cache *cache, const int32_t *q_dev, const int32_t *k_dev,

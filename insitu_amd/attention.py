@@ -97,3 +97,50 @@ class CompressedAttention:
     def attend_two_pass(self, q_rot, kv_head: int, seq: int = 0):
         """attention.py:429-449 for one KV group."""
         return self._group(q_rot, kv_head, seq, "two_pass")
+
+    # -- prefill: every query of a prompt at once (attention.py:517-871) --------
+
+    def attend_prefill(self, q_rot, base: int = 0, mode: str = "online", seq: int = 0, out=None,
+                       stats: bool = True):
+        """q_rot (n_q, n_q_heads, d) rotated: query i attends rows 0 .. base + i of
+        sequence `seq` (its own row included; the prompt's rows are appended
+        first). mode "online" is attend_online_batch (attention.py:794-871),
+        "two_pass" attend_causal_batch (:517-670), "serial" the token loop.
+        Returns (out torch int32 (n_q, n_q_heads, d), AttentionStats or None)."""
+        import torch
+        c = self.cache
+        q = self.ctx.to_device(q_rot, torch.int32)
+        if q.dim() != 3 or q.shape[1:] != (c.n_q_heads, c.head_dim):
+            raise ValueError(f"q_rot must be (n_q, {c.n_q_heads}, {c.head_dim}), got {tuple(q.shape)}")
+        q = q.contiguous()
+        if out is None:
+            out = torch.empty_like(q)
+        st = _lib.Stats() if stats else None
+        _lib.check(self.ctx.lib.insitu_attend_causal(c.handle, seq, base, q.shape[0], ptr(q), ptr(out),
+                                                     _lib.MODES[mode],
+                                                     ctypes.byref(st) if st is not None else None))
+        self._keep = q
+        return out, (AttentionStats.from_c(st) if st is not None else None)
+
+    def _group_batch(self, q_rot, kv_head: int, base: int, seq: int, mode: str):
+        c = self.cache
+        g = c.n_q_heads // c.n_kv_heads
+        qg = np.asarray(q_rot, dtype=np.int64)
+        if qg.ndim == 2:
+            qg = qg[:, None, :]
+        if qg.shape[1:] != (g, c.head_dim):
+            raise ValueError(f"expected (n_q, {g}, {c.head_dim}) for one KV group, got {qg.shape}")
+        q = np.zeros((qg.shape[0], c.n_q_heads, c.head_dim), dtype=np.int32)
+        q[:, kv_head * g:(kv_head + 1) * g] = qg
+        out, st = self.attend_prefill(q, base, mode, seq)
+        res = out[:, kv_head * g:(kv_head + 1) * g].cpu().numpy().astype(np.int64)
+        return res.reshape(np.shape(q_rot)[:-1] + (c.head_dim,)), st
+
+    def attend_causal_batch(self, q_rot, kv_head: int, base: int = 0, seq: int = 0):
+        """attention.py:517-670 for one KV group: q_rot (n_q, G, d); query i
+        attends rows 0 .. base + i by attend_two_pass. -> (out, stats)."""
+        return self._group_batch(q_rot, kv_head, base, seq, "two_pass")
+
+    def attend_online_batch(self, q_rot, kv_head: int, base: int = 0, seq: int = 0):
+        """attention.py:794-871 for one KV group, by attend_online."""
+        return self._group_batch(q_rot, kv_head, base, seq, "online")

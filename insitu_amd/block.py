@@ -9,7 +9,10 @@ AttentionBlock follows the pipeline order of AttentionKernel.forward
     merge_heads           kernel.py:352-353, ops/project.py:67-74
 
 It is one fused C call per decode step (insitu_step), the counterpart of
-the FPGA's CMD_STEP (host/attn_proto.py:65-72).
+the FPGA's CMD_STEP (host/attn_proto.py:65-72). A prompt of several tokens
+(kernel.py:316-332) rotates and appends all its rows, then attends every
+query at once (insitu_attend_causal: attend_online_batch in online mode,
+attend_causal_batch in two-pass mode), bit-identical to the token loop.
 """
 
 from __future__ import annotations
@@ -68,14 +71,39 @@ class AttentionBlock:
         self.last_stats = AttentionStats.from_c(st) if st is not None else None
         return out.reshape(self.batch, m.num_heads * m.head_dim)
 
-    def forward_seam(self, qi, ki, vi) -> np.ndarray:
-        """batch == 1: (tokens, heads, d) wire tensors, one decode step per token.
+    def prefill(self, qi, ki, vi, *, stats: bool = True):
+        """batch == 1, a prompt of n tokens: qi (n, num_heads, d), ki/vi
+        (n, num_kv_heads, d) wire Q8.16. Rotates all three, appends the n rows,
+        then query t attends rows 0 .. base + t (kernel.py:316-332). Returns
+        (n, num_heads * d) Q16, a torch int32 tensor."""
+        import torch
+        m = self.model
+        if self.batch != 1:
+            raise ValueError("prefill drives a batch-1 block")
+        q = self.ctx.to_device(qi, torch.int32)
+        n = int(q.shape[0])
+        q = q.reshape(n, m.num_heads, m.head_dim)
+        k = self.ctx.to_device(ki, torch.int32).reshape(n, m.num_kv_heads, m.head_dim)
+        v = self.ctx.to_device(vi, torch.int32).reshape(n, m.num_kv_heads, m.head_dim)
+        base = self.cache.length
+        qr = self.rotation.apply(q, self.ctx)
+        self.cache.append_rotated(self.rotation.apply(k, self.ctx), self.rotation.apply(v, self.ctx))
+        out, st = self.attn.attend_prefill(qr, base, self.softmax, stats=stats)
+        self.last_stats = st
+        return out.reshape(n, m.num_heads * m.head_dim)
 
-        Returns (tokens, num_heads * d) int64, the `out` tap of kernel.py:353.
+    def forward_seam(self, qi, ki, vi, *, force_token_loop: bool = False) -> np.ndarray:
+        """batch == 1: (tokens, heads, d) wire tensors.
+
+        Several tokens go through prefill (kernel.py:316-332), one token (or
+        force_token_loop, kernel.py:333-341) through decode steps. Returns
+        (tokens, num_heads * d) int64, the `out` tap of kernel.py:353.
         """
         qi, ki, vi = (np.asarray(a) for a in (qi, ki, vi))
         if self.batch != 1:
             raise ValueError("forward_seam drives a batch-1 block")
+        if qi.shape[0] > 1 and not force_token_loop:
+            return self.prefill(qi, ki, vi).cpu().numpy().astype(np.int64)
         outs = [self.step(qi[t][None], ki[t][None], vi[t][None]).cpu().numpy()
                 for t in range(qi.shape[0])]
         return np.concatenate(outs, axis=0).astype(np.int64)

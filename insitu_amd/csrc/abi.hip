@@ -106,6 +106,9 @@ struct insitu_cache {
     void *chunk_scratch = nullptr;        // run sums and counters of the chunked attend
     int64_t max_chunks = 0, pool = 0;
     uint32_t calls = 0;                   // chunked attends so far: tags this call's flags
+    // prefill (insitu_attend_causal): scratch for PREFILL_QB virtual sequences, their lengths
+    void *prefill_scratch = nullptr;
+    int64_t *prefill_len = nullptr;
 };
 
 namespace {
@@ -424,6 +427,8 @@ int insitu_cache_destroy(insitu_cache *k) {
     if (k->stats) hipFree(k->stats);
     if (k->wire_scratch) hipFree(k->wire_scratch);
     if (k->chunk_scratch) hipFree(k->chunk_scratch);
+    if (k->prefill_scratch) hipFree(k->prefill_scratch);
+    if (k->prefill_len) hipFree(k->prefill_len);
     delete k;
     return INSITU_OK;
 }
@@ -557,6 +562,72 @@ int insitu_attend(insitu_cache *k, const int32_t *q, int32_t *out, int32_t mode,
     if (rc) return rc;
     rc = attend_impl(k, q, out, mode, false);
     if (rc) return rc;
+    return copy_stats(k, stats);
+}
+
+// A prefill attend (attend_causal_batch / attend_online_batch, attention.py:517-871)
+// runs as a virtual batch: up to PREFILL_QB queries per launch, query i a
+// "sequence" of its own length base + i + 1 whose planes are those of the real
+// sequence (sequence stride 0). Every query then gets exactly the decode path's
+// arithmetic over rows 0 .. base + i.
+constexpr int64_t PREFILL_QB = 256;
+
+__global__ void prefill_lengths_kernel(int64_t *len, int64_t first, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) len[i] = first + i;
+}
+
+int insitu_attend_causal(insitu_cache *k, int32_t seq, int64_t base, int64_t n_q, const int32_t *q,
+                         int32_t *out, int32_t mode, insitu_stats *stats) {
+    if (!k || (n_q > 0 && (!q || !out))) return fail(INSITU_EINVAL, "null argument");
+    if (mode < INSITU_SEQUENTIAL || mode > INSITU_SERIAL) return fail(INSITU_EINVAL, "unknown mode");
+    const Geom &g = k->g;
+    if (seq < 0 || seq >= g.batch) return fail(INSITU_EINVAL, "no such sequence");
+    if (base < 0 || n_q < 0 || base + n_q > k->len_host[seq]) {
+        char buf[200];
+        snprintf(buf, sizeof buf, "queries %lld .. %lld attend rows 0 .. base + i, but the sequence "
+                 "holds %lld rows", (long long)base, (long long)(base + n_q - 1),
+                 (long long)k->len_host[seq]);
+        return fail(INSITU_EBADLEN, buf);
+    }
+    HIP_TRY(hipSetDevice(k->ctx->device), "hipSetDevice");
+    int rc = stats ? zero_stats(k) : INSITU_OK;
+    if (rc) return rc;
+    if (n_q == 0) return copy_stats(k, stats);
+    Geom gv = g;
+    gv.base = g.base + (int64_t)seq * g.seq_stride;
+    gv.seq_stride = 0;
+    const bool chunked = mode != INSITU_SERIAL && k->chunk_scratch;
+    if (!k->prefill_len) HIP_TRY(hipMalloc(&k->prefill_len, PREFILL_QB * sizeof(int64_t)), "hipMalloc");
+    if (chunked && !k->prefill_scratch) {
+        Geom gc = gv;
+        gc.batch = (int32_t)PREFILL_QB;
+        const size_t nb = chunked_scratch_bytes(gc, k->max_chunks, k->pool);
+        HIP_TRY(hipMalloc(&k->prefill_scratch, nb), "hipMalloc");
+        HIP_TRY(hipMemsetAsync(k->prefill_scratch, 0, nb, k->ctx->stream), "hipMemsetAsync");
+    }
+    const int64_t row = (int64_t)g.n_q * g.d;
+    for (int64_t i0 = 0; i0 < n_q; i0 += PREFILL_QB) {
+        const int64_t nb = n_q - i0 < PREFILL_QB ? n_q - i0 : PREFILL_QB;
+        gv.batch = (int32_t)nb;
+        hipLaunchKernelGGL(prefill_lengths_kernel, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0,
+                           k->ctx->stream, k->prefill_len, base + i0 + 1, nb);
+        HIP_TRY(hipGetLastError(), "prefill lengths");
+        LaunchEv ev;
+        rc = timing_events(k->ctx, &ev);
+        if (rc) return rc;
+        if (chunked) {
+            HIP_TRY(launch_attend_chunked(k->ctx->stream, gv, k->tabs, q + i0 * row, out + i0 * row,
+                                          k->prefill_len, k->prefill_scratch, k->max_chunks, k->pool,
+                                          k->calls++, mode == INSITU_TWO_PASS ? 1 : 0, false, nullptr,
+                                          ev, k->stats, PREFILL_QB),
+                    "prefill attend launch");
+        } else {
+            HIP_TRY(launch_attend_serial(k->ctx->stream, gv, k->tabs, q + i0 * row, out + i0 * row,
+                                         k->prefill_len, mode == INSITU_TWO_PASS ? 1 : 0, ev, k->stats),
+                    "prefill attend launch");
+        }
+    }
     return copy_stats(k, stats);
 }
 

@@ -1384,13 +1384,25 @@ void chunked_query_area(const Geom &g, int64_t max_chunks, int64_t pool, void *s
 hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
                                  int32_t *out, const int64_t *len, void *scratch, int64_t max_chunks,
                                  int64_t pool, uint32_t call, int two_pass, bool q_staged,
-                                 const StepIn *step, LaunchEv ev, DevStats *st) {
+                                 const StepIn *step, LaunchEv ev, DevStats *st,
+                                 int64_t carve_batch) {
     const int64_t chains = (int64_t)g.batch * g.n_kv;
     if (max_chunks > HMAX || chains > 65535 || max_chunks * chains > 0x7fffffff)
         return hipErrorInvalidValue;
+    if (carve_batch < g.batch) carve_batch = g.batch;
+    Geom gc = g;
+    gc.batch = (int32_t)carve_batch;
     Chunked ck;
-    carve(g, max_chunks, pool, (uint8_t *)scratch, &ck, nullptr);
+    size_t bytes = 0;
+    carve(gc, max_chunks, pool, (uint8_t *)scratch, &ck, &bytes);
     ck.ep = call % EPOCH_MASK + 1;     // 1 .. 2^14 - 1: zeroed scratch is never current
+    // The epoch wraps every 2^14 - 1 calls: a word last written exactly that
+    // many calls ago would read as current, so the words go back to zero (no
+    // epoch) first. Every chain's counter is zero between calls already.
+    if (call % EPOCH_MASK == 0 && call > 0) {
+        const hipError_t e = hipMemsetAsync(scratch, 0, bytes, s);
+        if (e != hipSuccess) return e;
+    }
 #define INSITU_FAST(DD, KK)                                                          \
     if (g.d == DD && g.kb == KK)                                                     \
         return launch_fast<DD, KK>(s, g, t, q, out, len, ck, two_pass, q_staged, step, ev, st);

@@ -208,10 +208,13 @@ void chunked_query_area(const Geom &g, int64_t max_chunks, int64_t pool, void *s
 // Whether insitu_step runs as one fused launch in sequential mode (the
 // register budget of the fused kernel allows it at d = 64).
 bool chunked_fused_step(const Geom &g);
+// carve_batch: the sequences the scratch is laid out for (g.batch when 0); a
+// launch over fewer sequences than its scratch holds passes the larger count.
 hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
                                  int32_t *out, const int64_t *len, void *scratch, int64_t max_chunks,
                                  int64_t pool, uint32_t call, int two_pass, bool q_staged,
-                                 const StepIn *step, LaunchEv ev, DevStats *st);
+                                 const StepIn *step, LaunchEv ev, DevStats *st,
+                                 int64_t carve_batch = 0);
 hipError_t launch_step_write(hipStream_t s, const Geom &g, const Tables *t, const int32_t *qw,
                              const int32_t *kw, const int32_t *vw, int rounds,
                              const uint64_t (*signs)[2], int32_t *qr, double *qd, int32_t *qok,

@@ -191,18 +191,19 @@ void orc_attend_two_pass(const orc_fmt *f, const orc_exp *e, int32_t G, const in
 }
 
 /* The config-1 check: one layer's sequential decode from an empty cache
- * (kernel.py:271-345, the token attends to itself). Step t attends its rotated
- * query rows q[t] (n_kv groups of G rows of d) over rows 0 .. t of each KV
- * head, exactly as orc_attend_online. k_idx/v_idx are (n_kv, cap, d) codes,
+ * (kernel.py:271-345, the token attends to itself), or a prefill's queries
+ * (attend_online_batch, attention.py:794-871). Step i attends its rotated
+ * query rows q[i] (n_kv groups of G rows of d) over rows 0 .. base + i of each
+ * KV head, exactly as orc_attend_online. k_idx/v_idx are (n_kv, cap, d) codes,
  * k_norm/v_norm (n_kv, cap); out is (steps, n_kv, G, d). Returns 0, or -1 when
- * scratch cannot be allocated. */
+ * scratch cannot be allocated or base + steps exceeds cap. */
 int orc_decode_steps(const orc_fmt *f, const orc_exp *e, int32_t n_kv, int32_t G, int64_t steps,
-                     int64_t cap, const int64_t *q, const uint8_t *k_idx, const int64_t *k_norm,
+                     int64_t base, int64_t cap, const int64_t *q, const uint8_t *k_idx, const int64_t *k_norm,
                      const uint8_t *v_idx, const int64_t *v_norm, const int64_t *kc,
                      const int64_t *vc, int64_t *out) {
     const int32_t d = f->d;
-    if (steps > cap) return -1;
-    int64_t *s = (int64_t *)malloc(sizeof(int64_t) * (size_t)G * (size_t)(steps > 0 ? steps : 1));
+    if (base < 0 || base + steps > cap) return -1;
+    int64_t *s = (int64_t *)malloc(sizeof(int64_t) * (size_t)G * (size_t)(base + steps > 0 ? base + steps : 1));
     int64_t *acc = (int64_t *)malloc(sizeof(int64_t) * (size_t)G * (size_t)d);
     int64_t *l = (int64_t *)malloc(sizeof(int64_t) * (size_t)G);
     int64_t *m = (int64_t *)malloc(sizeof(int64_t) * (size_t)G);
@@ -212,7 +213,7 @@ int orc_decode_steps(const orc_fmt *f, const orc_exp *e, int32_t n_kv, int32_t G
             orc_stats st;
             memset(&st, 0, sizeof st);
             const int64_t qo = (t * n_kv + h) * (int64_t)G * d;
-            orc_attend_online(f, e, G, q + qo, t + 1, k_idx + (int64_t)h * cap * d, k_norm + (int64_t)h * cap,
+            orc_attend_online(f, e, G, q + qo, base + t + 1, k_idx + (int64_t)h * cap * d, k_norm + (int64_t)h * cap,
                               v_idx + (int64_t)h * cap * d, v_norm + (int64_t)h * cap, kc, vc, s, acc, l,
                               m, out + qo, &st);
         }

@@ -168,13 +168,14 @@ def finalize(acc, l, fmt: Format):
     return out, r, sh
 
 
-def decode_steps(q_rot_steps, kv_heads, fmt: Format) -> np.ndarray:
+def decode_steps(q_rot_steps, kv_heads, fmt: Format, base: int = 0) -> np.ndarray:
     """One layer's sequential decode from an empty cache, every step at once.
 
     q_rot_steps: (steps, n_kv * G, d) rotated query rows; kv_heads: one
-    CompressedKV per KV head holding at least `steps` rows (row t is step t's
-    own token). Step t attends over rows 0 .. t (kernel.py:271-345: the token
-    attends to itself), as attend_online does. Returns (steps, n_kv * G, d).
+    CompressedKV per KV head holding at least base + steps rows. Step i attends
+    over rows 0 .. base + i (kernel.py:271-345: the token attends to itself; a
+    prefill from `base`, attention.py:794-871), as attend_online does.
+    Returns (steps, n_kv * G, d).
     """
     q = np.ascontiguousarray(q_rot_steps, dtype=np.int64)
     steps, rows, d = q.shape
@@ -192,9 +193,9 @@ def decode_steps(q_rot_steps, kv_heads, fmt: Format) -> np.ndarray:
     f = _fmt(fmt)
     e = _exp(fmt)
     rc = lib().orc_decode_steps(ctypes.byref(f), ctypes.byref(e), n_kv, G, ctypes.c_int64(steps),
-                                ctypes.c_int64(cap), _p(q, _I64P), _p(ki, _U8P), _p(kn, _I64P),
+                                ctypes.c_int64(base), ctypes.c_int64(cap), _p(q, _I64P), _p(ki, _U8P), _p(kn, _I64P),
                                 _p(vi, _U8P), _p(vn, _I64P), _p(kc, _I64P), _p(vc, _I64P),
                                 _p(out, _I64P))
     if rc:
-        raise MemoryError("orc_decode_steps: no scratch or steps > cache rows")
+        raise MemoryError("orc_decode_steps: no scratch, or base + steps > cache rows")
     return out

@@ -677,3 +677,108 @@ def test_attend_timing_hook_counts_every_attend(ctx):
         assert n.value == 0 and ms.value == 0.0
     finally:
         _lib.check(lib.insitu_ctx_timing(ctx.handle, 0))
+
+
+# -- prefill: every query of a prompt at once (attention.py:517-871) ------------------
+
+@pytest.mark.parametrize("kb,vb", [(4, 2), (3, 2), (2, 3)])
+@pytest.mark.parametrize("mode", ["online", "two_pass", "serial"])
+def test_prefill_is_the_token_loop(ctx, kb, vb, mode):
+    """attend_online_batch / attend_causal_batch are the per-query loop, bit for bit
+    (the reference's check_online_batch_is_bit_identical and
+    check_causal_batch_is_bit_identical): query t attends rows 0 .. t."""
+    from insitu_amd.attention import CompressedAttention
+    f = Format(key_bits=kb, value_bits=vb)
+    T = 53
+    rng = np.random.default_rng(kb * 10 + vb)
+    k, v = _random_cache_inputs(rng, T)
+    c = _cache(ctx, T, kb=kb, vb=vb)
+    c.append_rotated(k, v)
+    q = rng.integers(-(1 << 22), 1 << 22, size=(T, 32, 64))
+    out, st = CompressedAttention(c).attend_prefill(q, 0, mode)
+    out = out.cpu().numpy()
+    host = Cache(8, T, f)
+    host.append_rotated(k, v)
+    fn = attend_two_pass if mode == "two_pass" else attend_online
+    events = 0
+    for t in range(T):
+        for h in range(8):
+            want, s = fn(q[t, 4 * h:4 * h + 4], host.view(h).select(slice(0, t + 1)), f)
+            np.testing.assert_array_equal(out[t, 4 * h:4 * h + 4], want, err_msg=f"query {t} group {h}")
+            events += s.rescale_events
+    assert st.rescale_events == events
+    if mode != "two_pass":
+        assert events > 0
+
+
+@pytest.mark.parametrize("mode", ["online", "two_pass"])
+def test_prefill_from_a_base_across_chunks_and_query_batches(ctx, mode):
+    """600 queries from row 2,000 of a 2,600-row cache: the queries cross a
+    1,024-token chunk boundary and the 256-query launches of the virtual batch;
+    every query against the C oracle over rows 0 .. base + i."""
+    from insitu_amd.attention import CompressedAttention
+    base, n_q = 2000, 600
+    T = base + n_q
+    rng = np.random.default_rng(5)
+    k, v = _random_cache_inputs(rng, T)
+    c = _cache(ctx, T)
+    c.append_rotated(k, v)
+    q = rng.integers(-(1 << 22), 1 << 22, size=(n_q, 32, 64))
+    out, _ = CompressedAttention(c).attend_prefill(q, base, mode)
+    out = out.cpu().numpy()
+    host = Cache(8, T, FMT)
+    host.append_rotated(k, v)
+    heads = [host.view(h) for h in range(8)]
+    if mode == "online":
+        want = native.decode_steps(q, heads, FMT, base=base)
+        bad = np.nonzero((out != want).reshape(n_q, -1).any(axis=1))[0]
+        assert bad.size == 0, f"queries {bad[:10].tolist()} differ"
+    else:
+        for i in (0, 47, 255, 256, 511, n_q - 1):
+            want = np.concatenate([native.attend_two_pass(q[i, 4 * h:4 * h + 4],
+                                                          heads[h].select(slice(0, base + i + 1)), FMT)[0]
+                                   for h in range(8)])
+            np.testing.assert_array_equal(out[i], want, err_msg=f"query {i}")
+
+
+def test_prefill_group_interface_and_bounds(ctx):
+    """The reference-shaped per-group calls, and EBADLEN past the cache's rows."""
+    from insitu_amd import _lib
+    from insitu_amd.attention import CompressedAttention
+    T = 40
+    rng = np.random.default_rng(3)
+    k, v = _random_cache_inputs(rng, T)
+    c = _cache(ctx, T + 10)
+    c.append_rotated(k, v)
+    host = Cache(8, T, FMT)
+    host.append_rotated(k, v)
+    a = CompressedAttention(c)
+    q = rng.integers(-(1 << 22), 1 << 22, size=(12, 4, 64))
+    got, _ = a.attend_online_batch(q, kv_head=5, base=T - 12)
+    got2, _ = a.attend_causal_batch(q, kv_head=5, base=T - 12)
+    for i in range(12):
+        view = host.view(5).select(slice(0, T - 12 + i + 1))
+        np.testing.assert_array_equal(got[i], attend_online(q[i], view, FMT)[0])
+        np.testing.assert_array_equal(got2[i], attend_two_pass(q[i], view, FMT)[0])
+    with pytest.raises(_lib.InsituError, match="EBADLEN"):
+        a.attend_prefill(np.zeros((12, 32, 64), dtype=np.int32), T - 11, "online")
+
+
+@pytest.mark.parametrize("softmax", ["online", "two_pass"])
+def test_block_prefill_equals_the_decode_loop(ctx, softmax):
+    """kernel.py:316-341: a prompt through prefill gives the same outputs and the
+    same cache bytes as the same tokens one decode step at a time, also when
+    the prompt follows earlier tokens (base > 0)."""
+    from insitu_amd import ModelConfig, QuantConfig
+    from insitu_amd.block import AttentionBlock
+    from insitu_amd.workload import Workload
+    q, k, v = Workload(seed=7).steps(330)
+    q, k, v = q[0], k[0], v[0]
+    mk = lambda: AttentionBlock(ModelConfig.llama32_1b(), QuantConfig(key_bits=4, value_bits=2),
+                                capacity=330, softmax=softmax, ctx=ctx)
+    loop, pre = mk(), mk()
+    want = loop.forward_seam(q, k, v, force_token_loop=True)
+    got_a = pre.forward_seam(q[:30], k[:30], v[:30])          # a first prompt
+    got_b = pre.forward_seam(q[30:], k[30:], v[30:])          # continues at base 30
+    np.testing.assert_array_equal(np.concatenate([got_a, got_b]), want)
+    np.testing.assert_array_equal(pre.cache.buf, loop.cache.buf)

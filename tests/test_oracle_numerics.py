@@ -249,3 +249,10 @@ def test_native_decode_steps_equal_the_per_token_loop_step_by_step():
         for h in range(n_kv):
             want, _ = attend_online(q[t, 4 * h:4 * h + 4], heads[h].select(slice(0, t + 1)), FMT)
             np.testing.assert_array_equal(got[t, 4 * h:4 * h + 4], want, err_msg=f"step {t} head {h}")
+    # from a base: query i attends rows 0 .. base + i
+    base = 25
+    got = native.decode_steps(q[base:], heads, FMT, base=base)
+    for i in (0, 3, steps - base - 1):
+        for h in range(n_kv):
+            want, _ = attend_online(q[base + i, 4 * h:4 * h + 4], heads[h].select(slice(0, base + i + 1)), FMT)
+            np.testing.assert_array_equal(got[i, 4 * h:4 * h + 4], want, err_msg=f"base {base} query {i}")
