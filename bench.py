@@ -16,6 +16,7 @@ consecutive steps never re-read a cache that is still resident.
     python bench.py --copy-calibration      # a plain copy kernel of known size
     python bench.py --config c3|c4          # the larger configurations, attend only
     python bench.py --config c1             # config 1 in full, every step checked
+    python bench.py --config prefill        # a 4,096-token prompt through one layer
 
 C3: batch 64, one layer, per-sequence contexts uniform in
 [1024, 8192] from seed 3, one attend launch over the whole batch; 3 caches
@@ -62,7 +63,8 @@ def _args():
     ap.add_argument("--ctx", type=int, default=CTX)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "prefill"])
+    ap.add_argument("--prompt", type=int, default=4096)
     ap.add_argument("--c1-layers", type=int, default=16)
     ap.add_argument("--c1-steps", type=int, default=4096)
     return ap.parse_args()
@@ -325,6 +327,72 @@ def bench_c1(a) -> int:
     return 0 if not mism and not cache_bad else 1
 
 
+def bench_prefill(a) -> int:
+    """A prompt through one Llama-3.2-1B-shape layer: rotate, append, then every
+    query at once (insitu_attend_causal; query i attends rows 0 .. i)."""
+    import torch
+
+    from insitu_amd import ModelConfig, QuantConfig
+    from insitu_amd.block import AttentionBlock
+    from insitu_amd.runtime import default_context
+    from insitu_amd.workload import Workload
+    from oracle import native
+    from oracle.quantize import Format, encode
+    from oracle.rotate import rotate, signs_from_seed
+
+    n = a.prompt
+    ctx = default_context(0)
+    q, k, v = (x[0] for x in Workload(seed=0).steps(n))
+    blk = AttentionBlock(ModelConfig.llama32_1b(), QuantConfig(key_bits=4, value_bits=2),
+                         capacity=n, softmax=a.mode, ctx=ctx)
+    qd, kd, vd = (ctx.to_device(x, torch.int32) for x in (q, k, v))
+    reps = max(1, min(a.steps, 10))
+    for _ in range(max(1, a.warmup // 2)):
+        blk.reset()
+        blk.prefill(qd, kd, vd, stats=False)
+    torch.cuda.synchronize()
+    wall = 0.0
+    for _ in range(reps):
+        blk.reset()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        out = blk.prefill(qd, kd, vd, stats=False)
+        torch.cuda.synchronize()
+        wall += time.perf_counter() - t0
+    wall /= reps
+    # spot check against the C oracle: queries 0, n/2 and n-1 of every KV group
+    got = out.cpu().numpy().reshape(n, N_Q, D)
+    sg = signs_from_seed(D, 0, 1)
+    qr = rotate(np.asarray(q, dtype=np.int64).reshape(-1, D), sg).reshape(n, N_Q, D)
+    kr = rotate(np.asarray(k, dtype=np.int64).reshape(-1, D), sg).reshape(n, N_KV, D)
+    vr = rotate(np.asarray(v, dtype=np.int64).reshape(-1, D), sg).reshape(n, N_KV, D)
+    fmt = Format()
+    heads = [encode(kr[:, h], vr[:, h], fmt) for h in range(N_KV)]
+    bad = 0
+    for i in (0, n // 2, n - 1):
+        if a.mode == "two_pass":
+            want = np.concatenate([native.attend_two_pass(qr[i, 4 * h:4 * h + 4],
+                                                          heads[h].select(slice(0, i + 1)), fmt)[0]
+                                   for h in range(N_KV)])
+        else:
+            want = native.decode_steps(qr[i:i + 1], heads, fmt, base=i)[0]
+        bad += int((got[i] != want).any())
+    rows = N_KV * n * (n + 1) // 2
+    res = {
+        "metric": "prefill: prompt tokens per second through one layer (rotate, append, attend)",
+        "value": round(n / wall, 1), "unit": "tokens/s", "n_gpus": 1, "steps": reps,
+        "ms_per_prefill": round(wall * 1e3, 3), "higher_is_better": True, "dtype": "int64",
+        "data": "synthetic (seeded N(0,1) q/k/v with 4 outlier channels x8 per head, Q8.16)",
+        "config": {"workload": f"prefill of a {n}-token prompt, Llama-3.2-1B-shape layer, 4b K / 2b V",
+                   "mode": a.mode},
+        "scan_gb": round(rows * ROW / 1e9, 3),
+        "effective_scan_gbs": round(rows * ROW / wall / 1e9, 1),
+        "spot_check_queries_wrong": bad,
+    }
+    print(json.dumps(res))
+    return 0 if bad == 0 else 1
+
+
 def _kv_only(wl, n):
     """k and v (1, n, Hkv, d) of the workload's distribution, without q."""
     from insitu_amd.workload import to_fixed
@@ -344,6 +412,8 @@ def main() -> int:
         return 2
     if a.config == "c1":
         return bench_c1(a)
+    if a.config == "prefill":
+        return bench_prefill(a)
     if a.config != "c2":
         return bench_scale(a)
     import torch
