@@ -172,6 +172,37 @@ int insitu_attend_causal(insitu_cache *cache, int32_t seq, int64_t base, int64_t
                          const int32_t *q_rot_dev, int32_t *out_dev, int32_t mode,
                          insitu_stats *stats_host);
 
+/* -- the host half either side of the seam (kernel.py:198-249, 348-356) -------------- */
+
+/* A projection (ops/project.py:21-52, numerics/fp.py:25-44): y_dev fp32 (n, out_f) =
+ * fp16(x_dev) (n, in_f) @ w_dev^T + bias_dev, fp16 weights (out_f, in_f) in the
+ * checkpoint's layout, fp32 accumulation. x_dev fp32 is rounded to fp16 (nearest
+ * even) first. bias_dev (out_f) fp32 may be NULL. Stream-ordered on the context. */
+int insitu_project(insitu_ctx *ctx, const uint16_t *w_dev, int32_t out_f, int32_t in_f,
+                   const float *x_dev, int64_t n, const float *bias_dev, float *y_dev);
+
+/* The seam (kernel.py:209-249): p_dev fp32 (n, (n_q + 2 n_kv) d), the q|k|v projections
+ * of n tokens, bias_dev fp32 ((n_q + 2 n_kv) d) or NULL, added in fp32; q times
+ * attn_scale in float64; then cast_after_rope = 0: to_fixed (ops/convert.py:44-57) and
+ * RoPE in fixed point (ops/rope.py:144-174), or 1: RoPE in float64 (:176-198) and
+ * to_fixed. cos/sin_dev int64 (max_pos, d/2) Q(frac); pos_dev int64 (n). Writes the
+ * wire rows q_dev (n, n_q, d), k/v_dev (n, n_kv, d) int32 Q8.16 (RoPE's output is
+ * not clamped, as in the reference). counts_host (2) may be NULL; otherwise the call
+ * synchronises and returns {values saturated by to_fixed, rows whose position is
+ * beyond the table}, and ERANGE when the second is not 0. */
+int insitu_seam_wire(insitu_ctx *ctx, const float *p_dev, const float *bias_dev, int64_t n, int32_t n_q,
+                     int32_t n_kv, int32_t d, const int64_t *pos_dev, const int64_t *cos_dev,
+                     const int64_t *sin_dev, int64_t max_pos, int32_t frac, double attn_scale,
+                     int32_t cast_after_rope, int32_t *q_dev, int32_t *k_dev, int32_t *v_dev,
+                     unsigned long long *counts_host);
+
+/* The output side (kernel.py:348-356): out_dev int32 (n, width) Q(frac) -> float ->
+ * fp16, then y_dev fp32 (n, hidden) = that @ wo_dev^T + bias_dev with W_o' fp16
+ * (hidden, width), R^-1 folded in (ops/output.py:49-78). bias_dev may be NULL. */
+int insitu_output_projection(insitu_ctx *ctx, const int32_t *out_dev, int64_t n, int32_t width,
+                             int32_t frac, const uint16_t *wo_dev, int32_t hidden, const float *bias_dev,
+                             float *y_dev);
+
 /* One decode step from the wire (CMD_STEP, host/attn_proto.py:65-72; kernel.py:256-353):
  * q/k/v_dev int32 Q8.16 (batch, heads, d) -> rotate -> append -> attend -> out_dev. */
 int insitu_step(insitu_cache *cache, const int32_t *q_dev, const int32_t *k_dev,

@@ -10,7 +10,8 @@ Python host side that mirrors the reference's interfaces:
     Rotation                                ops/rotate.py
     KVCache, CompressedCache                cache/base.py, cache/compressed.py
     CompressedAttention, AttentionStats     ops/attention.py
-    AttentionBlock                          kernel.py (below the seam)
+    AttentionBlock, StepReport              kernel.py (forward, both halves)
+    Weights, HostHalf, RoPE, RopeScaling    weights.py, ops/rope.py, kernel.py:198-249
 """
 
 from .config import FixedFormat, ModelConfig, QuantConfig
@@ -18,7 +19,8 @@ from .codebook import Codebook
 
 __all__ = ["FixedFormat", "ModelConfig", "QuantConfig", "Codebook", "Rotation",
            "KVCache", "CompressedCache", "CompressedKV", "CompressedAttention",
-           "AttentionStats", "AttentionBlock"]
+           "AttentionStats", "AttentionBlock", "StepReport", "Weights", "HostHalf", "RoPE",
+           "RopeScaling"]
 
 
 def __getattr__(name):
@@ -33,7 +35,10 @@ def __getattr__(name):
     if name in ("CompressedAttention", "AttentionStats"):
         from . import attention
         return getattr(attention, name)
-    if name == "AttentionBlock":
-        from .block import AttentionBlock
-        return AttentionBlock
+    if name in ("AttentionBlock", "StepReport"):
+        from . import block
+        return getattr(block, name)
+    if name in ("Weights", "HostHalf", "RoPE", "RopeScaling"):
+        from . import host
+        return getattr(host, name)
     raise AttributeError(name)

@@ -1,7 +1,10 @@
-"""The seam half of one attention block: wire q/k/v in, Q16 out.
+"""One attention block: hidden states in, hidden states out.
 
 AttentionBlock follows the pipeline order of AttentionKernel.forward
-(kernel.py:253-353 of the reference), the part below the seam:
+(kernel.py:177-357 of the reference). forward() runs the host half in front
+of the seam (projections, attention scale, RoPE and the fp -> fixed cast,
+kernel.py:198-249, insitu_amd.host), the part below the seam, then the output
+side (to_float and W_o', kernel.py:348-356). The part below the seam is:
 
     rotate k, v, q        kernel.py:271-276
     append k, v           kernel.py:282-284 (the current token attends to itself)
@@ -18,6 +21,7 @@ attend_causal_batch in two-pass mode), bit-identical to the token loop.
 from __future__ import annotations
 
 import ctypes
+from dataclasses import dataclass, field
 
 import numpy as np
 
@@ -28,10 +32,34 @@ from .config import FixedFormat, ModelConfig, QuantConfig
 from .runtime import default_context, ptr
 
 
+@dataclass
+class StepReport:
+    """kernel.py:49-67: what one forward did. `saturated` counts the fp -> fixed
+    cast's clamped lanes (ConversionStats, ops/convert.py)."""
+
+    n_tokens: int = 0
+    context: int = 0
+    attention: AttentionStats | None = None
+    saturated: int = 0
+    conversions: int = 0
+
+    @property
+    def saturation_rate(self) -> float:
+        return self.saturated / self.conversions if self.conversions else 0.0
+
+    def summary(self) -> str:
+        a = self.attention or AttentionStats()
+        return (f"{self.n_tokens} token(s), context {self.context}\n"
+                f"  rescales {a.rescale_events}  score_ovf {a.score_overflows}  "
+                f"acc_ovf {a.acc_overflows}\n"
+                f"  fp->fixed saturation {self.saturation_rate:.2%}")
+
+
 class AttentionBlock:
     def __init__(self, model: ModelConfig, quant: QuantConfig | None = None,
                  fmt: FixedFormat | None = None, *, capacity: int = 2048, batch: int = 1,
-                 softmax: str = "online", ctx=None) -> None:
+                 softmax: str = "online", weights=None, cast_after_rope: bool = True,
+                 ctx=None) -> None:
         self.model = model
         self.quant = quant or QuantConfig()
         self.fmt = fmt or FixedFormat()
@@ -45,6 +73,13 @@ class AttentionBlock:
             raise ValueError(f"softmax={softmax!r}; expected one of {sorted(_lib.MODES)}")
         self.softmax = softmax
         self.last_stats: AttentionStats | None = None
+        # kernel.py:163: RoPE in float and one cast at the seam by default;
+        # False is the board's order (cast, then fixed-point RoPE)
+        self.cast_after_rope = cast_after_rope
+        self.force_token_loop = False
+        self.weights = weights
+        self._host = None
+        self.taps: dict = {}
 
     @property
     def batch(self) -> int:
@@ -107,6 +142,58 @@ class AttentionBlock:
         outs = [self.step(qi[t][None], ki[t][None], vi[t][None]).cpu().numpy()
                 for t in range(qi.shape[0])]
         return np.concatenate(outs, axis=0).astype(np.int64)
+
+    @property
+    def host(self):
+        if self.weights is None:
+            raise ValueError("forward needs weights: AttentionBlock(..., weights=Weights(...))")
+        if self._host is None or self._host.cast_after_rope != self.cast_after_rope:
+            from .host import HostHalf
+            self._host = HostHalf(self.model, self.weights, cast_after_rope=self.cast_after_rope,
+                                  ctx=self.ctx)
+        return self._host
+
+    def forward(self, hidden_states, positions=None):
+        """kernel.py:177-357, batch == 1: (tokens, hidden) float32 in, (tokens,
+        hidden) float32 out (a torch tensor on the device), and a StepReport.
+
+        positions default to cache.length .. cache.length + tokens - 1. The
+        wire rows and the Q16 `out` rows are kept in self.taps ("wire.q",
+        "wire.k", "wire.v", "out"), the reference's tap points.
+        """
+        import torch
+        m = self.model
+        if self.batch != 1:
+            raise ValueError("forward drives a batch-1 block")
+        x = self.ctx.to_device(hidden_states, torch.float32)
+        if x.dim() == 1:
+            x = x[None, :]
+        if x.shape[-1] != m.hidden_size:
+            raise ValueError(f"hidden size {x.shape[-1]} != {m.hidden_size}")
+        n = int(x.shape[0])
+        base = self.cache.length
+        if positions is None:
+            positions = np.arange(base, base + n)
+        positions = np.asarray(positions, dtype=np.int64)
+        if positions.shape != (n,):
+            raise ValueError(f"expected {n} positions, got {positions.shape}")
+        host = self.host
+        qi, ki, vi = host.wire(x, positions)
+        self.taps = {"wire.q": qi, "wire.k": ki, "wire.v": vi}
+        report = StepReport(n_tokens=n, saturated=host.last_saturated,
+                            conversions=n * (m.num_heads + 2 * m.num_kv_heads) * m.head_dim)
+        if n > 1 and not self.force_token_loop:
+            out = self.prefill(qi, ki, vi)
+            report.attention = self.last_stats
+        else:
+            rows, report.attention = [], AttentionStats()
+            for t in range(n):
+                rows.append(self.step(qi[t][None], ki[t][None], vi[t][None]))
+                report.attention.merge(self.last_stats)
+            out = torch.cat(rows, dim=0)
+        self.taps["out"] = out
+        report.context = base + n
+        return host.output(out), report
 
     def reset(self) -> None:
         """kernel.py:454-456: a new sequence; tables survive."""

@@ -14,12 +14,15 @@ from dataclasses import dataclass
 
 @dataclass(frozen=True)
 class ModelConfig:
-    """config.py:33-76 (shape only; RoPE belongs to the host half)."""
+    """config.py:33-76: the attention shape, and the RoPE settings the host half uses."""
 
     hidden_size: int
     num_heads: int
     num_kv_heads: int
     head_dim: int | None = None
+    rope_theta: float = 10000.0
+    max_position: int = 4096
+    rope_scaling: object | None = None     # insitu_amd.host.RopeScaling, or None for plain RoPE
 
     def __post_init__(self) -> None:
         d = self.head_dim if self.head_dim is not None else self.hidden_size // self.num_heads
@@ -36,6 +39,14 @@ class ModelConfig:
     @property
     def kv_groups(self) -> int:
         return self.num_heads // self.num_kv_heads
+
+    @property
+    def q_out_features(self) -> int:
+        return self.num_heads * self.head_dim
+
+    @property
+    def kv_out_features(self) -> int:
+        return self.num_kv_heads * self.head_dim
 
     @classmethod
     def llama32_1b(cls) -> "ModelConfig":

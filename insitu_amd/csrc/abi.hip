@@ -33,6 +33,12 @@ int hip_fail(hipError_t e, const char *what) {
         if (e_ != hipSuccess) return hip_fail(e_, what); \
     } while (0)
 
+}  // namespace
+
+int insitu::set_last_error(int code, const char *msg) { return fail(code, msg); }
+
+namespace {
+
 __global__ void zero_u64(unsigned long long *p, int n) {
     int i = threadIdx.x;
     if (i < n) p[i] = 0;
@@ -89,6 +95,9 @@ struct insitu_ctx {
     std::vector<hipEvent_t> ev;           // 2 per attend: start, end
     size_t ev_used = 0;
 };
+
+int insitu::ctx_device(insitu_ctx *c) { return c->device; }
+hipStream_t insitu::ctx_stream(insitu_ctx *c) { return c->stream; }
 
 struct insitu_cache {
     insitu_ctx *ctx = nullptr;

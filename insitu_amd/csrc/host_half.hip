@@ -1,0 +1,273 @@
+// The host half of the block on the GPU, either side of the seam.
+//
+// In front of the seam (kernel.py:198-249): the q/k/v projections
+// (ops/project.py:21-52: fp16 weights and activations, fp32 accumulation),
+// the attention scale on q, RoPE (ops/rope.py:144-198) and the one fp -> fixed
+// cast (ops/convert.py:44-57), giving the Q8.16 wire rows the attend path
+// takes. Behind it (kernel.py:348-356): the Q16 output back to float, and the
+// output projection through W_o' (R^-1 folded in, ops/output.py:49-78).
+//
+// The projections are plain fp16 GEMMs (fp32 accumulation) and run on
+// rocBLAS. Everything around them is a kernel of this file: the fp16 casts,
+// and the seam epilogue, whose float steps follow numpy's float64 arithmetic
+// operation by operation (no fused multiply-add), so that for the same fp32
+// projections the wire rows are the reference's integers exactly. Only the
+// GEMM's summation order differs from a CPU BLAS.
+
+#include <hip/hip_runtime.h>
+#include <rocblas/rocblas.h>
+
+#include <cmath>
+#include <cstdint>
+
+#include "insitu_internal.h"
+
+namespace insitu {
+
+// x fp32 -> fp16, round to nearest even (numerics/fp.py:20-22).
+__global__ void f32_to_f16_kernel(const float *__restrict__ x, _Float16 *__restrict__ y, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = (_Float16)x[i];
+}
+
+// Q(frac) int32 -> float64 (exact: the value over 2^frac) -> fp16, one rounding
+// (kernel.py:354 to_float, then the projection's fp16 cast).
+__global__ void fixed_to_f16_kernel(const int32_t *__restrict__ x, _Float16 *__restrict__ y, int64_t n,
+                                    double scale) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = (_Float16)((double)x[i] * scale);
+}
+
+// y[r][c] += bias[c] in fp32 (ops/project.py:45-46).
+__global__ void add_bias_kernel(float *__restrict__ y, const float *__restrict__ bias, int64_t rows,
+                                int32_t cols) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < rows * cols) y[i] = y[i] + bias[i % cols];
+}
+
+// numpy's rint (half to even), then the Q(24, 16) clamp (fixed.py:158-164).
+__device__ __forceinline__ int64_t to_fixed_q16(double a, unsigned long long *sat) {
+#pragma clang fp contract(off)
+    const double r = rint(a * 65536.0);
+    const double lo = -(double)(1 << 23), hi = (double)((1 << 23) - 1);
+    if (r < lo || r > hi) {
+        atomicAdd(sat, 1ull);
+        return r < lo ? -(int64_t)(1 << 23) : (int64_t)((1 << 23) - 1);
+    }
+    return (int64_t)r;
+}
+
+// The seam epilogue for one token and one head (one wave, lane = channel pair):
+// p = the fp32 projections (q, k, v concatenated), bias added in fp32; q times
+// the attention scale in float64; then either to_fixed and fixed-point RoPE
+// (cast_after_rope = 0, the board's order) or float RoPE and to_fixed (1).
+// RoPE pairs channel j with j + d/2 (the half split, rope.py:144-174).
+__global__ void seam_wire_kernel(const float *__restrict__ p, const float *__restrict__ bias, int64_t n,
+                                 int32_t n_q, int32_t n_kv, int32_t d, const int64_t *__restrict__ pos,
+                                 const int64_t *__restrict__ cos_t, const int64_t *__restrict__ sin_t,
+                                 int64_t max_pos, int32_t frac, double attn_scale, int32_t cast_after_rope,
+                                 int32_t *__restrict__ q, int32_t *__restrict__ k, int32_t *__restrict__ v,
+                                 unsigned long long *sat, unsigned long long *range_err) {
+#pragma clang fp contract(off)
+    const int heads = n_q + 2 * n_kv;
+    const int64_t wave = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (wave >= n * heads) return;
+    const int64_t t = wave / heads;
+    const int h = (int)(wave % heads);
+    const int half = d / 2;
+    const int kind = h < n_q ? 0 : (h < n_q + n_kv ? 1 : 2);       // q, k, v
+    const int hh = kind == 0 ? h : (kind == 1 ? h - n_q : h - n_q - n_kv);
+    const int64_t width = (int64_t)heads * d;
+    const float *row = p + t * width + (int64_t)h * d;
+    int32_t *dst = kind == 0 ? q + (t * n_q + hh) * d : (kind == 1 ? k + (t * n_kv + hh) * d
+                                                                     : v + (t * n_kv + hh) * d);
+    const int64_t ps = pos[t];
+    const bool rope = kind != 2;
+    if (rope && (ps < 0 || ps >= max_pos)) {
+        if (lane == 0) atomicAdd(range_err, 1ull);
+        return;
+    }
+    for (int j = lane; j < half; j += 64) {
+        float lo32 = row[j], hi32 = row[j + half];
+        if (bias) {
+            lo32 = lo32 + bias[h * d + j];
+            hi32 = hi32 + bias[h * d + j + half];
+        }
+        double lo = (double)lo32, hi = (double)hi32;
+        if (kind == 0) {
+            lo = lo * attn_scale;
+            hi = hi * attn_scale;
+        }
+        if (!rope) {
+            dst[j] = (int32_t)to_fixed_q16(lo, sat);
+            dst[j + half] = (int32_t)to_fixed_q16(hi, sat);
+            continue;
+        }
+        const int64_t c = cos_t[ps * half + j], s = sin_t[ps * half + j];
+        if (cast_after_rope) {
+            const double cf = (double)c / (double)(1ll << frac), sf = (double)s / (double)(1ll << frac);
+            const double a = lo * cf, b = hi * sf, e = lo * sf, f = hi * cf;
+            dst[j] = (int32_t)to_fixed_q16(a - b, sat);
+            dst[j + half] = (int32_t)to_fixed_q16(e + f, sat);
+        } else {
+            const int64_t li = to_fixed_q16(lo, sat), hi_ = to_fixed_q16(hi, sat);
+            // Q(16 + frac), one floor shift at the end; not clamped (the RTL flags range)
+            const int64_t ol = (li * c - hi_ * s) >> frac;
+            const int64_t oh = (li * s + hi_ * c) >> frac;
+            dst[j] = (int32_t)ol;
+            dst[j + half] = (int32_t)oh;
+        }
+    }
+}
+
+}  // namespace insitu
+
+using namespace insitu;
+
+namespace {
+
+int fail(int code, const char *msg) { return set_last_error(code, msg); }
+
+#define HIP_TRY(expr, what)                                                                 \
+    do {                                                                                    \
+        hipError_t e_ = (expr);                                                             \
+        if (e_ != hipSuccess) return set_last_error(INSITU_EHIP, hipGetErrorString(e_));    \
+    } while (0)
+
+struct Blas {
+    rocblas_handle h = nullptr;
+    _Float16 *x16 = nullptr;
+    size_t x16_n = 0;
+    unsigned long long *counters = nullptr;     // saturated, range errors
+};
+
+Blas &blas_of(insitu_ctx *c);
+
+int gemm_f16(insitu_ctx *c, const uint16_t *w, int32_t out_f, int32_t in_f, const _Float16 *x16,
+             int64_t n, float *y) {
+    Blas &b = blas_of(c);
+    if (!b.h) return fail(INSITU_EHIP, "rocBLAS handle");
+    const float one = 1.0f, zero = 0.0f;
+    // column-major: Y (out x n) = W^T (out x in) X (in x n); W is (out, in) row-major
+    const rocblas_status st = rocblas_gemm_ex(
+        b.h, rocblas_operation_transpose, rocblas_operation_none, out_f, (rocblas_int)n, in_f, &one, w,
+        rocblas_datatype_f16_r, in_f, x16, rocblas_datatype_f16_r, in_f, &zero, y, rocblas_datatype_f32_r,
+        out_f, y, rocblas_datatype_f32_r, out_f, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+    if (st != rocblas_status_success) return fail(INSITU_EHIP, "rocblas_gemm_ex failed");
+    return INSITU_OK;
+}
+
+int ensure_x16(insitu_ctx *c, size_t n) {
+    Blas &b = blas_of(c);
+    if (b.x16_n >= n) return INSITU_OK;
+    // the old staging may still feed a GEMM queued on the stream
+    if (b.x16) {
+        HIP_TRY(hipStreamSynchronize(ctx_stream(c)), "sync");
+        hipFree(b.x16);
+    }
+    b.x16 = nullptr;
+    b.x16_n = 0;
+    HIP_TRY(hipMalloc(&b.x16, n * sizeof(_Float16)), "hipMalloc");
+    b.x16_n = n;
+    return INSITU_OK;
+}
+
+}  // namespace
+
+// One rocBLAS handle and staging per context, made on first use on the
+// context's device and stream.
+static Blas g_blas[64];
+namespace {
+Blas &blas_of(insitu_ctx *c) {
+    Blas &b = g_blas[ctx_device(c) & 63];
+    if (!b.h) {
+        if (rocblas_create_handle(&b.h) != rocblas_status_success) b.h = nullptr;
+        if (b.h) rocblas_set_stream(b.h, ctx_stream(c));
+        if (hipMalloc(&b.counters, 2 * sizeof(unsigned long long)) != hipSuccess) b.counters = nullptr;
+    } else {
+        rocblas_set_stream(b.h, ctx_stream(c));
+    }
+    return b;
+}
+}  // namespace
+
+extern "C" {
+
+int insitu_project(insitu_ctx *c, const uint16_t *w, int32_t out_f, int32_t in_f, const float *x, int64_t n,
+                   const float *bias, float *y) {
+    if (!c || !w || (n && (!x || !y))) return fail(INSITU_EINVAL, "null argument");
+    if (out_f <= 0 || in_f <= 0 || n < 0) return fail(INSITU_EBADLEN, "bad projection shape");
+    if (n == 0) return INSITU_OK;
+    HIP_TRY(hipSetDevice(ctx_device(c)), "hipSetDevice");
+    int rc = ensure_x16(c, (size_t)n * in_f);
+    if (rc) return rc;
+    Blas &b = blas_of(c);
+    const int64_t nx = n * in_f;
+    hipLaunchKernelGGL(f32_to_f16_kernel, dim3((unsigned)((nx + 255) / 256)), dim3(256), 0, ctx_stream(c), x,
+                       b.x16, nx);
+    HIP_TRY(hipGetLastError(), "fp16 cast");
+    rc = gemm_f16(c, w, out_f, in_f, b.x16, n, y);
+    if (rc) return rc;
+    if (bias) {
+        const int64_t ny = n * out_f;
+        hipLaunchKernelGGL(add_bias_kernel, dim3((unsigned)((ny + 255) / 256)), dim3(256), 0, ctx_stream(c), y,
+                           bias, n, out_f);
+        HIP_TRY(hipGetLastError(), "bias");
+    }
+    return INSITU_OK;
+}
+
+int insitu_seam_wire(insitu_ctx *c, const float *p, const float *bias, int64_t n, int32_t n_q, int32_t n_kv,
+                     int32_t d, const int64_t *pos, const int64_t *cos_t, const int64_t *sin_t, int64_t max_pos,
+                     int32_t frac, double attn_scale, int32_t cast_after_rope, int32_t *q, int32_t *k,
+                     int32_t *v, unsigned long long *counts_host) {
+    if (!c || (n && (!p || !pos || !cos_t || !sin_t || !q || !k || !v))) return fail(INSITU_EINVAL, "null argument");
+    if (n < 0 || n_q <= 0 || n_kv <= 0 || d <= 0 || d % 2 || frac < 0 || frac > 30 || max_pos <= 0)
+        return fail(INSITU_EBADLEN, "bad seam shape");
+    HIP_TRY(hipSetDevice(ctx_device(c)), "hipSetDevice");
+    Blas &b = blas_of(c);
+    if (!b.counters) return fail(INSITU_EHIP, "counters");
+    if (counts_host) HIP_TRY(hipMemsetAsync(b.counters, 0, 2 * sizeof(unsigned long long), ctx_stream(c)), "memset");
+    if (n) {
+        const int64_t waves = n * (n_q + 2 * n_kv);
+        hipLaunchKernelGGL(seam_wire_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, ctx_stream(c), p,
+                           bias, n, n_q, n_kv, d, pos, cos_t, sin_t, max_pos, frac, attn_scale, cast_after_rope, q,
+                           k, v, b.counters, b.counters + 1);
+        HIP_TRY(hipGetLastError(), "seam epilogue");
+    }
+    if (counts_host) {
+        HIP_TRY(hipMemcpyAsync(counts_host, b.counters, 2 * sizeof(unsigned long long), hipMemcpyDeviceToHost,
+                               ctx_stream(c)),
+                "counts");
+        HIP_TRY(hipStreamSynchronize(ctx_stream(c)), "sync");
+        if (counts_host[1]) return fail(INSITU_ERANGE, "a position beyond the RoPE table (rope.py:163-167)");
+    }
+    return INSITU_OK;
+}
+
+int insitu_output_projection(insitu_ctx *c, const int32_t *out, int64_t n, int32_t width, int32_t frac,
+                             const uint16_t *wo, int32_t hidden, const float *bias, float *y) {
+    if (!c || !wo || (n && (!out || !y))) return fail(INSITU_EINVAL, "null argument");
+    if (n < 0 || width <= 0 || hidden <= 0 || frac < 0 || frac > 62) return fail(INSITU_EBADLEN, "bad shape");
+    if (n == 0) return INSITU_OK;
+    HIP_TRY(hipSetDevice(ctx_device(c)), "hipSetDevice");
+    int rc = ensure_x16(c, (size_t)n * width);
+    if (rc) return rc;
+    Blas &b = blas_of(c);
+    const int64_t nx = n * width;
+    hipLaunchKernelGGL(fixed_to_f16_kernel, dim3((unsigned)((nx + 255) / 256)), dim3(256), 0, ctx_stream(c), out,
+                       b.x16, nx, std::ldexp(1.0, -frac));
+    HIP_TRY(hipGetLastError(), "fixed to fp16");
+    rc = gemm_f16(c, wo, hidden, width, b.x16, n, y);
+    if (rc) return rc;
+    if (bias) {
+        const int64_t ny = n * hidden;
+        hipLaunchKernelGGL(add_bias_kernel, dim3((unsigned)((ny + 255) / 256)), dim3(256), 0, ctx_stream(c), y,
+                           bias, n, hidden);
+        HIP_TRY(hipGetLastError(), "bias");
+    }
+    return INSITU_OK;
+}
+
+}  // extern "C"

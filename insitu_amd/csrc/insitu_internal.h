@@ -223,4 +223,10 @@ hipError_t launch_attend_serial(hipStream_t s, const Geom &g, const Tables *t, c
                                 int32_t *out, const int64_t *len, int two_pass, LaunchEv ev,
                                 DevStats *st);
 
+// Shared with the files that add entry points beside abi.hip: the error
+// message for insitu_last_error, and a context's device and stream.
+int set_last_error(int code, const char *msg);
+int ctx_device(insitu_ctx *c);
+hipStream_t ctx_stream(insitu_ctx *c);
+
 }  // namespace insitu

@@ -134,3 +134,28 @@ def test_fp64_quotient_method_of_the_device_reciprocal():
     r = (4611686018427387904.0 / n.astype(np.float64)).astype(np.uint64)
     r = np.where(r * n > (np.uint64(1) << np.uint64(62)), r - np.uint64(1), r)
     np.testing.assert_array_equal(r, exact)
+
+
+def test_host_half_tables_and_fold_match_the_oracle():
+    """insitu_amd.host builds the RoPE tables and the W_o fold on the host; the
+    oracle's restatements (pinned to the reference's goldens) give the same."""
+    from insitu_amd.host import RoPE, RopeScaling, fold_o_proj
+    from oracle import host as oh
+    from oracle.rotate import matrix, signs_from_seed
+    for theta, scaling in ((10000.0, None), (500000.0, (32.0, 1.0, 4.0, 8192))):
+        t = RoPE.build(64, 3000, theta, scaling=RopeScaling(*scaling) if scaling else None)
+        cos, sin = oh.rope_tables(64, 3000, theta, scaling=oh.RopeScaling(*scaling) if scaling else None)
+        np.testing.assert_array_equal(t.cos, cos)
+        np.testing.assert_array_equal(t.sin, sin)
+    hf = RopeScaling.from_hf({"factor": 32.0, "low_freq_factor": 1.0, "high_freq_factor": 4.0,
+                              "original_max_position_embeddings": 8192, "rope_type": "llama3"})
+    assert hf == RopeScaling(32.0, 1.0, 4.0, 8192)
+    with pytest.raises(ValueError):
+        RopeScaling(8.0, 4.0, 1.0, 8192)
+    with pytest.raises(ValueError):
+        RoPE.build(63, 8)
+    sg = signs_from_seed(64, 0, 1)
+    wo = np.random.default_rng(2).standard_normal((32, 3 * 64))
+    np.testing.assert_allclose(fold_o_proj(wo, matrix(sg), 3), oh.fold_o_proj(wo, sg, 3), rtol=0, atol=1e-12)
+    with pytest.raises(ValueError):
+        fold_o_proj(wo, matrix(sg), 2)
