@@ -17,6 +17,7 @@ consecutive steps never re-read a cache that is still resident.
     python bench.py --config c3|c4          # the larger configurations, attend only
     python bench.py --config c1             # config 1 in full, every step checked
     python bench.py --config prefill        # a 4,096-token prompt through one layer
+    python bench.py --config block          # hidden states in, hidden states out, ctx 32k
 
 C3: batch 64, one layer, per-sequence contexts uniform in
 [1024, 8192] from seed 3, one attend launch over the whole batch; 3 caches
@@ -32,6 +33,11 @@ C4: Llama-3-8B shape (32 query heads, 8 KV heads, d=128,
 3-bit K and V), batch 16, ctx 131,072, 32 layers: one step is the 32 layers'
 attends, over a 53.7 GB resident cache. The k/v of one sequence (seeded, 1%
 outlier channels x16) are rotated and appended to every sequence and layer.
+Block: the whole attention block per decode token (AttentionBlock.forward,
+kernel.py:177-357): fp16 q/k/v projections, attention scale, RoPE and the cast
+to the wire, rotate, append, attend over ctx 32,768, to_float and W_o', with
+seeded random fp16 weights; 20 blocks (weights and caches, more than the
+Infinity Cache in total) rotate between steps.
 """
 
 from __future__ import annotations
@@ -63,7 +69,7 @@ def _args():
     ap.add_argument("--ctx", type=int, default=CTX)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "prefill"])
+    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "prefill", "block"])
     ap.add_argument("--prompt", type=int, default=4096)
     ap.add_argument("--c1-layers", type=int, default=16)
     ap.add_argument("--c1-steps", type=int, default=4096)
@@ -393,6 +399,106 @@ def bench_prefill(a) -> int:
     return 0 if bad == 0 else 1
 
 
+LLAMA32_1B_HF = {"hidden_size": 2048, "num_attention_heads": 32, "num_key_value_heads": 8,
+                 "head_dim": 64, "rope_theta": 500000.0, "max_position_embeddings": 131072,
+                 "rope_scaling": {"rope_type": "llama3", "factor": 32.0, "low_freq_factor": 1.0,
+                                  "high_freq_factor": 4.0, "original_max_position_embeddings": 8192}}
+
+
+def bench_block(a) -> int:
+    """One decode token through the whole block: hidden (1, 2048) float32 in,
+    (1, 2048) out; the last step of the last block checked against the oracle."""
+    import torch
+
+    from insitu_amd import ModelConfig, QuantConfig
+    from insitu_amd.block import AttentionBlock
+    from insitu_amd.host import Weights
+    from insitu_amd.runtime import default_context
+    from oracle import host as oh
+    from oracle import native
+    from oracle.quantize import Format
+    from oracle.rotate import rotate, signs_from_seed
+
+    ctx = default_context(0)
+    # Llama-3.2-1B's attention shape and RoPE (theta 5e5, llama3 scaling, 131,072
+    # positions): the decode tokens sit at positions 32,767 and on
+    model = ModelConfig.from_hf(LLAMA32_1B_HF)
+    quant = QuantConfig(key_bits=4, value_bits=2)
+    n_total = a.warmup + a.steps
+    per_block = (n_total + a.caches - 1) // a.caches
+    wl_rng = np.random.default_rng(0)
+    blocks = []
+    from insitu_amd.workload import Workload
+    _, kr_src, vr_src = Workload(seed=0).steps(a.ctx - 1)
+    for b in range(a.caches):
+        blk = AttentionBlock(model, quant, capacity=a.ctx - 1 + per_block, ctx=ctx)
+        blk.weights = Weights.random(model, blk.rotation, seed=b, ctx=ctx)
+        if b == 0:
+            kr = blk.rotation.apply(kr_src[0], ctx)
+            vr = blk.rotation.apply(vr_src[0], ctx)
+        blk.cache.append_rotated(kr, vr)
+        blocks.append(blk)
+    del kr_src, vr_src
+    x = torch.from_numpy(wl_rng.standard_normal((n_total, model.hidden_size)).astype(np.float32)
+                         * 0.02).to(ctx.torch_device)
+    ys = [None] * n_total
+
+    def step(i):
+        blk = blocks[i % a.caches]
+        ys[i], _ = blk.forward(x[i], stats=False)
+
+    for i in range(a.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(a.warmup, n_total):
+        step(i)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / a.steps
+    # the last step of its block: wire taps = the oracle's seam on the GPU's own
+    # projections; out = the online softmax over the block's device rows; y to the
+    # fp32 bound of the output GEMM
+    last = n_total - 1
+    blk = blocks[last % a.caches]
+    taps = {k: t.cpu().numpy() for k, t in blk.taps.items()}
+    pos = blk.cache.length - 1
+    p = blk.host.project_qkv(x[last]).cpu().numpy()
+    sc = model.rope_scaling
+    cos, sin = oh.rope_tables(D, model.max_position, model.rope_theta,
+                              scaling=oh.RopeScaling(sc.factor, sc.low_freq_factor, sc.high_freq_factor,
+                                                     sc.original_max_position))
+    (wq, wk, wv), _ = oh.seam(p, N_Q, N_KV, D, [pos], cos, sin)
+    bad = int(not (np.array_equal(taps["wire.q"], wq) and np.array_equal(taps["wire.k"], wk)
+                   and np.array_equal(taps["wire.v"], wv)))
+    sg = signs_from_seed(D, 0, 1)
+    qr = rotate(wq[0], sg)
+    fmt = Format()
+    want = np.concatenate([native.attend_online(qr[4 * h:4 * h + 4], blk.cache.view(h), fmt)[0]
+                           for h in range(N_KV)])
+    bad += int(not np.array_equal(taps["out"].reshape(-1), want.reshape(-1)))
+    wo = blk.weights.o.cpu().numpy().view(np.float16).astype(np.float64)
+    a16 = oh.to_fp16(taps["out"].reshape(1, -1) / 65536.0).astype(np.float64)
+    exact = a16 @ wo.T
+    tol = 2.0 * wo.shape[1] * 2.0 ** -24 * (np.abs(a16) @ np.abs(wo).T)
+    bad += int(not np.all(np.abs(ys[last].cpu().numpy().astype(np.float64) - exact) <= tol))
+    weights_mb = sum(b.weights.qkv.numel() * 2 + b.weights.o.numel() * 2 for b in blocks) / 2 ** 20
+    cache_mb = sum(b.cache.layout()["device_total_bytes"] for b in blocks) / 2 ** 20
+    res = {
+        "metric": "attention block decode step (hidden in -> hidden out) at ctx 32k, 1 GPU",
+        "value": round(wall * 1e6, 2), "unit": "us/token", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "higher_is_better": False, "dtype": "fp16 GEMMs, int64 seam",
+        "data": "synthetic (seeded N(0,1) fp16 weights / sqrt(hidden); hidden states N(0,1) x 0.02; "
+                "cache rows from the C2 generator)",
+        "config": {"workload": "Llama-3.2-1B-shape attention block, batch 1, ctx 32768, 4b K / 2b V, "
+                               "AttentionBlock.forward per token (projections, RoPE, cast, rotate, "
+                               "append, attend, W_o')",
+                   "rotating_blocks": a.caches, "rotating_mb": round(weights_mb + cache_mb, 1)},
+        "check_failures": bad,
+    }
+    print(json.dumps(res))
+    return 0 if bad == 0 else 1
+
+
 def _kv_only(wl, n):
     """k and v (1, n, Hkv, d) of the workload's distribution, without q."""
     from insitu_amd.workload import to_fixed
@@ -414,6 +520,8 @@ def main() -> int:
         return bench_c1(a)
     if a.config == "prefill":
         return bench_prefill(a)
+    if a.config == "block":
+        return bench_block(a)
     if a.config != "c2":
         return bench_scale(a)
     import torch

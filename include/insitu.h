@@ -189,7 +189,9 @@ int insitu_project(insitu_ctx *ctx, const uint16_t *w_dev, int32_t out_f, int32_
  * wire rows q_dev (n, n_q, d), k/v_dev (n, n_kv, d) int32 Q8.16 (RoPE's output is
  * not clamped, as in the reference). counts_host (2) may be NULL; otherwise the call
  * synchronises and returns {values saturated by to_fixed, rows whose position is
- * beyond the table}, and ERANGE when the second is not 0. */
+ * beyond the table}, and ERANGE when the second is not 0. With counts_host NULL the
+ * call is stream-ordered and checks nothing on the device: the caller keeps every
+ * position in [0, max_pos) (a q/k row at a position beyond it is left unwritten). */
 int insitu_seam_wire(insitu_ctx *ctx, const float *p_dev, const float *bias_dev, int64_t n, int32_t n_q,
                      int32_t n_kv, int32_t d, const int64_t *pos_dev, const int64_t *cos_dev,
                      const int64_t *sin_dev, int64_t max_pos, int32_t frac, double attn_scale,

@@ -153,13 +153,15 @@ class AttentionBlock:
                                   ctx=self.ctx)
         return self._host
 
-    def forward(self, hidden_states, positions=None):
+    def forward(self, hidden_states, positions=None, *, stats: bool = True):
         """kernel.py:177-357, batch == 1: (tokens, hidden) float32 in, (tokens,
         hidden) float32 out (a torch tensor on the device), and a StepReport.
 
         positions default to cache.length .. cache.length + tokens - 1. The
         wire rows and the Q16 `out` rows are kept in self.taps ("wire.q",
-        "wire.k", "wire.v", "out"), the reference's tap points.
+        "wire.k", "wire.v", "out"), the reference's tap points. stats=False
+        leaves the report's counters empty and the step stream-ordered (the
+        counters are the only values read back before the output).
         """
         import torch
         m = self.model
@@ -178,19 +180,23 @@ class AttentionBlock:
         if positions.shape != (n,):
             raise ValueError(f"expected {n} positions, got {positions.shape}")
         host = self.host
-        qi, ki, vi = host.wire(x, positions)
+        qi, ki, vi = host.wire(x, positions, counts=stats)
         self.taps = {"wire.q": qi, "wire.k": ki, "wire.v": vi}
-        report = StepReport(n_tokens=n, saturated=host.last_saturated,
-                            conversions=n * (m.num_heads + 2 * m.num_kv_heads) * m.head_dim)
+        report = StepReport(n_tokens=n)
+        if stats:
+            report.saturated = host.last_saturated
+            report.conversions = n * (m.num_heads + 2 * m.num_kv_heads) * m.head_dim
         if n > 1 and not self.force_token_loop:
-            out = self.prefill(qi, ki, vi)
+            out = self.prefill(qi, ki, vi, stats=stats)
             report.attention = self.last_stats
         else:
-            rows, report.attention = [], AttentionStats()
+            rows = []
+            report.attention = AttentionStats() if stats else None
             for t in range(n):
-                rows.append(self.step(qi[t][None], ki[t][None], vi[t][None]))
-                report.attention.merge(self.last_stats)
-            out = torch.cat(rows, dim=0)
+                rows.append(self.step(qi[t][None], ki[t][None], vi[t][None], stats=stats))
+                if stats:
+                    report.attention.merge(self.last_stats)
+            out = rows[0] if n == 1 else torch.cat(rows, dim=0)
         self.taps["out"] = out
         report.context = base + n
         return host.output(out), report

@@ -49,6 +49,42 @@ class ModelConfig:
         return self.num_kv_heads * self.head_dim
 
     @classmethod
+    def from_hf(cls, hf_config) -> "ModelConfig":
+        """config.py:78-120: from a transformers config (or anything duck-typed, a
+        dict included). rope_theta is read top-level or from rope_parameters and
+        never defaulted; "default" and "llama3" RoPE are modelled, any other
+        scaling type is refused."""
+        from .host import RopeScaling
+        get = (lambda k, d=None: hf_config.get(k, d)) if isinstance(hf_config, dict) \
+            else (lambda k, d=None: getattr(hf_config, k, d))
+        theta = get("rope_theta")
+        params = get("rope_parameters") or {}
+        if theta is None:
+            theta = params.get("rope_theta")
+        if theta is None:
+            raise ValueError("config exposes neither `rope_theta` nor `rope_parameters['rope_theta']`; "
+                             "pass ModelConfig directly rather than defaulting a value that decides "
+                             "token positions")
+        if not params and isinstance(get("rope_scaling"), dict):
+            params = get("rope_scaling")
+        rope_type = params.get("rope_type") or params.get("type") or "default"
+        if rope_type == "llama3":
+            scaling = RopeScaling.from_hf(params)
+        elif rope_type == "default":
+            scaling = None
+        else:
+            raise NotImplementedError(f"RoPE scaling {rope_type!r} is not modelled")
+        return cls(hidden_size=get("hidden_size"), num_heads=get("num_attention_heads"),
+                   num_kv_heads=get("num_key_value_heads", get("num_attention_heads")),
+                   head_dim=get("head_dim"), rope_theta=float(theta),
+                   max_position=get("max_position_embeddings", 4096), rope_scaling=scaling)
+
+    @classmethod
+    def tinyllama(cls) -> "ModelConfig":
+        """config.py:122-125: TinyLlama-1.1B."""
+        return cls(hidden_size=2048, num_heads=32, num_kv_heads=4, head_dim=64)
+
+    @classmethod
     def llama32_1b(cls) -> "ModelConfig":
         """Llama-3.2-1B attention shape (hw/vectors.py:831)."""
         return cls(hidden_size=2048, num_heads=32, num_kv_heads=8, head_dim=64)

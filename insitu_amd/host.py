@@ -94,7 +94,8 @@ def fold_o_proj(o_proj, rotation_matrix: np.ndarray, num_heads: int) -> np.ndarr
 
 class Weights:
     """weights.py:32-133: fp16 W_q | W_k | W_v stacked (the checkpoint's (out, in) layout),
-    fp16 W_o' (R^-1 folded), fp32 biases; device-resident."""
+    fp16 W_o' (R^-1 folded), fp32 biases; device-resident. rotation_matrix is the
+    cache's Rotation or its dense matrix (R_last ... R_0)."""
 
     def __init__(self, q, k, v, o, model, rotation_matrix, *, q_bias=None, k_bias=None,
                  v_bias=None, o_bias=None, ctx=None) -> None:
@@ -110,6 +111,8 @@ class Weights:
                 raise ValueError(f"W_{name} is {np.shape(arr)}, expected {shapes[name]}")
         f16 = lambda a: np.asarray(a, dtype=np.float16)
         qkv = np.concatenate([f16(q), f16(k), f16(v)])
+        if hasattr(rotation_matrix, "matrix"):              # a Rotation
+            rotation_matrix = rotation_matrix.matrix()
         o_folded = f16(fold_o_proj(o, rotation_matrix, model.num_heads))
         dev = self.ctx.torch_device
         self.qkv = torch.from_numpy(qkv.view(np.int16)).to(dev)
@@ -174,7 +177,12 @@ class HostHalf:
         m = self.model
         p = self.project_qkv(x)
         n = p.shape[0]
-        pos = self.ctx.to_device(np.asarray(positions, dtype=np.int64).reshape(n), torch.int64)
+        positions = np.asarray(positions, dtype=np.int64).reshape(n)
+        if n and (positions.min() < 0 or positions.max() >= m.max_position):
+            # rope.py:163-167; checked here so that counts=False needs no read-back
+            raise _lib.FormatError(_lib.ERANGE, f"position {int(positions.max())} beyond the RoPE "
+                                   f"table (max_position {m.max_position})")
+        pos = self.ctx.to_device(positions, torch.int64)
         dev = self.ctx.torch_device
         q = torch.empty((n, m.num_heads, m.head_dim), dtype=torch.int32, device=dev)
         k = torch.empty((n, m.num_kv_heads, m.head_dim), dtype=torch.int32, device=dev)

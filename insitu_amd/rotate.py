@@ -64,6 +64,17 @@ class Rotation:
             out.append((w[0], w[1]))
         return out
 
+    def matrix(self) -> np.ndarray:
+        """rotate.py:233-251: the dense float64 form R_last ... R_0 (H * signs / sqrt d
+        per round, round 0 applied first), for folding into W_o; never on a hot path."""
+        h = np.array([[1.0]])
+        while h.shape[0] < self.d:
+            h = np.block([[h, h], [h, -h]])
+        m = np.eye(self.d)
+        for r in range(self.rounds):
+            m = ((h * self.signs[r]) / np.sqrt(self.d)) @ m
+        return m
+
     def fill_format(self, f: "_lib.Format") -> None:
         if self.rounds > 8:
             raise ValueError("at most 8 rotation rounds fit the descriptor")

@@ -782,3 +782,31 @@ def test_block_prefill_equals_the_decode_loop(ctx, softmax):
     got_b = pre.forward_seam(q[30:], k[30:], v[30:])          # continues at base 30
     np.testing.assert_array_equal(np.concatenate([got_a, got_b]), want)
     np.testing.assert_array_equal(pre.cache.buf, loop.cache.buf)
+
+
+# -- cache image interop -----------------------------------------------------------
+
+def test_cache_image_round_trip_and_device_diff(ctx, fixture_cache):
+    """ddr_layout.py:227-257, CMD_LOAD and experiments/cache_diff.py: the golden
+    plane image installed verbatim into a fresh cache reads back as the golden
+    rows and attends to the golden output; the device diff of a cache against
+    its own rows matches, and a byte planted in the host's copy is named."""
+    from insitu_amd.attention import CompressedAttention
+    from insitu_amd.interop import DdrLayout, diff_device_cache
+    c0, rows = fixture_cache
+    c = _cache(ctx, 65)
+    lay = DdrLayout.for_cache(c)
+    img = lay.image(rows)
+    np.testing.assert_array_equal(img, hx.bytes_rows("ddr_image.hex").reshape(-1))
+    c.load_image(img)
+    c.set_length(65)
+    np.testing.assert_array_equal(c.buf, rows)
+    np.testing.assert_array_equal(c.image(), img)
+    q = hx.lanes("rot_q.hex", 24, 64)
+    out, _ = CompressedAttention(c).attend(q[None], "online")
+    np.testing.assert_array_equal(out.cpu().numpy().reshape(-1), hx.lanes("out.online.hex", 24, 2048)[0])
+    assert diff_device_cache(c, rows).match
+    host = rows.copy()
+    host[17, 6, 49] ^= 4
+    rep = diff_device_cache(c0, host)
+    assert [(r.head, r.token, r.fields) for r in rep.rows] == [(6, 17, ["norms"])]

@@ -159,3 +159,80 @@ def test_host_half_tables_and_fold_match_the_oracle():
     np.testing.assert_allclose(fold_o_proj(wo, matrix(sg), 3), oh.fold_o_proj(wo, sg, 3), rtol=0, atol=1e-12)
     with pytest.raises(ValueError):
         fold_o_proj(wo, matrix(sg), 2)
+
+
+def _ddr_fixture():
+    import json
+    from insitu_amd.interop import DdrLayout
+    with open(os.path.join(ROOT, "tests", "golden", "tb_vectors", "ddr_map.json")) as f:
+        d = json.load(f)
+    lay = DdrLayout.from_describe(d, ((0, 32), (32, 48), (48, 52)))
+    rows = np.stack([hx.bytes_rows(f"cache_rows_h{h}.hex") for h in range(8)], axis=1)
+    return d, lay, rows
+
+
+def test_interop_layout_builds_the_golden_ddr_image_and_inverts_it():
+    """hw/ddr_layout.py:227-274: the product's address map against ddr_map.json and
+    ddr_image.hex; rows() and row_at() invert image()."""
+    d, lay, rows = _ddr_fixture()
+    assert lay.describe() == d
+    img = lay.image(rows)
+    np.testing.assert_array_equal(img, hx.bytes_rows("ddr_image.hex").reshape(-1))
+    np.testing.assert_array_equal(lay.rows(img, 65), rows)
+    for h, t in ((0, 0), (7, 64), (3, 31)):
+        np.testing.assert_array_equal(lay.row_at(img, h, t), rows[t, h])
+    with pytest.raises(ValueError):
+        lay.image(rows[:, :7])
+    with pytest.raises(ValueError):
+        lay.rows(img[:100], 65)
+
+
+def test_cache_diff_names_the_field_of_every_differing_row():
+    """experiments/cache_diff.py:91-121: a planted byte in each field is reported
+    at its (head, token) with the field it lies in; equal caches match."""
+    from insitu_amd.interop import cache_diff
+    _, lay, rows = _ddr_fixture()
+    assert cache_diff(rows, rows.copy(), lay.fields).match
+    bad = rows.copy()
+    bad[5, 2, 3] ^= 0x10          # key codes
+    bad[64, 7, 40] ^= 1           # value codes
+    bad[0, 0, 50] ^= 0x80         # norms
+    bad[9, 4, [0, 33]] ^= 1       # key and value
+    rep = cache_diff(bad, rows, lay.fields)
+    got = [(r.head, r.token, r.fields, r.n_bytes) for r in rep.rows]
+    assert got == [(0, 0, ["norms"], 1), (2, 5, ["key"], 1), (4, 9, ["key", "value"], 2),
+                   (7, 64, ["value"], 1)]
+    assert "key+value+norms" in rep.verdict()
+    with pytest.raises(ValueError):
+        cache_diff(bad[:3], rows, lay.fields)
+
+
+def test_product_rotation_matrix_is_the_oracles():
+    from insitu_amd.rotate import Rotation
+    from oracle.rotate import matrix, signs_from_seed
+    for d, rounds in ((64, 1), (128, 2)):
+        r = Rotation.from_seed(d, 0, rounds)
+        np.testing.assert_array_equal(r.matrix(), matrix(signs_from_seed(d, 0, rounds)))
+        np.testing.assert_allclose(r.matrix() @ r.matrix().T, np.eye(d), atol=1e-12)
+
+
+def test_model_config_from_hf_reads_rope_settings_or_refuses():
+    """config.py:78-120: theta top-level or nested, llama3 scaling modelled, other
+    scaling types refused, a missing theta refused rather than defaulted."""
+    from insitu_amd import ModelConfig
+    from insitu_amd.host import RopeScaling
+    llama = {"hidden_size": 2048, "num_attention_heads": 32, "num_key_value_heads": 8, "head_dim": 64,
+             "rope_theta": 500000.0, "max_position_embeddings": 131072,
+             "rope_scaling": {"rope_type": "llama3", "factor": 32.0, "low_freq_factor": 1.0,
+                              "high_freq_factor": 4.0, "original_max_position_embeddings": 8192}}
+    m = ModelConfig.from_hf(llama)
+    assert (m.num_kv_heads, m.head_dim, m.max_position, m.rope_theta) == (8, 64, 131072, 500000.0)
+    assert m.rope_scaling == RopeScaling(32.0, 1.0, 4.0, 8192)
+    nested = {k: v for k, v in llama.items() if k not in ("rope_theta", "rope_scaling")}
+    nested["rope_parameters"] = {"rope_theta": 1e4, "rope_type": "default"}
+    m = ModelConfig.from_hf(nested)
+    assert m.rope_theta == 1e4 and m.rope_scaling is None
+    with pytest.raises(ValueError):
+        ModelConfig.from_hf({k: v for k, v in nested.items() if k != "rope_parameters"})
+    with pytest.raises(NotImplementedError):
+        ModelConfig.from_hf(dict(llama, rope_scaling={"rope_type": "yarn", "factor": 4.0}))
