@@ -14,8 +14,12 @@
 //     acc = floor(acc * f / 2^15) + S,   l = floor(l * f / 2^15) + L
 // over the runs in order is exactly the reference recurrence, provided the
 // per-token int32 clamp of acc (attention.py:502-503) never fires; that is
-// proven per run from a bound on |acc| plus the sum of per-term bounds, and a
-// head whose bound fails is recomputed on the serial path (serial_head.h).
+// proven per run from the exact acc where the run starts plus the largest
+// |prefix sum| of the run's terms (measured, per channel in chunk 0, over all
+// channels in the published runs), and a head where it fails is recomputed on
+// the serial path (serial_head.h). A run's prefix sums are kept in wrapping
+// int32, exact because the sum of their |terms| stays below 2^31 (else the
+// chunk flags the head wide and it goes serial too).
 //
 // Sequential (online) mode is one kernel. Workgroups are numbered chunk-major
 // (all chunk-0 workgroups, then all chunk-1 ...), score their chunk (lane =
@@ -68,6 +72,10 @@ constexpr unsigned long long ST_FLAGS = 3ull << 62;
 constexpr int EPOCH_BITS = 14;
 constexpr unsigned EPOCH_MASK = (1u << EPOCH_BITS) - 1u;
 constexpr int SPIN_LIMIT = 1 << 20;
+// A run whose sum of |term| bounds stays at or below this publishes that bound as
+// its peak |prefix sum|; only blocks of entries where a run may exceed it track
+// the actual prefix sums (sequential mode: flat softmax over large values).
+constexpr int64_t TRACK_B = 1ll << 24;
 constexpr double MAGIC = 6755399441055744.0;   // 1.5 * 2^52
 constexpr int64_t MAGIC_BITS = 0x4338000000000000LL;
 
@@ -76,7 +84,8 @@ constexpr int64_t MAGIC_BITS = 0x4338000000000000LL;
 // chunk, all heads). w0 is the flag the replaying workgroup polls: it goes out
 // after the head's run slots and w1 have completed. A run slot
 // holds lf = L | f << 32 (L = sum of p < 2^26, f = the factor opening the run,
-// <= 2^15) and b = B, the bound on |run sum| (< 2^31 unless FLAG_WIDE is set).
+// <= 2^15) and b = the largest |prefix sum| of the run over its tokens and
+// channels (sequential mode; the sum of |terms| is < 2^31 unless FLAG_WIDE is set).
 // Everything published between workgroups goes through relaxed agent-scope
 // atomics, which are coherent across the XCDs without writing back or
 // invalidating whole L2 caches.
@@ -98,6 +107,24 @@ __device__ __forceinline__ uint64_t get64(const void *p) {
 }
 __device__ __forceinline__ uint32_t get32(const void *p) {
     return __hip_atomic_load((uint32_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// The clamp certificate of one run: acc at its start plus every prefix sum of the
+// run stays within int32 when |acc| + peak <= 2^31 - 1, peak = max |prefix sum|
+// (0 <= peak < 2^31). In 32-bit unsigned: |acc| <= 2^31 - 1 - peak.
+__device__ __forceinline__ bool fits(int32_t acc, int32_t peak) {
+    const uint32_t a = acc < 0 ? 0u - (uint32_t)acc : (uint32_t)acc;
+    return a <= 0x7FFFFFFFu - (uint32_t)peak;
+}
+__device__ __forceinline__ int32_t run_peak(int32_t hi, int32_t lo) {
+    const uint32_t h = (uint32_t)hi, l = 0u - (uint32_t)lo;      // hi >= 0 >= lo
+    return (int32_t)(h > l ? h : l);
+}
+template <int N>
+__device__ __forceinline__ int64_t peak_of(const int32_t (&hi)[N], const int32_t (&lo)[N]) {
+    int32_t m = run_peak(hi[0], lo[0]);
+#pragma unroll
+    for (int k = 1; k < N; ++k) m = run_peak(hi[k], lo[k]) > m ? run_peak(hi[k], lo[k]) : m;
+    return m;
 }
 // Wait until this thread's stores (the relaxed atomics above) have completed.
 __device__ __forceinline__ void stores_done() {
@@ -795,9 +822,9 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
 
         // -- phase 4: run sums over the candidate list, wave = head, lane = channel -
         // Chunk 0 starts the sequence (acc = l = 0), so it replays its own runs
-        // here: acc, l and R (the bound on |acc|) after its last token stand in
-        // for all its runs. Every later chunk publishes its runs.
-        // acc stays in 32 bits in sequential mode: |acc| <= R <= 2^31 - 1
+        // here: acc and l after its last token stand in for all its runs. Every
+        // later chunk publishes its runs. acc stays in 32 bits in sequential
+        // mode: |acc at a run's start| + the run's largest |prefix sum| <= 2^31 - 1
         // whenever the result is used (past a failed check the head goes to the
         // serial path); two-pass sums need 64.
         using AccT = typename std::conditional<SEQ, int32_t, int64_t>::type;
@@ -805,7 +832,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
         AccT acc0[CPL];
 #pragma unroll
         for (int k = 0; k < CPL; ++k) acc0[k] = 0;
-        int64_t l0 = 0, R0 = 0;
+        int64_t l0 = 0;
         int n_ev0 = 0, flags0 = 0;
         if (ok && wv < GF) {
             const int h = wv;
@@ -836,17 +863,18 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                 const int64_t dm = tabs->delta_max;
                 SegMeta *meta = ck.meta + ((int64_t)chain * GF + h) * ck.pool + off;
                 int32_t *segS = ck.segS + (((int64_t)chain * GF + h) * ck.pool + off) * D;
-                // P: the running sum of the terms (wrapping int32), P0 its value
-                // where the open run began; a run's sum is their difference, exact
-                // because |run sum| <= B < 2^31 unless FLAG_WIDE is set.
-                int32_t P[CPL], P0[CPL];
+                // P: the open run's sum of terms so far, in int32: exact, because
+                // |every prefix sum| <= B < 2^31 unless FLAG_WIDE is set.
+                // hiP, loP: per channel, the largest and smallest P over the open run
+                int32_t P[CPL], hiP[CPL], loP[CPL];
 #pragma unroll
-                for (int k = 0; k < CPL; ++k) P[k] = P0[k] = 0;
+                for (int k = 0; k < CPL; ++k) P[k] = hiP[k] = loP[k] = 0;
                 int seg = 0;                  // runs closed so far
                 int64_t Lc = 0, Bc = 0;       // sums of p and of the term bounds so far
                 int64_t Ls = 0, Bs = 0;       // the same where the open run began
                 int64_t fkey = 0;             // the open run's event: (entry + 1) << 16 | f
                 bool wide = false;
+                bool trk_prev = false;        // the previous block of entries tracked prefix sums
                 for (int a0 = 0; a0 < n_act; a0 += 64) {
                     // Lane = entry: decode entry a0 + lane. An event's p is LUT(0)
                     // and its LUT value is the factor f opening its run; a candidate
@@ -882,9 +910,23 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                                                      (uint32_t)(evm >> 32),
                                                      __builtin_amdgcn_mbcnt_lo((uint32_t)evm, 0u));
                             pub64(&meta[ri].lf, (uint64_t)Lr | ((uint64_t)(kb & 0xFFFF) << 32));
-                            pub64(&meta[ri].b, (uint64_t)Br);
                         }
                     }
+                    // Tracking: any run with entries in this block has a bound of at
+                    // most B (block end) - B (where the run open at the block start
+                    // began). A run that starts tracking mid-way bounds its earlier
+                    // prefix sums by its bound so far; one that tracks keeps tracking
+                    // to its end, since its bound only grows.
+                    const bool trk = SEQ && readlane64(bp, 63) - Bs > TRACK_B;
+                    if (trk && !trk_prev) {
+                        const int32_t b0 = (int32_t)(Bc - Bs);    // <= TRACK_B
+#pragma unroll
+                        for (int k = 0; k < CPL; ++k) {
+                            hiP[k] = hiP[k] > b0 ? hiP[k] : b0;
+                            loP[k] = loP[k] < -b0 ? loP[k] : -b0;
+                        }
+                    }
+                    trk_prev = trk;
                     Lc = readlane64(lp, 63);
                     Bc = readlane64(bp, 63);
                     if (evm) {
@@ -917,28 +959,39 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                                 if ((evm >> j) & 1ull) {
                                     // the event closes the open run
                                     if (own) {
-                                        // acc = floor((acc + S) * f / 2^15), and l and R alike
+                                        // no clamp inside the run, then
+                                        // acc = floor((acc + S) * f / 2^15), and l alike
                                         const int64_t f = (uint32_t)__builtin_amdgcn_readlane(val_i, j);
                                         l0 = ((l0 + readlane64(Lr, j)) * f) >> PROB_FRAC;
-                                        R0 += readlane64(Br, j);
-                                        if (R0 > ACC_HI) wide = true;
-                                        R0 = ((R0 * f) >> PROB_FRAC) + 1;
+                                        const int32_t bj = (int32_t)readlane64(Br, j);
 #pragma unroll
-                                        for (int k = 0; k < CPL; ++k)
-                                            acc0[k] = (AccT)(((int64_t)(AccT)(acc0[k] + (AccT)(P[k] - P0[k])) * f) >> PROB_FRAC);
+                                        for (int k = 0; k < CPL; ++k) {
+                                            if (SEQ && !fits(acc0[k], trk ? run_peak(hiP[k], loP[k]) : bj)) wide = true;
+                                            acc0[k] = (AccT)(((int64_t)(AccT)(acc0[k] + (AccT)P[k]) * f) >> PROB_FRAC);
+                                        }
                                     } else {
 #pragma unroll
                                         for (int k = 0; k < CPL; ++k)
-                                            pub32(&segS[(int64_t)seg * D + lane + 64 * k], (uint32_t)(P[k] - P0[k]));
+                                            pub32(&segS[(int64_t)seg * D + lane + 64 * k], (uint32_t)P[k]);
+                                        if (SEQ) {
+                                            const int64_t m = trk ? wave_max_i64(peak_of<CPL>(hiP, loP))
+                                                                  : readlane64(Br, j);
+                                            if (lane == 0) pub64(&meta[seg].b, (uint64_t)m);
+                                        }
                                     }
 #pragma unroll
-                                    for (int k = 0; k < CPL; ++k) P0[k] = P[k];
+                                    for (int k = 0; k < CPL; ++k) P[k] = hiP[k] = loP[k] = 0;
                                     ++seg;
                                 }
                                 const int32_t w = __builtin_amdgcn_readlane(w_i, j);
 #pragma unroll
-                                for (int k = 0; k < CPL; ++k)
+                                for (int k = 0; k < CPL; ++k) {
                                     P[k] += (int32_t)(((int64_t)w * cv[jj][k]) >> acc_shift);
+                                    if (SEQ && trk) {
+                                        hiP[k] = P[k] > hiP[k] ? P[k] : hiP[k];
+                                        loP[k] = P[k] < loP[k] ? P[k] : loP[k];
+                                    }
+                                }
                             }
                         }
                     }
@@ -947,18 +1000,23 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                 wide = wide || Bc - Bs > ACC_HI;
                 if (own) {
 #pragma unroll
-                    for (int k = 0; k < CPL; ++k) acc0[k] += (AccT)(P[k] - P0[k]);
+                    for (int k = 0; k < CPL; ++k) {
+                        if (SEQ && !fits(acc0[k], trk_prev ? run_peak(hiP[k], loP[k])
+                                                           : (int32_t)(Bc - Bs > ACC_HI ? ACC_HI : Bc - Bs)))
+                            wide = true;
+                        acc0[k] += (AccT)P[k];
+                    }
                     l0 += Lc - Ls;
-                    R0 += Bc - Bs;
-                    if (SEQ && R0 > ACC_HI) wide = true;
                 } else {
+                    const int64_t m = !SEQ ? 0 : trk_prev ? wave_max_i64(peak_of<CPL>(hiP, loP))
+                                                          : (Bc - Bs > ACC_HI ? ACC_HI : Bc - Bs);
                     if (lane == 0) {
                         pub64(&meta[seg].lf, (uint64_t)(Lc - Ls) | ((uint64_t)(fkey & 0xFFFF) << 32));
-                        pub64(&meta[seg].b, (uint64_t)(Bc - Bs));
+                        pub64(&meta[seg].b, (uint64_t)m);
                     }
 #pragma unroll
                     for (int k = 0; k < CPL; ++k)
-                        pub32(&segS[(int64_t)seg * D + lane + 64 * k], (uint32_t)(P[k] - P0[k]));
+                        pub32(&segS[(int64_t)seg * D + lane + 64 * k], (uint32_t)P[k]);
                 }
                 if (__ballot(wide)) flags |= FLAG_WIDE;
             }
@@ -997,8 +1055,8 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
         __syncthreads();
         const bool last = S.last != 0;
         if (own && !last && wv < GF) {
-            // chunk 0's state in its slot: acc (|acc| < 2^31 whenever it is used),
-            // l | events << 32, and R
+            // chunk 0's state in its slot: acc (|acc| < 2^31 whenever it is used)
+            // and l | events << 32
             const int h = wv;
             const int64_t base = (int64_t)chain * GF + h;
 #pragma unroll
@@ -1006,7 +1064,6 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             ChunkHdr *hp = &ck.hdr[((int64_t)chain * ck.max_chunks) * GF + h];
             if (lane == 0) {
                 pub64(&ck.meta[base * ck.pool].lf, (uint64_t)(uint32_t)l0 | ((uint64_t)(uint32_t)n_ev0 << 32));
-                pub64(&ck.meta[base * ck.pool].b, (uint64_t)R0);
                 pub64(&hp->w1, ok ? S.mabs : 0ull);
             }
             stores_done();
@@ -1022,7 +1079,8 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             AccT aw[CPL];
 #pragma unroll
             for (int k = 0; k < CPL; ++k) aw[k] = 0;
-            int64_t l = 0, R = 0;
+            int64_t l = 0;
+            bool unsafe = false;                  // a run's certificate failed (sequential mode)
             unsigned long long events = 0;
             bool fb = !ok;
             const bool hdr_stats = ok;
@@ -1041,7 +1099,6 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
 #pragma unroll
                     for (int k = 0; k < CPL; ++k) aw[k] = acc0[k];
                     l = l0;
-                    R = R0;
                     events = (unsigned long long)n_ev0;
                     flags = flags0;
                     if (h == 0 && lane == 0) {
@@ -1067,7 +1124,6 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                         const uint64_t lf = get64(&meta[0].lf);
                         l = (int64_t)(uint32_t)lf;
                         events = lf >> 32;
-                        R = (int64_t)get64(&meta[0].b);
                         if (h == 0 && lane == 0) {
                             ovf = (int64_t)((h0 >> 24) & 0xFFFF);
                             mabs = (int64_t)get64(&hdr[0].w1);
@@ -1119,13 +1175,11 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                 fb = __builtin_amdgcn_readfirstlane((int)fb) != 0;
                 wave_sync();
                 // The walk, SB runs at a time. Lane i < SB holds run i's list entry
-                // and loads its L, f and B; every lane loads its channels' run sums
-                // (the slot ids read back with readlane). Within a stretch of runs
-                // without an event acc, l and R only add, and R only grows, so per
-                // run the walk does one add per channel; l and R are brought up to
-                // date from lane prefix sums at each event (before its rescale) and
-                // at the end of the batch, and R is checked there: a run-by-run check
-                // could not fail anywhere else.
+                // and loads its L, f and largest |prefix sum| m; every lane loads its
+                // channels' run sums (the slot ids read back with readlane). Per run
+                // the walk checks |acc| + m against 2^31 (no clamp can fire inside
+                // it) and adds the run sum; l is brought up to date from lane prefix
+                // sums at each event (before its rescale) and at the end of the batch.
                 for (int g0 = 0; g0 < total && !fb; g0 += SB) {
                     const int nb = total - g0 < SB ? total - g0 : SB;     // uniform
                     const int nblk = (nb + 7) >> 3;                        // blocks of 8 runs
@@ -1163,8 +1217,22 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     const uint64_t evm = SEQ ? __ballot(mine && (ent & RUN_EVENT)) : 0ull;
                     // inclusive prefix sums of L and B over the batch's runs
                     const int64_t PL = wave_scan64<OpAdd64>(mine ? (int64_t)(uint32_t)mlf : 0, 0);
-                    const int64_t PB = wave_scan64<OpAdd64>(mine ? (int64_t)(uint32_t)mb : 0, 0);
-                    int64_t done_L = 0, done_B = 0;     // prefix sums already added to l, R
+                    int64_t done_L = 0;                 // prefix sum already added to l
+                    // |acc| only shrinks at a rescale (f <= 2^15) and grows by at most
+                    // a run's peak per run, so |acc at the batch start| + the sum of the
+                    // batch's peaks certifies every run at once; only where that bound
+                    // fails does the walk check run by run
+                    bool check_runs = false;
+                    if (SEQ) {
+                        const int64_t psum = wave_sum_i64(mine ? (int64_t)(uint32_t)mb : 0);
+                        int64_t amax = 0;
+#pragma unroll
+                        for (int k = 0; k < CPL; ++k) {
+                            const int64_t a = aw[k] < 0 ? -(int64_t)aw[k] : (int64_t)aw[k];
+                            amax = a > amax ? a : amax;
+                        }
+                        check_runs = __ballot(amax + psum > ACC_HI) != 0ull;
+                    }
 #pragma unroll
                     for (int blk = 0; blk < SB / 8; ++blk) {
                         if (blk < nblk) {
@@ -1172,20 +1240,20 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                             for (int i = 8 * blk; i < 8 * blk + 8; ++i) {
                                 if (SEQ && ((evm >> i) & 1ull)) {
                                     const int64_t pl = i ? readlane64(PL, i - 1) : 0;
-                                    const int64_t pb = i ? readlane64(PB, i - 1) : 0;
                                     l += pl - done_L;
-                                    R += pb - done_B;
                                     done_L = pl;
-                                    done_B = pb;
-                                    if (R > ACC_HI) fb = true;
                                     const int64_t f =
                                         (uint32_t)__builtin_amdgcn_readlane((int)(mlf >> 32), i);
 #pragma unroll
                                     for (int k = 0; k < CPL; ++k)
                                         aw[k] = (AccT)(((int64_t)aw[k] * f) >> PROB_FRAC);
                                     l = wmul(l, f) >> PROB_FRAC;
-                                    R = (wmul(R, f) >> PROB_FRAC) + 1;
                                     ++events;
+                                }
+                                if (SEQ && check_runs) {
+                                    const int32_t m = __builtin_amdgcn_readlane((int)(uint32_t)mb, i);
+#pragma unroll
+                                    for (int k = 0; k < CPL; ++k) unsafe = unsafe || !fits((int32_t)aw[k], m);
                                 }
 #pragma unroll
                                 for (int k = 0; k < CPL; ++k) aw[k] += (AccT)sv[i][k];
@@ -1193,8 +1261,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                         }
                     }
                     l += readlane64(PL, nb - 1) - done_L;
-                    R += readlane64(PB, nb - 1) - done_B;
-                    if (SEQ && R > ACC_HI) fb = true;
+                    if (SEQ && __ballot(unsafe)) fb = true;
                 }
             }
             int64_t acc[CPL];

@@ -234,6 +234,72 @@ def test_acc_clamp_path_is_exact(ctx):
         assert st.max_abs_score == max(s.max_abs_score for s in sts)
 
 
+def _flat_cache(ctx, T, seed=31):
+    """Flat attention (small q and k: every p near 2^15) over same-sign values, so acc
+    climbs about 465,000 per token towards the int32 clamp, across several chunks."""
+    rng = np.random.default_rng(seed)
+    k = rng.integers(-(1 << 16), 1 << 16, size=(T, 8, 64))
+    v = 400_000 + rng.integers(-20_000, 20_000, size=(T, 8, 64))
+    q = rng.integers(-(1 << 8), 1 << 8, size=(32, 64))
+    c = _cache(ctx, T)
+    c.append_rotated(k, v)
+    host = Cache(8, T, FMT)
+    host.append_rotated(k, v)
+    return c, host, q
+
+
+def _online_against_oracle(c, host, q):
+    from insitu_amd.attention import CompressedAttention
+    out, st = CompressedAttention(c).attend(q[None], "online")
+    want, sts = [], []
+    for h in range(8):
+        o, s = native.attend_online(q[4 * h:4 * h + 4], host.view(h), FMT)
+        want.append(o)
+        sts.append(s)
+    np.testing.assert_array_equal(out.cpu().numpy()[0], np.concatenate(want))
+    assert st.acc_overflows == sum(s.acc_overflows for s in sts)
+    assert st.rescale_events == sum(s.rescale_events for s in sts)
+    assert st.max_abs_acc == max(s.max_abs_acc for s in sts)
+    return st
+
+
+def test_flat_attention_near_the_clamp_stays_on_the_chunked_path(ctx):
+    """acc reaches 0.9 x 2^31 in the fifth chunk without clamping: the runs' measured
+    prefix sums certify it, so no head needs the serial path (a sum of |terms| bound
+    would not)."""
+    c, host, q = _flat_cache(ctx, 4500)
+    st = _online_against_oracle(c, host, q)
+    assert st.acc_overflows == 0 and st.max_abs_acc > 0.9 * 2 ** 31
+    assert st.serial_fallbacks == 0
+
+
+def test_a_clamp_in_a_later_chunk_falls_back_exactly(ctx):
+    """The clamp first fires past token 4,600 (chunk 4): the replay's per-run check
+    sends every head to the serial path, which clamps token by token."""
+    c, host, q = _flat_cache(ctx, 6000)
+    st = _online_against_oracle(c, host, q)
+    assert st.acc_overflows > 0 and st.serial_fallbacks == 32
+
+
+def test_small_queries_over_a_long_context_need_no_serial_path(ctx):
+    """Projections of small hidden states: |q| < 2^9 against the workload's keys and
+    values over 9,000 tokens, a nearly uniform softmax."""
+    from insitu_amd.workload import Workload
+    from insitu_amd.rotate import Rotation
+    T = 9000
+    _, k, v = Workload(seed=5).steps(T)
+    rot = Rotation.from_seed(64, 0, 1)
+    kr = rot.apply(k[0], ctx).cpu().numpy()
+    vr = rot.apply(v[0], ctx).cpu().numpy()
+    c = _cache(ctx, T)
+    c.append_rotated(kr, vr)
+    host = Cache(8, T, FMT)
+    host.append_rotated(kr, vr)
+    q = np.random.default_rng(6).integers(-(1 << 9), 1 << 9, size=(32, 64))
+    st = _online_against_oracle(c, host, q)
+    assert st.serial_fallbacks == 0
+
+
 def test_d128_3b3b_against_native_oracle(ctx):
     from insitu_amd.attention import CompressedAttention
     f = Format(d=128, key_bits=3, value_bits=3)
