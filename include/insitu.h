@@ -185,7 +185,8 @@ int insitu_project(insitu_ctx *ctx, const uint16_t *w_dev, int32_t out_f, int32_
  * of n tokens, bias_dev fp32 ((n_q + 2 n_kv) d) or NULL, added in fp32; q times
  * attn_scale in float64; then cast_after_rope = 0: to_fixed (ops/convert.py:44-57) and
  * RoPE in fixed point (ops/rope.py:144-174), or 1: RoPE in float64 (:176-198) and
- * to_fixed. cos/sin_dev int64 (max_pos, d/2) Q(frac); pos_dev int64 (n). Writes the
+ * to_fixed. cos/sin_dev int64 (max_pos, d/2) Q(frac); pos_dev int64 (n), or NULL for the
+ * consecutive positions pos0 .. pos0 + n - 1 (a decode step needs no upload). Writes the
  * wire rows q_dev (n, n_q, d), k/v_dev (n, n_kv, d) int32 Q8.16 (RoPE's output is
  * not clamped, as in the reference). counts_host (2) may be NULL; otherwise the call
  * synchronises and returns {values saturated by to_fixed, rows whose position is
@@ -193,7 +194,7 @@ int insitu_project(insitu_ctx *ctx, const uint16_t *w_dev, int32_t out_f, int32_
  * call is stream-ordered and checks nothing on the device: the caller keeps every
  * position in [0, max_pos) (a q/k row at a position beyond it is left unwritten). */
 int insitu_seam_wire(insitu_ctx *ctx, const float *p_dev, const float *bias_dev, int64_t n, int32_t n_q,
-                     int32_t n_kv, int32_t d, const int64_t *pos_dev, const int64_t *cos_dev,
+                     int32_t n_kv, int32_t d, const int64_t *pos_dev, int64_t pos0, const int64_t *cos_dev,
                      const int64_t *sin_dev, int64_t max_pos, int32_t frac, double attn_scale,
                      int32_t cast_after_rope, int32_t *q_dev, int32_t *k_dev, int32_t *v_dev,
                      unsigned long long *counts_host);

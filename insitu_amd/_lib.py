@@ -114,7 +114,7 @@ def load(path: str | None = None):
         "insitu_attend": (i32, [vp, vp, vp, i32, P(Stats)]),
         "insitu_attend_causal": (i32, [vp, i32, i64, i64, vp, vp, i32, P(Stats)]),
         "insitu_project": (i32, [vp, vp, i32, i32, vp, i64, vp, vp]),
-        "insitu_seam_wire": (i32, [vp, vp, vp, i64, i32, i32, i32, vp, vp, vp, i64, i32,
+        "insitu_seam_wire": (i32, [vp, vp, vp, i64, i32, i32, i32, vp, i64, vp, vp, i64, i32,
                                    ctypes.c_double, i32, vp, vp, vp, P(ctypes.c_uint64)]),
         "insitu_output_projection": (i32, [vp, vp, i64, i32, i32, vp, i32, vp, vp]),
         "insitu_step": (i32, [vp, vp, vp, vp, vp, i32, P(Stats)]),

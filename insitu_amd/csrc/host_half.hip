@@ -7,12 +7,13 @@
 // takes. Behind it (kernel.py:348-356): the Q16 output back to float, and the
 // output projection through W_o' (R^-1 folded in, ops/output.py:49-78).
 //
-// The projections are plain fp16 GEMMs (fp32 accumulation) and run on
-// rocBLAS. Everything around them is a kernel of this file: the fp16 casts,
-// and the seam epilogue, whose float steps follow numpy's float64 arithmetic
-// operation by operation (no fused multiply-add), so that for the same fp32
-// projections the wire rows are the reference's integers exactly. Only the
-// GEMM's summation order differs from a CPU BLAS.
+// The projections are fp16 products with fp32 accumulation. A decode step (up
+// to 4 tokens) runs them as one GEMV kernel of this file that streams the
+// weights once and casts its inputs to fp16 itself; a prompt runs them as
+// rocBLAS GEMMs behind a cast kernel. The seam epilogue's float steps follow
+// numpy's float64 arithmetic operation by operation (no fused multiply-add), so
+// that for the same fp32 projections the wire rows are the reference's integers
+// exactly. Only the projections' summation order differs from a CPU BLAS.
 
 #include <hip/hip_runtime.h>
 #include <rocblas/rocblas.h>
@@ -45,6 +46,70 @@ __global__ void add_bias_kernel(float *__restrict__ y, const float *__restrict__
     if (i < rows * cols) y[i] = y[i] + bias[i % cols];
 }
 
+// y (n, out_f) = fp16(x) (n, in_f) . W^T, W fp16 (out_f, in_f) row-major, for n <= GEMV_N
+// tokens: the products are exact in fp32 (11 x 11 significant bits) and each is
+// added with one rounding (fmaf). The block stages fp16(x) in LDS (as float):
+// from fp32 (FIXED = false) or from Q(frac) int32 through float64 (FIXED = true,
+// one rounding, kernel.py:354 to_float). Wave = GEMV_RPW rows, lane = 8
+// consecutive columns per 16-byte load; a DPP-free shuffle tree sums the lanes.
+constexpr int GEMV_N = 4, GEMV_RPW = 2, GEMV_WAVES = 4;
+constexpr int64_t GEMV_LDS_FLOATS = 16384;     // n * in_f staged, 64 KB
+
+template <bool FIXED>
+__global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_f16_kernel(
+    const uint16_t *__restrict__ w, int32_t out_f, int32_t in_f, const void *__restrict__ xin, int32_t n,
+    double fscale, const float *__restrict__ bias, float *__restrict__ y) {
+    extern __shared__ float xs[];
+    for (int i = threadIdx.x; i < n * in_f; i += blockDim.x) {
+        _Float16 hv;
+        if (FIXED)
+            hv = (_Float16)((double)((const int32_t *)xin)[i] * fscale);
+        else
+            hv = (_Float16)((const float *)xin)[i];
+        xs[i] = (float)hv;
+    }
+    __syncthreads();
+    const int lane = threadIdx.x & 63;
+    const int row0 = (blockIdx.x * GEMV_WAVES + (threadIdx.x >> 6)) * GEMV_RPW;
+    float acc[GEMV_RPW][GEMV_N];
+#pragma unroll
+    for (int r = 0; r < GEMV_RPW; ++r)
+#pragma unroll
+        for (int t = 0; t < GEMV_N; ++t) acc[r][t] = 0.0f;
+#pragma unroll 2
+    for (int c = lane * 8; c < in_f; c += 512) {
+        uint4 wv[GEMV_RPW];
+#pragma unroll
+        for (int r = 0; r < GEMV_RPW; ++r) {
+            const int row = row0 + r < out_f ? row0 + r : out_f - 1;     // clamped: in bounds
+            wv[r] = *(const uint4 *)(w + (int64_t)row * in_f + c);
+        }
+#pragma unroll
+        for (int r = 0; r < GEMV_RPW; ++r) {
+            _Float16 hw[8];
+            __builtin_memcpy(hw, &wv[r], 16);
+#pragma unroll
+            for (int t = 0; t < GEMV_N; ++t) {
+                if (t < n) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[r][t] = fmaf((float)hw[e], xs[t * in_f + c + e], acc[r][t]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < GEMV_RPW; ++r) {
+#pragma unroll
+        for (int t = 0; t < GEMV_N; ++t) {
+            float v = acc[r][t];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+            const int row = row0 + r;
+            if (lane == 0 && t < n && row < out_f) y[(int64_t)t * out_f + row] = bias ? v + bias[row] : v;
+        }
+    }
+}
+
 // numpy's rint (half to even), then the Q(24, 16) clamp (fixed.py:158-164).
 __device__ __forceinline__ int64_t to_fixed_q16(double a, unsigned long long *sat) {
 #pragma clang fp contract(off)
@@ -64,7 +129,7 @@ __device__ __forceinline__ int64_t to_fixed_q16(double a, unsigned long long *sa
 // RoPE pairs channel j with j + d/2 (the half split, rope.py:144-174).
 __global__ void seam_wire_kernel(const float *__restrict__ p, const float *__restrict__ bias, int64_t n,
                                  int32_t n_q, int32_t n_kv, int32_t d, const int64_t *__restrict__ pos,
-                                 const int64_t *__restrict__ cos_t, const int64_t *__restrict__ sin_t,
+                                 int64_t pos0, const int64_t *__restrict__ cos_t, const int64_t *__restrict__ sin_t,
                                  int64_t max_pos, int32_t frac, double attn_scale, int32_t cast_after_rope,
                                  int32_t *__restrict__ q, int32_t *__restrict__ k, int32_t *__restrict__ v,
                                  unsigned long long *sat, unsigned long long *range_err) {
@@ -82,7 +147,7 @@ __global__ void seam_wire_kernel(const float *__restrict__ p, const float *__res
     const float *row = p + t * width + (int64_t)h * d;
     int32_t *dst = kind == 0 ? q + (t * n_q + hh) * d : (kind == 1 ? k + (t * n_kv + hh) * d
                                                                      : v + (t * n_kv + hh) * d);
-    const int64_t ps = pos[t];
+    const int64_t ps = pos ? pos[t] : pos0 + t;
     const bool rope = kind != 2;
     if (rope && (ps < 0 || ps >= max_pos)) {
         if (lane == 0) atomicAdd(range_err, 1ull);
@@ -173,6 +238,22 @@ int ensure_x16(insitu_ctx *c, size_t n) {
     return INSITU_OK;
 }
 
+bool gemv_fits(int64_t n, int32_t in_f) {
+    return n <= GEMV_N && in_f % 8 == 0 && n * in_f <= GEMV_LDS_FLOATS;
+}
+
+template <bool FIXED>
+int gemv(insitu_ctx *c, const uint16_t *w, int32_t out_f, int32_t in_f, const void *x, int64_t n, double fscale,
+         const float *bias, float *y) {
+    const int rows_per_block = GEMV_WAVES * GEMV_RPW;
+    const unsigned blocks = (unsigned)((out_f + rows_per_block - 1) / rows_per_block);
+    hipLaunchKernelGGL(gemv_f16_kernel<FIXED>, dim3(blocks), dim3(64 * GEMV_WAVES),
+                       (size_t)n * in_f * sizeof(float), ctx_stream(c), w, out_f, in_f, x, (int32_t)n, fscale,
+                       bias, y);
+    HIP_TRY(hipGetLastError(), "gemv");
+    return INSITU_OK;
+}
+
 }  // namespace
 
 // One rocBLAS handle and staging per context, made on first use on the
@@ -200,6 +281,7 @@ int insitu_project(insitu_ctx *c, const uint16_t *w, int32_t out_f, int32_t in_f
     if (out_f <= 0 || in_f <= 0 || n < 0) return fail(INSITU_EBADLEN, "bad projection shape");
     if (n == 0) return INSITU_OK;
     HIP_TRY(hipSetDevice(ctx_device(c)), "hipSetDevice");
+    if (gemv_fits(n, in_f)) return gemv<false>(c, w, out_f, in_f, x, n, 0.0, bias, y);
     int rc = ensure_x16(c, (size_t)n * in_f);
     if (rc) return rc;
     Blas &b = blas_of(c);
@@ -219,10 +301,10 @@ int insitu_project(insitu_ctx *c, const uint16_t *w, int32_t out_f, int32_t in_f
 }
 
 int insitu_seam_wire(insitu_ctx *c, const float *p, const float *bias, int64_t n, int32_t n_q, int32_t n_kv,
-                     int32_t d, const int64_t *pos, const int64_t *cos_t, const int64_t *sin_t, int64_t max_pos,
+                     int32_t d, const int64_t *pos, int64_t pos0, const int64_t *cos_t, const int64_t *sin_t, int64_t max_pos,
                      int32_t frac, double attn_scale, int32_t cast_after_rope, int32_t *q, int32_t *k,
                      int32_t *v, unsigned long long *counts_host) {
-    if (!c || (n && (!p || !pos || !cos_t || !sin_t || !q || !k || !v))) return fail(INSITU_EINVAL, "null argument");
+    if (!c || (n && (!p || !cos_t || !sin_t || !q || !k || !v))) return fail(INSITU_EINVAL, "null argument");
     if (n < 0 || n_q <= 0 || n_kv <= 0 || d <= 0 || d % 2 || frac < 0 || frac > 30 || max_pos <= 0)
         return fail(INSITU_EBADLEN, "bad seam shape");
     HIP_TRY(hipSetDevice(ctx_device(c)), "hipSetDevice");
@@ -232,7 +314,7 @@ int insitu_seam_wire(insitu_ctx *c, const float *p, const float *bias, int64_t n
     if (n) {
         const int64_t waves = n * (n_q + 2 * n_kv);
         hipLaunchKernelGGL(seam_wire_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, ctx_stream(c), p,
-                           bias, n, n_q, n_kv, d, pos, cos_t, sin_t, max_pos, frac, attn_scale, cast_after_rope, q,
+                           bias, n, n_q, n_kv, d, pos, pos0, cos_t, sin_t, max_pos, frac, attn_scale, cast_after_rope, q,
                            k, v, b.counters, b.counters + 1);
         HIP_TRY(hipGetLastError(), "seam epilogue");
     }
@@ -252,6 +334,7 @@ int insitu_output_projection(insitu_ctx *c, const int32_t *out, int64_t n, int32
     if (n < 0 || width <= 0 || hidden <= 0 || frac < 0 || frac > 62) return fail(INSITU_EBADLEN, "bad shape");
     if (n == 0) return INSITU_OK;
     HIP_TRY(hipSetDevice(ctx_device(c)), "hipSetDevice");
+    if (gemv_fits(n, width)) return gemv<true>(c, wo, hidden, width, out, n, std::ldexp(1.0, -frac), bias, y);
     int rc = ensure_x16(c, (size_t)n * width);
     if (rc) return rc;
     Blas &b = blas_of(c);

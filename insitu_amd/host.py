@@ -92,6 +92,15 @@ def fold_o_proj(o_proj, rotation_matrix: np.ndarray, num_heads: int) -> np.ndarr
     return out
 
 
+def _host_array(a):
+    """A checkpoint tensor (torch, on any device, with or without grad) or array -> numpy."""
+    if a is None or isinstance(a, np.ndarray):
+        return a
+    if hasattr(a, "detach"):
+        return a.detach().float().cpu().numpy()
+    return np.asarray(a)
+
+
 class Weights:
     """weights.py:32-133: fp16 W_q | W_k | W_v stacked (the checkpoint's (out, in) layout),
     fp16 W_o' (R^-1 folded), fp32 biases; device-resident. rotation_matrix is the
@@ -102,6 +111,8 @@ class Weights:
         import torch
         self.model = model
         self.ctx = ctx or default_context()
+        q, k, v, o, q_bias, k_bias, v_bias, o_bias = (
+            _host_array(a) for a in (q, k, v, o, q_bias, k_bias, v_bias, o_bias))
         shapes = {"q": (model.q_out_features, model.hidden_size),
                   "k": (model.kv_out_features, model.hidden_size),
                   "v": (model.kv_out_features, model.hidden_size),
@@ -182,7 +193,10 @@ class HostHalf:
             # rope.py:163-167; checked here so that counts=False needs no read-back
             raise _lib.FormatError(_lib.ERANGE, f"position {int(positions.max())} beyond the RoPE "
                                    f"table (max_position {m.max_position})")
-        pos = self.ctx.to_device(positions, torch.int64)
+        # consecutive positions (a decode step, a prompt) go as their first value
+        consecutive = n == 0 or bool(np.all(np.diff(positions) == 1))
+        pos = None if consecutive else self.ctx.to_device(positions, torch.int64)
+        pos0 = int(positions[0]) if n else 0
         dev = self.ctx.torch_device
         q = torch.empty((n, m.num_heads, m.head_dim), dtype=torch.int32, device=dev)
         k = torch.empty((n, m.num_kv_heads, m.head_dim), dtype=torch.int32, device=dev)
@@ -191,7 +205,8 @@ class HostHalf:
         bias = self.weights.qkv_bias
         _lib.check(self.ctx.lib.insitu_seam_wire(
             self.ctx.handle, ptr(p), ptr(bias) if bias is not None else None, n, m.num_heads,
-            m.num_kv_heads, m.head_dim, ptr(pos), ptr(self._cos), ptr(self._sin), m.max_position, ROPE_FRAC,
+            m.num_kv_heads, m.head_dim, ptr(pos) if pos is not None else None, pos0, ptr(self._cos),
+            ptr(self._sin), m.max_position, ROPE_FRAC,
             self.attn_scale, 1 if self.cast_after_rope else 0, ptr(q), ptr(k), ptr(v), cnt))
         if cnt is not None:
             self.last_saturated = int(cnt[0])

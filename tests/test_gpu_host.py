@@ -72,9 +72,11 @@ def test_seeded_weights_are_the_oracles(golden_half):
     np.testing.assert_allclose(got_o, oh.to_fp16(folded).astype(np.float64), rtol=2.0 ** -10, atol=2.0 ** -24)
 
 
-def test_fp16_casts_are_exact_through_an_identity_gemm(ctx):
+@pytest.mark.parametrize("n", [5, 3, 1])
+def test_fp16_casts_are_exact_through_an_identity_gemm(ctx, n):
     """W = I makes the GEMM exact, so y is the staging cast itself: fp32 -> fp16
-    half to even (numerics/fp.py:20-22) and Q16 -> float64 -> fp16 in one rounding."""
+    half to even (numerics/fp.py:20-22) and Q16 -> float64 -> fp16 in one rounding.
+    n = 5 tokens run the cast kernel and rocBLAS, n <= 4 the decode GEMV."""
     import torch
     from insitu_amd import _lib
     from insitu_amd.runtime import ptr
@@ -84,20 +86,22 @@ def test_fp16_casts_are_exact_through_an_identity_gemm(ctx):
     x = (rng.standard_normal((5, n_in)) * np.exp2(rng.integers(-20, 13, (5, n_in)))).astype(np.float32)
     x[0, :8] = [1.0 + 2.0 ** -11, 1.0 + 3 * 2.0 ** -11, -(1.0 + 2.0 ** -11), 65504.0, 2.0 ** -24,
                 2.0 ** -25, 3 * 2.0 ** -25, 0.0]                  # ties, the top, subnormals
+    x = np.ascontiguousarray(x[:n])
     bias = rng.standard_normal(n_in).astype(np.float32)
     xd = torch.from_numpy(x).to(ctx.torch_device)
     bd = torch.from_numpy(bias).to(ctx.torch_device)
-    y = torch.empty((5, n_in), dtype=torch.float32, device=ctx.torch_device)
-    _lib.check(ctx.lib.insitu_project(ctx.handle, ptr(eye), n_in, n_in, ptr(xd), 5, None, ptr(y)))
+    y = torch.empty((n, n_in), dtype=torch.float32, device=ctx.torch_device)
+    _lib.check(ctx.lib.insitu_project(ctx.handle, ptr(eye), n_in, n_in, ptr(xd), n, None, ptr(y)))
     np.testing.assert_array_equal(y.cpu().numpy(), oh.to_fp16(x).astype(np.float32))
-    _lib.check(ctx.lib.insitu_project(ctx.handle, ptr(eye), n_in, n_in, ptr(xd), 5, ptr(bd), ptr(y)))
+    _lib.check(ctx.lib.insitu_project(ctx.handle, ptr(eye), n_in, n_in, ptr(xd), n, ptr(bd), ptr(y)))
     np.testing.assert_array_equal(y.cpu().numpy(), oh.to_fp16(x).astype(np.float32) + bias)
 
     q16 = rng.integers(-(1 << 31), (1 << 31) - 1, size=(5, n_in), dtype=np.int64)
     q16[0, :6] = [1, -1, 0, (1 << 31) - 1, -(1 << 31), 65536 + 32]   # 1 + 2^-11: a tie to even
     q16[1] = rng.integers(-(1 << 18), 1 << 18, n_in)
+    q16 = np.ascontiguousarray(q16[:n])
     qd = torch.from_numpy(q16.astype(np.int32)).to(ctx.torch_device)
-    _lib.check(ctx.lib.insitu_output_projection(ctx.handle, ptr(qd), 5, n_in, 16, ptr(eye), n_in, None, ptr(y)))
+    _lib.check(ctx.lib.insitu_output_projection(ctx.handle, ptr(qd), n, n_in, 16, ptr(eye), n_in, None, ptr(y)))
     want = oh.to_fp16(q16.astype(np.float64) / 65536.0).astype(np.float32)
     np.testing.assert_array_equal(y.cpu().numpy(), want)
 
@@ -108,6 +112,8 @@ def test_projections_within_the_fp32_bound(golden_half):
     x = _golden_inputs()
     p = half.project_qkv(x).cpu().numpy()
     _check_gemm(p, np.concatenate([wq, wk, wv]), x)
+    for n in (1, 2, 4):                                   # the decode GEMV
+        _check_gemm(half.project_qkv(x[:n]).cpu().numpy(), np.concatenate([wq, wk, wv]), x[:n])
     # and against the oracle's float32 numpy product, to a few ulp
     ref = oh.project(np.concatenate([wq, wk, wv]), x)
     np.testing.assert_allclose(p, ref, rtol=0, atol=1e-6)
@@ -179,6 +185,8 @@ def test_output_side_within_the_fp32_bound(golden_half):
     y = half.output(out).cpu().numpy()
     wo = w.o.cpu().numpy().view(np.float16)
     _check_gemm(y, wo, out / 65536.0)
+    for n in (1, 3):                                      # the decode GEMV
+        _check_gemm(half.output(out[:n]).cpu().numpy(), wo, out[:n] / 65536.0)
     # the oracle's output side (float32 numpy sums) agrees to a few ulp
     np.testing.assert_allclose(y, oh.output_side(out, wo), rtol=0, atol=2e-5 * np.abs(y).max())
 
@@ -201,7 +209,8 @@ def test_forward_hidden_states_end_to_end(ctx, golden_half, cast_after_rope):
     assert (r0.n_tokens, r0.context, r1.n_tokens, r1.context) == (64, 64, 1, 65)
     wire = {k: np.concatenate([taps0[k], taps1[k]]) for k in ("wire.q", "wire.k", "wire.v")}
 
-    p = blk.host.project_qkv(x).cpu().numpy()
+    # the prompt's projections ran as one GEMM, the decode step's as the GEMV
+    p = np.concatenate([blk.host.project_qkv(x[:64]).cpu().numpy(), blk.host.project_qkv(x[64:]).cpu().numpy()])
     cos, sin = oh.rope_tables(D, model.max_position)
     (wq_, wk_, wv_), _ = oh.seam(p, NQ, NKV, D, np.arange(65), cos, sin, cast_after_rope=cast_after_rope)
     np.testing.assert_array_equal(wire["wire.q"], wq_)

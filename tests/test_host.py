@@ -236,3 +236,13 @@ def test_model_config_from_hf_reads_rope_settings_or_refuses():
         ModelConfig.from_hf({k: v for k, v in nested.items() if k != "rope_parameters"})
     with pytest.raises(NotImplementedError):
         ModelConfig.from_hf(dict(llama, rope_scaling={"rope_type": "yarn", "factor": 4.0}))
+
+
+def test_checkpoint_tensors_convert_for_the_weights():
+    import torch
+    from insitu_amd.host import _host_array
+    w = torch.randn(4, 3, requires_grad=True).half()
+    got = _host_array(w)
+    assert got.dtype == np.float32 and got.shape == (4, 3)
+    np.testing.assert_array_equal(got.astype(np.float16), w.detach().numpy())
+    assert _host_array(None) is None
