@@ -213,6 +213,7 @@ struct ChunkLds {
     int64_t kc[16];
     int64_t vc[16];
     int32_t vc32[16];
+    int32_t tt[GF][64];            // run sums: 8 records' terms for every value code, [record][code]
     int64_t vcmax;
     int32_t expt[256];
     int32_t cntw[GF][CT / 64];     // candidate tokens per head and wave
@@ -938,7 +939,15 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     // Lane = channel: the terms of the entries in order, 8 at a time.
                     const int cnt = n_act - a0 < 64 ? n_act - a0 : 64;
                     for (int j0 = 0; j0 < cnt; j0 += 8) {
-                        // the centroids of the next 8 entries first (independent LDS reads)
+                        // The 8 entries' terms for every value code, lane = (entry, code):
+                        // floor(w * c[code] / 2^acc_shift), the per-entry 64-bit product
+                        // done once for all channels.
+                        {
+                            const int32_t w_l = __shfl(w_i, j0 + (lane >> 3));
+                            const int32_t c_l = S.vc32[lane & 7 & (int)vmask];
+                            S.tt[h][lane] = (int32_t)(((int64_t)w_l * c_l) >> acc_shift);
+                        }
+                        // then each channel's term of the next 8 entries (independent LDS reads)
                         int32_t cv[8][CPL];
 #pragma unroll
                         for (int jj = 0; jj < 8; ++jj) {
@@ -949,7 +958,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                                 // the next one (the last word never has a code crossing out)
                                 const uint32_t lo = S.u.ph.vw[tl][wi[k]];
                                 const uint32_t hi = S.u.ph.vw[tl][wi1[k]];
-                                cv[jj][k] = S.vc32[__builtin_amdgcn_alignbit(hi, lo, sh[k]) & vmask];
+                                cv[jj][k] = S.tt[h][jj * 8 + (int)(__builtin_amdgcn_alignbit(hi, lo, sh[k]) & vmask)];
                             }
                         }
 #pragma unroll
@@ -983,10 +992,9 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                                     for (int k = 0; k < CPL; ++k) P[k] = hiP[k] = loP[k] = 0;
                                     ++seg;
                                 }
-                                const int32_t w = __builtin_amdgcn_readlane(w_i, j);
 #pragma unroll
                                 for (int k = 0; k < CPL; ++k) {
-                                    P[k] += (int32_t)(((int64_t)w * cv[jj][k]) >> acc_shift);
+                                    P[k] += cv[jj][k];
                                     if (SEQ && trk) {
                                         hiP[k] = P[k] > hiP[k] ? P[k] : hiP[k];
                                         loP[k] = P[k] < loP[k] ? P[k] : loP[k];
