@@ -52,7 +52,7 @@ __global__ void add_bias_kernel(float *__restrict__ y, const float *__restrict__
 // from fp32 (FIXED = false) or from Q(frac) int32 through float64 (FIXED = true,
 // one rounding, kernel.py:354 to_float). Wave = GEMV_RPW rows, lane = 8
 // consecutive columns per 16-byte load; a DPP-free shuffle tree sums the lanes.
-constexpr int GEMV_N = 4, GEMV_RPW = 2, GEMV_WAVES = 4;
+constexpr int GEMV_N = 4, GEMV_RPW = 2, GEMV_WAVES = 4, GEMV_UNR = 4;
 constexpr int64_t GEMV_LDS_FLOATS = 16384;     // n * in_f staged, 64 KB
 
 template <bool FIXED>
@@ -60,52 +60,88 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_f16_kernel(
     const uint16_t *__restrict__ w, int32_t out_f, int32_t in_f, const void *__restrict__ xin, int32_t n,
     double fscale, const float *__restrict__ bias, float *__restrict__ y) {
     extern __shared__ float xs[];
-    for (int i = threadIdx.x; i < n * in_f; i += blockDim.x) {
-        _Float16 hv;
-        if (FIXED)
-            hv = (_Float16)((double)((const int32_t *)xin)[i] * fscale);
-        else
-            hv = (_Float16)((const float *)xin)[i];
-        xs[i] = (float)hv;
-    }
-    __syncthreads();
     const int lane = threadIdx.x & 63;
     const int row0 = (blockIdx.x * GEMV_WAVES + (threadIdx.x >> 6)) * GEMV_RPW;
+    // GEMV_UNR 16-byte chunks of each row per batch: for in_f <= 2,048 one batch, all of the
+    // wave's weight loads in flight before the inputs are staged
+    uint4 wv[GEMV_UNR][GEMV_RPW];
+    auto load = [&](int cb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < GEMV_UNR; ++u) {
+            const int c = cb + 512 * u;
+#pragma unroll
+            for (int r = 0; r < GEMV_RPW; ++r) {
+                const int row = row0 + r < out_f ? row0 + r : out_f - 1;     // clamped: in bounds
+                wv[u][r] = c < in_f ? *(const uint4 *)(w + (int64_t)row * in_f + c) : make_uint4(0, 0, 0, 0);
+            }
+        }
+    };
+    load(lane * 8);
+    // the inputs, 4 values per 16-byte load and 4 loads per thread in flight (n * in_f is a
+    // multiple of 8)
+    const int total = n * in_f;
+    for (int i0 = threadIdx.x * 4; i0 < total; i0 += 64 * GEMV_WAVES * 16) {
+        uint4 xv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = i0 + u * 64 * GEMV_WAVES * 4;
+            xv[u] = i < total ? *(const uint4 *)((const char *)xin + (int64_t)i * 4) : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = i0 + u * 64 * GEMV_WAVES * 4;
+            if (i < total) {
+                const uint32_t wd[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    _Float16 hv;
+                    if (FIXED)
+                        hv = (_Float16)((double)(int32_t)wd[e] * fscale);
+                    else
+                        hv = (_Float16)__builtin_bit_cast(float, wd[e]);
+                    xs[i + e] = (float)hv;
+                }
+            }
+        }
+    }
+    __syncthreads();
     float acc[GEMV_RPW][GEMV_N];
 #pragma unroll
     for (int r = 0; r < GEMV_RPW; ++r)
 #pragma unroll
         for (int t = 0; t < GEMV_N; ++t) acc[r][t] = 0.0f;
-#pragma unroll 2
-    for (int c = lane * 8; c < in_f; c += 512) {
-        uint4 wv[GEMV_RPW];
+    for (int cb = lane * 8; cb < in_f; cb += 512 * GEMV_UNR) {
 #pragma unroll
-        for (int r = 0; r < GEMV_RPW; ++r) {
-            const int row = row0 + r < out_f ? row0 + r : out_f - 1;     // clamped: in bounds
-            wv[r] = *(const uint4 *)(w + (int64_t)row * in_f + c);
-        }
+        for (int u = 0; u < GEMV_UNR; ++u) {
+            const int c = cb + 512 * u;
+            if (c < in_f) {
 #pragma unroll
-        for (int r = 0; r < GEMV_RPW; ++r) {
-            _Float16 hw[8];
-            __builtin_memcpy(hw, &wv[r], 16);
+                for (int r = 0; r < GEMV_RPW; ++r) {
+                    _Float16 hw[8];
+                    __builtin_memcpy(hw, &wv[u][r], 16);
 #pragma unroll
-            for (int t = 0; t < GEMV_N; ++t) {
-                if (t < n) {
+                    for (int t = 0; t < GEMV_N; ++t) {
+                        if (t < n) {
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) acc[r][t] = fmaf((float)hw[e], xs[t * in_f + c + e], acc[r][t]);
+                            for (int e = 0; e < 8; ++e)
+                                acc[r][t] = fmaf((float)hw[e], xs[t * in_f + c + e], acc[r][t]);
+                        }
+                    }
                 }
             }
         }
+        if (cb + 512 * GEMV_UNR < in_f) load(cb + 512 * GEMV_UNR);
     }
 #pragma unroll
     for (int r = 0; r < GEMV_RPW; ++r) {
 #pragma unroll
         for (int t = 0; t < GEMV_N; ++t) {
+            if (t >= n) break;                       // uniform: only the tokens there are
             float v = acc[r][t];
 #pragma unroll
             for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
             const int row = row0 + r;
-            if (lane == 0 && t < n && row < out_f) y[(int64_t)t * out_f + row] = bias ? v + bias[row] : v;
+            if (lane == 0 && row < out_f) y[(int64_t)t * out_f + row] = bias ? v + bias[row] : v;
         }
     }
 }
