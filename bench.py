@@ -18,6 +18,7 @@ consecutive steps never re-read a cache that is still resident.
     python bench.py --config c1             # config 1 in full, every step checked
     python bench.py --config prefill        # a 4,096-token prompt through one layer
     python bench.py --config block          # hidden states in, hidden states out, ctx 32k
+    python bench.py --config probe          # bytes-only read of the C2 scan size: the launch ceiling
 
 C3: batch 64, one layer, per-sequence contexts uniform in
 [1024, 8192] from seed 3, one attend launch over the whole batch; 3 caches
@@ -69,7 +70,8 @@ def _args():
     ap.add_argument("--ctx", type=int, default=CTX)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
-    ap.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "prefill", "block"])
+    ap.add_argument("--config", default="c2",
+                    choices=["c1", "c2", "c3", "c4", "prefill", "block", "probe"])
     ap.add_argument("--prompt", type=int, default=4096)
     ap.add_argument("--c1-layers", type=int, default=16)
     ap.add_argument("--c1-steps", type=int, default=4096)
@@ -134,6 +136,87 @@ def cpu_baseline(cache, q_rot_all, out_gpu, budget_s: float = 20.0):
                       f"of the last timed step's cache ({int(rows_t)} rows, {t_all:.1f} s); "
                       f"affinity {len(os.sched_getaffinity(0))} cores, numpy single-threaded loop",
             "s_per_decode_step_extrapolated": round(t_all / done * N_KV, 3)}
+
+
+def _timed_each(ctx, launch, reps: int):
+    """Per-launch kernel times (us) of `reps` calls of launch(i), from HIP events attached to
+    the dispatches on the library's stream (insitu_ctx_timing_read_each)."""
+    import ctypes
+    from insitu_amd import _lib
+    lib = ctx.lib
+    _lib.check(lib.insitu_ctx_timing(ctx.handle, 1))
+    for i in range(reps):
+        launch(i)
+    ms = (ctypes.c_double * reps)()
+    n = ctypes.c_int64()
+    _lib.check(lib.insitu_ctx_timing_read_each(ctx.handle, ms, reps, ctypes.byref(n)))
+    _lib.check(lib.insitu_ctx_timing(ctx.handle, 0))
+    if n.value != reps:
+        raise RuntimeError(f"timed {n.value} launches of {reps}")
+    return np.array(ms[:reps]) * 1e3
+
+
+def bench_probe(a) -> int:
+    """The ceiling of one launch: a bytes-only read of the C2 scan size (13,631,488 B) at
+    several grid shapes, rotating over 40 buffers (545 MB, more than twice the 256 MB
+    Infinity Cache), and an empty launch. No attention work; the analogue of the
+    reference's DDR probe (rtl/ddr_probe.sv)."""
+    import torch
+
+    from insitu_amd import _lib
+    from insitu_amd.runtime import default_context, ptr
+
+    ctx = default_context(0)
+    lib = ctx.lib
+    nbytes = N_KV * CTX * ROW
+    nbuf = 40
+    g = torch.Generator(device=ctx.torch_device).manual_seed(0)
+    bufs = [torch.randint(0, 2 ** 31 - 1, (nbytes // 4,), dtype=torch.int32, device=ctx.torch_device,
+                          generator=g) for _ in range(nbuf)]
+    sink = torch.zeros(256, dtype=torch.int32, device=ctx.torch_device)
+    reps = max(a.steps, 50)
+    rows = []
+    for layout in (0, 1):
+        for n_wg in (256, 512, 1024, 2048, 4096):
+            def launch(i, layout=layout, n_wg=n_wg):
+                _lib.check(lib.insitu_probe_read(ctx.handle, ptr(bufs[i % nbuf]), nbytes, n_wg, layout,
+                                                 ptr(sink)))
+            for i in range(a.warmup):
+                launch(i)
+            torch.cuda.synchronize()
+            us = _timed_each(ctx, launch, reps)
+            med = float(np.median(us))
+            rows.append({"kernel": "probe_read_kernel", "layout": ["grid-stride", "span per workgroup"][layout],
+                         "workgroups": n_wg, "median_us": round(med, 3), "min_us": round(float(us.min()), 3),
+                         "gbs_median": round(nbytes / med / 1e3, 1)})
+            print(f"probe: layout {layout} wg {n_wg}: {med:.2f} us", file=sys.stderr, flush=True)
+    # the same buffer every time: what a launch reads when the bytes sit in the Infinity Cache
+    def launch_hot(i):
+        _lib.check(lib.insitu_probe_read(ctx.handle, ptr(bufs[0]), nbytes, 1024, 0, ptr(sink)))
+    for i in range(a.warmup):
+        launch_hot(i)
+    us = _timed_each(ctx, launch_hot, reps)
+    rows.append({"kernel": "probe_read_kernel", "layout": "grid-stride, one buffer (Infinity Cache resident)",
+                 "workgroups": 1024, "median_us": round(float(np.median(us)), 3),
+                 "gbs_median": round(nbytes / float(np.median(us)) / 1e3, 1)})
+    for n_wg in (256, 1024):
+        def launch_empty(i, n_wg=n_wg):
+            _lib.check(lib.insitu_probe_empty(ctx.handle, n_wg, ptr(sink)))
+        for i in range(a.warmup):
+            launch_empty(i)
+        us = _timed_each(ctx, launch_empty, reps)
+        rows.append({"kernel": "probe_empty_kernel", "workgroups": n_wg,
+                     "median_us": round(float(np.median(us)), 3)})
+    best = min((r for r in rows if r["kernel"] == "probe_read_kernel" and "one buffer" not in r["layout"]),
+               key=lambda r: r["median_us"])
+    res = {"metric": "bytes-only HBM read of the C2 scan size in one launch (the single-launch ceiling)",
+           "value": best["gbs_median"], "unit": "GB/s", "n_gpus": 1, "steps": reps, "warmup": a.warmup,
+           "higher_is_better": True, "dtype": "u8", "data": "random bytes",
+           "config": {"workload": f"read {nbytes} B per launch, {nbuf} rotating buffers "
+                                  f"({nbuf * nbytes / 2 ** 20:.0f} MiB)"},
+           "frac_of_peak": round(best["gbs_median"] / HBM_PEAK_GBS, 4), "rows": rows}
+    print(json.dumps(res))
+    return 0
 
 
 def bench_scale(a) -> int:
@@ -522,6 +605,8 @@ def main() -> int:
         return bench_prefill(a)
     if a.config == "block":
         return bench_block(a)
+    if a.config == "probe":
+        return bench_probe(a)
     if a.config != "c2":
         return bench_scale(a)
     import torch

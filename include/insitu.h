@@ -117,6 +117,9 @@ void *insitu_ctx_stream(insitu_ctx *ctx);
  * not been read. */
 int insitu_ctx_timing(insitu_ctx *ctx, int32_t enable);
 int insitu_ctx_timing_read(insitu_ctx *ctx, double *total_ms, int64_t *n_attends);
+/* The same, one time per attend in launch order: ms_each (cap) receives n_attends values
+ * (EBADLEN when more than cap were timed). */
+int insitu_ctx_timing_read_each(insitu_ctx *ctx, double *ms_each, int64_t cap, int64_t *n_attends);
 
 /* --- rotation: Rotation.apply (ops/rotate.py:170-197) -------------------- */
 /* x_dev, y_dev: int32 (n_vec, d). y may alias x. */
@@ -222,6 +225,18 @@ int insitu_load_rows(insitu_cache *cache, int32_t seq, int32_t head, int64_t t0,
  * nbytes must equal insitu_layout.seq_stride. Synchronous. */
 int insitu_read_image(insitu_cache *cache, int32_t seq, uint8_t *image_host, int64_t nbytes);
 int insitu_load_image(insitu_cache *cache, int32_t seq, const uint8_t *image_host, int64_t nbytes);
+
+/* -- measurement probes (no counterpart in the reference's path: the analogue of its
+ *    DDR bandwidth probe, rtl/ddr_probe.sv) ------------------------------------- */
+
+/* Read nbytes (a positive multiple of 64) of src_dev with n_wg workgroups of 256 threads,
+ * 16-byte loads; layout 0 grid-stride, 1 one contiguous span per workgroup. Writes nothing
+ * of use to sink_dev (uint32 [256]). Stream-ordered; timed like an attend while
+ * insitu_ctx_timing is on. */
+int insitu_probe_read(insitu_ctx *ctx, const void *src_dev, int64_t nbytes, int32_t n_wg,
+                      int32_t layout, uint32_t *sink_dev);
+/* An empty kernel of n_wg workgroups: the launch floor. */
+int insitu_probe_empty(insitu_ctx *ctx, int32_t n_wg, uint32_t *sink_dev);
 
 /* Message of the last failing call on this thread. */
 const char *insitu_last_error(void);

@@ -22,12 +22,13 @@ STATUS_NAMES = {OK: "OK", EBADLEN: "EBADLEN", ERANGE: "ERANGE", EHIP: "EHIP",
 
 EXPORTS = (
     "insitu_ctx_create", "insitu_ctx_destroy", "insitu_ctx_sync", "insitu_ctx_stream",
-    "insitu_ctx_timing", "insitu_ctx_timing_read", "insitu_rotate", "insitu_encode", "insitu_qtab", "insitu_exp_lut", "insitu_finalize",
+    "insitu_ctx_timing", "insitu_ctx_timing_read", "insitu_ctx_timing_read_each",
+    "insitu_rotate", "insitu_encode", "insitu_qtab", "insitu_exp_lut", "insitu_finalize",
     "insitu_cache_create", "insitu_cache_destroy", "insitu_cache_reset", "insitu_cache_length",
     "insitu_cache_set_length", "insitu_cache_layout", "insitu_append", "insitu_append_seq",
     "insitu_attend", "insitu_attend_causal", "insitu_step", "insitu_project", "insitu_seam_wire",
     "insitu_output_projection", "insitu_read_rows", "insitu_load_rows", "insitu_read_image",
-    "insitu_load_image", "insitu_last_error",
+    "insitu_load_image", "insitu_probe_read", "insitu_probe_empty", "insitu_last_error",
 )
 
 
@@ -98,6 +99,7 @@ def load(path: str | None = None):
         "insitu_ctx_stream": (vp, [vp]),
         "insitu_ctx_timing": (i32, [vp, i32]),
         "insitu_ctx_timing_read": (i32, [vp, P(ctypes.c_double), P(i64)]),
+        "insitu_ctx_timing_read_each": (i32, [vp, P(ctypes.c_double), i64, P(i64)]),
         "insitu_rotate": (i32, [vp, vp, vp, i64, P(Format)]),
         "insitu_encode": (i32, [vp, vp, i64, P(Format), P(i64), i32, vp, vp]),
         "insitu_qtab": (i32, [vp, vp, i32, i32, P(i64), i32, vp]),
@@ -122,6 +124,8 @@ def load(path: str | None = None):
         "insitu_load_rows": (i32, [vp, i32, i32, i64, i64, vp]),
         "insitu_read_image": (i32, [vp, i32, vp, i64]),
         "insitu_load_image": (i32, [vp, i32, vp, i64]),
+        "insitu_probe_read": (i32, [vp, vp, i64, i32, i32, vp]),
+        "insitu_probe_empty": (i32, [vp, i32, vp]),
         "insitu_last_error": (ctypes.c_char_p, []),
     }
     for name, (res, args) in sig.items():

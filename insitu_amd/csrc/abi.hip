@@ -166,6 +166,21 @@ int zero_stats(insitu_cache *c) {
 
 }  // namespace
 
+// The start/stop events of an attend when timing is on (null events otherwise),
+// from the context's pool; the launches record them.
+int insitu::timing_events(insitu_ctx *c, LaunchEv *ev) {
+    *ev = LaunchEv{};
+    if (!c->timing) return INSITU_OK;
+    while (c->ev.size() < c->ev_used + 2) {
+        hipEvent_t e;
+        HIP_TRY(hipEventCreate(&e), "hipEventCreate");
+        c->ev.push_back(e);
+    }
+    ev->start = c->ev[c->ev_used++];
+    ev->stop = c->ev[c->ev_used++];
+    return INSITU_OK;
+}
+
 extern "C" {
 
 const char *insitu_last_error(void) { return g_last_error.c_str(); }
@@ -235,6 +250,22 @@ int insitu_ctx_timing_read(insitu_ctx *c, double *total_ms, int64_t *n_attends) 
     }
     *total_ms = sum;
     *n_attends = (int64_t)(c->ev_used / 2);
+    c->ev_used = 0;
+    return INSITU_OK;
+}
+
+int insitu_ctx_timing_read_each(insitu_ctx *c, double *ms_each, int64_t cap, int64_t *n_attends) {
+    if (!c || !n_attends || (!ms_each && cap)) return fail(INSITU_EINVAL, "null argument");
+    HIP_TRY(hipSetDevice(c->device), "hipSetDevice");
+    const int64_t n = (int64_t)(c->ev_used / 2);
+    if (n > cap) return fail(INSITU_EBADLEN, "more timed attends than the array holds");
+    if (c->ev_used) HIP_TRY(hipEventSynchronize(c->ev[c->ev_used - 1]), "hipEventSynchronize");
+    for (int64_t i = 0; i < n; ++i) {
+        float ms = 0.0f;
+        HIP_TRY(hipEventElapsedTime(&ms, c->ev[2 * i], c->ev[2 * i + 1]), "hipEventElapsedTime");
+        ms_each[i] = ms;
+    }
+    *n_attends = n;
     c->ev_used = 0;
     return INSITU_OK;
 }
@@ -523,20 +554,6 @@ int insitu_append_seq(insitu_cache *k, int32_t seq, const int32_t *kr, const int
     return append_impl(k, seq, seq + 1, kr, vr, n_tok);
 }
 
-// The start/stop events of an attend when timing is on (null events otherwise),
-// from the context's pool; the launches record them.
-static int timing_events(insitu_ctx *c, LaunchEv *ev) {
-    *ev = LaunchEv{};
-    if (!c->timing) return INSITU_OK;
-    while (c->ev.size() < c->ev_used + 2) {
-        hipEvent_t e;
-        HIP_TRY(hipEventCreate(&e), "hipEventCreate");
-        c->ev.push_back(e);
-    }
-    ev->start = c->ev[c->ev_used++];
-    ev->stop = c->ev[c->ev_used++];
-    return INSITU_OK;
-}
 
 // q_staged: the chunked path's fp64 query staging already holds q (the step's
 // write kernel filled it). step: the whole decode step in the attend launch
