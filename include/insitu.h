@@ -238,6 +238,16 @@ int insitu_probe_read(insitu_ctx *ctx, const void *src_dev, int64_t nbytes, int3
 /* An empty kernel of n_wg workgroups: the launch floor. */
 int insitu_probe_empty(insitu_ctx *ctx, int32_t n_wg, uint32_t *sink_dev);
 
+/* -- test hooks (no counterpart in the reference) ----------------------------------- */
+enum {
+    INSITU_DEBUG_DECODE_CALLS = 1,   /* attends the decode scratch has served (its epoch counter) */
+    INSITU_DEBUG_PREFILL_CALLS = 2,  /* the same for the prefill scratch                         */
+    INSITU_DEBUG_SPIN_LIMIT = 3      /* polls before a wait on another workgroup gives up; 0 gives
+                                        up at once, sending every chain with a predecessor to the
+                                        exact serial path                                       */
+};
+int insitu_cache_debug(insitu_cache *cache, int32_t what, int64_t value);
+
 /* Message of the last failing call on this thread. */
 const char *insitu_last_error(void);
 

@@ -14,6 +14,7 @@ LIB_PATH = os.path.join(HERE, "libinsitu_hip.so")
 
 OK, EBADLEN, ERANGE, EHIP, EINVAL, ECAPACITY, ENOMEM, EFAULT = range(8)
 SEQUENTIAL, TWO_PASS, SPLIT, SERIAL = range(4)
+DEBUG_DECODE_CALLS, DEBUG_PREFILL_CALLS, DEBUG_SPIN_LIMIT = 1, 2, 3
 MODES = {"online": SEQUENTIAL, "sequential": SEQUENTIAL, "two_pass": TWO_PASS,
          "split": SPLIT, "serial": SERIAL}
 
@@ -28,7 +29,8 @@ EXPORTS = (
     "insitu_cache_set_length", "insitu_cache_layout", "insitu_append", "insitu_append_seq",
     "insitu_attend", "insitu_attend_causal", "insitu_step", "insitu_project", "insitu_seam_wire",
     "insitu_output_projection", "insitu_read_rows", "insitu_load_rows", "insitu_read_image",
-    "insitu_load_image", "insitu_probe_read", "insitu_probe_empty", "insitu_last_error",
+    "insitu_load_image", "insitu_probe_read", "insitu_probe_empty", "insitu_cache_debug",
+    "insitu_last_error",
 )
 
 
@@ -126,6 +128,7 @@ def load(path: str | None = None):
         "insitu_load_image": (i32, [vp, i32, vp, i64]),
         "insitu_probe_read": (i32, [vp, vp, i64, i32, i32, vp]),
         "insitu_probe_empty": (i32, [vp, i32, vp]),
+        "insitu_cache_debug": (i32, [vp, i32, i64]),
         "insitu_last_error": (ctypes.c_char_p, []),
     }
     for name, (res, args) in sig.items():

@@ -112,12 +112,13 @@ struct insitu_cache {
     std::vector<int64_t> len_host;
     DevStats *stats = nullptr;
     int32_t *wire_scratch = nullptr;      // insitu_step: the rotated queries
-    void *chunk_scratch = nullptr;        // run sums and counters of the chunked attend
+    bool chunked = false;                 // the chunked attend handles this format and capacity
+    ChunkScratch scr;                     // decode attends: run sums and counters, one call's worth
     int64_t max_chunks = 0, pool = 0;
-    uint32_t calls = 0;                   // chunked attends so far: tags this call's flags
-    // prefill (insitu_attend_causal): scratch for PREFILL_QB virtual sequences, their lengths
-    void *prefill_scratch = nullptr;
+    // prefill (insitu_attend_causal): scratch for a virtual batch of queries, their lengths
+    ChunkScratch prefill_scr;
     int64_t *prefill_len = nullptr;
+    int32_t spin_limit = 1 << 20;         // insitu_cache_debug
 };
 
 namespace {
@@ -204,7 +205,7 @@ int insitu_ctx_create(int32_t device, void *hip_stream, insitu_ctx **out) {
     if (e == hipSuccess) e = hipMalloc(&c->hook_flags, 64);
     if (e != hipSuccess) {
         insitu_ctx_destroy(c);
-        return hip_fail(e, "ctx tables");
+        return hip_fail(e, "ctx set-up");
     }
     *out = c;
     return INSITU_OK;
@@ -438,11 +439,13 @@ int insitu_cache_create(insitu_ctx *c, const insitu_cache_desc *desc, insitu_cac
         e = hipMalloc(&k->wire_scratch,
                       sizeof(int32_t) * (size_t)g.batch * (g.n_q + 2 * g.n_kv) * g.d);
     if (e == hipSuccess && chunked_supported(g, desc->capacity)) {
+        k->chunked = true;
         k->max_chunks = chunked_max_chunks(desc->capacity);
         k->pool = chunked_pool_slots(k->max_chunks);
         const size_t nb = chunked_scratch_bytes(g, k->max_chunks, k->pool);
-        e = hipMalloc(&k->chunk_scratch, nb);
-        if (e == hipSuccess) e = hipMemsetAsync(k->chunk_scratch, 0, nb, c->stream);
+        e = hipMalloc(&k->scr.p, nb);
+        k->scr.bytes = nb;
+        if (e == hipSuccess) e = hipMemsetAsync(k->scr.p, 0, nb, c->stream);
     }
     if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
     if (e != hipSuccess) {
@@ -466,8 +469,8 @@ int insitu_cache_destroy(insitu_cache *k) {
         if (p) hipFree(p);
     if (k->stats) hipFree(k->stats);
     if (k->wire_scratch) hipFree(k->wire_scratch);
-    if (k->chunk_scratch) hipFree(k->chunk_scratch);
-    if (k->prefill_scratch) hipFree(k->prefill_scratch);
+    if (k->scr.p) hipFree(k->scr.p);
+    if (k->prefill_scr.p) hipFree(k->prefill_scr.p);
     if (k->prefill_len) hipFree(k->prefill_len);
     delete k;
     return INSITU_OK;
@@ -558,17 +561,19 @@ int insitu_append_seq(insitu_cache *k, int32_t seq, const int32_t *kr, const int
 // q_staged: the chunked path's fp64 query staging already holds q (the step's
 // write kernel filled it). step: the whole decode step in the attend launch
 // (chunked sequential mode; the lengths are those before the step).
+// ep: the attend's epoch from scratch_begin (0: take one here).
 static int attend_impl(insitu_cache *k, const int32_t *q, int32_t *out, int32_t mode,
-                       bool q_staged, const StepIn *step = nullptr) {
+                       bool q_staged, const StepIn *step = nullptr, uint32_t ep = 0) {
     const int64_t *len = k->len_dev[k->cur];
     const int two_pass = mode == INSITU_TWO_PASS ? 1 : 0;
     LaunchEv ev;
     int rc = timing_events(k->ctx, &ev);
     if (rc) return rc;
-    if (mode != INSITU_SERIAL && k->chunk_scratch) {
-        HIP_TRY(launch_attend_chunked(k->ctx->stream, k->g, k->tabs, q, out, len, k->chunk_scratch,
-                                      k->max_chunks, k->pool, k->calls++, two_pass, q_staged, step,
-                                      ev, k->stats),
+    if (mode != INSITU_SERIAL && k->chunked) {
+        if (!ep) HIP_TRY(scratch_begin(k->ctx->stream, k->scr, &ep), "scratch clear");
+        k->scr.spin_limit = k->spin_limit;
+        HIP_TRY(launch_attend_chunked(k->ctx->stream, k->g, k->tabs, q, out, len, k->scr, ep,
+                                      k->max_chunks, k->pool, two_pass, q_staged, step, ev, k->stats),
                 "chunked attend launch");
         return INSITU_OK;
     }
@@ -592,19 +597,87 @@ int insitu_attend(insitu_cache *k, const int32_t *q, int32_t *out, int32_t mode,
 }
 
 // A prefill attend (attend_causal_batch / attend_online_batch, attention.py:517-871)
-// runs as a virtual batch: up to PREFILL_QB queries per launch, query i a
-// "sequence" of its own length base + i + 1 whose planes are those of the real
-// sequence (sequence stride 0). Every query then gets exactly the decode path's
-// arithmetic over rows 0 .. base + i.
+// runs as a virtual batch: query i a "sequence" of its own length base + i + 1
+// whose planes are those of the real sequence (sequence stride 0). Every query
+// then gets exactly the decode path's arithmetic over rows 0 .. base + i.
+//
+// The chunk scratch of a launch is laid out for its own longest query (its
+// chunk count, not the cache's capacity), and a launch takes as many queries as
+// fit PREFILL_SCRATCH_BUDGET (at most PREFILL_QB): at ctx 32k and d = 64 about
+// 2.2 MB per query, so 116 queries per launch; at d = 128 and ctx 131,072 about
+// 17 MB per query, so 15.
 constexpr int64_t PREFILL_QB = 256;
+constexpr size_t PREFILL_SCRATCH_BUDGET = (size_t)256 << 20;
 
 __global__ void prefill_lengths_kernel(int64_t *len, int64_t first, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) len[i] = first + i;
 }
 
-int insitu_attend_causal(insitu_cache *k, int32_t seq, int64_t base, int64_t n_q, const int32_t *q,
-                         int32_t *out, int32_t mode, insitu_stats *stats) {
+namespace {
+
+// How many queries one prefill launch takes, and the scratch it needs: the
+// launch's chunk count is that of its longest query, base + n_q rows.
+struct PrefillPlan {
+    int64_t qb, max_chunks, pool;
+    size_t bytes;
+};
+PrefillPlan prefill_plan(const Geom &gv, int64_t base, int64_t n_q, size_t budget) {
+    PrefillPlan pl{};
+    pl.max_chunks = chunked_max_chunks(base + n_q);
+    pl.pool = chunked_pool_slots(pl.max_chunks);
+    Geom one = gv;
+    one.batch = 1;
+    const size_t per_q = chunked_scratch_bytes(one, pl.max_chunks, pl.pool);
+    pl.qb = (int64_t)(budget / (per_q ? per_q : 1));
+    if (pl.qb > PREFILL_QB) pl.qb = PREFILL_QB;
+    if (pl.qb > n_q) pl.qb = n_q;
+    Geom all = gv;
+    all.batch = (int32_t)(pl.qb > 0 ? pl.qb : 1);
+    pl.bytes = chunked_scratch_bytes(all, pl.max_chunks, pl.pool);
+    return pl;
+}
+
+}  // namespace
+
+// The prefill launches over a scratch the caller provides (scr, lengths len_dev for
+// PREFILL_QB queries); shared by insitu_attend_causal and its allocation-free variant.
+static int prefill_launches(insitu_cache *k, const Geom &gv, const PrefillPlan &pl, ChunkScratch &scr,
+                            int64_t *len_dev, int64_t base, int64_t n_q, const int32_t *q, int32_t *out,
+                            int32_t mode, bool timed = true) {
+    const Geom &g = k->g;
+    const bool chunked = mode != INSITU_SERIAL && k->chunked;
+    const int64_t row = (int64_t)g.n_q * g.d;
+    const int64_t qb = chunked ? pl.qb : PREFILL_QB;
+    Geom gb = gv;
+    for (int64_t i0 = 0; i0 < n_q; i0 += qb) {
+        const int64_t nb = n_q - i0 < qb ? n_q - i0 : qb;
+        gb.batch = (int32_t)nb;
+        hipLaunchKernelGGL(prefill_lengths_kernel, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0,
+                           k->ctx->stream, len_dev, base + i0 + 1, nb);
+        HIP_TRY(hipGetLastError(), "prefill lengths");
+        LaunchEv ev;
+        int rc = timed ? timing_events(k->ctx, &ev) : INSITU_OK;
+        if (rc) return rc;
+        if (chunked) {
+            uint32_t ep = 0;
+            HIP_TRY(scratch_begin(k->ctx->stream, scr, &ep), "scratch clear");
+            scr.spin_limit = k->spin_limit;
+            HIP_TRY(launch_attend_chunked(k->ctx->stream, gb, k->tabs, q + i0 * row, out + i0 * row, len_dev,
+                                          scr, ep, pl.max_chunks, pl.pool, mode == INSITU_TWO_PASS ? 1 : 0,
+                                          false, nullptr, ev, k->stats, pl.qb),
+                    "prefill attend launch");
+        } else {
+            HIP_TRY(launch_attend_serial(k->ctx->stream, gb, k->tabs, q + i0 * row, out + i0 * row, len_dev,
+                                         mode == INSITU_TWO_PASS ? 1 : 0, ev, k->stats),
+                    "prefill attend launch");
+        }
+    }
+    return INSITU_OK;
+}
+
+static int prefill_check(insitu_cache *k, int32_t seq, int64_t base, int64_t n_q, const int32_t *q,
+                         int32_t *out, int32_t mode) {
     if (!k || (n_q > 0 && (!q || !out))) return fail(INSITU_EINVAL, "null argument");
     if (mode < INSITU_SEQUENTIAL || mode > INSITU_SERIAL) return fail(INSITU_EINVAL, "unknown mode");
     const Geom &g = k->g;
@@ -616,44 +689,36 @@ int insitu_attend_causal(insitu_cache *k, int32_t seq, int64_t base, int64_t n_q
                  (long long)k->len_host[seq]);
         return fail(INSITU_EBADLEN, buf);
     }
+    return INSITU_OK;
+}
+
+int insitu_attend_causal(insitu_cache *k, int32_t seq, int64_t base, int64_t n_q, const int32_t *q,
+                         int32_t *out, int32_t mode, insitu_stats *stats) {
+    int rc = prefill_check(k, seq, base, n_q, q, out, mode);
+    if (rc) return rc;
     HIP_TRY(hipSetDevice(k->ctx->device), "hipSetDevice");
-    int rc = stats ? zero_stats(k) : INSITU_OK;
+    rc = stats ? zero_stats(k) : INSITU_OK;
     if (rc) return rc;
     if (n_q == 0) return copy_stats(k, stats);
+    const Geom &g = k->g;
     Geom gv = g;
     gv.base = g.base + (int64_t)seq * g.seq_stride;
     gv.seq_stride = 0;
-    const bool chunked = mode != INSITU_SERIAL && k->chunk_scratch;
+    const PrefillPlan pl = prefill_plan(gv, base, n_q, PREFILL_SCRATCH_BUDGET);
     if (!k->prefill_len) HIP_TRY(hipMalloc(&k->prefill_len, PREFILL_QB * sizeof(int64_t)), "hipMalloc");
-    if (chunked && !k->prefill_scratch) {
-        Geom gc = gv;
-        gc.batch = (int32_t)PREFILL_QB;
-        const size_t nb = chunked_scratch_bytes(gc, k->max_chunks, k->pool);
-        HIP_TRY(hipMalloc(&k->prefill_scratch, nb), "hipMalloc");
-        HIP_TRY(hipMemsetAsync(k->prefill_scratch, 0, nb, k->ctx->stream), "hipMemsetAsync");
+    if (mode != INSITU_SERIAL && k->chunked && k->prefill_scr.bytes < pl.bytes) {
+        // grow: the old buffer may still be in use by queued launches
+        HIP_TRY(hipStreamSynchronize(k->ctx->stream), "sync");
+        if (k->prefill_scr.p) HIP_TRY(hipFree(k->prefill_scr.p), "hipFree");
+        k->prefill_scr.p = nullptr;
+        k->prefill_scr.bytes = 0;
+        HIP_TRY(hipMalloc(&k->prefill_scr.p, pl.bytes), "hipMalloc");
+        HIP_TRY(hipMemsetAsync(k->prefill_scr.p, 0, pl.bytes, k->ctx->stream), "hipMemsetAsync");
+        k->prefill_scr.bytes = pl.bytes;
+        k->prefill_scr.calls = 0;
     }
-    const int64_t row = (int64_t)g.n_q * g.d;
-    for (int64_t i0 = 0; i0 < n_q; i0 += PREFILL_QB) {
-        const int64_t nb = n_q - i0 < PREFILL_QB ? n_q - i0 : PREFILL_QB;
-        gv.batch = (int32_t)nb;
-        hipLaunchKernelGGL(prefill_lengths_kernel, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0,
-                           k->ctx->stream, k->prefill_len, base + i0 + 1, nb);
-        HIP_TRY(hipGetLastError(), "prefill lengths");
-        LaunchEv ev;
-        rc = timing_events(k->ctx, &ev);
-        if (rc) return rc;
-        if (chunked) {
-            HIP_TRY(launch_attend_chunked(k->ctx->stream, gv, k->tabs, q + i0 * row, out + i0 * row,
-                                          k->prefill_len, k->prefill_scratch, k->max_chunks, k->pool,
-                                          k->calls++, mode == INSITU_TWO_PASS ? 1 : 0, false, nullptr,
-                                          ev, k->stats, PREFILL_QB),
-                    "prefill attend launch");
-        } else {
-            HIP_TRY(launch_attend_serial(k->ctx->stream, gv, k->tabs, q + i0 * row, out + i0 * row,
-                                         k->prefill_len, mode == INSITU_TWO_PASS ? 1 : 0, ev, k->stats),
-                    "prefill attend launch");
-        }
-    }
+    rc = prefill_launches(k, gv, pl, k->prefill_scr, k->prefill_len, base, n_q, q, out, mode);
+    if (rc) return rc;
     return copy_stats(k, stats);
 }
 
@@ -677,7 +742,7 @@ int insitu_step(insitu_cache *k, const int32_t *q, const int32_t *kw, const int3
     // token attends to itself), then the attend (:337-345). In chunked
     // sequential mode at d = 64 that is one launch; otherwise one write kernel
     // (which also stages the rotated queries for a chunked attend) and the attend.
-    const bool chunked = mode != INSITU_SERIAL && k->chunk_scratch;
+    const bool chunked = mode != INSITU_SERIAL && k->chunked;
     if (chunked && mode != INSITU_TWO_PASS && chunked_fused_step(g)) {
         StepIn si;
         si.qw = q;
@@ -694,16 +759,41 @@ int insitu_step(insitu_cache *k, const int32_t *q, const int32_t *kw, const int3
     }
     double *qd = nullptr;
     int32_t *qok = nullptr;
-    if (chunked) chunked_query_area(g, k->max_chunks, k->pool, k->chunk_scratch, &qd, &qok);
+    uint32_t ep = 0;
+    if (chunked) {
+        // the epoch (and the wrap's clear) before the write kernel stages the queries
+        HIP_TRY(scratch_begin(k->ctx->stream, k->scr, &ep), "scratch clear");
+        chunked_query_area(g, k->max_chunks, k->pool, k->scr.p, &qd, &qok);
+    }
     HIP_TRY(launch_step_write(k->ctx->stream, g, k->tabs, q, kw, vw, k->desc.fmt.rot_rounds,
                               k->desc.fmt.rot_signs, qr, qd, qok, k->len_dev[k->cur],
                               k->len_dev[k->cur ^ 1], k->stats),
             "step write launch");
     k->cur ^= 1;
     for (int b = 0; b < g.batch; ++b) k->len_host[b] += 1;
-    rc = attend_impl(k, qr, out, mode, chunked);
+    rc = attend_impl(k, qr, out, mode, chunked, nullptr, ep);
     if (rc) return rc;
     return copy_stats(k, stats);
+}
+
+int insitu_cache_debug(insitu_cache *k, int32_t what, int64_t value) {
+    if (!k) return fail(INSITU_EINVAL, "cache is NULL");
+    switch (what) {
+    case INSITU_DEBUG_DECODE_CALLS:
+        if (value < 0 || value > 0xFFFFFFFFll) return fail(INSITU_EINVAL, "call count out of range");
+        k->scr.calls = (uint32_t)value;
+        return INSITU_OK;
+    case INSITU_DEBUG_PREFILL_CALLS:
+        if (value < 0 || value > 0xFFFFFFFFll) return fail(INSITU_EINVAL, "call count out of range");
+        k->prefill_scr.calls = (uint32_t)value;
+        return INSITU_OK;
+    case INSITU_DEBUG_SPIN_LIMIT:
+        if (value < 0 || value > (1 << 30)) return fail(INSITU_EINVAL, "spin limit out of range");
+        k->spin_limit = (int32_t)value;
+        return INSITU_OK;
+    default:
+        return fail(INSITU_EINVAL, "unknown debug setting");
+    }
 }
 
 int insitu_read_rows(insitu_cache *k, int32_t seq, int32_t head, int64_t t0, int64_t n,

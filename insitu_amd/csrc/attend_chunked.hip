@@ -71,7 +71,6 @@ constexpr unsigned long long ST_AGG = 1ull << 62, ST_INC = 2ull << 62;
 constexpr unsigned long long ST_FLAGS = 3ull << 62;
 constexpr int EPOCH_BITS = 14;
 constexpr unsigned EPOCH_MASK = (1u << EPOCH_BITS) - 1u;
-constexpr int SPIN_LIMIT = 1 << 20;
 // A run whose sum of |term| bounds stays at or below this publishes that bound as
 // its peak |prefix sum|; only blocks of entries where a run may exceed it track
 // the actual prefix sums (sequential mode: flat softmax over large values).
@@ -145,6 +144,7 @@ struct Chunked {
     int32_t *qok;                  // [chain]  nonzero: every score of the group is exact in fp64
     int32_t max_chunks, pool;
     uint32_t ep;                   // this call's epoch, 1 .. 2^14 - 1
+    int32_t spin_limit;            // polls before a wait gives up (0: at once)
 };
 
 template <int D, int KB>
@@ -672,7 +672,8 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                                        __HIP_MEMORY_SCOPE_AGENT);
                 int64_t base = chunk - 1;       // the predecessor lane 0 reads
                 int spins = 0;
-                for (;;) {
+                fail = ck.spin_limit == 0;
+                while (!fail) {
                     const int64_t pc = base - lane;
                     unsigned long long flag = ST_INC;
                     int64_t val = SCORE_LO;
@@ -687,7 +688,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     const int nearest = inc ? __ffsll((long long)inc) - 1 : 64;
                     const unsigned long long wait = __ballot(flag == 0 && lane <= nearest);
                     if (wait) {
-                        if (++spins > SPIN_LIMIT) {
+                        if (++spins > ck.spin_limit) {
                             fail = true;
                             break;
                         }
@@ -1097,7 +1098,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                 const SegMeta *meta = ck.meta + ((int64_t)chain * GF + h) * ck.pool;
                 const int32_t *segS = ck.segS + ((int64_t)chain * GF + h) * ck.pool * D;
                 uint16_t *sl = S.u.rp.slot[h];
-                const int zslot = ck.pool - 1;    // never written: all zero
+                const int zslot = ck.pool - 1;    // a valid slot for the lanes past a batch to read
                 const uint32_t ep = ck.ep;
                 auto cur = [ep](uint64_t w) __attribute__((always_inline)) { return (uint32_t)(w >> 40) == ep; };
                 // Chunk 0's state: in the registers, or out of its slot once its header is up.
@@ -1116,10 +1117,11 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                 } else if (!fb) {
                     uint64_t h0 = 0;
                     int spins = 0;
-                    for (;;) {
+                    fb = ck.spin_limit == 0;
+                    while (!fb) {
                         h0 = (uint64_t)uni64((int64_t)get64(&hdr[0].w0));   // all lanes, one word
                         if (cur(h0)) break;
-                        if (++spins > SPIN_LIMIT) {
+                        if (++spins > ck.spin_limit) {
                             fb = true;
                             break;
                         }
@@ -1193,7 +1195,8 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     const int nblk = (nb + 7) >> 3;                        // blocks of 8 runs
                     const bool mine = lane < nb;
                     const uint32_t ent = mine ? (uint32_t)sl[g0 + lane] : (uint32_t)zslot;
-                    // lane i: the byte offset of run i's row (lanes past the batch: the zero slot)
+                    // lane i: the byte offset of run i's row (lanes past the batch: the spare
+                    // slot, whose contents are read but never added)
                     const uint32_t roff = (ent & (RUN_EVENT - 1)) * (uint32_t)(D * 4);
                     const char *sbase = (const char *)segS + 4 * lane;
                     int32_t sv[SB][CPL];
@@ -1201,7 +1204,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     for (int blk = 0; blk < SB / 8; ++blk) {
                         if (blk < nblk) {
                             // no branch between the loads of a block; past the batch
-                            // they read the zero slot
+                            // they read the spare slot
 #pragma unroll
                             for (int i = 8 * blk; i < 8 * blk + 8; ++i) {
                                 const uint32_t o = (uint32_t)__builtin_amdgcn_readlane((int)roff, i);
@@ -1264,7 +1267,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                                     for (int k = 0; k < CPL; ++k) unsafe = unsafe || !fits((int32_t)aw[k], m);
                                 }
 #pragma unroll
-                                for (int k = 0; k < CPL; ++k) aw[k] += (AccT)sv[i][k];
+                                for (int k = 0; k < CPL; ++k) aw[k] += i < nb ? (AccT)sv[i][k] : (AccT)0;
                             }
                         }
                     }
@@ -1412,9 +1415,9 @@ bool chunked_supported(const Geom &g, int64_t capacity) {
 }
 
 
-// The run slots of every chunk, plus one last slot that is never written (the
-// scratch is zeroed when the cache is created): the replay pads its batches
-// with it.
+// The run slots of every chunk, plus one spare slot that is never written: the
+// replay's lanes past the end of a batch load from it (and add nothing), so the
+// loads of a batch need no branch.
 int64_t chunked_pool_slots(int64_t max_chunks) { return 1 + (max_chunks - 1) * SLOTS + 1; }
 
 static void carve(const Geom &g, int64_t max_chunks, int64_t pool, uint8_t *p, Chunked *ck,
@@ -1456,10 +1459,33 @@ void chunked_query_area(const Geom &g, int64_t max_chunks, int64_t pool, void *s
     *qok = ck.qok;
 }
 
+__global__ void clear_scratch_kernel(uint4 *p, int64_t n16) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+hipError_t scratch_begin(hipStream_t s, ChunkScratch &cs, uint32_t *ep) {
+    const uint32_t call = cs.calls++;
+    // 1 .. 2^14 - 1: the zeroed scratch of a new buffer is never current. At
+    // the wrap the words go back to zero (no epoch); every chain's completion
+    // counter is zero between attends already.
+    if (call % EPOCH_MASK == 0 && call > 0) {
+        const int64_t n16 = (int64_t)(cs.bytes / 16);     // carve() rounds every area to 256 B
+        const unsigned blocks = (unsigned)(n16 < 65536 * 256 ? (n16 + 255) / 256 : 65536);
+        if (n16 > 0) {
+            hipLaunchKernelGGL(clear_scratch_kernel, dim3(blocks), dim3(256), 0, s, (uint4 *)cs.p, n16);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        }
+    }
+    *ep = call % EPOCH_MASK + 1;
+    return hipSuccess;
+}
+
 hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
-                                 int32_t *out, const int64_t *len, void *scratch, int64_t max_chunks,
-                                 int64_t pool, uint32_t call, int two_pass, bool q_staged,
-                                 const StepIn *step, LaunchEv ev, DevStats *st,
+                                 int32_t *out, const int64_t *len, ChunkScratch &cs,
+                                 uint32_t ep, int64_t max_chunks, int64_t pool, int two_pass,
+                                 bool q_staged, const StepIn *step, LaunchEv ev, DevStats *st,
                                  int64_t carve_batch) {
     const int64_t chains = (int64_t)g.batch * g.n_kv;
     if (max_chunks > HMAX || chains > 65535 || max_chunks * chains > 0x7fffffff)
@@ -1469,14 +1495,20 @@ hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, 
     gc.batch = (int32_t)carve_batch;
     Chunked ck;
     size_t bytes = 0;
-    carve(gc, max_chunks, pool, (uint8_t *)scratch, &ck, &bytes);
-    ck.ep = call % EPOCH_MASK + 1;     // 1 .. 2^14 - 1: zeroed scratch is never current
-    // The epoch wraps every 2^14 - 1 calls: a word last written exactly that
-    // many calls ago would read as current, so the words go back to zero (no
-    // epoch) first. Every chain's counter is zero between calls already.
-    if (call % EPOCH_MASK == 0 && call > 0) {
-        const hipError_t e = hipMemsetAsync(scratch, 0, bytes, s);
+    carve(gc, max_chunks, pool, (uint8_t *)cs.p, &ck, &bytes);
+    if (bytes > cs.bytes || ep == 0 || ep > EPOCH_MASK) return hipErrorInvalidValue;
+    ck.ep = ep;
+    ck.spin_limit = cs.spin_limit;
+    const uint64_t layout = ((uint64_t)max_chunks << 48) ^ ((uint64_t)pool << 24) ^ ((uint64_t)carve_batch << 8) ^
+                            (uint64_t)g.n_kv ^ ((uint64_t)g.d << 40) ^ 1ull;
+    if (layout != cs.layout) {
+        // c.done is 256-byte aligned and padded (carve), so whole uint4 words
+        const int64_t n16 = (chains * (int64_t)sizeof(unsigned int) + 255) / 256 * 16;
+        hipLaunchKernelGGL(clear_scratch_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, s,
+                           (uint4 *)ck.done, n16);
+        const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
+        cs.layout = layout;
     }
 #define INSITU_FAST(DD, KK)                                                          \
     if (g.d == DD && g.kb == KK)                                                     \

@@ -208,12 +208,36 @@ void chunked_query_area(const Geom &g, int64_t max_chunks, int64_t pool, void *s
 // Whether insitu_step runs as one fused launch in sequential mode (the
 // register budget of the fused kernel allows it at d = 64).
 bool chunked_fused_step(const Geom &g);
+// A chunked attend's scratch: look-back words, chunk headers, run slots, the
+// query staging. Its words carry the epoch of the attend that wrote them (the
+// attend's number among the buffer's attends, 1 .. 2^14 - 1), so a word from an
+// earlier attend reads as unpublished and nothing is reset between attends.
+// Each buffer counts its own attends. spin_limit bounds every wait of the
+// kernel on another workgroup (0: give up at once, which sends the chain to the
+// exact serial path; a test hook).
+// The per-chain completion counters are the only words that must read zero
+// when an attend starts (its last workgroup puts them back to zero); when a
+// launch lays the buffer out differently from the previous one (a prefill's
+// chunk count follows its prompt), they are cleared first.
+struct ChunkScratch {
+    void *p = nullptr;
+    size_t bytes = 0;
+    uint32_t calls = 0;
+    int32_t spin_limit = 1 << 20;
+    uint64_t layout = 0;          // the carve of the last launch (0: none yet)
+};
+// The epoch of the next attend on the buffer. Every 2^14 - 1 attends the epoch
+// wraps, and the whole buffer is cleared first (a fill kernel on the stream):
+// a word written exactly that many attends ago would otherwise read as current.
+// Call it before any work of the attend writes the buffer (the query staging of
+// a two-launch step included).
+hipError_t scratch_begin(hipStream_t s, ChunkScratch &cs, uint32_t *ep);
 // carve_batch: the sequences the scratch is laid out for (g.batch when 0); a
 // launch over fewer sequences than its scratch holds passes the larger count.
 hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
-                                 int32_t *out, const int64_t *len, void *scratch, int64_t max_chunks,
-                                 int64_t pool, uint32_t call, int two_pass, bool q_staged,
-                                 const StepIn *step, LaunchEv ev, DevStats *st,
+                                 int32_t *out, const int64_t *len, ChunkScratch &cs,
+                                 uint32_t ep, int64_t max_chunks, int64_t pool, int two_pass,
+                                 bool q_staged, const StepIn *step, LaunchEv ev, DevStats *st,
                                  int64_t carve_batch = 0);
 hipError_t launch_step_write(hipStream_t s, const Geom &g, const Tables *t, const int32_t *qw,
                              const int32_t *kw, const int32_t *vw, int rounds,
