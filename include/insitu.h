@@ -175,6 +175,18 @@ int insitu_attend_causal(insitu_cache *cache, int32_t seq, int64_t base, int64_t
                          const int32_t *q_rot_dev, int32_t *out_dev, int32_t mode,
                          insitu_stats *stats_host);
 
+/* insitu_attend_causal without allocating: no counterpart in the reference; for callers
+ * that cannot call hipMalloc (code under HIP graph capture, tight serving loops). The same
+ * launches and results as insitu_attend_causal, but the chunk scratch and the lengths of
+ * the virtual batch live in a fixed device array of the library (64 MiB, one per device,
+ * set up by insitu_ctx_create) instead of buffers the cache allocates. A launch takes as
+ * many queries as fit it; EBADLEN when a single query's scratch does not (its size is in
+ * the message). No statistics (nothing is copied back) and no timing events. Every call on
+ * a device shares that device's array: calls that overlap on one device (two streams, two
+ * threads) race and must not. Stream-ordered on the cache's context. */
+int insitu_attend_causal_static(insitu_cache *cache, int32_t seq, int64_t base, int64_t n_q,
+                                const int32_t *q_rot_dev, int32_t *out_dev, int32_t mode);
+
 /* -- the host half either side of the seam (kernel.py:198-249, 348-356) -------------- */
 
 /* A projection (ops/project.py:21-52, numerics/fp.py:25-44): y_dev fp32 (n, out_f) =

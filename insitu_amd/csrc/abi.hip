@@ -7,6 +7,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -95,6 +96,55 @@ struct insitu_ctx {
     std::vector<hipEvent_t> ev;           // 2 per attend: start, end
     size_t ev_used = 0;
 };
+
+// The allocation-free prefill (insitu_attend_causal_static) keeps its chunk
+// scratch and the virtual batch's lengths in this array: one copy per device,
+// held until the process ends, shared by every call on that device. Host code
+// never passes the array's name to a kernel or a copy: it is a host-side
+// stand-in; the device address comes from hipGetSymbolAddress, once per device,
+// in insitu_ctx_create.
+constexpr size_t STATIC_SCRATCH_BYTES = (size_t)64 << 20;
+constexpr size_t STATIC_LEN_BYTES = 4096;      // PREFILL_QB int64 lengths, rounded up
+static __device__ __align__(256) uint8_t scratch[STATIC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int MAX_DEVICES = 64;
+struct StaticScratch {
+    uint8_t *ptr = nullptr;     // the device's copy of `scratch`
+    ChunkScratch cs;            // its chunk-scratch part and attend count
+    int64_t *len = nullptr;     // its lengths part
+};
+StaticScratch g_static[MAX_DEVICES];
+std::mutex g_static_mu;
+
+__global__ void clear_bytes_kernel(uint4 *p, int64_t n16) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// With `device` current: look the array up and clear it, once per device.
+hipError_t static_scratch_setup(int device, hipStream_t stream) {
+    std::lock_guard<std::mutex> lock(g_static_mu);
+    if (device < 0 || device >= MAX_DEVICES) return hipErrorInvalidDevice;
+    StaticScratch &ss = g_static[device];
+    if (ss.ptr) return hipSuccess;
+    void *p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    const int64_t n16 = (int64_t)(STATIC_SCRATCH_BYTES / 16);
+    hipLaunchKernelGGL(clear_bytes_kernel, dim3(4096), dim3(256), 0, stream, (uint4 *)p, n16);
+    e = hipGetLastError();
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) return e;
+    ss.ptr = (uint8_t *)p;
+    ss.cs.p = p;
+    ss.cs.bytes = STATIC_SCRATCH_BYTES - STATIC_LEN_BYTES;
+    ss.len = (int64_t *)((uint8_t *)p + ss.cs.bytes);
+    return hipSuccess;
+}
+
+}  // namespace
 
 int insitu::ctx_device(insitu_ctx *c) { return c->device; }
 hipStream_t insitu::ctx_stream(insitu_ctx *c) { return c->stream; }
@@ -203,6 +253,7 @@ int insitu_ctx_create(int32_t device, void *hip_stream, insitu_ctx **out) {
     hipError_t e = hipMalloc(&c->hook_tables, sizeof(Tables));
     if (e == hipSuccess) e = hipMemcpy(c->hook_tables, &t, sizeof(Tables), hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMalloc(&c->hook_flags, 64);
+    if (e == hipSuccess) e = static_scratch_setup(device, c->stream);
     if (e != hipSuccess) {
         insitu_ctx_destroy(c);
         return hip_fail(e, "ctx set-up");
@@ -720,6 +771,36 @@ int insitu_attend_causal(insitu_cache *k, int32_t seq, int64_t base, int64_t n_q
     rc = prefill_launches(k, gv, pl, k->prefill_scr, k->prefill_len, base, n_q, q, out, mode);
     if (rc) return rc;
     return copy_stats(k, stats);
+}
+
+int insitu_attend_causal_static(insitu_cache *k, int32_t seq, int64_t base, int64_t n_q, const int32_t *q,
+                                int32_t *out, int32_t mode) {
+    int rc = prefill_check(k, seq, base, n_q, q, out, mode);
+    if (rc) return rc;
+    if (n_q == 0) return INSITU_OK;
+    const int dev = k->ctx->device;
+    if (dev < 0 || dev >= MAX_DEVICES || !g_static[dev].ptr)
+        return fail(INSITU_EINVAL, "the device's static scratch is not set up (insitu_ctx_create)");
+    StaticScratch &ss = g_static[dev];
+    HIP_TRY(hipSetDevice(dev), "hipSetDevice");
+    const Geom &g = k->g;
+    Geom gv = g;
+    gv.base = g.base + (int64_t)seq * g.seq_stride;
+    gv.seq_stride = 0;
+    PrefillPlan pl{};
+    if (mode != INSITU_SERIAL && k->chunked) {
+        pl = prefill_plan(gv, base, n_q, ss.cs.bytes);
+        if (pl.qb < 1) {
+            Geom one = gv;
+            one.batch = 1;
+            char buf[240];
+            snprintf(buf, sizeof buf, "one query over %lld rows needs %zu B of chunk scratch; the static "
+                     "scratch holds %zu B (insitu_attend_causal allocates instead)", (long long)(base + n_q),
+                     chunked_scratch_bytes(one, pl.max_chunks, pl.pool), ss.cs.bytes);
+            return fail(INSITU_EBADLEN, buf);
+        }
+    }
+    return prefill_launches(k, gv, pl, ss.cs, ss.len, base, n_q, q, out, mode, false);
 }
 
 int insitu_step(insitu_cache *k, const int32_t *q, const int32_t *kw, const int32_t *vw,
