@@ -2,15 +2,17 @@
 
 Workload: one Llama-3.2-1B-shape layer (32 query heads,
 8 KV heads, d=64, 4-bit keys / 2-bit values), batch 1. Each cache is filled by
-32,767 GPU appends of seeded synthetic q/k/v (insitu_amd/workload.py), then
-every timed step is one decode step from the wire: rotate q/k/v, append the
-token's compressed k/v row, attend over the whole cache (ctx 32,768 at the
-first step), Q16 out. The scan bytes are the compressed-cache bytes the
-attend reads: sum over KV heads of ctx * 52 B.
+32,767 GPU appends of seeded synthetic q/k/v (insitu_amd/workload.py); every
+timed step is then the configuration's one decode step from the wire: rotate
+q/k/v, append the token's compressed k/v row (row 32,767), attend over all
+32,768 rows, Q16 out. The scan bytes are the compressed-cache bytes the attend
+reads: 8 KV heads x 32,768 rows x 52 B = 13,631,488 B.
 
-Defeating the 256 MB Infinity Cache: R >= 20 caches of ~17 MB each (more than
-256 MB in total) are filled identically and the steps rotate through them, so
-consecutive steps never re-read a cache that is still resident.
+Defeating the 256 MB Infinity Cache: a pass of K timed steps uses K distinct
+caches (at least 40 of ~13.6 MB, more than twice the Infinity Cache in total),
+and between passes each cache is rewound to 32,767 rows (a length reset,
+outside the timed region), so every timed step is at ctx 32,768 and no step
+reads a cache that is still resident from the step before.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode online]
     python bench.py --copy-calibration      # a plain copy kernel of known size
@@ -66,7 +68,7 @@ def _args():
     ap.add_argument("--steps", type=int, default=40)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--mode", default="online", choices=["online", "two_pass", "split", "serial"])
-    ap.add_argument("--caches", type=int, default=20)
+    ap.add_argument("--caches", type=int, default=40)
     ap.add_argument("--ctx", type=int, default=CTX)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
@@ -81,16 +83,32 @@ def _args():
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "chunk_kernel_c2_traffic.json")
 
 
-def measured_traffic(mode: str, ctx: int):
-    """HBM bytes per attend launch from the committed FETCH_SIZE/WRITE_SIZE passes.
+# The kernels insitu_step launches for one decode step, per mode, at C2's format
+# (d = 64, 4-bit keys, 2-bit values, 4 query heads per KV head): online and split
+# mode are the one fused chunk_kernel launch.
+STEP_KERNEL = {
+    "online": "insitu::chunk_kernel<64, 4, true, false, true>",
+    "split": "insitu::chunk_kernel<64, 4, true, false, true>",
+    "two_pass": "insitu::step_write_kernel + insitu::chunk_max_kernel + insitu::chunk_kernel",
+    "serial": "insitu::step_write_kernel + insitu::attend_serial_kernel",
+}
 
-    Those passes profile the sequential attend at ctx 32,768; any other mode or
-    context has no measurement, and the field is null.
+
+def measured_traffic(kernel: str, ctx: int):
+    """HBM bytes per attend launch from the committed FETCH_SIZE/WRITE_SIZE passes,
+    and where they come from.
+
+    The passes profile one kernel at ctx 32,768; for another kernel or context there
+    is no measurement, and the field is null.
     """
-    if mode != "online" or ctx != CTX or not os.path.exists(TRAFFIC_FILE):
-        return None
+    if ctx != CTX or not os.path.exists(TRAFFIC_FILE):
+        return None, None
     with open(TRAFFIC_FILE) as f:
-        return json.load(f).get("traffic_bytes")
+        t = json.load(f)
+    if t.get("kernel") != kernel:
+        return None, f"none for {kernel} ({os.path.relpath(TRAFFIC_FILE, ROOT)} covers {t.get('kernel')})"
+    return t.get("traffic_bytes"), (f"{os.path.relpath(TRAFFIC_FILE, ROOT)}: rocprofv3 FETCH_SIZE + WRITE_SIZE "
+                                    f"per dispatch, each scaled by a plain copy's counters")
 
 
 def copy_calibration() -> None:
@@ -620,13 +638,14 @@ def main() -> int:
 
     ctx = default_context(0)
     quant = QuantConfig(key_bits=4, value_bits=2)
-    model = ModelConfig.llama32_1b()
     rot = Rotation.for_quant(quant, D)
-    # warmup, then the timed steps twice: once bare (value), once with the
-    # attend kernels' dispatches carrying timing events (roofline)
+    # Every timed step is the configuration's one decode step: the cache holds
+    # ctx - 1 rows, the step appends row ctx - 1 and attends over all ctx. A pass
+    # of K steps uses K distinct caches (at least --caches of them, whose total is
+    # more than twice the Infinity Cache); between passes every cache is rewound
+    # to ctx - 1 rows (a length reset, outside the timed region).
+    n_caches = max(a.caches, a.steps, a.warmup, 1)
     n_steps_total = a.warmup + 2 * a.steps
-    per_cache = (n_steps_total + a.caches - 1) // a.caches
-    capacity = a.ctx + per_cache
 
     # Prefill data: ctx-1 tokens of seeded wire k/v, rotated and appended on the GPU.
     wl = Workload(seed=0)
@@ -636,11 +655,10 @@ def main() -> int:
     qs, ks, vs = wl.steps(n_steps_total)      # the decode tokens
     del k, v
     caches = []
-    for _ in range(a.caches):
-        c = CompressedCache(N_KV, D, capacity, quant, batch=1, n_q_heads=N_Q, ctx=ctx)
+    for _ in range(n_caches):
+        c = CompressedCache(N_KV, D, a.ctx, quant, batch=1, n_q_heads=N_Q, ctx=ctx)
         c.append_rotated(kr, vr)
         caches.append(c)
-    attn = [CompressedAttention(c) for c in caches]
     qs_d = ctx.to_device(qs[0], torch.int32)
     ks_d = ctx.to_device(ks[0], torch.int32)
     vs_d = ctx.to_device(vs[0], torch.int32)
@@ -654,59 +672,69 @@ def main() -> int:
     from insitu_amd.runtime import ptr
     import ctypes
     mode = _lib.MODES[a.mode]
-    scan_bytes = []
+    step_bytes = float(N_KV * ROW * a.ctx)      # the rows one attend scans
 
-    def step(i):
-        c = caches[i % a.caches]
+    def step(i, j):
         # One decode step from the wire, CMD_STEP (kernel.py:271-345): rotate q/k/v,
         # append the k/v row, attend -- one launch in online mode.
-        _lib.check(lib.insitu_step(c.handle, ptr(qs_d[i]), ptr(ks_d[i]), ptr(vs_d[i]),
+        _lib.check(lib.insitu_step(caches[j].handle, ptr(qs_d[i]), ptr(ks_d[i]), ptr(vs_d[i]),
                                    ptr(outs[i]), mode, None))
-        scan_bytes.append(N_KV * ROW * (a.ctx + i // a.caches))
+
+    def rewind():
+        for c in caches:
+            c.set_length(a.ctx - 1)
+        torch.cuda.synchronize()
 
     def timed_pass(i0, timing):
-        ms_sum, n_att = ctypes.c_double(), ctypes.c_int64()
+        rewind()
         _lib.check(lib.insitu_ctx_timing(ctx.handle, 1 if timing else 0))
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for i in range(i0, i0 + a.steps):
-            step(i)
+        for j in range(a.steps):
+            step(i0 + j, j)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        _lib.check(lib.insitu_ctx_timing_read(ctx.handle, ctypes.byref(ms_sum), ctypes.byref(n_att)))
+        ms = (ctypes.c_double * a.steps)()
+        n_att = ctypes.c_int64()
+        _lib.check(lib.insitu_ctx_timing_read_each(ctx.handle, ms, a.steps, ctypes.byref(n_att)))
         _lib.check(lib.insitu_ctx_timing(ctx.handle, 0))
         if n_att.value != (a.steps if timing else 0):
             raise RuntimeError(f"timed {n_att.value} attends for {a.steps} steps")
-        return wall, ms_sum.value
+        return wall, np.array(ms[:n_att.value]) * 1e3
 
     for i in range(a.warmup):
-        step(i)
+        step(i, i)
     torch.cuda.synchronize()
-    # value: the steps with nothing attached; roofline: the attend kernels' own
-    # time, from HIP events attached to their dispatches on the stream they run
-    # on (insitu_ctx_timing), over a second pass of as many steps (the events
+    # value: the steps with nothing attached; roofline: the attend kernel's own
+    # time, from HIP events attached to its dispatches on the stream it runs on
+    # (insitu_ctx_timing), over a second pass of as many steps (the events
     # themselves cost the step a few microseconds, so that pass is not `value`)
     wall, _ = timed_pass(a.warmup, False)
-    wall_ev, ms_sum = timed_pass(a.warmup + a.steps, True)
-
-    attend_ms_mean = ms_sum / a.steps
-    bytes_timed = np.array([scan_bytes[i] for i in range(a.warmup, a.warmup + a.steps)],
-                           dtype=np.float64)
-    bytes_ev = np.array([scan_bytes[i] for i in range(a.warmup + a.steps, n_steps_total)],
-                        dtype=np.float64)
-    kernel_gbs = float(bytes_ev.sum() / (ms_sum / 1e3) / 1e9)
-    whole_gbs = float(bytes_timed.sum() / wall / 1e9)
-    per_launch_bytes = float(bytes_ev.mean())
+    wall_ev, us_each = timed_pass(a.warmup + a.steps, True)
+    us_med = float(np.median(us_each))
+    us_mean = float(us_each.mean())
+    kernel_gbs = step_bytes / (us_med * 1e-6) / 1e9
+    whole_gbs = step_bytes * a.steps / wall / 1e9
 
     # Correctness of the timed work: the last step against the oracle (and the CPU baseline).
     last = n_steps_total - 1
     out_last = outs[last].cpu().numpy()[0].astype(np.int64)
-    cache_last = caches[last % a.caches]
+    cache_last = caches[a.steps - 1]
+    if cache_last.length != a.ctx:
+        raise RuntimeError(f"the last step's cache holds {cache_last.length} rows, not {a.ctx}")
+    from oracle import native
+    from oracle.quantize import Format
+    from oracle.rotate import rotate, signs_from_seed
+    q_rot_last = rotate(qs[0, last].astype(np.int64), signs_from_seed(D, 0, 1))
+    want = np.concatenate([native.attend_online(q_rot_last[4 * h:4 * h + 4], cache_last.view(h), Format())[0]
+                           for h in range(N_KV)]) if a.mode != "two_pass" else None
+    if want is not None and not np.array_equal(want, out_last):
+        raise AssertionError("the last timed step disagrees with the oracle")
     cpu = None
     if not a.no_cpu_baseline:
-        from oracle.rotate import rotate, signs_from_seed
-        q_rot_last = rotate(qs[0, last].astype(np.int64), signs_from_seed(D, 0, 1))
         cpu = cpu_baseline(cache_last, q_rot_last, out_last)
+    kernel = STEP_KERNEL.get(a.mode, a.mode)
+    traffic, traffic_src = measured_traffic(kernel, a.ctx)
 
     res = {
         "metric": "compressed-KV scan GB/s (% HBM peak) + us/decode-step at ctx 32k, 1 GPU",
@@ -725,17 +753,21 @@ def main() -> int:
         "data": "synthetic (seeded N(0,1) q/k/v with 4 outlier channels x8 per head, Q8.16)",
         "config": {"workload": "C2: Llama-3.2-1B-shape single layer, batch 1, ctx 32768, "
                                "4b K / 2b V, decode step = insitu_step: rotate + append + attend",
-                   "mode": a.mode, "ctx_first_step": a.ctx, "rotating_caches": a.caches,
+                   "mode": a.mode, "ctx": a.ctx, "rotating_caches": n_caches,
                    "rotating_mb": round(total_mb, 1), "kv_heads": N_KV, "q_heads": N_Q,
                    "head_dim": D, "row_bytes": ROW},
         "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 3), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(kernel_gbs / HBM_PEAK_GBS, 5),
-                     "traffic": measured_traffic(a.mode, a.ctx),
-                     "kernel": "chunk_kernel (the one launch of insitu_attend; two-pass mode adds chunk_max_kernel)",
-                     "algorithmic_bytes_per_launch": per_launch_bytes,
-                     "avg_attend_us": round(attend_ms_mean * 1e3, 3),
+                     "traffic": traffic, "traffic_source": traffic_src,
+                     "kernel": kernel,
+                     "algorithmic_bytes_per_launch": step_bytes,
+                     "attend_us_median": round(us_med, 3),
+                     "attend_us_mean": round(us_mean, 3),
+                     "attend_us_min": round(float(us_each.min()), 3),
+                     "attend_us_max": round(float(us_each.max()), 3),
                      "cycles_per_row_gpu_wide_2p4ghz": round(
-                         attend_ms_mean * 1e-3 * 2.4e9 / (per_launch_bytes / ROW), 4)},
+                         us_med * 1e-6 * 2.4e9 / (step_bytes / ROW), 4)},
+        "checked": "the last timed step equal to oracle/c attend_online" if want is not None else None,
         "cpu_baseline": cpu,
     }
     print(json.dumps(res))

@@ -254,9 +254,13 @@ int insitu_probe_empty(insitu_ctx *ctx, int32_t n_wg, uint32_t *sink_dev);
 enum {
     INSITU_DEBUG_DECODE_CALLS = 1,   /* attends the decode scratch has served (its epoch counter) */
     INSITU_DEBUG_PREFILL_CALLS = 2,  /* the same for the prefill scratch                         */
-    INSITU_DEBUG_SPIN_LIMIT = 3      /* polls before a wait on another workgroup gives up; 0 gives
+    INSITU_DEBUG_SPIN_LIMIT = 3,     /* polls before a wait on another workgroup gives up; 0 gives
                                         up at once, sending every chain with a predecessor to the
                                         exact serial path                                       */
+    INSITU_DEBUG_PATH = 4            /* the kernel of a sequential-mode attend: 0 automatic (the
+                                        chunked attend where it handles the cache, the scan attend
+                                        elsewhere), 1 the scan attend, 2 the chunked attend;
+                                        INSITU_EINVAL if the kernel does not handle the cache   */
 };
 int insitu_cache_debug(insitu_cache *cache, int32_t what, int64_t value);
 

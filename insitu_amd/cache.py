@@ -260,6 +260,13 @@ class CompressedCache(KVCache):
     def set_length(self, n: int, seq: int = 0) -> None:
         _lib.check(self.ctx.lib.insitu_cache_set_length(self.handle, seq, n))
 
+    def pin_kernel(self, path: str) -> None:
+        """Test hook: the kernel of sequential-mode attends on this cache, "auto" (the
+        chunked attend where it handles the format and capacity, the scan attend
+        elsewhere), "scan" or "chunked". Raises if that kernel does not handle the cache."""
+        code = {"auto": _lib.PATH_AUTO, "scan": _lib.PATH_SCAN, "chunked": _lib.PATH_CHUNKED}[path]
+        _lib.check(self.ctx.lib.insitu_cache_debug(self.handle, _lib.DEBUG_PATH, code))
+
     @property
     def buf(self) -> np.ndarray:
         """(length, n_kv_heads, row_bytes) of sequence 0, read from the device."""

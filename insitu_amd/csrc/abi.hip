@@ -163,12 +163,15 @@ struct insitu_cache {
     DevStats *stats = nullptr;
     int32_t *wire_scratch = nullptr;      // insitu_step: the rotated queries
     bool chunked = false;                 // the chunked attend handles this format and capacity
+    bool scan = false;                    // the scan attend does (sequential mode)
     ChunkScratch scr;                     // decode attends: run sums and counters, one call's worth
-    int64_t max_chunks = 0, pool = 0;
+    int64_t max_chunks = 0, pool = 0;     // the chunked attend's layout
+    int64_t scan_mc = 0;                  // the scan attend's: chunks per sequence
     // prefill (insitu_attend_causal): scratch for a virtual batch of queries, their lengths
     ChunkScratch prefill_scr;
     int64_t *prefill_len = nullptr;
     int32_t spin_limit = 1 << 20;         // insitu_cache_debug
+    int32_t path = 0;                     // insitu_cache_debug: 0 auto, 1 scan, 2 chunked
 };
 
 namespace {
@@ -489,11 +492,20 @@ int insitu_cache_create(insitu_ctx *c, const insitu_cache_desc *desc, insitu_cac
     if (e == hipSuccess)
         e = hipMalloc(&k->wire_scratch,
                       sizeof(int32_t) * (size_t)g.batch * (g.n_q + 2 * g.n_kv) * g.d);
-    if (e == hipSuccess && chunked_supported(g, desc->capacity)) {
-        k->chunked = true;
-        k->max_chunks = chunked_max_chunks(desc->capacity);
-        k->pool = chunked_pool_slots(k->max_chunks);
-        const size_t nb = chunked_scratch_bytes(g, k->max_chunks, k->pool);
+    k->chunked = chunked_supported(g, desc->capacity);
+    k->scan = scan_supported(g, desc->capacity);
+    if (e == hipSuccess && (k->chunked || k->scan)) {
+        size_t nb = 0;
+        if (k->chunked) {
+            k->max_chunks = chunked_max_chunks(desc->capacity);
+            k->pool = chunked_pool_slots(k->max_chunks);
+            nb = chunked_scratch_bytes(g, k->max_chunks, k->pool);
+        }
+        if (k->scan) {
+            k->scan_mc = scan_max_chunks(desc->capacity);
+            const size_t ns = scan_scratch_bytes(g, k->scan_mc);
+            nb = ns > nb ? ns : nb;
+        }
         e = hipMalloc(&k->scr.p, nb);
         k->scr.bytes = nb;
         if (e == hipSuccess) e = hipMemsetAsync(k->scr.p, 0, nb, c->stream);
@@ -609,6 +621,17 @@ int insitu_append_seq(insitu_cache *k, int32_t seq, const int32_t *kr, const int
 }
 
 
+// Sequential (and split) mode: the chunked attend where it handles the format and
+// capacity (d = 64 or 128, 4 query heads per KV head, up to 512 chunks), the scan
+// attend elsewhere (8 query heads per KV head; longer contexts); a test hook can
+// pin either.
+static bool use_scan(const insitu_cache *k, int32_t mode) {
+    if (mode == INSITU_SERIAL || mode == INSITU_TWO_PASS || !k->scan) return false;
+    if (k->path == 1) return true;
+    if (k->path == 2) return false;
+    return !k->chunked;
+}
+
 // q_staged: the chunked path's fp64 query staging already holds q (the step's
 // write kernel filled it). step: the whole decode step in the attend launch
 // (chunked sequential mode; the lengths are those before the step).
@@ -620,6 +643,18 @@ static int attend_impl(insitu_cache *k, const int32_t *q, int32_t *out, int32_t 
     LaunchEv ev;
     int rc = timing_events(k->ctx, &ev);
     if (rc) return rc;
+    if (use_scan(k, mode)) {
+        // the scan attend, its grid sized by the longest sequence
+        if (!ep) HIP_TRY(scratch_begin(k->ctx->stream, k->scr, &ep), "scratch clear");
+        k->scr.spin_limit = k->spin_limit;
+        int64_t longest = 0;
+        for (int64_t n : k->len_host) longest = n > longest ? n : longest;
+        const int64_t chunks = scan_max_chunks(longest + (step ? 1 : 0));
+        HIP_TRY(launch_attend_scan(k->ctx->stream, k->g, k->tabs, q, out, len, k->scr, ep, k->scan_mc, chunks,
+                                   step, ev, k->stats),
+                "scan attend launch");
+        return INSITU_OK;
+    }
     if (mode != INSITU_SERIAL && k->chunked) {
         if (!ep) HIP_TRY(scratch_begin(k->ctx->stream, k->scr, &ep), "scratch clear");
         k->scr.spin_limit = k->spin_limit;
@@ -823,8 +858,10 @@ int insitu_step(insitu_cache *k, const int32_t *q, const int32_t *kw, const int3
     // token attends to itself), then the attend (:337-345). In chunked
     // sequential mode at d = 64 that is one launch; otherwise one write kernel
     // (which also stages the rotated queries for a chunked attend) and the attend.
-    const bool chunked = mode != INSITU_SERIAL && k->chunked;
-    if (chunked && mode != INSITU_TWO_PASS && chunked_fused_step(g)) {
+    const bool scan = use_scan(k, mode);
+    const bool chunked = !scan && mode != INSITU_SERIAL && k->chunked;
+    const bool fused = scan || (mode != INSITU_TWO_PASS && chunked && chunked_fused_step(g));
+    if (fused) {
         StepIn si;
         si.qw = q;
         si.kw = kw;
@@ -871,6 +908,12 @@ int insitu_cache_debug(insitu_cache *k, int32_t what, int64_t value) {
     case INSITU_DEBUG_SPIN_LIMIT:
         if (value < 0 || value > (1 << 30)) return fail(INSITU_EINVAL, "spin limit out of range");
         k->spin_limit = (int32_t)value;
+        return INSITU_OK;
+    case INSITU_DEBUG_PATH:
+        if (value == 1 && !k->scan) return fail(INSITU_EINVAL, "the scan attend does not handle this cache");
+        if (value == 2 && !k->chunked) return fail(INSITU_EINVAL, "the chunked attend does not handle this cache");
+        if (value < 0 || value > 2) return fail(INSITU_EINVAL, "path is 0 (auto), 1 (scan) or 2 (chunked)");
+        k->path = (int32_t)value;
         return INSITU_OK;
     default:
         return fail(INSITU_EINVAL, "unknown debug setting");

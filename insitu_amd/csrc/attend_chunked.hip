@@ -1429,14 +1429,15 @@ static void carve(const Geom &g, int64_t max_chunks, int64_t pool, uint8_t *p, C
         o += (n + 255) / 256 * 256;
         return p ? p + at : nullptr;
     };
+    // the words read before their epoch is known to be current come first (scratch_layout)
     Chunked c{};
     c.cmax = (int64_t *)take(chains * max_chunks * GF * sizeof(int64_t));
     c.status = (unsigned long long *)take(chains * max_chunks * GF * sizeof(unsigned long long));
     c.hdr = (ChunkHdr *)take(chains * max_chunks * GF * sizeof(ChunkHdr));
-    c.meta = (SegMeta *)take(chains * GF * pool * sizeof(SegMeta));
-    c.segS = (int32_t *)take(chains * GF * pool * g.d * sizeof(int32_t));
     c.done = (unsigned int *)take(chains * sizeof(unsigned int));
     c.chain_fb = (unsigned int *)take(chains * sizeof(unsigned int));
+    c.meta = (SegMeta *)take(chains * GF * pool * sizeof(SegMeta));
+    c.segS = (int32_t *)take(chains * GF * pool * g.d * sizeof(int32_t));
     c.qd = (double *)take(chains * g.d * GF * sizeof(double));
     c.qok = (int32_t *)take(chains * sizeof(int32_t));
     c.max_chunks = (int32_t)max_chunks;
@@ -1482,6 +1483,19 @@ hipError_t scratch_begin(hipStream_t s, ChunkScratch &cs, uint32_t *ep) {
     return hipSuccess;
 }
 
+hipError_t scratch_layout(hipStream_t s, ChunkScratch &cs, uint64_t layout, size_t front) {
+    if (layout == cs.layout) return hipSuccess;
+    const int64_t n16 = (int64_t)(front / 16);          // carve() rounds every area to 256 B
+    if (n16 > 0) {
+        const unsigned blocks = (unsigned)(n16 < 65536 * 256 ? (n16 + 255) / 256 : 65536);
+        hipLaunchKernelGGL(clear_scratch_kernel, dim3(blocks), dim3(256), 0, s, (uint4 *)cs.p, n16);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    cs.layout = layout;
+    return hipSuccess;
+}
+
 hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
                                  int32_t *out, const int64_t *len, ChunkScratch &cs,
                                  uint32_t ep, int64_t max_chunks, int64_t pool, int two_pass,
@@ -1500,15 +1514,10 @@ hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, 
     ck.ep = ep;
     ck.spin_limit = cs.spin_limit;
     const uint64_t layout = ((uint64_t)max_chunks << 48) ^ ((uint64_t)pool << 24) ^ ((uint64_t)carve_batch << 8) ^
-                            (uint64_t)g.n_kv ^ ((uint64_t)g.d << 40) ^ 1ull;
-    if (layout != cs.layout) {
-        // c.done is 256-byte aligned and padded (carve), so whole uint4 words
-        const int64_t n16 = (chains * (int64_t)sizeof(unsigned int) + 255) / 256 * 16;
-        hipLaunchKernelGGL(clear_scratch_kernel, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, s,
-                           (uint4 *)ck.done, n16);
-        const hipError_t e = hipGetLastError();
+                            (uint64_t)g.n_kv ^ ((uint64_t)g.d << 40) ^ (1ull << 62);
+    {
+        const hipError_t e = scratch_layout(s, cs, layout, (size_t)((uint8_t *)ck.meta - (uint8_t *)cs.p));
         if (e != hipSuccess) return e;
-        cs.layout = layout;
     }
 #define INSITU_FAST(DD, KK)                                                          \
     if (g.d == DD && g.kb == KK)                                                     \

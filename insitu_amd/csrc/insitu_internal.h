@@ -232,6 +232,22 @@ struct ChunkScratch {
 // Call it before any work of the attend writes the buffer (the query staging of
 // a two-launch step included).
 hipError_t scratch_begin(hipStream_t s, ChunkScratch &cs, uint32_t *ep);
+// A launch lays the buffer out as `layout` (a signature of its carve) with its
+// epoch-checked words (look-back words, headers, completion counters) in the
+// first `front` bytes: when the previous launch laid it out differently, those
+// bytes are zeroed first (a fill kernel), since stale words of another layout
+// could otherwise carry the current epoch by chance.
+hipError_t scratch_layout(hipStream_t s, ChunkScratch &cs, uint64_t layout, size_t front);
+// The scan attend (attend_scan.hip): sequential mode, 16 waves per 1,024-token
+// chunk, queries staged per workgroup and read as scalar operands, the chain's
+// last chunk replays. mc: chunks per sequence the scratch is laid out for (the
+// capacity's); grid_chunks: chunks of the longest sequence of this launch.
+bool scan_supported(const Geom &g, int64_t capacity);
+int64_t scan_max_chunks(int64_t tokens);
+size_t scan_scratch_bytes(const Geom &g, int64_t mc);
+hipError_t launch_attend_scan(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q, int32_t *out,
+                              const int64_t *len, ChunkScratch &cs, uint32_t ep, int64_t mc, int64_t grid_chunks,
+                              const StepIn *step, LaunchEv ev, DevStats *st);
 // carve_batch: the sequences the scratch is laid out for (g.batch when 0); a
 // launch over fewer sequences than its scratch holds passes the larger count.
 hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
