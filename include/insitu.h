@@ -175,6 +175,18 @@ int insitu_attend_causal(insitu_cache *cache, int32_t seq, int64_t base, int64_t
                          const int32_t *q_rot_dev, int32_t *out_dev, int32_t mode,
                          insitu_stats *stats_host);
 
+/* The same for the G query heads of one KV head (CompressedAttention holds one KV
+ * head's cache in the reference: attend_online / attend_two_pass, ops/attention.py:
+ * 429-513, called from kernel.py:385-392 with kv = cache.view(h).select(slice(0, ctx));
+ * attend_online_batch / attend_causal_batch, :517-871, called from kernel.py:317-331).
+ * Query i (i < n_q) of (seq, kv_head) attends that head's rows 0 .. base + i; a decode
+ * step over rows 0 .. n - 1 is base = n - 1, n_q = 1. q_rot_dev int32 (n_q, G, d)
+ * rotated; out_dev int32 (n_q, G, d) Q16; the statistics are this head's alone.
+ * EBADLEN when base + n_q exceeds the sequence's length. */
+int insitu_attend_causal_head(insitu_cache *cache, int32_t seq, int32_t kv_head, int64_t base,
+                              int64_t n_q, const int32_t *q_rot_dev, int32_t *out_dev, int32_t mode,
+                              insitu_stats *stats_host);
+
 /* insitu_attend_causal without allocating: no counterpart in the reference; for callers
  * that cannot call hipMalloc (code under HIP graph capture, tight serving loops). The same
  * launches and results as insitu_attend_causal, but the chunk scratch and the lengths of

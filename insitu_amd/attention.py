@@ -15,7 +15,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from . import _lib
-from .cache import CompressedCache
+from .cache import CompressedCache, DeviceKV
 from .runtime import ptr
 
 
@@ -45,6 +45,10 @@ class AttentionStats:
     @classmethod
     def from_c(cls, s: "_lib.Stats") -> "AttentionStats":
         return cls(*(int(getattr(s, n)) for n, _ in _lib.Stats._fields_))
+
+
+def _shape(a) -> tuple:
+    return tuple(a.shape) if hasattr(a, "shape") else np.shape(a)
 
 
 class CompressedAttention:
@@ -78,25 +82,49 @@ class CompressedAttention:
         self._keep = q
         return out, (AttentionStats.from_c(st) if st is not None else None)
 
-    def _group(self, q_rot, kv_head: int, seq: int, mode: str):
+    # -- one KV head: the reference's call forms (kernel.py:317-331, 385-392) --------
+
+    score_mode = "fused"     # attention.py:323: scores on the codes (architecture B)
+
+    def _kv(self, kv, seq: int) -> DeviceKV:
+        if isinstance(kv, (int, np.integer)):
+            return self.cache.view(int(kv), seq=seq)
+        if not isinstance(kv, DeviceKV) or kv.cache is not self.cache:
+            raise TypeError("kv must be this cache's view (CompressedCache.view) or a KV head index")
+        return kv
+
+    def _head(self, q_rot, kv: DeviceKV, base: int, n_q: int, mode: str):
+        import torch
         c = self.cache
         g = c.n_q_heads // c.n_kv_heads
-        q = np.zeros((c.batch, c.n_q_heads, c.head_dim), dtype=np.int32)
-        qg = np.atleast_2d(np.asarray(q_rot, dtype=np.int64))
-        if qg.shape != (g, c.head_dim):
-            raise ValueError(f"expected the {g} query heads of one KV group, got {qg.shape}")
-        q[seq, kv_head * g:(kv_head + 1) * g] = qg
-        out, st = self.attend(q, mode)
-        res = out[seq, kv_head * g:(kv_head + 1) * g].cpu().numpy().astype(np.int64)
-        return res.reshape(np.shape(q_rot)[:-1] + (c.head_dim,)), st
+        q = self.ctx.to_device(q_rot, torch.int32)
+        if q.numel() != n_q * g * c.head_dim:
+            raise ValueError(f"expected {n_q} x {g} query heads of {c.head_dim} for one KV group, "
+                             f"got {tuple(q.shape)}")
+        if base < 0 or base + n_q > kv.stop:
+            raise ValueError(f"queries {base} .. {base + n_q - 1} attend rows 0 .. base + i, "
+                             f"but the view holds {kv.stop} rows")
+        q = q.reshape(n_q, g, c.head_dim).contiguous()
+        out = torch.empty_like(q)
+        st = _lib.Stats()
+        _lib.check(self.ctx.lib.insitu_attend_causal_head(c.handle, kv.seq, kv.kv_head, base, n_q, ptr(q),
+                                                          ptr(out), _lib.MODES[mode], ctypes.byref(st)))
+        res = out.cpu().numpy().astype(np.int64)
+        return res.reshape(_shape(q_rot)[:-1] + (c.head_dim,)), AttentionStats.from_c(st)
 
-    def attend_online(self, q_rot, kv_head: int, seq: int = 0):
-        """attention.py:451-513 for one KV group: q_rot (G, d) -> (out (G, d), stats)."""
-        return self._group(q_rot, kv_head, seq, "online")
+    def attend_online(self, q_rot, kv, trace=None, *, seq: int = 0):
+        """attention.py:451-513: the G query heads of one KV head (q_rot (G, d) or (d,))
+        against every row of `kv` -> (out int64 of q_rot's shape, AttentionStats).
+        kv: this cache's view of the head (cache.view(h).select(slice(0, ctx)), the
+        call of kernel.py:385-392), or the KV head's index (all its rows, sequence
+        `seq`). trace is accepted for the reference's call form and left untouched."""
+        kv = self._kv(kv, seq)
+        return self._head(q_rot, kv, kv.stop - 1, 1, "online")
 
-    def attend_two_pass(self, q_rot, kv_head: int, seq: int = 0):
-        """attention.py:429-449 for one KV group."""
-        return self._group(q_rot, kv_head, seq, "two_pass")
+    def attend_two_pass(self, q_rot, kv, trace=None, *, seq: int = 0):
+        """attention.py:429-449, the same call form."""
+        kv = self._kv(kv, seq)
+        return self._head(q_rot, kv, kv.stop - 1, 1, "two_pass")
 
     # -- prefill: every query of a prompt at once (attention.py:517-871) --------
 
@@ -122,25 +150,15 @@ class CompressedAttention:
         self._keep = q
         return out, (AttentionStats.from_c(st) if st is not None else None)
 
-    def _group_batch(self, q_rot, kv_head: int, base: int, seq: int, mode: str):
-        c = self.cache
-        g = c.n_q_heads // c.n_kv_heads
-        qg = np.asarray(q_rot, dtype=np.int64)
-        if qg.ndim == 2:
-            qg = qg[:, None, :]
-        if qg.shape[1:] != (g, c.head_dim):
-            raise ValueError(f"expected (n_q, {g}, {c.head_dim}) for one KV group, got {qg.shape}")
-        q = np.zeros((qg.shape[0], c.n_q_heads, c.head_dim), dtype=np.int32)
-        q[:, kv_head * g:(kv_head + 1) * g] = qg
-        out, st = self.attend_prefill(q, base, mode, seq)
-        res = out[:, kv_head * g:(kv_head + 1) * g].cpu().numpy().astype(np.int64)
-        return res.reshape(np.shape(q_rot)[:-1] + (c.head_dim,)), st
+    def attend_causal_batch(self, q_rot, kv, base: int = 0, tile: int = 256, trace=None, *, seq: int = 0):
+        """attention.py:517-670 for one KV head, the call of kernel.py:329-331:
+        q_rot (n_q, G, d); query i attends rows 0 .. base + i of kv by
+        attend_two_pass. tile is the reference's memory bound on its float64
+        evaluation and changes nothing here. -> (out (n_q, G, d) int64, stats)."""
+        kv = self._kv(kv, seq)
+        return self._head(q_rot, kv, base, int(_shape(q_rot)[0]), "two_pass")
 
-    def attend_causal_batch(self, q_rot, kv_head: int, base: int = 0, seq: int = 0):
-        """attention.py:517-670 for one KV group: q_rot (n_q, G, d); query i
-        attends rows 0 .. base + i by attend_two_pass. -> (out, stats)."""
-        return self._group_batch(q_rot, kv_head, base, seq, "two_pass")
-
-    def attend_online_batch(self, q_rot, kv_head: int, base: int = 0, seq: int = 0):
-        """attention.py:794-871 for one KV group, by attend_online."""
-        return self._group_batch(q_rot, kv_head, base, seq, "online")
+    def attend_online_batch(self, q_rot, kv, base: int = 0, trace=None, *, seq: int = 0):
+        """attention.py:794-871 for one KV head (kernel.py:326-327), by attend_online."""
+        kv = self._kv(kv, seq)
+        return self._head(q_rot, kv, base, int(_shape(q_rot)[0]), "online")

@@ -68,6 +68,62 @@ class CompressedKV:
         return CompressedKV(self.k_idx[sl], self.k_norm[sl], self.v_idx[sl], self.v_norm[sl])
 
 
+class DeviceKV:
+    """compressed.py:95-121's view of one KV head, left where it lies: rows
+    [0, stop) of (sequence, KV head) in device memory.
+
+    CompressedAttention attends it on the GPU (kernel.py:385-392 hands the
+    reference's attention `cache.view(h).select(slice(0, ctx))`). It also reads
+    as the reference's CompressedKV: k_idx / k_norm / v_idx / v_norm read the
+    rows back and decode them, once, for host code that wants the arrays.
+    """
+
+    def __init__(self, cache: "CompressedCache", kv_head: int, seq: int = 0, stop: int | None = None):
+        self.cache = cache
+        self.kv_head = int(kv_head)
+        self.seq = int(seq)
+        self.stop = cache.lengths()[seq] if stop is None else int(stop)
+        self._host: CompressedKV | None = None
+
+    @property
+    def n_tokens(self) -> int:
+        return self.stop
+
+    def __len__(self) -> int:
+        return self.stop
+
+    def select(self, sl):
+        """A prefix (slice(0, n), the causal context of a token) stays on the device;
+        any other selection is a host CompressedKV."""
+        if isinstance(sl, slice) and sl.step in (None, 1) and sl.start in (None, 0):
+            stop = range(self.stop)[sl].stop if sl.stop is not None else self.stop
+            return DeviceKV(self.cache, self.kv_head, self.seq, max(0, min(stop, self.stop)))
+        return self.host().select(sl)
+
+    def host(self) -> CompressedKV:
+        if self._host is None:
+            q = self.cache.quant
+            rows = self.cache.read_rows(self.kv_head, 0, self.stop, self.seq)
+            self._host = unpack_rows(rows, self.cache.head_dim, q.key_bits, q.value_bits, q.norm_bits)
+        return self._host
+
+    @property
+    def k_idx(self) -> np.ndarray:
+        return self.host().k_idx
+
+    @property
+    def k_norm(self) -> np.ndarray:
+        return self.host().k_norm
+
+    @property
+    def v_idx(self) -> np.ndarray:
+        return self.host().v_idx
+
+    @property
+    def v_norm(self) -> np.ndarray:
+        return self.host().v_norm
+
+
 def unpack_rows(buf: np.ndarray, d: int, key_bits: int, value_bits: int,
                 norm_bits: int = 16) -> CompressedKV:
     """quantize.py:254-296: row bytes -> codes (LSB-first bitstreams) and sign-extended norms."""
@@ -276,9 +332,13 @@ class CompressedCache(KVCache):
             out[:, h] = self.read_rows(h, 0, n)
         return out
 
-    def view(self, kv_head: int, trace=None, n_reads: int = 1, seq: int = 0) -> CompressedKV:
-        """compressed.py:95-121: one KV head in causal order (decoded from device bytes)."""
-        return self.view_from_buffer(kv_head, seq=seq)
+    def view(self, kv_head: int, trace=None, n_reads: int = 1, seq: int = 0) -> DeviceKV:
+        """compressed.py:95-121: one KV head in causal order, as a device view
+        (DeviceKV). trace and n_reads are the reference's cycle-model bookkeeping;
+        the device records nothing into them."""
+        if not 0 <= kv_head < self.n_kv_heads:
+            raise IndexError(f"KV head {kv_head} of {self.n_kv_heads}")
+        return DeviceKV(self, kv_head, seq)
 
     def view_from_buffer(self, kv_head: int, seq: int = 0) -> CompressedKV:
         rows = self.read_rows(kv_head, 0, None, seq)

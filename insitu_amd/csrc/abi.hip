@@ -778,18 +778,14 @@ static int prefill_check(insitu_cache *k, int32_t seq, int64_t base, int64_t n_q
     return INSITU_OK;
 }
 
-int insitu_attend_causal(insitu_cache *k, int32_t seq, int64_t base, int64_t n_q, const int32_t *q,
-                         int32_t *out, int32_t mode, insitu_stats *stats) {
-    int rc = prefill_check(k, seq, base, n_q, q, out, mode);
-    if (rc) return rc;
+// The prefill attend over the geometry gv: the whole sequence (every KV head), or
+// one KV head of it (n_kv = 1, planes from that head's).
+static int causal_impl(insitu_cache *k, const Geom &gv, int64_t base, int64_t n_q, const int32_t *q,
+                       int32_t *out, int32_t mode, insitu_stats *stats) {
     HIP_TRY(hipSetDevice(k->ctx->device), "hipSetDevice");
-    rc = stats ? zero_stats(k) : INSITU_OK;
+    int rc = stats ? zero_stats(k) : INSITU_OK;
     if (rc) return rc;
     if (n_q == 0) return copy_stats(k, stats);
-    const Geom &g = k->g;
-    Geom gv = g;
-    gv.base = g.base + (int64_t)seq * g.seq_stride;
-    gv.seq_stride = 0;
     const PrefillPlan pl = prefill_plan(gv, base, n_q, PREFILL_SCRATCH_BUDGET);
     if (!k->prefill_len) HIP_TRY(hipMalloc(&k->prefill_len, PREFILL_QB * sizeof(int64_t)), "hipMalloc");
     if (mode != INSITU_SERIAL && k->chunked && k->prefill_scr.bytes < pl.bytes) {
@@ -806,6 +802,31 @@ int insitu_attend_causal(insitu_cache *k, int32_t seq, int64_t base, int64_t n_q
     rc = prefill_launches(k, gv, pl, k->prefill_scr, k->prefill_len, base, n_q, q, out, mode);
     if (rc) return rc;
     return copy_stats(k, stats);
+}
+
+int insitu_attend_causal(insitu_cache *k, int32_t seq, int64_t base, int64_t n_q, const int32_t *q,
+                         int32_t *out, int32_t mode, insitu_stats *stats) {
+    int rc = prefill_check(k, seq, base, n_q, q, out, mode);
+    if (rc) return rc;
+    const Geom &g = k->g;
+    Geom gv = g;
+    gv.base = g.base + (int64_t)seq * g.seq_stride;
+    gv.seq_stride = 0;
+    return causal_impl(k, gv, base, n_q, q, out, mode, stats);
+}
+
+int insitu_attend_causal_head(insitu_cache *k, int32_t seq, int32_t kv_head, int64_t base, int64_t n_q,
+                              const int32_t *q, int32_t *out, int32_t mode, insitu_stats *stats) {
+    int rc = prefill_check(k, seq, base, n_q, q, out, mode);
+    if (rc) return rc;
+    const Geom &g = k->g;
+    if (kv_head < 0 || kv_head >= g.n_kv) return fail(INSITU_EINVAL, "no such KV head");
+    Geom gv = g;
+    gv.base = g.base + (int64_t)seq * g.seq_stride + (int64_t)kv_head * g.head_stride;
+    gv.seq_stride = 0;
+    gv.n_kv = 1;
+    gv.n_q = g.G;
+    return causal_impl(k, gv, base, n_q, q, out, mode, stats);
 }
 
 int insitu_attend_causal_static(insitu_cache *k, int32_t seq, int64_t base, int64_t n_q, const int32_t *q,

@@ -820,8 +820,8 @@ def test_prefill_group_interface_and_bounds(ctx):
     host.append_rotated(k, v)
     a = CompressedAttention(c)
     q = rng.integers(-(1 << 22), 1 << 22, size=(12, 4, 64))
-    got, _ = a.attend_online_batch(q, kv_head=5, base=T - 12)
-    got2, _ = a.attend_causal_batch(q, kv_head=5, base=T - 12)
+    got, _ = a.attend_online_batch(q, c.view(5), base=T - 12)
+    got2, _ = a.attend_causal_batch(q, c.view(5), base=T - 12)
     for i in range(12):
         view = host.view(5).select(slice(0, T - 12 + i + 1))
         np.testing.assert_array_equal(got[i], attend_online(q[i], view, FMT)[0])
