@@ -23,8 +23,10 @@ reads a cache that is still resident from the step before.
     python bench.py --config probe          # bytes-only read of the C2 scan size: the launch ceiling
 
 C3: batch 64, one layer, per-sequence contexts uniform in
-[1024, 8192] from seed 3, one attend launch over the whole batch; 3 caches
-(more than the 256 MB Infinity Cache in total) rotate between steps.
+[1024, 8192] from seed 3, each sequence its own seeded k/v and query, one
+attend launch over the whole batch; 3 caches (more than the 256 MB Infinity
+Cache in total) rotate between steps; every group of the last timed launch is
+checked against the oracle.
 C1: all 16 layers of a Llama-3.2-1B-shape block, batch 1,
 4,096 sequential decode steps from an empty cache, each step one insitu_step
 (rotate, append, attend) per layer; layer l draws its q/k/v from its own
@@ -34,8 +36,9 @@ byte with the oracle's packed rows. It is a parity run with its timing, not
 the headline line.
 C4: Llama-3-8B shape (32 query heads, 8 KV heads, d=128,
 3-bit K and V), batch 16, ctx 131,072, 32 layers: one step is the 32 layers'
-attends, over a 53.7 GB resident cache. The k/v of one sequence (seeded, 1%
-outlier channels x16) are rotated and appended to every sequence and layer.
+attends, over a 53.7 GB resident cache. Every sequence of every layer has its
+own k/v (drawn on the GPU, seeded, 1% outlier channels x16) and query; the last
+timed launch is checked against the oracle on two KV heads of every sequence.
 Block: the whole attention block per decode token (AttentionBlock.forward,
 kernel.py:177-357): fp16 q/k/v projections, attention scale, RoPE and the cast
 to the wire, rotate, append, attend over ctx 32,768, to_float and W_o', with
@@ -237,8 +240,32 @@ def bench_probe(a) -> int:
     return 0
 
 
+def _check_groups(cache, out, q, groups, fmt, G=4):
+    """The checker leg of C3/C4: oracle/c's attend_online over the device's own rows for
+    each (sequence, KV head) in groups, against `out` (batch, n_q, d). The rows are read
+    on this thread; decoding and the oracle run in threads. Returns the groups that differ."""
+    import concurrent.futures
+
+    from insitu_amd.cache import unpack_rows
+    from oracle import native
+    rows = {bh: cache.read_rows(bh[1], 0, None, bh[0]) for bh in groups}
+    kb, vb = cache.quant.key_bits, cache.quant.value_bits
+
+    def check(bh):
+        b, h = bh
+        kv = unpack_rows(rows[bh], cache.head_dim, kb, vb)
+        want, _ = native.attend_online(q[b, G * h:G * (h + 1)], kv, fmt)
+        return bh, bool(np.array_equal(out[b, G * h:G * (h + 1)], want))
+
+    workers = max(1, min(16, len(os.sched_getaffinity(0))))
+    with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as ex:
+        return [bh for bh, ok in ex.map(check, groups) if not ok]
+
+
 def bench_scale(a) -> int:
-    """C3 / C4: the attend launches alone, over caches filled by GPU appends."""
+    """C3 / C4: the attend launches alone, over caches filled by GPU appends, each
+    sequence with its own seeded k/v and query; the last timed launch checked against
+    the oracle."""
     import torch
 
     from insitu_amd import QuantConfig
@@ -246,61 +273,61 @@ def bench_scale(a) -> int:
     from insitu_amd.cache import CompressedCache
     from insitu_amd.rotate import Rotation
     from insitu_amd.runtime import default_context
-    from insitu_amd.workload import Workload
+    from insitu_amd.workload import fill_on_device, fill_ragged
+    from oracle.quantize import Format
 
     ctx = default_context(0)
     if a.config == "c3":
         d, kb, vb, batch, n_caches, row = 64, 4, 2, 64, 3, 52
         lens = np.random.default_rng(3).integers(1024, 8193, size=batch)
-        wl = Workload(seed=0)
-        block = int(lens.max())
         workload = ("C3: Llama-3.2-1B-shape single layer, batch 64, ragged contexts "
                     "uniform in [1024, 8192] (seed 3), 4b K / 2b V, one attend launch")
+        data = ("synthetic: per sequence b of cache i, Workload(seed=3000 + 100 i + b) k/v "
+                "(N(0,1), 4 outlier channels x8 per head, Q8.16) and one query row per head")
     else:
         d, kb, vb, batch, n_caches, row = 128, 3, 3, 16, 32, 100
         lens = np.full(batch, 131072)
-        wl = Workload(head_dim=128, seed=0, outlier_mode="percent")
-        block = 16384
         workload = ("C4: Llama-3-8B shape (32 q heads, 8 KV heads, d=128), 3b K / 3b V, "
                     "batch 16, ctx 131072, 32 layers (one step = 32 attend launches)")
+        data = ("synthetic, drawn on the GPU: per layer i and sequence b, torch.Generator seed "
+                "4000 + 100 i + b, N(0,1) k/v with 1% of channels per head x16, Q8.16; one query "
+                "row per head per sequence")
     quant = QuantConfig(key_bits=kb, value_bits=vb)
+    fmt = Format(d=d, key_bits=kb, value_bits=vb)
     rot = Rotation.for_quant(quant, d)
     caches = [CompressedCache(N_KV, d, int(lens.max()), quant, batch=batch, n_q_heads=N_Q, ctx=ctx)
               for _ in range(n_caches)]
-    # fill: blocks of seeded k/v (one sequence's worth), rotated once, appended everywhere
-    done = 0
     t_fill = time.perf_counter()
-    while done < lens.max():
-        n = int(min(block, lens.max() - done))
-        _, k, v = wl.steps(n) if a.config == "c3" else (None,) + _kv_only(wl, n)
-        kr = rot.apply(k[0], ctx)
-        vr = rot.apply(v[0], ctx)
-        for c in caches:
-            for b in range(batch):
-                m = int(min(n, lens[b] - done))
-                if m > 0:
-                    c.append_rotated(kr[:m], vr[:m], seq=b)
-        done += n
+    qs = []
+    for i, c in enumerate(caches):
+        if a.config == "c3":
+            q, _ = fill_ragged(c, lens, 3000 + 100 * i, rot, ctx)
+        else:
+            q, _ = fill_on_device(c, int(lens[0]), 4000 + 100 * i, rot, ctx)
+        qs.append(q)
         torch.cuda.synchronize()
+        print(f"{a.config}: cache {i + 1} of {n_caches} filled", file=sys.stderr, flush=True)
     t_fill = time.perf_counter() - t_fill
-    qs = [rot.apply(wl.steps(1)[0][0, 0][None].repeat(batch, 0).reshape(batch * N_Q, d), ctx)
-          .reshape(batch, N_Q, d) for _ in range(min(n_caches, 4))]
+    qd = [ctx.to_device(q, torch.int32) for q in qs]
     attn = [CompressedAttention(c) for c in caches]
     outs = [torch.empty((batch, N_Q, d), dtype=torch.int32, device=ctx.torch_device) for _ in caches]
     step_bytes = float(N_KV * row * lens.sum()) * (n_caches if a.config == "c4" else 1)
+    last = {"cache": 0}
 
     def step(i):
         if a.config == "c4":
             for l, at in enumerate(attn):
-                at.attend(qs[l % len(qs)], a.mode, out=outs[l], stats=False)
+                at.attend(qd[l], a.mode, out=outs[l], stats=False)
+            last["cache"] = n_caches - 1
         else:
-            at = attn[i % n_caches]
-            at.attend(qs[i % len(qs)], a.mode, out=outs[i % n_caches], stats=False)
+            j = i % n_caches
+            attn[j].attend(qd[j], a.mode, out=outs[j], stats=False)
+            last["cache"] = j
 
     import ctypes
     from insitu_amd import _lib
     lib = ctx.lib
-    ms_sum, n_att = ctypes.c_double(), ctypes.c_int64()
+    n_launch = a.steps * (n_caches if a.config == "c4" else 1)
     for i in range(a.warmup):
         step(i)
     torch.cuda.synchronize()
@@ -313,13 +340,26 @@ def bench_scale(a) -> int:
     e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    _lib.check(lib.insitu_ctx_timing_read(ctx.handle, ctypes.byref(ms_sum), ctypes.byref(n_att)))
+    ms = (ctypes.c_double * n_launch)()
+    n_att = ctypes.c_int64()
+    _lib.check(lib.insitu_ctx_timing_read_each(ctx.handle, ms, n_launch, ctypes.byref(n_att)))
     _lib.check(lib.insitu_ctx_timing(ctx.handle, 0))
+    us_each = np.array(ms[:n_att.value]) * 1e3
     ev_s = e0.elapsed_time(e1) / 1e3          # the launches with their query staging
-    kern_s = ms_sum.value / 1e3               # the attend kernels alone
-    # correctness spot check of the timed work: the first sequence's first KV group
-    _, st = attn[0].attend(qs[0], a.mode, out=outs[0])
-    gbs = step_bytes * a.steps / kern_s / 1e9
+    kern_s = us_each.sum() / 1e6              # the attend kernels alone
+    per_launch = step_bytes / (n_caches if a.config == "c4" else 1)
+    us_med = float(np.median(us_each))
+    # the checker leg: the last timed launch's output against the oracle on the device's rows
+    j = last["cache"]
+    out = outs[j].cpu().numpy()
+    if a.config == "c3":
+        groups = [(b, h) for b in range(batch) for h in range(N_KV)]
+    else:
+        groups = [(b, h) for b in range(batch) for h in (0, 5)]
+    t_chk = time.perf_counter()
+    bad = _check_groups(caches[j], out, qs[j], groups, fmt)
+    t_chk = time.perf_counter() - t_chk
+    gbs = per_launch / (us_med * 1e-6) / 1e9
     res = {
         "metric": "compressed-KV scan GB/s (% HBM peak)",
         "value": round(step_bytes * a.steps / wall / 1e9, 3),
@@ -332,7 +372,7 @@ def bench_scale(a) -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int64",
-        "data": "synthetic (seeded N(0,1) k/v, one sequence's tokens appended to every sequence)",
+        "data": data,
         "config": {"workload": workload, "mode": a.mode, "batch": batch,
                    "ctx_total": int(lens.sum()), "ctx_min": int(lens.min()), "ctx_max": int(lens.max()),
                    "caches": n_caches, "head_dim": d, "row_bytes": row,
@@ -340,14 +380,19 @@ def bench_scale(a) -> int:
                    "fill_s": round(t_fill, 1)},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 3), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 5), "traffic": None,
-                     "kernel": "chunk_kernel", "algorithmic_bytes_per_step": step_bytes,
+                     "kernel": "insitu::chunk_kernel (sequential, d = %d)" % d,
+                     "algorithmic_bytes_per_launch": per_launch,
+                     "attend_us_median": round(us_med, 3), "attend_us_mean": round(float(us_each.mean()), 3),
+                     "launches_timed": int(n_att.value),
                      "us_per_step_kernels": round(kern_s / a.steps * 1e6, 2),
                      "us_per_step_events_with_query_prep": round(ev_s / a.steps * 1e6, 2)},
         "cpu_baseline": None,
-        "stats_check": {"serial_fallbacks": st.serial_fallbacks, "rescale_events": st.rescale_events},
+        "checked": {"launch": f"the last timed launch (cache {j})", "groups": len(groups),
+                    "mismatched": [list(g) for g in bad], "oracle": "oracle/c attend_online on the "
+                    "device's rows", "check_s": round(t_chk, 1)},
     }
     print(json.dumps(res))
-    return 0
+    return 0 if not bad else 1
 
 
 def bench_c1(a) -> int:
@@ -598,14 +643,6 @@ def bench_block(a) -> int:
     }
     print(json.dumps(res))
     return 0 if bad == 0 else 1
-
-
-def _kv_only(wl, n):
-    """k and v (1, n, Hkv, d) of the workload's distribution, without q."""
-    from insitu_amd.workload import to_fixed
-    k = wl.rng.standard_normal((1, n, wl.n_kv_heads, wl.head_dim), dtype=np.float32) * wl.k_scale
-    v = wl.rng.standard_normal((1, n, wl.n_kv_heads, wl.head_dim), dtype=np.float32) * wl.v_scale
-    return to_fixed(k).astype(np.int32), to_fixed(v).astype(np.int32)
 
 
 def main() -> int:
