@@ -21,6 +21,7 @@ reads a cache that is still resident from the step before.
     python bench.py --config prefill        # a 4,096-token prompt through one layer
     python bench.py --config block          # hidden states in, hidden states out, ctx 32k
     python bench.py --config probe          # bytes-only read of the C2 scan size: the launch ceiling
+    python bench.py --config short          # ctx 100 in a 131,072-token cache vs a 256-token one
 
 C3: batch 64, one layer, per-sequence contexts uniform in
 [1024, 8192] from seed 3, each sequence its own seeded k/v and query, one
@@ -76,7 +77,7 @@ def _args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--config", default="c2",
-                    choices=["c1", "c2", "c3", "c4", "prefill", "block", "probe"])
+                    choices=["c1", "c2", "c3", "c4", "prefill", "block", "probe", "short"])
     ap.add_argument("--prompt", type=int, default=4096)
     ap.add_argument("--c1-layers", type=int, default=16)
     ap.add_argument("--c1-steps", type=int, default=4096)
@@ -395,6 +396,58 @@ def bench_scale(a) -> int:
     return 0 if not bad else 1
 
 
+def bench_short(a) -> int:
+    """Decode at a short context in a large cache: ctx 100 (C2's format) in caches sized for
+    131,072 tokens and for 256, the same steps on each, per-launch event times. The attend
+    grid follows the longest sequence, so the capacity costs nothing."""
+    import torch
+
+    from insitu_amd import QuantConfig, _lib
+    from insitu_amd.cache import CompressedCache
+    from insitu_amd.rotate import Rotation
+    from insitu_amd.runtime import default_context, ptr
+    from insitu_amd.workload import Workload
+
+    ctx = default_context(0)
+    quant = QuantConfig(key_bits=4, value_bits=2)
+    rot = Rotation.for_quant(quant, D)
+    n0 = 99
+    wl = Workload(seed=0)
+    _, k, v = wl.steps(n0)
+    kr, vr = rot.apply(k[0], ctx), rot.apply(v[0], ctx)
+    reps = max(a.steps, 50)
+    q, kw, vw = (ctx.to_device(x[0], torch.int32) for x in wl.steps(reps))
+    out = torch.empty((N_Q, D), dtype=torch.int32, device=ctx.torch_device)
+    lib = ctx.lib
+    res_caps = {}
+    for cap in (131072, 256):
+        c = CompressedCache(N_KV, D, cap, quant, n_q_heads=N_Q, ctx=ctx)
+        c.append_rotated(kr, vr)
+
+        def launch(i, c=c):
+            _lib.check(lib.insitu_step(c.handle, ptr(q[i]), ptr(kw[i]), ptr(vw[i]), ptr(out),
+                                       _lib.MODES[a.mode], None))
+
+        for i in range(a.warmup):
+            launch(i)
+        c.set_length(n0)                       # the timed steps start at ctx n0 + 1 again
+        us = _timed_each(ctx, launch, reps)
+        res_caps[cap] = {"attend_us_median": round(float(np.median(us)), 3),
+                         "attend_us_min": round(float(us.min()), 3), "ctx_first": n0 + 1,
+                         "ctx_last": n0 + reps}
+    res = {
+        "metric": "decode step at a short context: attend us by cache capacity",
+        "value": res_caps[131072]["attend_us_median"], "unit": "us", "n_gpus": 1, "steps": reps,
+        "higher_is_better": False, "dtype": "int64",
+        "data": "synthetic (seeded N(0,1) q/k/v with 4 outlier channels x8 per head, Q8.16)",
+        "config": {"workload": "C2's format (8 KV heads, d=64, 4b/2b), batch 1, insitu_step from "
+                               f"ctx {n0 + 1} on, caches of capacity 131,072 and 256", "mode": a.mode},
+        "by_capacity": res_caps,
+    }
+    print(json.dumps(res))
+    return 0
+
+
 def bench_c1(a) -> int:
     """Config 1 in full: 16 layers x 4,096 decode steps from empty, every step checked."""
     import concurrent.futures
@@ -662,6 +715,8 @@ def main() -> int:
         return bench_block(a)
     if a.config == "probe":
         return bench_probe(a)
+    if a.config == "short":
+        return bench_short(a)
     if a.config != "c2":
         return bench_scale(a)
     import torch

@@ -658,8 +658,11 @@ static int attend_impl(insitu_cache *k, const int32_t *q, int32_t *out, int32_t 
     if (mode != INSITU_SERIAL && k->chunked) {
         if (!ep) HIP_TRY(scratch_begin(k->ctx->stream, k->scr, &ep), "scratch clear");
         k->scr.spin_limit = k->spin_limit;
+        int64_t longest = 0;
+        for (int64_t n : k->len_host) longest = n > longest ? n : longest;
         HIP_TRY(launch_attend_chunked(k->ctx->stream, k->g, k->tabs, q, out, len, k->scr, ep,
-                                      k->max_chunks, k->pool, two_pass, q_staged, step, ev, k->stats),
+                                      k->max_chunks, k->pool, two_pass, q_staged, step, ev, k->stats, 0,
+                                      chunked_max_chunks(longest + (step ? 1 : 0))),
                 "chunked attend launch");
         return INSITU_OK;
     }

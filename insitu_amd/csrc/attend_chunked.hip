@@ -1366,13 +1366,14 @@ bool chunked_fused_step(const Geom &g) { return g.d <= 64; }
 template <int D, int KB>
 static hipError_t launch_fast(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
                               int32_t *out, const int64_t *len, const Chunked &ck, int two_pass,
-                              bool q_staged, const StepIn *step, LaunchEv ev, DevStats *st) {
+                              bool q_staged, const StepIn *step, LaunchEv ev, DevStats *st,
+                              int64_t grid_chunks) {
     const unsigned chains = (unsigned)(g.batch * g.n_kv);
     const StepIn si = step ? *step : StepIn{};
     if (two_pass) {
         if (step) return hipErrorInvalidValue;
         // the chunk-max kernel stages the query rows for the chunk kernel when the caller has not
-        dim3 grid((unsigned)ck.max_chunks, chains), block(CT);
+        dim3 grid((unsigned)grid_chunks, chains), block(CT);
         if (q_staged)
             hipExtLaunchKernelGGL((chunk_max_kernel<D, KB, true>), grid, block, 0, s, ev.start, nullptr,
                                   0, g, t, q, ck.qd, ck.qok, len, ck, st);
@@ -1385,7 +1386,7 @@ static hipError_t launch_fast(hipStream_t s, const Geom &g, const Tables *t, con
                               ev.stop, 0, g, t, q, ck.qd, ck.qok, out, len, ck, st, si);
         return hipGetLastError();
     }
-    dim3 grid((unsigned)ck.max_chunks * chains), block(CT);
+    dim3 grid((unsigned)grid_chunks * chains), block(CT);
     if constexpr (stage_queries_first<D>()) {
         if (step) return hipErrorInvalidValue;
         if (!q_staged) {
@@ -1500,10 +1501,13 @@ hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, 
                                  int32_t *out, const int64_t *len, ChunkScratch &cs,
                                  uint32_t ep, int64_t max_chunks, int64_t pool, int two_pass,
                                  bool q_staged, const StepIn *step, LaunchEv ev, DevStats *st,
-                                 int64_t carve_batch) {
+                                 int64_t carve_batch, int64_t grid_chunks) {
     const int64_t chains = (int64_t)g.batch * g.n_kv;
     if (max_chunks > HMAX || chains > 65535 || max_chunks * chains > 0x7fffffff)
         return hipErrorInvalidValue;
+    // the grid: the chunks of the longest sequence (workgroups past a chain's last
+    // chunk have nothing to do), at most the layout's
+    if (grid_chunks < 1 || grid_chunks > max_chunks) grid_chunks = max_chunks;
     if (carve_batch < g.batch) carve_batch = g.batch;
     Geom gc = g;
     gc.batch = (int32_t)carve_batch;
@@ -1521,7 +1525,7 @@ hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, 
     }
 #define INSITU_FAST(DD, KK)                                                          \
     if (g.d == DD && g.kb == KK)                                                     \
-        return launch_fast<DD, KK>(s, g, t, q, out, len, ck, two_pass, q_staged, step, ev, st);
+        return launch_fast<DD, KK>(s, g, t, q, out, len, ck, two_pass, q_staged, step, ev, st, grid_chunks);
     INSITU_FAST(64, 2)
     INSITU_FAST(64, 3)
     INSITU_FAST(64, 4)

@@ -254,7 +254,8 @@ hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, 
                                  int32_t *out, const int64_t *len, ChunkScratch &cs,
                                  uint32_t ep, int64_t max_chunks, int64_t pool, int two_pass,
                                  bool q_staged, const StepIn *step, LaunchEv ev, DevStats *st,
-                                 int64_t carve_batch = 0);
+                                 int64_t carve_batch = 0,
+                                 int64_t grid_chunks = 0);
 hipError_t launch_step_write(hipStream_t s, const Geom &g, const Tables *t, const int32_t *qw,
                              const int32_t *kw, const int32_t *vw, int rounds,
                              const uint64_t (*signs)[2], int32_t *qr, double *qd, int32_t *qok,

@@ -171,6 +171,48 @@ def test_out_two_pass_golden(fixture_cache):
     assert st.rescale_events == 0
 
 
+def test_signed_norm_edge_rows_on_the_device(ctx):
+    """score_edge_rows.hex: five rows whose signed key norms are 0, 1, 2^15 - 1, -2^15 and
+    -1, which only a loaded image can hold (the encoder never writes them). Loaded with
+    load_rows into KV head 0 and attended by the device: alone, each row's |score|
+    comes back as max_abs_score and equals score_edge_gold.hex (the reference's scores
+    of those rows against rot_q[0]); all five together give the oracle's attend_online
+    output and statistics, on both sequential kernels."""
+    from insitu_amd.attention import CompressedAttention
+    rows = hx.bytes_rows("score_edge_rows.hex")
+    gold = hx.scalars("score_edge_gold.hex", 48)
+    rq = hx.lanes("rot_q.hex", 24, 64)
+    assert list(unpack(rows, FMT).k_norm) == [0, 1, 32767, -32768, -1]
+    q = np.zeros((1, 32, 64), dtype=np.int64)
+    q[0, 0] = rq[0]                      # the only nonzero query: head 0, KV group 0
+    for i in range(5):
+        c = _cache(ctx, 5)
+        c.load_rows(rows[i:i + 1], 0)
+        c.set_length(1)
+        for mode in ("serial", "online"):
+            _, st = CompressedAttention(c).attend(q, mode)
+            assert st.max_abs_score == abs(int(gold[i])), f"row {i}, {mode}"
+        one = unpack(rows[i:i + 1], FMT)
+        _, hst = CompressedAttention(c).attend_online(rq[0:4], c.view(0))
+        assert hst.max_abs_score == int(np.abs(native.scores(rq[0:4], one, FMT)[0]).max())
+    c = _cache(ctx, 5)
+    c.load_rows(rows, 0)
+    c.set_length(5)
+    want, wst = attend_online(rq[:4], unpack(rows, FMT), FMT)
+    got, st = CompressedAttention(c).attend_online(rq[:4], c.view(0))      # the per-head entry
+    np.testing.assert_array_equal(got, want)
+    assert (st.max_abs_score, st.rescale_events, st.max_abs_acc) == \
+        (wst.max_abs_score, wst.rescale_events, wst.max_abs_acc)
+    q4 = np.zeros((1, 32, 64), dtype=np.int64)
+    q4[0, :4] = rq[:4]
+    for pin in ("scan", "chunked"):                                            # the whole-cache attend
+        c.pin_kernel(pin)
+        out, st = CompressedAttention(c).attend(q4, "online")
+        np.testing.assert_array_equal(out.cpu().numpy()[0, :4], want, err_msg=pin)
+        assert st.max_abs_score == wst.max_abs_score, pin
+    assert wst.max_abs_score >= max(abs(int(x)) for x in gold)
+
+
 def test_stress_query_group0_matches_oracle_stats(fixture_cache):
     from insitu_amd.attention import CompressedAttention
     c, rows = fixture_cache
@@ -616,6 +658,42 @@ def test_a_later_chunk_replays_from_chunk_zeros_published_state(ctx):
             np.testing.assert_array_equal(out.cpu().numpy()[0], want, err_msg=f"{mode} rep {rep}")
             assert st.serial_fallbacks == 0
             assert st.rescale_events == sum(s.rescale_events for s in sts)
+
+
+@pytest.mark.parametrize("pin", ["chunked", "scan"])
+def test_short_contexts_in_a_large_cache(ctx, pin):
+    """A cache sized for 131,072 tokens holding 1, 100 and then 1,500 rows: the grid
+    follows the longest sequence, not the capacity, and every length is exact (the
+    fused step included, whose grid covers the new row's chunk)."""
+    from insitu_amd import ModelConfig, QuantConfig
+    from insitu_amd.attention import CompressedAttention
+    from insitu_amd.block import AttentionBlock
+    rng = np.random.default_rng(61)
+    blk = AttentionBlock(ModelConfig.llama32_1b(), QuantConfig(key_bits=4, value_bits=2),
+                         capacity=131072, softmax="online", ctx=ctx)
+    blk.cache.pin_kernel(pin)
+    host = Cache(8, 1600, FMT)
+    sg = signs_from_seed(64, 0, 1)
+    done = 0
+    for n in (1, 99, 1400):
+        k, v = _random_cache_inputs(rng, n)
+        blk.cache.append_rotated(k, v)
+        host.append_rotated(k, v)
+        done += n
+        q = rng.integers(-(1 << 22), 1 << 22, size=(32, 64))
+        out, st = CompressedAttention(blk.cache).attend(q[None], "online")
+        want = np.concatenate([native.attend_online(q[4 * h:4 * h + 4], host.view(h), FMT)[0]
+                               for h in range(8)])
+        np.testing.assert_array_equal(out.cpu().numpy()[0], want, err_msg=f"ctx {done}")
+        assert st.serial_fallbacks == 0 and st.n_tokens == done
+        qw, kw, vw = (rng.integers(-(1 << 22), 1 << 22, size=(1, h, 64)) for h in (32, 8, 8))
+        got = blk.step(qw, kw, vw).cpu().numpy()[0]
+        host.append_rotated(rotate(kw[0], sg)[None], rotate(vw[0], sg)[None])
+        done += 1
+        qr = rotate(qw[0], sg)
+        want = np.concatenate([native.attend_online(qr[4 * h:4 * h + 4], host.view(h), FMT)[0]
+                               for h in range(8)])
+        np.testing.assert_array_equal(got, want.reshape(-1), err_msg=f"step at ctx {done}")
 
 
 def test_repeated_calls_reuse_the_counters(ctx):
