@@ -127,37 +127,75 @@ def copy_calibration() -> None:
     print(json.dumps({"copy_bytes_per_dispatch": n, "dispatches": 5}))
 
 
-def cpu_baseline(cache, q_rot_all, out_gpu, budget_s: float = 20.0):
-    """The oracle's numpy attend_online on this step's cache, KV group by KV group.
-
-    A bounded sample: as many KV groups as fit `budget_s` (at least one). Also
-    checks the GPU output of the same groups bit-for-bit.
-    """
-    from oracle.attention import attend_online
-    from oracle.quantize import Format
+def cpu_baseline(cache, q_rot_all, out_gpu, wire, budget_s: float = 20.0):
+    """The oracle's numpy restatement of the decode step, timed on this box's host cores
+    (BASELINE.md's CPU plan): rotate the step's q/k/v, encode and pack its k/v row, then
+    attend_online (the per-token loop, the parity golden) on the step's cache, KV group
+    by KV group within `budget_s` (at least one group; the GPU output of every timed
+    group is checked bit for bit), and the vectorized attend_two_pass on every group.
+    Also a whole C0 step (ctx 512) timed end to end."""
+    from oracle.attention import attend_online, attend_two_pass
+    from oracle.quantize import Cache, Format, encode, pack
+    from oracle.rotate import rotate, signs_from_seed
+    from insitu_amd.workload import Workload
     fmt = Format()
-    rows_t = 0.0
-    done = 0
-    t_all = 0.0
+    sg = signs_from_seed(D, 0, 1)
+    qw, kw, vw = (np.asarray(x, dtype=np.int64) for x in wire)
+    t0 = time.perf_counter()
+    qr = rotate(qw.reshape(-1, D), sg)
+    kr = rotate(kw.reshape(-1, D), sg)
+    vr = rotate(vw.reshape(-1, D), sg)
+    t_rot = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    rows = [pack(encode(kr[h][None], vr[h][None], fmt), fmt) for h in range(N_KV)]
+    t_enc = time.perf_counter() - t0
+    if not np.array_equal(qr, q_rot_all):
+        raise AssertionError("the oracle's rotation of the step's query differs from the GPU's")
+    kvs = [cache.view(h).host() for h in range(N_KV)]
+    n = kvs[0].k_idx.shape[0]
     for h in range(N_KV):
-        kv = cache.view(h)
+        if not np.array_equal(cache.read_rows(h, n - 1, 1), rows[h]):
+            raise AssertionError(f"the step's row of KV head {h} differs from the oracle's encode + pack")
+    rows_t, done, t_on = 0, 0, 0.0
+    for h in range(N_KV):
         q = q_rot_all[4 * h:4 * h + 4]
         t0 = time.perf_counter()
-        want, _ = attend_online(q, kv, fmt)
-        dt = time.perf_counter() - t0
+        want, _ = attend_online(q, kvs[h], fmt)
+        t_on += time.perf_counter() - t0
         if not np.array_equal(want, out_gpu[4 * h:4 * h + 4]):
             raise AssertionError(f"bench step disagrees with the oracle on KV group {h}")
-        t_all += dt
-        rows_t += kv.k_idx.shape[0]
+        rows_t += kvs[h].k_idx.shape[0]
         done += 1
-        if t_all > budget_s:
+        if t_on > budget_s:
             break
-    gbs = rows_t * ROW / t_all / 1e9
+    t0 = time.perf_counter()
+    for h in range(N_KV):
+        attend_two_pass(q_rot_all[4 * h:4 * h + 4], kvs[h], fmt)
+    t_two = time.perf_counter() - t0
+    # C0: one decode step at ctx 512 (the token attends to itself), end to end
+    q0, k0, v0 = (x[0] for x in Workload(seed=0).steps(512))
+    host = Cache(N_KV, 512, fmt)
+    host.append_rotated(rotate(k0[:511].reshape(-1, D), sg).reshape(511, N_KV, D),
+                        rotate(v0[:511].reshape(-1, D), sg).reshape(511, N_KV, D))
+    t0 = time.perf_counter()
+    qs = rotate(q0[511].reshape(-1, D), sg)
+    host.append_rotated(rotate(k0[511].reshape(-1, D), sg)[None], rotate(v0[511].reshape(-1, D), sg)[None])
+    for h in range(N_KV):
+        attend_online(qs[4 * h:4 * h + 4], host.view(h), fmt)
+    t_c0 = time.perf_counter() - t0
+    gbs = rows_t * ROW / t_on / 1e9
+    per_group = t_on / done
+    env = {k: os.environ.get(k) for k in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS")}
     return {"value": round(gbs, 6), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"oracle numpy attend_online (per-token loop) on {done} of {N_KV} KV groups "
-                      f"of the last timed step's cache ({int(rows_t)} rows, {t_all:.1f} s); "
-                      f"affinity {len(os.sched_getaffinity(0))} cores, numpy single-threaded loop",
-            "s_per_decode_step_extrapolated": round(t_all / done * N_KV, 3)}
+                      f"of the last timed step's cache ({int(rows_t)} rows, {t_on:.1f} s)",
+            "affinity_cores": len(os.sched_getaffinity(0)), "thread_env": env,
+            "threads_used": "1 (a Python loop; int64 einsum has no BLAS path)",
+            "s_rotate_step": round(t_rot, 5), "s_encode_pack_step": round(t_enc, 5),
+            "s_attend_online_per_kv_group": round(per_group, 3),
+            "s_attend_two_pass_all_groups": round(t_two, 3),
+            "s_per_decode_step_c2_extrapolated": round(t_rot + t_enc + per_group * N_KV, 3),
+            "s_per_decode_step_c0_measured": round(t_c0, 4)}
 
 
 def _timed_each(ctx, launch, reps: int):
@@ -824,7 +862,7 @@ def main() -> int:
         raise AssertionError("the last timed step disagrees with the oracle")
     cpu = None
     if not a.no_cpu_baseline:
-        cpu = cpu_baseline(cache_last, q_rot_last, out_last)
+        cpu = cpu_baseline(cache_last, q_rot_last, out_last, (qs[0, last], ks[0, last], vs[0, last]))
     kernel = STEP_KERNEL.get(a.mode, a.mode)
     traffic, traffic_src = measured_traffic(kernel, a.ctx)
 

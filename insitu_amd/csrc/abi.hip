@@ -95,6 +95,7 @@ struct insitu_ctx {
     bool timing = false;
     std::vector<hipEvent_t> ev;           // 2 per attend: start, end
     size_t ev_used = 0;
+    void *blas = nullptr;                 // the host half's rocBLAS state (host_half.hip)
 };
 
 // The allocation-free prefill (insitu_attend_causal_static) keeps its chunk
@@ -148,6 +149,7 @@ hipError_t static_scratch_setup(int device, hipStream_t stream) {
 
 int insitu::ctx_device(insitu_ctx *c) { return c->device; }
 hipStream_t insitu::ctx_stream(insitu_ctx *c) { return c->stream; }
+void *&insitu::ctx_blas(insitu_ctx *c) { return c->blas; }
 
 struct insitu_cache {
     insitu_ctx *ctx = nullptr;
@@ -273,6 +275,7 @@ int insitu_ctx_destroy(insitu_ctx *c) {
     if (c->hook_tables) hipFree(c->hook_tables);
     if (c->hook_flags) hipFree(c->hook_flags);
     if (c->hook_i64) hipFree(c->hook_i64);
+    blas_release(c);
     if (c->own_stream && c->stream) hipStreamDestroy(c->stream);
     delete c;
     return INSITU_OK;

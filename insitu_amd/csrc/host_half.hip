@@ -292,22 +292,32 @@ int gemv(insitu_ctx *c, const uint16_t *w, int32_t out_f, int32_t in_f, const vo
 
 }  // namespace
 
-// One rocBLAS handle and staging per context, made on first use on the
-// context's device and stream.
-static Blas g_blas[64];
+// One rocBLAS handle, staging buffer and counter pair per context, made on first
+// use on the context's device and stream, released by insitu_ctx_destroy.
 namespace {
 Blas &blas_of(insitu_ctx *c) {
-    Blas &b = g_blas[ctx_device(c) & 63];
+    void *&p = ctx_blas(c);
+    if (!p) p = new Blas();
+    Blas &b = *(Blas *)p;
     if (!b.h) {
         if (rocblas_create_handle(&b.h) != rocblas_status_success) b.h = nullptr;
         if (b.h) rocblas_set_stream(b.h, ctx_stream(c));
-        if (hipMalloc(&b.counters, 2 * sizeof(unsigned long long)) != hipSuccess) b.counters = nullptr;
-    } else {
-        rocblas_set_stream(b.h, ctx_stream(c));
+        if (!b.counters && hipMalloc(&b.counters, 2 * sizeof(unsigned long long)) != hipSuccess)
+            b.counters = nullptr;
     }
     return b;
 }
 }  // namespace
+
+void insitu::blas_release(insitu_ctx *c) {
+    Blas *b = (Blas *)ctx_blas(c);
+    if (!b) return;
+    if (b->h) rocblas_destroy_handle(b->h);
+    if (b->x16) hipFree(b->x16);
+    if (b->counters) hipFree(b->counters);
+    delete b;
+    ctx_blas(c) = nullptr;
+}
 
 extern "C" {
 

@@ -269,6 +269,11 @@ hipError_t launch_attend_serial(hipStream_t s, const Geom &g, const Tables *t, c
 int set_last_error(int code, const char *msg);
 int ctx_device(insitu_ctx *c);
 hipStream_t ctx_stream(insitu_ctx *c);
+// The host half's rocBLAS handle, staging buffer and counters (host_half.hip): one
+// set per context, made on first use on the context's device and stream, and
+// released with the context.
+void *&ctx_blas(insitu_ctx *c);
+void blas_release(insitu_ctx *c);
 // The start/stop events of the next timed launch (null events when timing is off).
 int timing_events(insitu_ctx *c, LaunchEv *ev);
 

@@ -227,3 +227,44 @@ def test_forward_hidden_states_end_to_end(ctx, golden_half, cast_after_rope):
 
     y = np.concatenate([y0.cpu().numpy(), y1.cpu().numpy()])
     _check_gemm(y, w.o.cpu().numpy().view(np.float16), out / 65536.0)
+
+
+def test_two_contexts_on_one_device_keep_their_own_blas_state(ctx, golden_half):
+    """Each context has its own rocBLAS handle, fp16 staging and counters: two contexts
+    on two streams of one device, used in turn with prompts of different lengths (the
+    staging grows), give the single-context results and their own saturation counts,
+    and destroying one leaves the other working."""
+    import torch
+    from insitu_amd.host import HostHalf, Weights
+    from insitu_amd.runtime import Context
+    model, _, _ = golden_half
+    rng = np.random.default_rng(5)
+    xs = [(rng.standard_normal((n, HIDDEN)) * s).astype(np.float32)
+          for n, s in ((3, 0.02), (40, 50.0), (7, 0.02), (65, 50.0))]
+    pos = [np.arange(x.shape[0]) for x in xs]
+    ref = []
+    w0 = Weights.random(model, matrix(signs_from_seed(D, 0, 1)), seed=0, ctx=ctx)
+    h0 = HostHalf(model, w0, cast_after_rope=False, ctx=ctx)
+    for x, p in zip(xs, pos):
+        q, k, v = (t.cpu().numpy() for t in h0.wire(x, p))
+        ref.append((q, k, v, h0.last_saturated))
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    ctxs = [Context(0, s) for s in streams]
+    halves = []
+    for c, s in zip(ctxs, streams):
+        with torch.cuda.stream(s):
+            w = Weights.random(model, matrix(signs_from_seed(D, 0, 1)), seed=0, ctx=c)
+            halves.append(HostHalf(model, w, cast_after_rope=False, ctx=c))
+    for i, (x, p) in enumerate(zip(xs, pos)):
+        for j in (i % 2, 1 - i % 2):
+            with torch.cuda.stream(streams[j]):
+                q, k, v = halves[j].wire(x, p)
+                got = (q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy(), halves[j].last_saturated)
+            for a, b in zip(got[:3], ref[i][:3]):
+                np.testing.assert_array_equal(a, b, err_msg=f"prompt {i}, context {j}")
+            assert got[3] == ref[i][3] and (ref[i][3] > 0) == (i % 2 == 1), (i, j)
+    torch.cuda.synchronize()
+    ctxs[0].close()
+    with torch.cuda.stream(streams[1]):
+        q, _, _ = halves[1].wire(xs[3], pos[3])
+        np.testing.assert_array_equal(q.cpu().numpy(), ref[3][0])
