@@ -190,6 +190,7 @@ struct ChunkLds {
     struct Phase {
         uint32_t rec[GF][CHUNK];   // each head's candidate tokens in order (act_rec)
         uint32_t vw[CHUNK][KF<D, KB>::VW];
+        uint32_t vpad;             // the word after the last token's: read as the pair of its last word
         int16_t vn[CHUNK];
     };
     struct Replay {
@@ -205,7 +206,10 @@ struct ChunkLds {
         NewRow nr;
         SerialLds<KF<D, KB>::RS> fb[GF];
     } u;
-    double qf[D * GF];             // the group's query rows [c][h] (unless staged)
+    union alignas(16) {            // 16-byte aligned: the score loop reads the rows as 128-bit words
+        double qf[D * GF];         // the group's query rows [c][h] (unless staged), until the scores
+        int32_t tt[GF][64][8];     // run sums: a block of 64 entries' terms for every value code
+    } qt;
     int32_t qi[GF][D];             // the fused step: the rotated rows, for the serial path
     uint32_t row[32];              // the fused step: the new token's packed row
     int64_t norms[2];
@@ -213,7 +217,6 @@ struct ChunkLds {
     int64_t kc[16];
     int64_t vc[16];
     int32_t vc32[16];
-    int32_t tt[GF][64];            // run sums: 8 records' terms for every value code, [record][code]
     int64_t vcmax;
     int32_t expt[256];
     int32_t cntw[GF][CT / 64];     // candidate tokens per head and wave
@@ -557,7 +560,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
         } else {
             // Chunk 0 counts the range errors of the rotated queries, once per call.
             if (wv < GF) {
-                const bool okh = stage_query_head<D / 64>(q_t, D, wv, S.qf, tabs->kc_absmax,
+                const bool okh = stage_query_head<D / 64>(q_t, D, wv, S.qt.qf, tabs->kc_absmax,
                                                           chunk == 0 ? &st->range_errors : nullptr);
                 if (lane == 0 && !okh) atomicAnd(&S.qok, 0);
                 if (STEP) {
@@ -575,7 +578,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             }
             __syncthreads();
             ok = S.qok != 0;
-            qc = S.qf;
+            qc = S.qt.qf;
         }
         if (new_row) {
             // Pack the new row, store it into the planes (agent-coherent stores:
@@ -861,6 +864,9 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                 }
                 const uint32_t vmask = (1u << g.vb) - 1u;
                 const uint64_t vcmax = (uint64_t)uni64(S.vcmax);
+                int32_t vcr[8];                             // the value centroids (0 past nv)
+#pragma unroll
+                for (int c = 0; c < 8; ++c) vcr[c] = S.vc32[c];
                 const int32_t pev = uni32(S.expt[0]);       // p of an event token: LUT(0)
                 const int64_t dm = tabs->delta_max;
                 SegMeta *meta = ck.meta + ((int64_t)chain * GF + h) * ck.pool + off;
@@ -889,6 +895,15 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     const int val_i = exp_lut((int64_t)(r >> 11), S.expt, dm);
                     const int32_t p_i = in ? (ev_i ? pev : val_i) : 0;
                     const int32_t w_i = (int32_t)S.u.ph.vn[tl_i] * p_i;       // |w| <= 2^30
+                    // the entry's term for every value code: floor(w * c[code] / 2^acc_shift),
+                    // the per-entry 64-bit products done once for all channels
+                    {
+                        int32_t tv[8];
+#pragma unroll
+                        for (int c = 0; c < 8; ++c) tv[c] = (int32_t)(((int64_t)w_i * vcr[c]) >> acc_shift);
+                        *(int4 *)&S.qt.tt[h][lane][0] = make_int4(tv[0], tv[1], tv[2], tv[3]);
+                        *(int4 *)&S.qt.tt[h][lane][4] = make_int4(tv[4], tv[5], tv[6], tv[7]);
+                    }
                     const uint64_t aw = (uint64_t)(w_i < 0 ? -(int64_t)w_i : (int64_t)w_i);
                     const int64_t bw_i = w_i != 0 ? (int64_t)((aw * vcmax) >> acc_shift) + 1 : 0;
                     const uint64_t evm = __ballot(ev_i);
@@ -937,40 +952,89 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                         Bs = readlane64(bx, le);
                         fkey = readlane64(key, le);
                     }
-                    // Lane = channel: the terms of the entries in order, 8 at a time.
+                    // Lane = channel: each channel's term of the entries in order, NG at
+                    // a time (independent LDS reads: the code's word pair, then the table
+                    // entry), then the group's entries in one of three ways.
+                    constexpr int NG = CPL == 1 ? 16 : 8;
                     const int cnt = n_act - a0 < 64 ? n_act - a0 : 64;
-                    for (int j0 = 0; j0 < cnt; j0 += 8) {
-                        // The 8 entries' terms for every value code, lane = (entry, code):
-                        // floor(w * c[code] / 2^acc_shift), the per-entry 64-bit product
-                        // done once for all channels.
-                        {
-                            const int32_t w_l = __shfl(w_i, j0 + (lane >> 3));
-                            const int32_t c_l = S.vc32[lane & 7 & (int)vmask];
-                            S.tt[h][lane] = (int32_t)(((int64_t)w_l * c_l) >> acc_shift);
-                        }
-                        // then each channel's term of the next 8 entries (independent LDS reads)
-                        int32_t cv[8][CPL];
+                    const int roff_i = tl_i * (K::VW * 4);       // the entry's value words, bytes
+                    for (int j0 = 0; j0 < cnt; j0 += NG) {
+                        int32_t cv[NG][CPL];
 #pragma unroll
-                        for (int jj = 0; jj < 8; ++jj) {
-                            const int tl = __builtin_amdgcn_readlane(tl_i, j0 + jj);
+                        for (int jj = 0; jj < NG; ++jj) {
+                            // past cnt: token 0 and a stale table row, read but never added
+                            const uint32_t *row = (const uint32_t *)((const char *)&S.u.ph.vw[0][0] +
+                                                                     __builtin_amdgcn_readlane(roff_i, j0 + jj));
 #pragma unroll
                             for (int k = 0; k < CPL; ++k) {
-                                // both words, unconditionally: a 3-bit code may cross into
-                                // the next one (the last word never has a code crossing out)
-                                const uint32_t lo = S.u.ph.vw[tl][wi[k]];
-                                const uint32_t hi = S.u.ph.vw[tl][wi1[k]];
-                                cv[jj][k] = S.tt[h][jj * 8 + (int)(__builtin_amdgcn_alignbit(hi, lo, sh[k]) & vmask)];
+                                // the code's word and the next (a 3-bit code may cross into it;
+                                // past a row's last word the bits read are never used)
+                                const uint32_t lo = row[wi[k]];
+                                const uint32_t hi = row[wi[k] + 1];
+                                cv[jj][k] = S.qt.tt[h][j0 + jj][__builtin_amdgcn_alignbit(hi, lo, sh[k]) & vmask];
                             }
                         }
+                        const int ng = cnt - j0 < NG ? cnt - j0 : NG;
+                        const uint32_t gev = (uint32_t)(evm >> j0) & ((1u << ng) - 1u);
+                        if (!gev && !(SEQ && trk)) {
+                            // no event and no prefix tracking: the entries only add
 #pragma unroll
-                        for (int jj = 0; jj < 8; ++jj) {
+                            for (int jj = 0; jj < NG; ++jj)
+#pragma unroll
+                                for (int k = 0; k < CPL; ++k) P[k] += jj < ng ? cv[jj][k] : 0;
+                            continue;
+                        }
+                        if constexpr (SEQ) {
+                            if (!trk) {
+                                // Events, no tracking: an event closes the open run, whose
+                                // bound Br came from the entry pass. Chunk 0 folds the run
+                                // into its state, acc = floor((acc + S) * f / 2^15) (no clamp
+                                // inside the run), and l alike; a later chunk publishes it.
+                                auto events = [&](auto own_c) __attribute__((always_inline)) {
+                                    constexpr bool OWN = decltype(own_c)::value;
+#pragma unroll
+                                    for (int jj = 0; jj < NG; ++jj) {
+                                        if ((gev >> jj) & 1u) {
+                                            const int j = j0 + jj;
+                                            const int32_t bj = __builtin_amdgcn_readlane((int)Br, j);
+                                            if (OWN) {
+                                                const int32_t f = __builtin_amdgcn_readlane(val_i, j);   // <= 2^15
+                                                l0 = ((l0 + (uint32_t)__builtin_amdgcn_readlane((int)Lr, j)) * f) >>
+                                                     PROB_FRAC;
+#pragma unroll
+                                                for (int k = 0; k < CPL; ++k) {
+                                                    if (!fits(acc0[k], bj)) wide = true;
+                                                    acc0[k] = (AccT)(((int64_t)(acc0[k] + P[k]) * f) >> PROB_FRAC);
+                                                }
+                                            } else {
+#pragma unroll
+                                                for (int k = 0; k < CPL; ++k)
+                                                    pub32(&segS[(int64_t)seg * D + lane + 64 * k], (uint32_t)P[k]);
+                                                if (lane == 0) pub64(&meta[seg].b, (uint64_t)(uint32_t)bj);
+                                            }
+#pragma unroll
+                                            for (int k = 0; k < CPL; ++k) P[k] = 0;
+                                            ++seg;
+                                        }
+#pragma unroll
+                                        for (int k = 0; k < CPL; ++k) P[k] += jj < ng ? cv[jj][k] : 0;
+                                    }
+                                };
+                                if (own)
+                                    events(std::true_type{});
+                                else
+                                    events(std::false_type{});
+                                continue;
+                            }
+                        }
+                        // Prefix tracking (a run whose bound may pass TRACK_B): entry by entry.
+#pragma unroll
+                        for (int jj = 0; jj < NG; ++jj) {
                             const int j = j0 + jj;
                             if (j < cnt) {
                                 if ((evm >> j) & 1ull) {
                                     // the event closes the open run
                                     if (own) {
-                                        // no clamp inside the run, then
-                                        // acc = floor((acc + S) * f / 2^15), and l alike
                                         const int64_t f = (uint32_t)__builtin_amdgcn_readlane(val_i, j);
                                         l0 = ((l0 + readlane64(Lr, j)) * f) >> PROB_FRAC;
                                         const int32_t bj = (int32_t)readlane64(Br, j);
@@ -1040,6 +1104,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                 if (lane == 0)
                     pub64(&hp->w0, (uint64_t)(uint32_t)n_seg | ((uint64_t)(uint32_t)flags << 16) |
                                        ((uint64_t)(S.ovf & 0xFFFF) << 24) | ((uint64_t)ck.ep << 40));
+                stores_done();    // the header is out before this chunk counts itself done
             }
         } else if (!ok && wv < GF && !own) {
             // q failed its range check: the chain goes to the serial path, which counts its own
@@ -1047,6 +1112,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             if (lane == 0) pub64(&hp->w1, 0);
             stores_done();
             if (lane == 0) pub64(&hp->w0, 1ull | ((uint64_t)ck.ep << 40));
+            stores_done();
         }
 
         // -- phase 5: the last workgroup of the chain replays -----------------------
@@ -1101,6 +1167,9 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                 const int zslot = ck.pool - 1;    // a valid slot for the lanes past a batch to read
                 const uint32_t ep = ck.ep;
                 auto cur = [ep](uint64_t w) __attribute__((always_inline)) { return (uint32_t)(w >> 40) == ep; };
+                // A chunk whose look-back timed out flagged the chain before its header
+                // (every chunk has counted itself done: read with the headers).
+                const bool chain_fb = get32(&ck.chain_fb[chain]) == ep;
                 // Chunk 0's state: in the registers, or out of its slot once its header is up.
                 int flags = 0;
                 int64_t ovf = 0, mabs = 0;
@@ -1172,8 +1241,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                 }
                 total = uni32(total);
                 if (__ballot(flags != 0) || total > NSEG) fb = true;
-                // A chunk whose look-back timed out flagged the chain before its header.
-                if (get32(&ck.chain_fb[chain]) == ep) fb = true;
+                if (chain_fb) fb = true;
                 if (h == 0) {
                     ovf = wave_sum_i64(ovf);
                     mabs = wave_max_i64(mabs);
@@ -1209,8 +1277,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                             for (int i = 8 * blk; i < 8 * blk + 8; ++i) {
                                 const uint32_t o = (uint32_t)__builtin_amdgcn_readlane((int)roff, i);
 #pragma unroll
-                                for (int k = 0; k < CPL; ++k)
-                                    sv[i][k] = (int32_t)get32(sbase + o + 256 * k);
+                                for (int k = 0; k < CPL; ++k) sv[i][k] = (int32_t)get32(sbase + o + 256 * k);
                             }
                         } else {
 #pragma unroll
@@ -1229,24 +1296,39 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     // inclusive prefix sums of L and B over the batch's runs
                     const int64_t PL = wave_scan64<OpAdd64>(mine ? (int64_t)(uint32_t)mlf : 0, 0);
                     int64_t done_L = 0;                 // prefix sum already added to l
-                    // |acc| only shrinks at a rescale (f <= 2^15) and grows by at most
-                    // a run's peak per run, so |acc at the batch start| + the sum of the
-                    // batch's peaks certifies every run at once; only where that bound
+                    // |acc| only shrinks at a rescale (f <= 2^15) and grows by at most a
+                    // run's peak per run, so |acc at a block's start| + the sum of the
+                    // block's peaks certifies its 8 runs at once; only where that bound
                     // fails does the walk check run by run
-                    bool check_runs = false;
-                    if (SEQ) {
-                        const int64_t psum = wave_sum_i64(mine ? (int64_t)(uint32_t)mb : 0);
-                        int64_t amax = 0;
-#pragma unroll
-                        for (int k = 0; k < CPL; ++k) {
-                            const int64_t a = aw[k] < 0 ? -(int64_t)aw[k] : (int64_t)aw[k];
-                            amax = a > amax ? a : amax;
-                        }
-                        check_runs = __ballot(amax + psum > ACC_HI) != 0ull;
-                    }
+                    const int64_t PB = SEQ ? wave_scan64<OpAdd64>(mine ? (int64_t)(uint32_t)mb : 0, 0) : 0;
 #pragma unroll
                     for (int blk = 0; blk < SB / 8; ++blk) {
                         if (blk < nblk) {
+                            const uint32_t bev = SEQ ? (uint32_t)(evm >> (8 * blk)) & 0xFFu : 0u;
+                            bool bcheck = false;
+                            if (SEQ) {
+                                const int64_t bsum = readlane64(PB, 8 * blk + 7) - (blk ? readlane64(PB, 8 * blk - 1) : 0);
+                                int64_t amax = 0;
+#pragma unroll
+                                for (int k = 0; k < CPL; ++k) {
+                                    const int64_t a = aw[k] < 0 ? -(int64_t)aw[k] : (int64_t)aw[k];
+                                    amax = a > amax ? a : amax;
+                                }
+                                bcheck = __ballot(amax + bsum > ACC_HI) != 0ull;
+                            }
+                            if (!bev && !bcheck) {
+                                // no rescale and no certificate to check in these 8 runs:
+                                // they only add (the runs past the batch read the spare slot,
+                                // which is never added)
+#pragma unroll
+                                for (int k = 0; k < CPL; ++k) {
+                                    AccT v[8];
+#pragma unroll
+                                    for (int r = 0; r < 8; ++r) v[r] = 8 * blk + r < nb ? (AccT)sv[8 * blk + r][k] : (AccT)0;
+                                    aw[k] += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+                                }
+                                continue;
+                            }
 #pragma unroll
                             for (int i = 8 * blk; i < 8 * blk + 8; ++i) {
                                 if (SEQ && ((evm >> i) & 1ull)) {
@@ -1261,7 +1343,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                                     l = wmul(l, f) >> PROB_FRAC;
                                     ++events;
                                 }
-                                if (SEQ && check_runs) {
+                                if (SEQ && bcheck) {
                                     const int32_t m = __builtin_amdgcn_readlane((int)(uint32_t)mb, i);
 #pragma unroll
                                     for (int k = 0; k < CPL; ++k) unsafe = unsafe || !fits((int32_t)aw[k], m);
