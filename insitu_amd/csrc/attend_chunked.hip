@@ -134,7 +134,7 @@ __device__ __forceinline__ void stores_done() {
 
 struct Chunked {
     int64_t *cmax;                 // [chain][max_chunks][GF]   (two-pass)
-    unsigned long long *status;    // [chain][max_chunks][GF]   look-back words
+    unsigned long long *status;    // [chain][GF][2][max_chunks] look-back words: inclusive, aggregate
     ChunkHdr *hdr;                 // [chain][max_chunks][GF]
     SegMeta *meta;                 // [chain][GF][pool]
     int32_t *segS;                 // [chain][GF][pool][d]
@@ -185,7 +185,15 @@ __device__ __forceinline__ uint32_t act_rec(int tl, bool ev, uint32_t dist) {
     return (uint32_t)tl | (ev ? 1u << 10 : 0u) | (dist << 11);
 }
 
-template <int D, int KB>
+// The fused step's new token: boundaries and codes, live through the score phase.
+struct NewRowLds {
+    int64_t bnd[2][255];           // key and value boundaries
+    int32_t kv[2][MAX_D];          // the rotated key and value
+    uint8_t codes[2][MAX_D];
+};
+struct NoNewRow {};
+
+template <int D, int KB, bool STEP>
 struct ChunkLds {
     struct Phase {
         uint32_t rec[GF][CHUNK];   // each head's candidate tokens in order (act_rec)
@@ -196,23 +204,18 @@ struct ChunkLds {
     struct Replay {
         uint16_t slot[GF][NSEG];   // the runs in order: slot | RUN_EVENT when a rescale opens it
     };
-    struct NewRow {                // the fused step's new token, before the score phase
-        int64_t bnd[2][255];       // key and value boundaries
-        uint8_t codes[2][MAX_D];
-    };
     union {
         Phase ph;
         Replay rp;
-        NewRow nr;
         SerialLds<KF<D, KB>::RS> fb[GF];
     } u;
+    typename std::conditional<STEP, NewRowLds, NoNewRow>::type nr;
+    int64_t newsc[GF];             // the fused step: the new token's scores
     union alignas(16) {            // 16-byte aligned: the score loop reads the rows as 128-bit words
         double qf[D * GF];         // the group's query rows [c][h] (unless staged), until the scores
         int32_t tt[GF][64][8];     // run sums: a block of 64 entries' terms for every value code
     } qt;
     int32_t qi[GF][D];             // the fused step: the rotated rows, for the serial path
-    uint32_t row[32];              // the fused step: the new token's packed row
-    int64_t norms[2];
     double kcf[16];
     int64_t kc[16];
     int64_t vc[16];
@@ -455,7 +458,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
     static_assert(!STEP || (SEQ && !QS), "the fused step is the sequential kernel with LDS queries");
     using K = KF<D, KB>;
     constexpr int CPL = K::CPL;
-    __shared__ ChunkLds<D, KB> S;
+    __shared__ ChunkLds<D, KB, STEP> S;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);      // wave index, scalar
     const int n_chains = g.batch * g.n_kv;
@@ -549,7 +552,15 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                 rotate_loaded<D / 64>(q_t, D, si.rounds, si.sg, q_t, chunk == 0 ? &st->range_errors : nullptr);
             else if (new_row && wv < GF + 2)
                 rotate_loaded<D / 64>(kv_t, D, si.rounds, si.sg, kv_t, &st->range_errors);
-            if (new_row) stage_bounds(tabs, g, S.u.nr.bnd);
+            if constexpr (STEP) {
+                if (new_row) {
+                    stage_bounds(tabs, g, S.nr.bnd);
+                    if (wv == GF || wv == GF + 1) {
+#pragma unroll
+                        for (int k = 0; k < D / 64; ++k) S.nr.kv[wv - GF][lane + 64 * k] = kv_t[k];
+                    }
+                }
+            }
         }
         __syncthreads();
         // Whether every score of the group stays an exact fp64 integer (query.h).
@@ -567,42 +578,81 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
 #pragma unroll
                     for (int k = 0; k < D / 64; ++k) S.qi[wv][lane + 64 * k] = q_t[k];
                 }
-            } else if (new_row && wv < GF + 2) {
-                const int f = wv - GF;         // 0: key, 1: value
-                int64_t x[D / 64];
-#pragma unroll
-                for (int k = 0; k < D / 64; ++k) x[k] = kv_t[k];
-                const int64_t n = encode_field<D / 64>(x, D, g.norm_frac, S.u.nr.bnd[f],
-                                                       (1 << (f == 0 ? g.kb : g.vb)) - 1, S.u.nr.codes[f]);
-                if (lane == 0) S.norms[f] = n;
             }
             __syncthreads();
             ok = S.qok != 0;
             qc = S.qt.qf;
         }
-        if (new_row) {
-            // Pack the new row, store it into the planes (agent-coherent stores:
-            // a serial fallback elsewhere reads it), and give it to the thread
-            // that holds token T - 1 in place of what its loads found there.
-            const int nwords = g.row_bytes / 4, kwords = g.key_bytes / 4, vwords = g.value_bytes / 4;
-            if (wv == GF && lane < nwords) {
-                const uint32_t w = pack_row_word(g, S.u.nr.codes, S.norms[0], S.norms[1], lane);
-                S.row[lane] = w;
-                pub32(row_word_ptr(g, b, kvh, T - 1, lane), w);
-            }
-            __syncthreads();
-            const int tl = (int)(T - 1 - t0);
-            if (tid == tl / TPT) {
+        // The fused step's new token, beside the score phase: wave 0 encodes its
+        // key (rotated by wave GF), stores the key words into the planes and
+        // scores it for the GF heads (lane = channel; the partial sums are exact
+        // integers, so their sum is the score loop's); wave 1 encodes its value,
+        // stores the value words and stages them for the run sums. Waves 0 and 1
+        // are the older wave of their SIMD, whose instructions issue first, so this
+        // latency-bound work runs beside waves GF and GF + 1's scores instead of
+        // after them. The stores are agent-coherent: a serial fallback elsewhere
+        // reads the row. The thread that holds token T - 1 scores what its loads
+        // found there and sets the result aside; it takes the new scores after the
+        // score phase.
+        int64_t nmx[GF];                  // wave 0, lane 0: the new token's clamped scores
+        unsigned long long novf = 0;
+        int64_t nmabs = 0;
 #pragma unroll
-                for (int j = 0; j < TPT; ++j)
-                    if (j == tl % TPT) {
+        for (int h = 0; h < GF; ++h) nmx[h] = SCORE_LO;
+        if constexpr (STEP) {
+            if (new_row && wv < 2) {
+                const int f = wv;              // 0: key, 1: value
+                int64_t x[D / 64];
 #pragma unroll
-                        for (int i = 0; i < K::KWORDS; ++i) kw[j][i] = S.row[i];
-                        nw[j] = S.row[nwords - 1];
+                for (int k = 0; k < D / 64; ++k) x[k] = S.nr.kv[f][lane + 64 * k];
+                const int64_t n = encode_field<D / 64>(x, D, g.norm_frac, S.nr.bnd[f],
+                                                       (1 << (f == 0 ? g.kb : g.vb)) - 1, S.nr.codes[f]);
+                const int kwords = g.key_bytes / 4, vwords = g.value_bytes / 4, nwords = g.row_bytes / 4;
+                const int tln = (int)(T - 1 - t0);
+                uint16_t *nword = (uint16_t *)row_word_ptr(g, b, kvh, T - 1, nwords - 1);
+                if (f == 0) {
+                    if (lane < kwords) pub32(row_word_ptr(g, b, kvh, T - 1, lane), pack_row_word(g, S.nr.codes, n, 0, lane));
+                    if (lane == 0) __hip_atomic_store(nword, (uint16_t)(n & 0xFFFF), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    if (ok) {
+                        int64_t part[GF];
 #pragma unroll
-                        for (int i = 0; i < K::VW; ++i)
-                            if (i < vwords) vreg[j][i] = S.row[kwords + i];
+                        for (int h = 0; h < GF; ++h) {
+                            double a = 0.0;
+#pragma unroll
+                            for (int k = 0; k < D / 64; ++k) {
+                                const int c = lane + 64 * k;
+                                a = fma(S.qt.qf[c * GF + h], S.kcf[S.nr.codes[0][c]], a);
+                            }
+                            part[h] = dbl_to_i64(a);
+                        }
+                        const int64_t kn = sext16((uint32_t)(n & 0xFFFF));
+#pragma unroll
+                        for (int h = 0; h < GF; ++h) {
+                            int64_t v = wmul(wave_sum_i64(part[h]), kn) >> score_shift;
+                            if (v < SCORE_LO || v > SCORE_HI) {
+                                ++novf;
+                                v = v < SCORE_LO ? SCORE_LO : SCORE_HI;
+                            }
+                            const int64_t a = v < 0 ? -v : v;
+                            nmabs = a > nmabs ? a : nmabs;
+                            if (lane == 0) {
+                                nmx[h] = v;
+                                S.newsc[h] = v;
+                            }
+                        }
+                        if (lane != 0) novf = 0, nmabs = 0;
                     }
+                } else {
+                    if (lane < vwords) {
+                        const uint32_t w = pack_row_word(g, S.nr.codes, 0, n, kwords + lane);
+                        pub32(row_word_ptr(g, b, kvh, T - 1, kwords + lane), w);
+                        S.u.ph.vw[tln][lane] = w;
+                    }
+                    if (lane == 0) {
+                        __hip_atomic_store(nword + 1, (uint16_t)(n & 0xFFFF), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        S.u.ph.vn[tln] = (int16_t)(n & 0xFFFF);
+                    }
+                }
             }
         }
 
@@ -611,17 +661,18 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
         int64_t mx[GF];
         int64_t sv[GF][TPT];      // clamped scores, SCORE_LO past the end
 #pragma unroll
-        for (int h = 0; h < GF; ++h) mx[h] = SCORE_LO;
+        for (int h = 0; h < GF; ++h) mx[h] = nmx[h];
         if (ok) {
             int64_t s[TPT][GF];
             score_keys<D, KB>(kw, nw, qc, S.kcf, score_shift, s);
-            unsigned long long ovf = 0;
-            int64_t mabs = 0;
+            unsigned long long ovf = novf;
+            int64_t mabs = nmabs;
 #pragma unroll
             for (int j = 0; j < TPT; ++j) {
                 const int tl = tid * TPT + j;
                 const int64_t t = t0 + tl;
-                if (t < T) {
+                const bool fresh = STEP && new_row && t == T - 1;     // scored by wave 0
+                if (t < T && !fresh) {
 #pragma unroll
                     for (int h = 0; h < GF; ++h) {
                         int64_t v = s[j][h];
@@ -641,7 +692,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
 #pragma unroll
                     for (int h = 0; h < GF; ++h) sv[h][j] = SCORE_LO;
                 }
-                S.u.ph.vn[tl] = (int16_t)(nw[j] >> 16);
+                if (!fresh) S.u.ph.vn[tl] = (int16_t)(nw[j] >> 16);
             }
             ovf = (unsigned long long)wave_sum_i64((int64_t)ovf);
             mabs = wave_max_i64(mabs);
@@ -656,62 +707,80 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             if (lane == 0) S.red[wv][h] = m;
         }
         __syncthreads();
+        if (STEP && new_row && ok) {
+            const int tln = (int)(T - 1 - t0);
+            if (tid == tln / TPT) {
+#pragma unroll
+                for (int j = 0; j < TPT; ++j)
+                    if (j == tln % TPT) {
+#pragma unroll
+                        for (int h = 0; h < GF; ++h) sv[h][j] = S.newsc[h];
+                    }
+            }
+        }
 
         // -- phase 2: the maximum before this chunk (sequential) or of all chunks --
-        if (SEQ && wv < GF) {
-            const int h = wv;
+        // Two look-back words per (chunk, head): the inclusive maximum and this
+        // chunk's own (aggregate). Wave GF + h publishes head h's aggregate (chunk
+        // 0: its inclusive maximum) while wave h looks back, so that the polling
+        // wave has no store in flight: its loads' waits would drain it.
+        static_assert(CT / 64 == 2 * GF, "a publishing wave beside each polling wave");
+        if (SEQ) {
+            const int h = wv & (GF - 1);
             int64_t local = S.red[0][h];
             for (int w = 1; w < CT / 64; ++w) local = S.red[w][h] > local ? S.red[w][h] : local;
-            unsigned long long *my = ck.status + ((int64_t)chain * ck.max_chunks + chunk) * GF + h;
-            int64_t run = SCORE_LO;
-            bool fail = false;
-            if (chunk == 0) {
+            // [chain][head][inclusive, aggregate][chunk]: the lanes of a poll (consecutive
+            // predecessors) read consecutive words
+            unsigned long long *wi0 = ck.status + ((int64_t)chain * GF + h) * 2 * ck.max_chunks;
+            unsigned long long *wa0 = wi0 + ck.max_chunks;
+            if (wv >= GF) {
                 if (lane == 0)
-                    __hip_atomic_store(my, st_pack(ST_INC, ck.ep, local), __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
+                    __hip_atomic_store((chunk == 0 ? wi0 : wa0) + chunk, st_pack(chunk == 0 ? ST_INC : ST_AGG, ck.ep, local),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             } else {
-                if (lane == 0)
-                    __hip_atomic_store(my, st_pack(ST_AGG, ck.ep, local), __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-                int64_t base = chunk - 1;       // the predecessor lane 0 reads
-                int spins = 0;
-                fail = ck.spin_limit == 0;
-                while (!fail) {
-                    const int64_t pc = base - lane;
-                    unsigned long long flag = ST_INC;
-                    int64_t val = SCORE_LO;
-                    if (pc >= 0) {
-                        const unsigned long long w = __hip_atomic_load(
-                            ck.status + ((int64_t)chain * ck.max_chunks + pc) * GF + h,
-                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        flag = st_flag(w, ck.ep);
-                        val = st_val(w);
-                    }
-                    const unsigned long long inc = __ballot(flag == ST_INC);
-                    const int nearest = inc ? __ffsll((long long)inc) - 1 : 64;
-                    const unsigned long long wait = __ballot(flag == 0 && lane <= nearest);
-                    if (wait) {
-                        if (++spins > ck.spin_limit) {
-                            fail = true;
-                            break;
+                int64_t run = SCORE_LO;
+                bool fail = false;
+                if (chunk > 0) {
+                    int64_t base = chunk - 1;       // the predecessor lane 0 reads
+                    int spins = 0;
+                    fail = ck.spin_limit == 0;
+                    while (!fail) {
+                        const int64_t pc = base - lane;
+                        unsigned long long flag = ST_INC;
+                        int64_t val = SCORE_LO;
+                        if (pc >= 0) {
+                            const unsigned long long wi = __hip_atomic_load(wi0 + pc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            const unsigned long long wa = __hip_atomic_load(wa0 + pc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                            const bool has_inc = st_flag(wi, ck.ep) == ST_INC;
+                            flag = has_inc ? ST_INC : st_flag(wa, ck.ep);
+                            val = st_val(has_inc ? wi : wa);
                         }
-                        __builtin_amdgcn_s_sleep(2);
-                        continue;
+                        const unsigned long long inc = __ballot(flag == ST_INC);
+                        const int nearest = inc ? __ffsll((long long)inc) - 1 : 64;
+                        const unsigned long long wait = __ballot(flag == 0 && lane <= nearest);
+                        if (wait) {
+                            if (++spins > ck.spin_limit) {
+                                fail = true;
+                                break;
+                            }
+                            __builtin_amdgcn_s_sleep(2);
+                            continue;
+                        }
+                        const int64_t v = wave_max_i64(lane <= nearest ? val : SCORE_LO);
+                        run = v > run ? v : run;
+                        if (nearest < 64) break;
+                        base -= 64;
                     }
-                    const int64_t v = wave_max_i64(lane <= nearest ? val : SCORE_LO);
-                    run = v > run ? v : run;
-                    if (nearest < 64) break;
-                    base -= 64;
+                    const int64_t incl = run > local ? run : local;
+                    if (lane == 0)
+                        __hip_atomic_store(wi0 + chunk, st_pack(ST_INC, ck.ep, incl), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
                 }
-                const int64_t incl = run > local ? run : local;
-                if (lane == 0)
-                    __hip_atomic_store(my, st_pack(ST_INC, ck.ep, incl), __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-            }
-            if (lane == 0) {
-                S.min_[h] = run;
-                S.lmax[h] = local;
-                if (fail) S.lb_fail = 1;
+                if (lane == 0) {
+                    S.min_[h] = run;
+                    S.lmax[h] = local;
+                    if (fail) S.lb_fail = 1;
+                }
             }
         } else if (!SEQ && wv < GF) {
             int64_t m = SCORE_LO;
@@ -1120,7 +1189,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
         // first, so that when it is the last (its many rescale events make it the
         // slowest) its state never leaves the registers. Otherwise it publishes
         // the state after counting, and the last workgroup waits for its header.
-        if (new_row && wv == GF) stores_done();   // the new row is out before this chunk counts
+        if (new_row && wv < 2) stores_done();   // the new row is out before this chunk counts
         __syncthreads();
         if (tid == 0) {
             const unsigned prior = __hip_atomic_fetch_add(&ck.done[chain], 1u, __ATOMIC_RELAXED,
@@ -1515,7 +1584,7 @@ static void carve(const Geom &g, int64_t max_chunks, int64_t pool, uint8_t *p, C
     // the words read before their epoch is known to be current come first (scratch_layout)
     Chunked c{};
     c.cmax = (int64_t *)take(chains * max_chunks * GF * sizeof(int64_t));
-    c.status = (unsigned long long *)take(chains * max_chunks * GF * sizeof(unsigned long long));
+    c.status = (unsigned long long *)take(chains * max_chunks * GF * 2 * sizeof(unsigned long long));
     c.hdr = (ChunkHdr *)take(chains * max_chunks * GF * sizeof(ChunkHdr));
     c.done = (unsigned int *)take(chains * sizeof(unsigned int));
     c.chain_fb = (unsigned int *)take(chains * sizeof(unsigned int));
