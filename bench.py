@@ -674,6 +674,7 @@ def bench_block(a) -> int:
             kr = blk.rotation.apply(kr_src[0], ctx)
             vr = blk.rotation.apply(vr_src[0], ctx)
         blk.cache.append_rotated(kr, vr)
+        blk.host  # the host half (projection weights on the device, RoPE tables) before timing
         blocks.append(blk)
     del kr_src, vr_src
     x = torch.from_numpy(wl_rng.standard_normal((n_total, model.hidden_size)).astype(np.float32)

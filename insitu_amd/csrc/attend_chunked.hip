@@ -185,13 +185,18 @@ __device__ __forceinline__ uint32_t act_rec(int tl, bool ev, uint32_t dist) {
     return (uint32_t)tl | (ev ? 1u << 10 : 0u) | (dist << 11);
 }
 
-// The fused step's new token: boundaries and codes, live through the score phase.
-struct NewRowLds {
+// What only the fused step keeps in LDS: the new token's boundaries, rows, codes
+// and scores (live through the score phase), and the rotated query rows for the
+// serial path.
+template <int D>
+struct StepLds {
     int64_t bnd[2][255];           // key and value boundaries
     int32_t kv[2][MAX_D];          // the rotated key and value
     uint8_t codes[2][MAX_D];
+    int64_t newsc[GF];             // the new token's scores
+    int32_t qi[GF][D];             // the rotated query rows
 };
-struct NoNewRow {};
+struct NoStep {};
 
 template <int D, int KB, bool STEP>
 struct ChunkLds {
@@ -209,13 +214,11 @@ struct ChunkLds {
         Replay rp;
         SerialLds<KF<D, KB>::RS> fb[GF];
     } u;
-    typename std::conditional<STEP, NewRowLds, NoNewRow>::type nr;
-    int64_t newsc[GF];             // the fused step: the new token's scores
+    typename std::conditional<STEP, StepLds<D>, NoStep>::type nr;
     union alignas(16) {            // 16-byte aligned: the score loop reads the rows as 128-bit words
         double qf[D * GF];         // the group's query rows [c][h] (unless staged), until the scores
         int32_t tt[GF][64][8];     // run sums: a block of 64 entries' terms for every value code
     } qt;
-    int32_t qi[GF][D];             // the fused step: the rotated rows, for the serial path
     double kcf[16];
     int64_t kc[16];
     int64_t vc[16];
@@ -574,9 +577,9 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                 const bool okh = stage_query_head<D / 64>(q_t, D, wv, S.qt.qf, tabs->kc_absmax,
                                                           chunk == 0 ? &st->range_errors : nullptr);
                 if (lane == 0 && !okh) atomicAnd(&S.qok, 0);
-                if (STEP) {
+                if constexpr (STEP) {
 #pragma unroll
-                    for (int k = 0; k < D / 64; ++k) S.qi[wv][lane + 64 * k] = q_t[k];
+                    for (int k = 0; k < D / 64; ++k) S.nr.qi[wv][lane + 64 * k] = q_t[k];
                 }
             }
             __syncthreads();
@@ -637,7 +640,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                             nmabs = a > nmabs ? a : nmabs;
                             if (lane == 0) {
                                 nmx[h] = v;
-                                S.newsc[h] = v;
+                                S.nr.newsc[h] = v;
                             }
                         }
                         if (lane != 0) novf = 0, nmabs = 0;
@@ -707,15 +710,17 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             if (lane == 0) S.red[wv][h] = m;
         }
         __syncthreads();
-        if (STEP && new_row && ok) {
-            const int tln = (int)(T - 1 - t0);
-            if (tid == tln / TPT) {
+        if constexpr (STEP) {
+            if (new_row && ok) {
+                const int tln = (int)(T - 1 - t0);
+                if (tid == tln / TPT) {
 #pragma unroll
-                for (int j = 0; j < TPT; ++j)
-                    if (j == tln % TPT) {
+                    for (int j = 0; j < TPT; ++j)
+                        if (j == tln % TPT) {
 #pragma unroll
-                        for (int h = 0; h < GF; ++h) sv[h][j] = S.newsc[h];
-                    }
+                            for (int h = 0; h < GF; ++h) sv[h][j] = S.nr.newsc[h];
+                        }
+                }
             }
         }
 
@@ -1437,7 +1442,11 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                 // The serial path counts score statistics only when the headers did not.
                 // The fused step's new row came from another workgroup: acquire it.
                 if (STEP) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-                const int32_t *qrow = STEP ? &S.qi[h][0] : q + ((int64_t)b * g.n_q + qh) * D;
+                const int32_t *qrow;
+                if constexpr (STEP)
+                    qrow = &S.nr.qi[h][0];
+                else
+                    qrow = q + ((int64_t)b * g.n_q + qh) * D;
                 serial_head<CPL, K::RS>(g, tabs, S.kc, S.vc, qrow, b, kvh, T, SEQ ? 0 : 1, !hdr_stats,
                                         S.u.fb[h], orow, st);
                 if (lane == 0) atomicAdd(&st->serial_fallbacks, 1ull);
