@@ -1,6 +1,6 @@
 // The row codec shared by the write path and the fused decode step: the
 // randomized Hadamard rotation (ops/rotate.py:170-197, one wave per vector,
-// lane = channel, the FWHT butterflies as cross-lane xor shuffles), the norm
+// lane = channel, the FWHT butterflies by DPP and permlane swaps), the norm
 // and threshold encoder (ops/quantize.py:164-196: wave reduction for sum(x^2),
 // exact isqrt, half-even requantize, strict '>' compares) and the row packing
 // into the plane layout (quantize.py:237-252, hw/ddr_layout.py:198-214).
@@ -11,18 +11,62 @@
 
 namespace insitu {
 
+// The value of lane ^ H (H = 1 .. 32), by DPP within a row of 16 and by the
+// gfx950 permlane swaps across rows: no LDS permute round trip.
+//   H = 1, 2: quad permutes; H = 4: row_shl:4 / row_shr:4 by the lane's bit;
+//   H = 8: row_ror:8 (within 16 lanes a rotation by 8 is xor 8);
+//   H = 16, 32: v_permlane16/32_swap of v with itself leaves lane ^ H's value in
+//   the second result where bit H of the lane is clear and in the first where
+//   it is set.
+template <int H>
+__device__ __forceinline__ uint32_t xor_lane32(uint32_t v, int lane) {
+    if constexpr (H == 1) {
+        return dpp32<DPP_QUAD_1032>(v, v);
+    } else if constexpr (H == 2) {
+        return dpp32<DPP_QUAD_2301>(v, v);
+    } else if constexpr (H == 4) {
+        const uint32_t up = dpp32<DPP_ROW_SHL4>(v, v), down = dpp32<DPP_ROW_SHR4>(v, v);
+        return (lane & 4) ? down : up;
+    } else if constexpr (H == 8) {
+        return dpp32<DPP_ROW_ROR8>(v, v);
+    } else if constexpr (H == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap((int)v, (int)v, false, false);
+        return (uint32_t)((lane & 16) ? r[0] : r[1]);
+    } else {
+        static_assert(H == 32, "a lane xor within the wave");
+        const auto r = __builtin_amdgcn_permlane32_swap((int)v, (int)v, false, false);
+        return (uint32_t)((lane & 32) ? r[0] : r[1]);
+    }
+}
+template <int H>
+__device__ __forceinline__ int64_t xor_lane64(int64_t v, int lane) {
+    const uint32_t lo = xor_lane32<H>((uint32_t)v, lane);
+    const uint32_t hi = xor_lane32<H>((uint32_t)((uint64_t)v >> 32), lane);
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+// One butterfly stage of the FWHT: x' = x + x[lane ^ H] below, x[lane ^ H] - x above.
+template <int H, int CPL>
+__device__ __forceinline__ void fwht_stage(int64_t (&x)[CPL], int lane, int hmax) {
+    if (H < hmax) {
+#pragma unroll
+        for (int k = 0; k < CPL; ++k) {
+            const int64_t other = xor_lane64<H>(x[k], lane);
+            x[k] = (lane & H) ? (other - x[k]) : (x[k] + other);
+        }
+    }
+}
+
 // Up to two channels per lane (d <= 128): channel lane and lane + 64.
 template <int CPL>
 __device__ __forceinline__ void fwht_wave(int64_t (&x)[CPL], int d) {
     const int lane = threadIdx.x & 63;
     const int hmax = d < 64 ? d : 64;
-    for (int h = 1; h < hmax; h <<= 1) {
-#pragma unroll
-        for (int k = 0; k < CPL; ++k) {
-            int64_t other = __shfl_xor(x[k], h, 64);
-            x[k] = (lane & h) ? (other - x[k]) : (x[k] + other);
-        }
-    }
+    fwht_stage<1>(x, lane, hmax);
+    fwht_stage<2>(x, lane, hmax);
+    fwht_stage<4>(x, lane, hmax);
+    fwht_stage<8>(x, lane, hmax);
+    fwht_stage<16>(x, lane, hmax);
+    fwht_stage<32>(x, lane, hmax);
     if (CPL == 2 && d == 128) {
         int64_t a = x[0], b = x[CPL - 1];
         x[0] = a + b;

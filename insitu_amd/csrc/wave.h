@@ -18,6 +18,8 @@ constexpr int DPP_ROW_SHR1 = 0x111;
 constexpr int DPP_ROW_SHR2 = 0x112;
 constexpr int DPP_ROW_SHR4 = 0x114;
 constexpr int DPP_ROW_SHR8 = 0x118;
+constexpr int DPP_ROW_SHL4 = 0x104;          // lane i <- lane i + 4 within a row
+constexpr int DPP_ROW_ROR8 = 0x128;          // lane i <- lane (i + 8) mod 16 within a row
 constexpr int DPP_ROW_MIRROR = 0x140;        // lane i <-> 15 - i within a row
 constexpr int DPP_ROW_HALF_MIRROR = 0x141;   // lane i <-> 7 - i within 8 lanes
 constexpr int DPP_ROW_BCAST15 = 0x142;       // lane 15 of each row -> the next row
