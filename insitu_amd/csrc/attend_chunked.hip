@@ -1170,31 +1170,34 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             n_ev0 = n_ev;
             flags0 = flags;
             if (!own) {
-                // The header: w1 goes out with the run sums, w0 once this head's
-                // stores have completed.
+                // The header goes out with the run sums: the replay reads it only after
+                // this wave has counted itself done, which waits for all of them.
                 ChunkHdr *hp = &ck.hdr[((int64_t)chain * ck.max_chunks + chunk) * GF + h];
-                if (lane == 0) pub64(&hp->w1, S.mabs);
-                stores_done();
-                if (lane == 0)
+                if (lane == 0) {
+                    pub64(&hp->w1, S.mabs);
                     pub64(&hp->w0, (uint64_t)(uint32_t)n_seg | ((uint64_t)(uint32_t)flags << 16) |
                                        ((uint64_t)(S.ovf & 0xFFFF) << 24) | ((uint64_t)ck.ep << 40));
-                stores_done();    // the header is out before this chunk counts itself done
+                }
             }
         } else if (!ok && wv < GF && !own) {
             // q failed its range check: the chain goes to the serial path, which counts its own
             ChunkHdr *hp = &ck.hdr[((int64_t)chain * ck.max_chunks + chunk) * GF + wv];
-            if (lane == 0) pub64(&hp->w1, 0);
-            stores_done();
-            if (lane == 0) pub64(&hp->w0, 1ull | ((uint64_t)ck.ep << 40));
-            stores_done();
+            if (lane == 0) {
+                pub64(&hp->w1, 0);
+                pub64(&hp->w0, 1ull | ((uint64_t)ck.ep << 40));
+            }
         }
 
         // -- phase 5: the last workgroup of the chain replays -----------------------
-        // Chunks 1 .. nch-1 count themselves done once their runs are out; chunk 0
-        // first, so that when it is the last (its many rescale events make it the
-        // slowest) its state never leaves the registers. Otherwise it publishes
-        // the state after counting, and the last workgroup waits for its header.
-        if (new_row && wv < 2) stores_done();   // the new row is out before this chunk counts
+        // A chunk counts itself done once the stores of its head waves (their runs
+        // and headers; waves 0 and 1 also the new row; wave 0 the chain's fallback
+        // flag) have completed, so the workgroup whose count completes the chain
+        // finds everything out. One count per chunk: the counts of a chain meet at
+        // one address, where the device applies them one at a time. Chunk 0's
+        // state stays in the registers when its workgroup is the last (its many
+        // rescale events make it the slowest); otherwise it publishes the state
+        // after counting, and the last workgroup waits for its header.
+        if (wv < GF) stores_done();
         __syncthreads();
         if (tid == 0) {
             const unsigned prior = __hip_atomic_fetch_add(&ck.done[chain], 1u, __ATOMIC_RELAXED,
