@@ -1224,6 +1224,16 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                                    ((uint64_t)(ok ? S.ovf & 0xFFFF : 0) << 24) | ((uint64_t)ck.ep << 40));
         }
         if (last) {
+            // Every head's wave merges its statistics into the call's totals with global
+            // atomics. The device applies the atomics on one word one at a time, so with
+            // many chains ending together (C3's 512 chains: 132 -> 120 us per launch) the
+            // heads merge in LDS first and the chain sends them once. With few chains the
+            // heads send their own, in parallel; the fused step (one token per sequence,
+            // C2's 8 chains: 28.5 -> 29.0 us the other way, its SGPR spills up by a third
+            // with the merge compiled in) always does.
+            const bool merge_stats = !STEP && n_chains > 32;
+            if (merge_stats && tid < 4) S.red[4][tid] = 0;    // the heads' merged statistics
+            if (merge_stats && tid == 4) S.red[5][0] = 0;     // and how many heads have merged theirs
             const bool hw = wv < GF;              // wave h < GF replays query head h, lane = channel
             const int h = hw ? wv : 0;
             constexpr int HPL = HMAX / 64;
@@ -1473,18 +1483,45 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                 }
                 amax = wave_max_i64(amax);
                 if (!SEQ) aovf = (unsigned long long)wave_sum_i64((int64_t)aovf);
-                // each head's wave merges its own statistics (the serial path merges its own)
-                if (lane == 0) {
+                if (lane == 0 && !merge_stats) {
                     atomicMax(&st->n_tokens, (unsigned long long)T);
                     if (events) atomicAdd(&st->rescale_events, events);
                     atomicMax(&st->max_abs_acc, (unsigned long long)amax);
                     if (aovf) atomicAdd(&st->acc_overflows, aovf);
+                } else if (lane == 0) {
+                    unsigned long long *m = (unsigned long long *)&S.red[4][0];
+                    if (events) atomicAdd(&m[0], events);
+                    atomicMax(&m[1], (unsigned long long)amax);
+                    if (aovf) atomicAdd(&m[2], aovf);
+                    atomicOr(&m[3], 1ull);
                 }
             }
-            // the chain's score statistics, once (from the headers when they cover it)
-            if (hw && h == 0 && lane == 0 && hdr_stats) {
-                if (S.ovf) atomicAdd(&st->score_overflows, S.ovf);
-                atomicMax(&st->max_abs_score, S.mabs);
+            if (!merge_stats) {
+                // the chain's score statistics, once (from the headers when they cover it)
+                if (hw && h == 0 && lane == 0 && hdr_stats) {
+                    if (S.ovf) atomicAdd(&st->score_overflows, S.ovf);
+                    atomicMax(&st->max_abs_score, S.mabs);
+                }
+            } else if (hw && lane == 0) {
+                // The statistics of the heads that did not take the serial path (which
+                // merges its own), merged in LDS; the last head's wave to get here sends
+                // them once for the chain.
+                unsigned long long *m = (unsigned long long *)&S.red[4][0];
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");    // this head's merge first
+                if (atomicAdd((unsigned int *)&S.red[5][0], 1u) == GF - 1) {
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+                    if (m[3]) {
+                        atomicMax(&st->n_tokens, (unsigned long long)T);
+                        if (m[0]) atomicAdd(&st->rescale_events, m[0]);
+                        atomicMax(&st->max_abs_acc, m[1]);
+                        if (m[2]) atomicAdd(&st->acc_overflows, m[2]);
+                    }
+                    // the chain's score statistics, once (from the headers when they cover it)
+                    if (hdr_stats) {
+                        if (S.ovf) atomicAdd(&st->score_overflows, S.ovf);
+                        atomicMax(&st->max_abs_score, S.mabs);
+                    }
+                }
             }
             if (tid == 0) ck.done[chain] = 0;    // every workgroup of the chain has counted itself
         }

@@ -589,6 +589,42 @@ def test_ragged_batch_multi_chunk(ctx):
             np.testing.assert_array_equal(out[b], want, err_msg=f"{mode} seq {b}")
 
 
+@pytest.mark.parametrize("mode", ["online", "two_pass"])
+def test_many_chains_merge_their_statistics(ctx, mode):
+    """With more than 32 (sequence, KV head) chains the attend merges each chain's four
+    heads' statistics in LDS and sends them once. Here 48 ragged chains, and one KV group
+    whose queries are out of range goes to the serial path, which merges its own: every
+    total equals the oracle's over all chains."""
+    from insitu_amd.attention import CompressedAttention
+    rng = np.random.default_rng(25)
+    lens = [1500, 1, 513, 2049, 700, 1024]
+    c = _cache(ctx, 2100, batch=len(lens))
+    data = []
+    for b, T in enumerate(lens):
+        k, v = _random_cache_inputs(rng, T)
+        c.append_rotated(k, v, seq=b)
+        data.append((k, v))
+    q = rng.integers(-(1 << 22), 1 << 22, size=(len(lens), 32, 64))
+    q[3, 4:8] = rng.integers(1 << 29, 1 << 30, size=(4, 64)) * rng.choice([-1, 1], size=(4, 64))
+    out, st = CompressedAttention(c).attend(q, mode)
+    out = out.cpu().numpy()
+    sts = []
+    for b, (k, v) in enumerate(data):
+        want, s = _host_reference(k, v, q[b], two_pass=(mode == "two_pass"))
+        np.testing.assert_array_equal(out[b], want, err_msg=f"{mode} seq {b}")
+        sts += s
+    if mode == "online":
+        assert st.serial_fallbacks == 4
+    assert st.range_errors > 0
+    assert st.n_tokens == max(lens)
+    assert st.rescale_events == sum(s.rescale_events for s in sts)
+    assert st.rescale_events > 0 or mode == "two_pass"      # two-pass never rescales
+    assert st.max_abs_acc == max(s.max_abs_acc for s in sts)
+    assert st.acc_overflows == sum(s.acc_overflows for s in sts)
+    assert st.max_abs_score == max(s.max_abs_score for s in sts)
+    assert st.score_overflows == sum(s.score_overflows for s in sts)
+
+
 def _host_reference_kv(k, v, q, n_kv, two_pass=False):
     """Per KV group oracle outputs for any number of KV heads (4 query heads each)."""
     T = k.shape[0]
