@@ -937,6 +937,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     sh[k] = bit & 31;
                 }
                 const uint32_t vmask = (1u << g.vb) - 1u;
+                const bool vcross = (32 % g.vb) != 0;        // a code may straddle two words
                 const uint64_t vcmax = (uint64_t)uni64(S.vcmax);
                 int32_t vcr[8];                             // the value centroids (0 past nv)
 #pragma unroll
@@ -1034,18 +1035,30 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     const int roff_i = tl_i * (K::VW * 4);       // the entry's value words, bytes
                     for (int j0 = 0; j0 < cnt; j0 += NG) {
                         int32_t cv[NG][CPL];
+                        if (vcross) {
 #pragma unroll
-                        for (int jj = 0; jj < NG; ++jj) {
-                            // past cnt: token 0 and a stale table row, read but never added
-                            const uint32_t *row = (const uint32_t *)((const char *)&S.u.ph.vw[0][0] +
-                                                                     __builtin_amdgcn_readlane(roff_i, j0 + jj));
+                            for (int jj = 0; jj < NG; ++jj) {
+                                // past cnt: token 0 and a stale table row, read but never added
+                                const uint32_t *row = (const uint32_t *)((const char *)&S.u.ph.vw[0][0] +
+                                                                         __builtin_amdgcn_readlane(roff_i, j0 + jj));
 #pragma unroll
-                            for (int k = 0; k < CPL; ++k) {
-                                // the code's word and the next (a 3-bit code may cross into it;
-                                // past a row's last word the bits read are never used)
-                                const uint32_t lo = row[wi[k]];
-                                const uint32_t hi = row[wi[k] + 1];
-                                cv[jj][k] = S.qt.tt[h][j0 + jj][__builtin_amdgcn_alignbit(hi, lo, sh[k]) & vmask];
+                                for (int k = 0; k < CPL; ++k) {
+                                    // the code's word and the next (a 3-bit code may cross into it;
+                                    // past a row's last word the bits read are never used)
+                                    const uint32_t lo = row[wi[k]];
+                                    const uint32_t hi = row[wi[k] + 1];
+                                    cv[jj][k] = S.qt.tt[h][j0 + jj][__builtin_amdgcn_alignbit(hi, lo, sh[k]) & vmask];
+                                }
+                            }
+                        } else {
+                            // the codes never cross a word (vb divides 32): one read per entry
+#pragma unroll
+                            for (int jj = 0; jj < NG; ++jj) {
+                                const uint32_t *row = (const uint32_t *)((const char *)&S.u.ph.vw[0][0] +
+                                                                         __builtin_amdgcn_readlane(roff_i, j0 + jj));
+#pragma unroll
+                                for (int k = 0; k < CPL; ++k)
+                                    cv[jj][k] = S.qt.tt[h][j0 + jj][(row[wi[k]] >> sh[k]) & vmask];
                             }
                         }
                         const int ng = cnt - j0 < NG ? cnt - j0 : NG;
@@ -1102,6 +1115,19 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                             }
                         }
                         // Prefix tracking (a run whose bound may pass TRACK_B): entry by entry.
+                        if (!gev) {
+                            // no event in the group: no branch per entry (an entry past the
+                            // chunk adds 0, which leaves P and its extremes as they are)
+#pragma unroll
+                            for (int jj = 0; jj < NG; ++jj)
+#pragma unroll
+                                for (int k = 0; k < CPL; ++k) {
+                                    P[k] += jj < ng ? cv[jj][k] : 0;
+                                    hiP[k] = P[k] > hiP[k] ? P[k] : hiP[k];
+                                    loP[k] = P[k] < loP[k] ? P[k] : loP[k];
+                                }
+                            continue;
+                        }
 #pragma unroll
                         for (int jj = 0; jj < NG; ++jj) {
                             const int j = j0 + jj;
