@@ -796,6 +796,42 @@ def test_fused_step_ragged_batch_multi_chunk(ctx, mode, d, kb, vb):
                                           hosts[b].buf[T:T + steps, g])
 
 
+def test_fused_step_over_a_flat_softmax(ctx):
+    """insitu_step with small queries over the workload's rows: nearly every token of every
+    chunk is a candidate, so the fused step's run-sum walk takes its long paths (event-free
+    groups, prefix tracking of runs whose bound passes 2^24) that peaked queries skip."""
+    from insitu_amd import ModelConfig, QuantConfig
+    from insitu_amd.block import AttentionBlock
+    from insitu_amd.workload import Workload
+    T, steps = 3000, 3
+    q_w, k_w, v_w = Workload(seed=7).steps(T + steps)
+    sg = signs_from_seed(64, 0, 1)
+    blk = AttentionBlock(ModelConfig.llama32_1b(), QuantConfig(key_bits=4, value_bits=2),
+                         capacity=T + steps, ctx=ctx)
+    kr = rotate(k_w[0, :T].astype(np.int64), sg)
+    vr = rotate(v_w[0, :T].astype(np.int64), sg)
+    blk.cache.append_rotated(kr, vr)
+    host = Cache(8, T + steps, FMT)
+    host.append_rotated(kr, vr)
+    rng = np.random.default_rng(8)
+    for t in range(steps):
+        qw = rng.integers(-(1 << 9), 1 << 9, size=(1, 32, 64))
+        kw, vw = k_w[:, T + t], v_w[:, T + t]
+        out = blk.step(qw, kw, vw).cpu().numpy().reshape(32, 64)
+        host.append_rotated(rotate(kw[0].astype(np.int64), sg)[None], rotate(vw[0].astype(np.int64), sg)[None])
+        qr = rotate(qw[0], sg)
+        want, sts = [], []
+        for g in range(8):
+            o, st_g = native.attend_online(qr[4 * g:4 * g + 4], host.view(g), FMT)
+            want.append(o)
+            sts.append(st_g)
+        np.testing.assert_array_equal(out, np.concatenate(want), err_msg=f"step {t}")
+        st = blk.last_stats
+        assert st.serial_fallbacks == 0
+        assert st.rescale_events == sum(x.rescale_events for x in sts)
+        assert st.max_abs_acc == max(x.max_abs_acc for x in sts)
+
+
 @pytest.mark.parametrize("mode", ["online", "serial"])
 def test_fused_step_counts_rotated_queries_beyond_the_seam_range(ctx, mode):
     """A wire query of 2^30 on one channel rotates to +-2^27 on every channel,
