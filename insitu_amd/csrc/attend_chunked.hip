@@ -195,6 +195,10 @@ struct StepLds {
     uint8_t codes[2][MAX_D];
     int64_t newsc[GF];             // the new token's scores
     int32_t qi[GF][D];             // the rotated query rows
+    // the run-sum walk (codes of at most 2 bits at d = 64): each head's entries of the
+    // block, their value words word-major, so that a lane reads its word of entry j at a
+    // fixed offset
+    uint32_t crow[GF][4][64];
 };
 struct NoStep {};
 
@@ -938,6 +942,9 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                 }
                 const uint32_t vmask = (1u << g.vb) - 1u;
                 const bool vcross = (32 % g.vb) != 0;        // a code may straddle two words
+                // the fused step copies the block's value words word-major (codes of at most 2
+                // bits at d = 64: 2 or 4 words a row)
+                const bool crow_ok = STEP && CPL == 1 && g.vb <= 2;
                 const uint64_t vcmax = (uint64_t)uni64(S.vcmax);
                 int32_t vcr[8];                             // the value centroids (0 past nv)
 #pragma unroll
@@ -970,6 +977,13 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     const int val_i = exp_lut((int64_t)(r >> 11), S.expt, dm);
                     const int32_t p_i = in ? (ev_i ? pev : val_i) : 0;
                     const int32_t w_i = (int32_t)S.u.ph.vn[tl_i] * p_i;       // |w| <= 2^30
+                    if constexpr (STEP && CPL == 1) {
+                        if (crow_ok) {
+#pragma unroll
+                            for (int w = 0; w < 4; ++w)
+                                if (w < 2 * g.vb && w < K::VW) S.nr.crow[h][w][lane] = S.u.ph.vw[tl_i][w];
+                        }
+                    }
                     // the entry's term for every value code: floor(w * c[code] / 2^acc_shift),
                     // the per-entry 64-bit products done once for all channels
                     {
@@ -1051,24 +1065,48 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                                 }
                             }
                         } else {
-                            // the codes never cross a word (vb divides 32): one read per entry
+                            bool read = false;
+                            if constexpr (STEP && CPL == 1) {
+                                if (crow_ok) {
+                                    // the block's words word-major: entry j's at a fixed offset,
+                                    // one bit-field extract for the code
 #pragma unroll
-                            for (int jj = 0; jj < NG; ++jj) {
-                                const uint32_t *row = (const uint32_t *)((const char *)&S.u.ph.vw[0][0] +
-                                                                         __builtin_amdgcn_readlane(roff_i, j0 + jj));
+                                    for (int jj = 0; jj < NG; ++jj) {
+                                        const uint32_t word = S.nr.crow[h][wi[0]][j0 + jj];
+                                        cv[jj][0] = S.qt.tt[h][j0 + jj][__builtin_amdgcn_ubfe(word, (uint32_t)sh[0],
+                                                                                               (uint32_t)g.vb)];
+                                    }
+                                    read = true;
+                                }
+                            }
+                            if (!read) {
+                                // the codes never cross a word (vb divides 32): one read per entry
 #pragma unroll
-                                for (int k = 0; k < CPL; ++k)
-                                    cv[jj][k] = S.qt.tt[h][j0 + jj][(row[wi[k]] >> sh[k]) & vmask];
+                                for (int jj = 0; jj < NG; ++jj) {
+                                    const uint32_t *row = (const uint32_t *)((const char *)&S.u.ph.vw[0][0] +
+                                                                             __builtin_amdgcn_readlane(roff_i, j0 + jj));
+#pragma unroll
+                                    for (int k = 0; k < CPL; ++k)
+                                        cv[jj][k] = S.qt.tt[h][j0 + jj][(row[wi[k]] >> sh[k]) & vmask];
+                                }
                             }
                         }
                         const int ng = cnt - j0 < NG ? cnt - j0 : NG;
                         const uint32_t gev = (uint32_t)(evm >> j0) & ((1u << ng) - 1u);
                         if (!gev && !(SEQ && trk)) {
-                            // no event and no prefix tracking: the entries only add
+                            // no event and no prefix tracking: the entries only add (only the
+                            // chunk's last group is partial)
+                            if (ng == NG) {
 #pragma unroll
-                            for (int jj = 0; jj < NG; ++jj)
+                                for (int jj = 0; jj < NG; ++jj)
 #pragma unroll
-                                for (int k = 0; k < CPL; ++k) P[k] += jj < ng ? cv[jj][k] : 0;
+                                    for (int k = 0; k < CPL; ++k) P[k] += cv[jj][k];
+                            } else {
+#pragma unroll
+                                for (int jj = 0; jj < NG; ++jj)
+#pragma unroll
+                                    for (int k = 0; k < CPL; ++k) P[k] += jj < ng ? cv[jj][k] : 0;
+                            }
                             continue;
                         }
                         if constexpr (SEQ) {
@@ -1117,15 +1155,27 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                         // Prefix tracking (a run whose bound may pass TRACK_B): entry by entry.
                         if (!gev) {
                             // no event in the group: no branch per entry (an entry past the
-                            // chunk adds 0, which leaves P and its extremes as they are)
+                            // chunk adds 0, which leaves P and its extremes as they are; only
+                            // the chunk's last group is partial)
+                            if (ng == NG) {
 #pragma unroll
-                            for (int jj = 0; jj < NG; ++jj)
+                                for (int jj = 0; jj < NG; ++jj)
 #pragma unroll
-                                for (int k = 0; k < CPL; ++k) {
-                                    P[k] += jj < ng ? cv[jj][k] : 0;
-                                    hiP[k] = P[k] > hiP[k] ? P[k] : hiP[k];
-                                    loP[k] = P[k] < loP[k] ? P[k] : loP[k];
-                                }
+                                    for (int k = 0; k < CPL; ++k) {
+                                        P[k] += cv[jj][k];
+                                        hiP[k] = P[k] > hiP[k] ? P[k] : hiP[k];
+                                        loP[k] = P[k] < loP[k] ? P[k] : loP[k];
+                                    }
+                            } else {
+#pragma unroll
+                                for (int jj = 0; jj < NG; ++jj)
+#pragma unroll
+                                    for (int k = 0; k < CPL; ++k) {
+                                        P[k] += jj < ng ? cv[jj][k] : 0;
+                                        hiP[k] = P[k] > hiP[k] ? P[k] : hiP[k];
+                                        loP[k] = P[k] < loP[k] ? P[k] : loP[k];
+                                    }
+                            }
                             continue;
                         }
 #pragma unroll
