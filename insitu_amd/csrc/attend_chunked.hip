@@ -942,9 +942,10 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                 }
                 const uint32_t vmask = (1u << g.vb) - 1u;
                 const bool vcross = (32 % g.vb) != 0;        // a code may straddle two words
-                // the fused step copies the block's value words word-major (codes of at most 2
-                // bits at d = 64: 2 or 4 words a row)
-                const bool crow_ok = STEP && CPL == 1 && g.vb <= 2;
+                // the fused step at d = 64 copies the block's value words word-major wherever the
+                // codes never straddle (1 or 2 bits: 2 or 4 words a row)
+                static_assert(VB_MAX <= 3, "codes that never straddle a word are 1 or 2 bits wide");
+                const bool crow_ok = STEP && CPL == 1 && !vcross;
                 const uint64_t vcmax = (uint64_t)uni64(S.vcmax);
                 int32_t vcr[8];                             // the value centroids (0 past nv)
 #pragma unroll
@@ -1064,31 +1065,27 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                                     cv[jj][k] = S.qt.tt[h][j0 + jj][__builtin_amdgcn_alignbit(hi, lo, sh[k]) & vmask];
                                 }
                             }
-                        } else {
-                            bool read = false;
-                            if constexpr (STEP && CPL == 1) {
-                                if (crow_ok) {
-                                    // the block's words word-major: entry j's at a fixed offset,
-                                    // one bit-field extract for the code
+                        } else if constexpr (STEP && CPL == 1) {
+                            // the block's words word-major (crow_ok holds): entry j's at a fixed
+                            // offset, one bit-field extract for the code
 #pragma unroll
-                                    for (int jj = 0; jj < NG; ++jj) {
-                                        const uint32_t word = S.nr.crow[h][wi[0]][j0 + jj];
-                                        cv[jj][0] = S.qt.tt[h][j0 + jj][__builtin_amdgcn_ubfe(word, (uint32_t)sh[0],
-                                                                                               (uint32_t)g.vb)];
-                                    }
-                                    read = true;
-                                }
+                            for (int jj = 0; jj < NG; ++jj) {
+                                const uint32_t word = S.nr.crow[h][wi[0]][j0 + jj];
+                                cv[jj][0] = S.qt.tt[h][j0 + jj][__builtin_amdgcn_ubfe(word, (uint32_t)sh[0],
+                                                                                       (uint32_t)g.vb)];
                             }
-                            if (!read) {
-                                // the codes never cross a word (vb divides 32): one read per entry
+                            // keeps these table reads in this branch: merged with the other
+                            // branch's, their addresses lose the entry's constant offset
+                            __builtin_amdgcn_sched_barrier(0);
+                        } else {
+                            // the codes never cross a word (vb divides 32): one read per entry
 #pragma unroll
-                                for (int jj = 0; jj < NG; ++jj) {
-                                    const uint32_t *row = (const uint32_t *)((const char *)&S.u.ph.vw[0][0] +
-                                                                             __builtin_amdgcn_readlane(roff_i, j0 + jj));
+                            for (int jj = 0; jj < NG; ++jj) {
+                                const uint32_t *row = (const uint32_t *)((const char *)&S.u.ph.vw[0][0] +
+                                                                         __builtin_amdgcn_readlane(roff_i, j0 + jj));
 #pragma unroll
-                                    for (int k = 0; k < CPL; ++k)
-                                        cv[jj][k] = S.qt.tt[h][j0 + jj][(row[wi[k]] >> sh[k]) & vmask];
-                                }
+                                for (int k = 0; k < CPL; ++k)
+                                    cv[jj][k] = S.qt.tt[h][j0 + jj][(row[wi[k]] >> sh[k]) & vmask];
                             }
                         }
                         const int ng = cnt - j0 < NG ? cnt - j0 : NG;
