@@ -987,7 +987,13 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     }
                     // the entry's term for every value code: floor(w * c[code] / 2^acc_shift),
                     // the per-entry 64-bit products done once for all channels
-                    {
+                    if (g.vb <= 2) {
+                        // codes of at most 2 bits index the first four terms only
+                        int32_t tv[4];
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) tv[c] = (int32_t)(((int64_t)w_i * vcr[c]) >> acc_shift);
+                        *(int4 *)&S.qt.tt[h][lane][0] = make_int4(tv[0], tv[1], tv[2], tv[3]);
+                    } else {
                         int32_t tv[8];
 #pragma unroll
                         for (int c = 0; c < 8; ++c) tv[c] = (int32_t)(((int64_t)w_i * vcr[c]) >> acc_shift);
@@ -997,28 +1003,10 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     const uint64_t aw = (uint64_t)(w_i < 0 ? -(int64_t)w_i : (int64_t)w_i);
                     const int64_t bw_i = w_i != 0 ? (int64_t)((aw * vcmax) >> acc_shift) + 1 : 0;
                     const uint64_t evm = __ballot(ev_i);
-                    // L and B of every run an event of this block closes: prefix sums
-                    // over the entries, less their values where that run began (at
-                    // the previous event, or where the open run began before the
-                    // block -- prefix sums never decrease, so an exclusive max-scan
-                    // over the events finds it). f comes the same way, keyed by entry.
-                    const int64_t lp = Lc + wave_scan64<OpAdd64>(p_i, 0);
+                    // prefix sums of p and of the term bounds over the block (p <= 2^15, so
+                    // 64 of them fit 32 bits)
+                    const int64_t lp = Lc + (int64_t)wave_scan_add32((uint32_t)p_i);
                     const int64_t bp = Bc + wave_scan64<OpAdd64>(bw_i, 0);
-                    const int64_t lx = lp - p_i, bx = bp - bw_i;              // before the entry
-                    const int64_t key = ev_i ? (int64_t)(e + 1) << 16 | val_i : fkey;
-                    const int64_t lb = wave_shr1_64(wave_scan64<OpMax64>(ev_i ? lx : Ls, Ls), Ls);
-                    const int64_t bb = wave_shr1_64(wave_scan64<OpMax64>(ev_i ? bx : Bs, Bs), Bs);
-                    const int64_t kb = wave_shr1_64(wave_scan64<OpMax64>(key, fkey), fkey);
-                    const int64_t Lr = lx - lb, Br = bx - bb;   // at an event: the run it closes
-                    if (ev_i) {
-                        wide = wide || Br > ACC_HI;
-                        if (!own) {
-                            const int ri = seg + (int)__builtin_amdgcn_mbcnt_hi(
-                                                     (uint32_t)(evm >> 32),
-                                                     __builtin_amdgcn_mbcnt_lo((uint32_t)evm, 0u));
-                            pub64(&meta[ri].lf, (uint64_t)Lr | ((uint64_t)(kb & 0xFFFF) << 32));
-                        }
-                    }
                     // Tracking: any run with entries in this block has a bound of at
                     // most B (block end) - B (where the run open at the block start
                     // began). A run that starts tracking mid-way bounds its earlier
@@ -1034,14 +1022,37 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                         }
                     }
                     trk_prev = trk;
-                    Lc = readlane64(lp, 63);
-                    Bc = readlane64(bp, 63);
+                    // L and B of every run an event of this block closes: prefix sums
+                    // over the entries, less their values where that run began (at
+                    // the previous event, or where the open run began before the
+                    // block -- prefix sums never decrease, so an exclusive max-scan
+                    // over the events finds it). f comes the same way, keyed by entry.
+                    // Only event entries read them, so a block without one skips them.
+                    int64_t Lr = 0, Br = 0;
                     if (evm) {
+                        const int64_t lx = lp - p_i, bx = bp - bw_i;              // before the entry
+                        const int64_t key = ev_i ? (int64_t)(e + 1) << 16 | val_i : fkey;
+                        const int64_t lb = wave_shr1_64(wave_scan64<OpMax64>(ev_i ? lx : Ls, Ls), Ls);
+                        const int64_t bb = wave_shr1_64(wave_scan64<OpMax64>(ev_i ? bx : Bs, Bs), Bs);
+                        const int64_t kb = wave_shr1_64(wave_scan64<OpMax64>(key, fkey), fkey);
+                        Lr = lx - lb;   // at an event: the run it closes
+                        Br = bx - bb;
+                        if (ev_i) {
+                            wide = wide || Br > ACC_HI;
+                            if (!own) {
+                                const int ri = seg + (int)__builtin_amdgcn_mbcnt_hi(
+                                                         (uint32_t)(evm >> 32),
+                                                         __builtin_amdgcn_mbcnt_lo((uint32_t)evm, 0u));
+                                pub64(&meta[ri].lf, (uint64_t)Lr | ((uint64_t)(kb & 0xFFFF) << 32));
+                            }
+                        }
                         const int le = 63 - __clzll((long long)evm);        // the block's last event
                         Ls = readlane64(lx, le);
                         Bs = readlane64(bx, le);
                         fkey = readlane64(key, le);
                     }
+                    Lc = readlane64(lp, 63);
+                    Bc = readlane64(bp, 63);
                     // Lane = channel: each channel's term of the entries in order, NG at
                     // a time (independent LDS reads: the code's word pair, then the table
                     // entry), then the group's entries in one of three ways.
