@@ -1059,6 +1059,36 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     constexpr int NG = CPL == 1 ? 16 : 8;
                     const int cnt = n_act - a0 < 64 ? n_act - a0 : 64;
                     const int roff_i = tl_i * (K::VW * 4);       // the entry's value words, bytes
+                    if constexpr (STEP && CPL == 1) {
+                        if (crow_ok && !evm && cnt == 64) {
+                            // A full block without an event (the common block of a flat
+                            // softmax): its 64 entries in one straight run, so that the reads
+                            // are issued well ahead of the adds that wait for them.
+                            // Every word first, then every table read: LDS returns in order, so a
+                            // word read issued after a table read would wait for it.
+                            uint32_t cw[64];
+                            int32_t cb[64];
+#pragma unroll
+                            for (int j = 0; j < 64; j += 4)
+                                *(uint4 *)&cw[j] = *(const uint4 *)&S.nr.crow[h][wi[0]][j];
+                            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                            for (int j = 0; j < 64; ++j)
+                                cb[j] = S.qt.tt[h][j][__builtin_amdgcn_ubfe(cw[j], (uint32_t)sh[0], (uint32_t)g.vb)];
+                            if (SEQ && trk) {
+#pragma unroll
+                                for (int j = 0; j < 64; ++j) {
+                                    P[0] += cb[j];
+                                    hiP[0] = P[0] > hiP[0] ? P[0] : hiP[0];
+                                    loP[0] = P[0] < loP[0] ? P[0] : loP[0];
+                                }
+                            } else {
+#pragma unroll
+                                for (int j = 0; j < 64; ++j) P[0] += cb[j];
+                            }
+                            continue;
+                        }
+                    }
                     for (int j0 = 0; j0 < cnt; j0 += NG) {
                         int32_t cv[NG][CPL];
                         if (vcross) {
