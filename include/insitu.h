@@ -75,7 +75,8 @@ typedef struct {
     int32_t batch;          /* sequences                                   */
     int32_t n_kv_heads;
     int32_t n_q_heads;      /* multiple of n_kv_heads (config.py:49-53)     */
-    int32_t reserved;
+    int32_t chunk_tokens;   /* tokens per chunk of the chunked attend: 0 or 1024, or 512; no
+                               counterpart in the reference (an MI355X tuning of this build) */
     insitu_format fmt;
     const int64_t *key_centroids_host;
     const int64_t *key_bounds_host;

@@ -59,7 +59,7 @@ class Format(ctypes.Structure):
 class CacheDesc(ctypes.Structure):
     _fields_ = [("capacity", ctypes.c_int64), ("batch", ctypes.c_int32),
                 ("n_kv_heads", ctypes.c_int32), ("n_q_heads", ctypes.c_int32),
-                ("reserved", ctypes.c_int32), ("fmt", Format),
+                ("chunk_tokens", ctypes.c_int32), ("fmt", Format),
                 ("key_centroids_host", ctypes.POINTER(ctypes.c_int64)),
                 ("key_bounds_host", ctypes.POINTER(ctypes.c_int64)),
                 ("value_centroids_host", ctypes.POINTER(ctypes.c_int64)),

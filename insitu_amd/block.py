@@ -59,14 +59,16 @@ class AttentionBlock:
     def __init__(self, model: ModelConfig, quant: QuantConfig | None = None,
                  fmt: FixedFormat | None = None, *, capacity: int = 2048, batch: int = 1,
                  softmax: str = "online", weights=None, cast_after_rope: bool = True,
-                 ctx=None) -> None:
+                 chunk_tokens: int = 512, ctx=None) -> None:
         self.model = model
         self.quant = quant or QuantConfig()
         self.fmt = fmt or FixedFormat()
         self.ctx = ctx or default_context()
+        # 512-token chunks: a model's queries (projections of unit-scale hidden states) give a
+        # flat softmax, whose run-sum walk they split over twice the workgroups
         self.cache = CompressedCache(model.num_kv_heads, model.head_dim, capacity, self.quant,
                                      self.fmt, batch=batch, n_q_heads=model.num_heads,
-                                     ctx=self.ctx)
+                                     chunk_tokens=chunk_tokens, ctx=self.ctx)
         self.attn = CompressedAttention(self.cache)
         self.rotation = self.cache.rotation
         if softmax not in _lib.MODES:

@@ -31,9 +31,15 @@ FLAGS = [
 ]
 
 
-def _compile(src: str) -> str:
-    obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+# Sources built more than once, each time with other defines: the chunked attend with
+# 512-token chunks (namespace insitu::c512) beside its default 1,024-token build.
+VARIANTS = {"attend_chunked.hip": [("c512", ["-DINSITU_CHUNK_TPT=1"])]}
+
+
+def _compile(job) -> str:
+    src, tag, defs = job
+    obj = os.path.join(BUILD, os.path.basename(src) + (f".{tag}" if tag else "") + ".o")
+    cmd = [HIPCC, *FLAGS, *defs, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stdout}\n{r.stderr}")
@@ -43,8 +49,10 @@ def _compile(src: str) -> str:
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
-    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(_compile, srcs))
+    jobs = [(src, "", []) for src in srcs]
+    jobs += [(os.path.join(CSRC, name), tag, defs) for name, vs in VARIANTS.items() for tag, defs in vs]
+    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(jobs))) as ex:
+        objs = list(ex.map(_compile, jobs))
     tmp = OUT + ".tmp"
     # rocBLAS runs the host half's plain fp16 GEMMs (host_half.hip)
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, "-lrocblas"]

@@ -159,8 +159,12 @@ class CompressedCache(KVCache):
 
     def __init__(self, n_kv_heads: int, head_dim: int, capacity: int,
                  quant: QuantConfig, fmt: FixedFormat | None = None, qk_frac: int | None = None,
-                 *, batch: int = 1, n_q_heads: int | None = None, ctx=None) -> None:
+                 *, batch: int = 1, n_q_heads: int | None = None, chunk_tokens: int = 0,
+                 ctx=None) -> None:
         super().__init__(n_kv_heads, head_dim, capacity)
+        # tokens per chunk of the chunked attend: 0 (the default, 1,024) or 512, which doubles
+        # the workgroups that walk a flat softmax's candidates
+        self.chunk_tokens = chunk_tokens
         self.ctx = ctx or default_context()
         self.quant = quant
         self.fmt = fmt or FixedFormat()
@@ -185,6 +189,7 @@ class CompressedCache(KVCache):
         desc.batch = batch
         desc.n_kv_heads = n_kv_heads
         desc.n_q_heads = self.n_q_heads
+        desc.chunk_tokens = chunk_tokens
         desc.fmt = self.format
         desc.key_centroids_host = i64p(kc)
         desc.key_bounds_host = i64p(kbd)

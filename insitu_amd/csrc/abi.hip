@@ -151,6 +151,15 @@ int insitu::ctx_device(insitu_ctx *c) { return c->device; }
 hipStream_t insitu::ctx_stream(insitu_ctx *c) { return c->stream; }
 void *&insitu::ctx_blas(insitu_ctx *c) { return c->blas; }
 
+// The chunked attend's two builds (attend_chunked.hip): 1,024-token chunks, the default, and
+// 512-token chunks (insitu_cache_desc.chunk_tokens = 512).
+static const insitu::ChunkedApi k_chunk1024 = {
+    1024, insitu::chunked_supported, insitu::chunked_max_chunks, insitu::chunked_pool_slots,
+    insitu::chunked_scratch_bytes, insitu::chunked_query_area, insitu::launch_attend_chunked};
+static const insitu::ChunkedApi k_chunk512 = {
+    512, insitu::c512::chunked_supported, insitu::c512::chunked_max_chunks, insitu::c512::chunked_pool_slots,
+    insitu::c512::chunked_scratch_bytes, insitu::c512::chunked_query_area, insitu::c512::launch_attend_chunked};
+
 struct insitu_cache {
     insitu_ctx *ctx = nullptr;
     insitu_cache_desc desc{};
@@ -164,6 +173,7 @@ struct insitu_cache {
     std::vector<int64_t> len_host;
     DevStats *stats = nullptr;
     int32_t *wire_scratch = nullptr;      // insitu_step: the rotated queries
+    const ChunkedApi *api = nullptr;      // the chunked attend's build: 1,024- or 512-token chunks
     bool chunked = false;                 // the chunked attend handles this format and capacity
     bool scan = false;                    // the scan attend does (sequential mode)
     ChunkScratch scr;                     // decode attends: run sums and counters, one call's worth
@@ -405,6 +415,8 @@ int insitu_cache_create(insitu_ctx *c, const insitu_cache_desc *desc, insitu_cac
     if (desc->n_q_heads / desc->n_kv_heads > MAX_G)
         return fail(INSITU_EINVAL, "more than 8 query heads per KV head is not supported");
     if (desc->batch < 1 || desc->capacity < 1) return fail(INSITU_EINVAL, "batch and capacity >= 1");
+    if (desc->chunk_tokens != 0 && desc->chunk_tokens != 512 && desc->chunk_tokens != 1024)
+        return fail(INSITU_EINVAL, "chunk_tokens is 0 (the default, 1,024), 512 or 1,024");
     if (!desc->key_centroids_host || !desc->key_bounds_host || !desc->value_centroids_host ||
         !desc->value_bounds_host)
         return fail(INSITU_EINVAL, "codebooks are required");
@@ -495,14 +507,15 @@ int insitu_cache_create(insitu_ctx *c, const insitu_cache_desc *desc, insitu_cac
     if (e == hipSuccess)
         e = hipMalloc(&k->wire_scratch,
                       sizeof(int32_t) * (size_t)g.batch * (g.n_q + 2 * g.n_kv) * g.d);
-    k->chunked = chunked_supported(g, desc->capacity);
+    k->api = desc->chunk_tokens == 512 ? &k_chunk512 : &k_chunk1024;
+    k->chunked = k->api->supported(g, desc->capacity);
     k->scan = scan_supported(g, desc->capacity);
     if (e == hipSuccess && (k->chunked || k->scan)) {
         size_t nb = 0;
         if (k->chunked) {
-            k->max_chunks = chunked_max_chunks(desc->capacity);
-            k->pool = chunked_pool_slots(k->max_chunks);
-            nb = chunked_scratch_bytes(g, k->max_chunks, k->pool);
+            k->max_chunks = k->api->max_chunks(desc->capacity);
+            k->pool = k->api->pool_slots(k->max_chunks);
+            nb = k->api->scratch_bytes(g, k->max_chunks, k->pool);
         }
         if (k->scan) {
             k->scan_mc = scan_max_chunks(desc->capacity);
@@ -663,9 +676,9 @@ static int attend_impl(insitu_cache *k, const int32_t *q, int32_t *out, int32_t 
         k->scr.spin_limit = k->spin_limit;
         int64_t longest = 0;
         for (int64_t n : k->len_host) longest = n > longest ? n : longest;
-        HIP_TRY(launch_attend_chunked(k->ctx->stream, k->g, k->tabs, q, out, len, k->scr, ep,
-                                      k->max_chunks, k->pool, two_pass, q_staged, step, ev, k->stats, 0,
-                                      chunked_max_chunks(longest + (step ? 1 : 0))),
+        HIP_TRY(k->api->launch(k->ctx->stream, k->g, k->tabs, q, out, len, k->scr, ep,
+                               k->max_chunks, k->pool, two_pass, q_staged, step, ev, k->stats, 0,
+                               k->api->max_chunks(longest + (step ? 1 : 0))),
                 "chunked attend launch");
         return INSITU_OK;
     }
@@ -714,19 +727,19 @@ struct PrefillPlan {
     int64_t qb, max_chunks, pool;
     size_t bytes;
 };
-PrefillPlan prefill_plan(const Geom &gv, int64_t base, int64_t n_q, size_t budget) {
+PrefillPlan prefill_plan(const ChunkedApi &api, const Geom &gv, int64_t base, int64_t n_q, size_t budget) {
     PrefillPlan pl{};
-    pl.max_chunks = chunked_max_chunks(base + n_q);
-    pl.pool = chunked_pool_slots(pl.max_chunks);
+    pl.max_chunks = api.max_chunks(base + n_q);
+    pl.pool = api.pool_slots(pl.max_chunks);
     Geom one = gv;
     one.batch = 1;
-    const size_t per_q = chunked_scratch_bytes(one, pl.max_chunks, pl.pool);
+    const size_t per_q = api.scratch_bytes(one, pl.max_chunks, pl.pool);
     pl.qb = (int64_t)(budget / (per_q ? per_q : 1));
     if (pl.qb > PREFILL_QB) pl.qb = PREFILL_QB;
     if (pl.qb > n_q) pl.qb = n_q;
     Geom all = gv;
     all.batch = (int32_t)(pl.qb > 0 ? pl.qb : 1);
-    pl.bytes = chunked_scratch_bytes(all, pl.max_chunks, pl.pool);
+    pl.bytes = api.scratch_bytes(all, pl.max_chunks, pl.pool);
     return pl;
 }
 
@@ -755,9 +768,9 @@ static int prefill_launches(insitu_cache *k, const Geom &gv, const PrefillPlan &
             uint32_t ep = 0;
             HIP_TRY(scratch_begin(k->ctx->stream, scr, &ep), "scratch clear");
             scr.spin_limit = k->spin_limit;
-            HIP_TRY(launch_attend_chunked(k->ctx->stream, gb, k->tabs, q + i0 * row, out + i0 * row, len_dev,
-                                          scr, ep, pl.max_chunks, pl.pool, mode == INSITU_TWO_PASS ? 1 : 0,
-                                          false, nullptr, ev, k->stats, pl.qb),
+            HIP_TRY(k->api->launch(k->ctx->stream, gb, k->tabs, q + i0 * row, out + i0 * row, len_dev,
+                                   scr, ep, pl.max_chunks, pl.pool, mode == INSITU_TWO_PASS ? 1 : 0,
+                                   false, nullptr, ev, k->stats, pl.qb, 0),
                     "prefill attend launch");
         } else {
             HIP_TRY(launch_attend_serial(k->ctx->stream, gb, k->tabs, q + i0 * row, out + i0 * row, len_dev,
@@ -792,7 +805,7 @@ static int causal_impl(insitu_cache *k, const Geom &gv, int64_t base, int64_t n_
     int rc = stats ? zero_stats(k) : INSITU_OK;
     if (rc) return rc;
     if (n_q == 0) return copy_stats(k, stats);
-    const PrefillPlan pl = prefill_plan(gv, base, n_q, PREFILL_SCRATCH_BUDGET);
+    const PrefillPlan pl = prefill_plan(*k->api, gv, base, n_q, PREFILL_SCRATCH_BUDGET);
     if (!k->prefill_len) HIP_TRY(hipMalloc(&k->prefill_len, PREFILL_QB * sizeof(int64_t)), "hipMalloc");
     if (mode != INSITU_SERIAL && k->chunked && k->prefill_scr.bytes < pl.bytes) {
         // grow: the old buffer may still be in use by queued launches
@@ -851,14 +864,14 @@ int insitu_attend_causal_static(insitu_cache *k, int32_t seq, int64_t base, int6
     gv.seq_stride = 0;
     PrefillPlan pl{};
     if (mode != INSITU_SERIAL && k->chunked) {
-        pl = prefill_plan(gv, base, n_q, ss.cs.bytes);
+        pl = prefill_plan(*k->api, gv, base, n_q, ss.cs.bytes);
         if (pl.qb < 1) {
             Geom one = gv;
             one.batch = 1;
             char buf[240];
             snprintf(buf, sizeof buf, "one query over %lld rows needs %zu B of chunk scratch; the static "
                      "scratch holds %zu B (insitu_attend_causal allocates instead)", (long long)(base + n_q),
-                     chunked_scratch_bytes(one, pl.max_chunks, pl.pool), ss.cs.bytes);
+                     k->api->scratch_bytes(one, pl.max_chunks, pl.pool), ss.cs.bytes);
             return fail(INSITU_EBADLEN, buf);
         }
     }
@@ -908,7 +921,7 @@ int insitu_step(insitu_cache *k, const int32_t *q, const int32_t *kw, const int3
     if (chunked) {
         // the epoch (and the wrap's clear) before the write kernel stages the queries
         HIP_TRY(scratch_begin(k->ctx->stream, k->scr, &ep), "scratch clear");
-        chunked_query_area(g, k->max_chunks, k->pool, k->scr.p, &qd, &qok);
+        k->api->query_area(g, k->max_chunks, k->pool, k->scr.p, &qd, &qok);
     }
     HIP_TRY(launch_step_write(k->ctx->stream, g, k->tabs, q, kw, vw, k->desc.fmt.rot_rounds,
                               k->desc.fmt.rot_signs, qr, qd, qok, k->len_dev[k->cur],

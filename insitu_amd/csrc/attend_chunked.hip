@@ -52,10 +52,22 @@
 #include "serial_head.h"
 #include "wave.h"
 
+// The file is built twice: with 1,024-token chunks (two tokens per thread, the default) and,
+// with INSITU_CHUNK_TPT=1, with 512-token chunks in namespace insitu::c512. A cache picks one
+// at creation: the smaller chunks double the workgroups that walk a flat softmax's candidates,
+// the larger ones halve the chunks that a peaked softmax looks back over and replays.
+#ifndef INSITU_CHUNK_TPT
+#define INSITU_CHUNK_TPT 2
+#endif
+static_assert(INSITU_CHUNK_TPT == 1 || INSITU_CHUNK_TPT == 2, "1,024- or 512-token chunks");
+
 namespace insitu {
+#if INSITU_CHUNK_TPT == 1
+namespace c512 {
+#endif
 
 constexpr int CT = 512;              // threads per workgroup: 8 waves, 2 per SIMD
-constexpr int TPT = 2;               // tokens per thread in the score phase
+constexpr int TPT = INSITU_CHUNK_TPT;  // tokens per thread in the score phase
 constexpr int CHUNK = CT * TPT;      // tokens per workgroup
 constexpr int VB_MAX = 3;            // widest value code staged in LDS
 constexpr int HMAX = 512;            // chunks per (sequence, KV head) on the chunked path
@@ -1780,6 +1792,8 @@ __global__ void clear_scratch_kernel(uint4 *p, int64_t n16) {
         p[i] = make_uint4(0u, 0u, 0u, 0u);
 }
 
+#if INSITU_CHUNK_TPT == 2
+// (one definition: the 512-token build uses these)
 hipError_t scratch_begin(hipStream_t s, ChunkScratch &cs, uint32_t *ep) {
     const uint32_t call = cs.calls++;
     // 1 .. 2^14 - 1: the zeroed scratch of a new buffer is never current. At
@@ -1810,6 +1824,7 @@ hipError_t scratch_layout(hipStream_t s, ChunkScratch &cs, uint64_t layout, size
     cs.layout = layout;
     return hipSuccess;
 }
+#endif
 
 hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
                                  int32_t *out, const int64_t *len, ChunkScratch &cs,
@@ -1850,4 +1865,7 @@ hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, 
     return hipErrorInvalidValue;
 }
 
+#if INSITU_CHUNK_TPT == 1
+}  // namespace c512
+#endif
 }  // namespace insitu

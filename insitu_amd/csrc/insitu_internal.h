@@ -256,6 +256,35 @@ hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, 
                                  bool q_staged, const StepIn *step, LaunchEv ev, DevStats *st,
                                  int64_t carve_batch = 0,
                                  int64_t grid_chunks = 0);
+// The same entry points of the chunked attend built with 512-token chunks
+// (attend_chunked.hip with INSITU_CHUNK_TPT=1). A cache uses one build for all
+// its attends, so its scratch is laid out by that build's carve.
+namespace c512 {
+bool chunked_supported(const Geom &g, int64_t capacity);
+int64_t chunked_max_chunks(int64_t capacity);
+int64_t chunked_pool_slots(int64_t max_chunks);
+size_t chunked_scratch_bytes(const Geom &g, int64_t max_chunks, int64_t pool);
+void chunked_query_area(const Geom &g, int64_t max_chunks, int64_t pool, void *scratch,
+                        double **qd, int32_t **qok);
+hipError_t launch_attend_chunked(hipStream_t s, const Geom &g, const Tables *t, const int32_t *q,
+                                 int32_t *out, const int64_t *len, ChunkScratch &cs,
+                                 uint32_t ep, int64_t max_chunks, int64_t pool, int two_pass,
+                                 bool q_staged, const StepIn *step, LaunchEv ev, DevStats *st,
+                                 int64_t carve_batch = 0,
+                                 int64_t grid_chunks = 0);
+}  // namespace c512
+// One chunk size's entry points, as a cache holds them.
+struct ChunkedApi {
+    int32_t tokens;   // tokens per chunk
+    bool (*supported)(const Geom &, int64_t);
+    int64_t (*max_chunks)(int64_t);
+    int64_t (*pool_slots)(int64_t);
+    size_t (*scratch_bytes)(const Geom &, int64_t, int64_t);
+    void (*query_area)(const Geom &, int64_t, int64_t, void *, double **, int32_t **);
+    hipError_t (*launch)(hipStream_t, const Geom &, const Tables *, const int32_t *, int32_t *,
+                         const int64_t *, ChunkScratch &, uint32_t, int64_t, int64_t, int, bool,
+                         const StepIn *, LaunchEv, DevStats *, int64_t, int64_t);
+};
 hipError_t launch_step_write(hipStream_t s, const Geom &g, const Tables *t, const int32_t *qw,
                              const int32_t *kw, const int32_t *vw, int rounds,
                              const uint64_t (*signs)[2], int32_t *qr, double *qd, int32_t *qok,

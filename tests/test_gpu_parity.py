@@ -19,11 +19,11 @@ pytestmark = pytest.mark.gpu
 FMT = Format()
 
 
-def _cache(ctx, capacity, *, d=64, kb=4, vb=2, batch=1, n_kv=8, n_q=32):
+def _cache(ctx, capacity, *, d=64, kb=4, vb=2, batch=1, n_kv=8, n_q=32, chunk_tokens=0):
     from insitu_amd import QuantConfig
     from insitu_amd.cache import CompressedCache
     return CompressedCache(n_kv, d, capacity, QuantConfig(key_bits=kb, value_bits=vb),
-                           batch=batch, n_q_heads=n_q, ctx=ctx)
+                           batch=batch, n_q_heads=n_q, chunk_tokens=chunk_tokens, ctx=ctx)
 
 
 @pytest.fixture(scope="module")
