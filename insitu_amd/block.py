@@ -59,13 +59,18 @@ class AttentionBlock:
     def __init__(self, model: ModelConfig, quant: QuantConfig | None = None,
                  fmt: FixedFormat | None = None, *, capacity: int = 2048, batch: int = 1,
                  softmax: str = "online", weights=None, cast_after_rope: bool = True,
-                 chunk_tokens: int = 512, ctx=None) -> None:
+                 chunk_tokens: int | None = None, ctx=None) -> None:
         self.model = model
         self.quant = quant or QuantConfig()
         self.fmt = fmt or FixedFormat()
         self.ctx = ctx or default_context()
-        # 512-token chunks: a model's queries (projections of unit-scale hidden states) give a
-        # flat softmax, whose run-sum walk they split over twice the workgroups
+        # 512-token chunks for the online softmax: a model's queries (projections of unit-scale
+        # hidden states) give a flat softmax, whose run-sum walk they split over twice the
+        # workgroups. Two-pass keeps 1,024 (its chunk-max launch and the prefill's query
+        # batches favour fewer chunks: a 4,096-token two-pass prefill takes 10.7 ms on 1,024-
+        # and 17.0 ms on 512-token chunks).
+        if chunk_tokens is None:
+            chunk_tokens = 1024 if softmax == "two_pass" else 512
         self.cache = CompressedCache(model.num_kv_heads, model.head_dim, capacity, self.quant,
                                      self.fmt, batch=batch, n_q_heads=model.num_heads,
                                      chunk_tokens=chunk_tokens, ctx=self.ctx)

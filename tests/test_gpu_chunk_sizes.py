@@ -82,12 +82,15 @@ def test_block_prefill_on_1024_token_chunks(ctx, blocks1024, softmax):
     P.test_block_prefill_equals_the_decode_loop(ctx, softmax)
 
 
-def test_the_block_uses_512_token_chunks_and_a_bare_cache_1024(ctx):
+def test_the_online_block_uses_512_token_chunks_two_pass_and_a_bare_cache_1024(ctx):
     from insitu_amd import ModelConfig, QuantConfig
     from insitu_amd.block import AttentionBlock
     blk = AttentionBlock(ModelConfig.llama32_1b(), QuantConfig(key_bits=4, value_bits=2),
                          capacity=600, ctx=ctx)
     assert blk.cache.chunk_tokens == 512
+    two = AttentionBlock(ModelConfig.llama32_1b(), QuantConfig(key_bits=4, value_bits=2),
+                         capacity=600, softmax="two_pass", ctx=ctx)
+    assert two.cache.chunk_tokens == 1024
     assert P._cache(ctx, 600).chunk_tokens == 0
 
 
