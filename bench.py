@@ -72,6 +72,8 @@ def _args():
     ap.add_argument("--steps", type=int, default=40)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--mode", default="online", choices=["online", "two_pass", "split", "serial"])
+    ap.add_argument("--chunk-tokens", type=int, default=0, choices=[0, 512, 1024],
+                    help="tokens per chunk of the chunked attend for C2/C3/C4 (0: the cache default, 1,024)")
     ap.add_argument("--caches", type=int, default=40)
     ap.add_argument("--ctx", type=int, default=CTX)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -334,7 +336,8 @@ def bench_scale(a) -> int:
     quant = QuantConfig(key_bits=kb, value_bits=vb)
     fmt = Format(d=d, key_bits=kb, value_bits=vb)
     rot = Rotation.for_quant(quant, d)
-    caches = [CompressedCache(N_KV, d, int(lens.max()), quant, batch=batch, n_q_heads=N_Q, ctx=ctx)
+    caches = [CompressedCache(N_KV, d, int(lens.max()), quant, batch=batch, n_q_heads=N_Q,
+                              chunk_tokens=a.chunk_tokens, ctx=ctx)
               for _ in range(n_caches)]
     t_fill = time.perf_counter()
     qs = []
@@ -412,7 +415,7 @@ def bench_scale(a) -> int:
         "vs_baseline": None,
         "dtype": "int64",
         "data": data,
-        "config": {"workload": workload, "mode": a.mode, "batch": batch,
+        "config": {"workload": workload, "mode": a.mode, "chunk_tokens": a.chunk_tokens or 1024, "batch": batch,
                    "ctx_total": int(lens.sum()), "ctx_min": int(lens.min()), "ctx_max": int(lens.max()),
                    "caches": n_caches, "head_dim": d, "row_bytes": row,
                    "resident_gb": round(sum(c.layout()["device_total_bytes"] for c in caches) / 1e9, 2),
@@ -787,7 +790,7 @@ def main() -> int:
     del k, v
     caches = []
     for _ in range(n_caches):
-        c = CompressedCache(N_KV, D, a.ctx, quant, batch=1, n_q_heads=N_Q, ctx=ctx)
+        c = CompressedCache(N_KV, D, a.ctx, quant, batch=1, n_q_heads=N_Q, chunk_tokens=a.chunk_tokens, ctx=ctx)
         c.append_rotated(kr, vr)
         caches.append(c)
     qs_d = ctx.to_device(qs[0], torch.int32)
@@ -884,7 +887,7 @@ def main() -> int:
         "data": "synthetic (seeded N(0,1) q/k/v with 4 outlier channels x8 per head, Q8.16)",
         "config": {"workload": "C2: Llama-3.2-1B-shape single layer, batch 1, ctx 32768, "
                                "4b K / 2b V, decode step = insitu_step: rotate + append + attend",
-                   "mode": a.mode, "ctx": a.ctx, "rotating_caches": n_caches,
+                   "mode": a.mode, "chunk_tokens": a.chunk_tokens or 1024, "ctx": a.ctx, "rotating_caches": n_caches,
                    "rotating_mb": round(total_mb, 1), "kv_heads": N_KV, "q_heads": N_Q,
                    "head_dim": D, "row_bytes": ROW},
         "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 3), "peak": HBM_PEAK_GBS,
