@@ -94,6 +94,14 @@ def test_the_online_block_uses_512_token_chunks_two_pass_and_a_bare_cache_1024(c
     assert P._cache(ctx, 600).chunk_tokens == 0
 
 
+@pytest.mark.parametrize("mode", ["online", "two_pass"])
+def test_static_prefill_on_512_token_chunks(ctx, monkeypatch, mode):
+    """The allocation-free prefill lays its static array out by the cache's build."""
+    import test_zz_no_alloc as Z
+    monkeypatch.setattr(Z, "_cache", functools.partial(Z._cache, chunk_tokens=512))
+    Z.test_static_prefill_equals_the_allocating_prefill_twice(ctx, mode)
+
+
 @pytest.mark.parametrize("bad", [256, 1023, 2048, -1])
 def test_other_chunk_sizes_are_refused(ctx, bad):
     from insitu_amd._lib import InsituError

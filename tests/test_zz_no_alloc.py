@@ -18,11 +18,11 @@ from oracle.rotate import rotate, signs_from_seed
 pytestmark = pytest.mark.gpu
 
 
-def _cache(ctx, capacity, *, d=64, kb=4, vb=2, n_kv=8, n_q=32):
+def _cache(ctx, capacity, *, d=64, kb=4, vb=2, n_kv=8, n_q=32, chunk_tokens=0):
     from insitu_amd import QuantConfig
     from insitu_amd.cache import CompressedCache
     return CompressedCache(n_kv, d, capacity, QuantConfig(key_bits=kb, value_bits=vb),
-                           n_q_heads=n_q, ctx=ctx)
+                           n_q_heads=n_q, chunk_tokens=chunk_tokens, ctx=ctx)
 
 
 def _static(ctx, c, base, q, mode):
