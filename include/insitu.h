@@ -271,8 +271,10 @@ enum {
                                         up at once, sending every chain with a predecessor to the
                                         exact serial path                                       */
     INSITU_DEBUG_PATH = 4            /* the kernel of a sequential-mode attend: 0 automatic (the
-                                        chunked attend where it handles the cache, the scan attend
-                                        elsewhere), 1 the scan attend, 2 the chunked attend;
+                                        decode step on its own kernel where it handles the cache,
+                                        the chunked attend where it handles the cache, the scan
+                                        attend elsewhere), 1 the scan attend, 2 the chunked attend
+                                        (the decode step too), 3 the decode step's own kernel;
                                         INSITU_EINVAL if the kernel does not handle the cache   */
 };
 int insitu_cache_debug(insitu_cache *cache, int32_t what, int64_t value);

@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(HERE, "libinsitu_hip.so")
 OK, EBADLEN, ERANGE, EHIP, EINVAL, ECAPACITY, ENOMEM, EFAULT = range(8)
 SEQUENTIAL, TWO_PASS, SPLIT, SERIAL = range(4)
 DEBUG_DECODE_CALLS, DEBUG_PREFILL_CALLS, DEBUG_SPIN_LIMIT, DEBUG_PATH = 1, 2, 3, 4
-PATH_AUTO, PATH_SCAN, PATH_CHUNKED = 0, 1, 2
+PATH_AUTO, PATH_SCAN, PATH_CHUNKED, PATH_STEP = 0, 1, 2, 3
 MODES = {"online": SEQUENTIAL, "sequential": SEQUENTIAL, "two_pass": TWO_PASS,
          "split": SPLIT, "serial": SERIAL}
 

@@ -323,9 +323,12 @@ class CompressedCache(KVCache):
 
     def pin_kernel(self, path: str) -> None:
         """Test hook: the kernel of sequential-mode attends on this cache, "auto" (the
-        chunked attend where it handles the format and capacity, the scan attend
-        elsewhere), "scan" or "chunked". Raises if that kernel does not handle the cache."""
-        code = {"auto": _lib.PATH_AUTO, "scan": _lib.PATH_SCAN, "chunked": _lib.PATH_CHUNKED}[path]
+        decode step's own kernel for insitu_step where it handles the format, the chunked
+        attend where it handles the format and capacity, the scan attend elsewhere),
+        "scan", "chunked" (the decode step too) or "step" (the decode step's own kernel).
+        Raises if that kernel does not handle the cache."""
+        code = {"auto": _lib.PATH_AUTO, "scan": _lib.PATH_SCAN, "chunked": _lib.PATH_CHUNKED,
+                "step": _lib.PATH_STEP}[path]
         _lib.check(self.ctx.lib.insitu_cache_debug(self.handle, _lib.DEBUG_PATH, code))
 
     @property

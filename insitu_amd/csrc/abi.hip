@@ -176,6 +176,8 @@ struct insitu_cache {
     const ChunkedApi *api = nullptr;      // the chunked attend's build: 1,024- or 512-token chunks
     bool chunked = false;                 // the chunked attend handles this format and capacity
     bool scan = false;                    // the scan attend does (sequential mode)
+    bool step = false;                    // the fused step's own kernel does (sequential mode)
+    int64_t step_mc = 0;                  // its layout: chunks per sequence
     ChunkScratch scr;                     // decode attends: run sums and counters, one call's worth
     int64_t max_chunks = 0, pool = 0;     // the chunked attend's layout
     int64_t scan_mc = 0;                  // the scan attend's: chunks per sequence
@@ -183,7 +185,7 @@ struct insitu_cache {
     ChunkScratch prefill_scr;
     int64_t *prefill_len = nullptr;
     int32_t spin_limit = 1 << 20;         // insitu_cache_debug
-    int32_t path = 0;                     // insitu_cache_debug: 0 auto, 1 scan, 2 chunked
+    int32_t path = 0;                     // insitu_cache_debug: 0 auto, 1 scan, 2 chunked, 3 step kernel
 };
 
 namespace {
@@ -510,12 +512,18 @@ int insitu_cache_create(insitu_ctx *c, const insitu_cache_desc *desc, insitu_cac
     k->api = desc->chunk_tokens == 512 ? &k_chunk512 : &k_chunk1024;
     k->chunked = k->api->supported(g, desc->capacity);
     k->scan = scan_supported(g, desc->capacity);
-    if (e == hipSuccess && (k->chunked || k->scan)) {
+    k->step = step_supported(g, desc->capacity);
+    if (e == hipSuccess && (k->chunked || k->scan || k->step)) {
         size_t nb = 0;
+        if (k->step) {
+            k->step_mc = step_max_chunks(desc->capacity);
+            nb = step_scratch_bytes(g, k->step_mc);
+        }
         if (k->chunked) {
             k->max_chunks = k->api->max_chunks(desc->capacity);
             k->pool = k->api->pool_slots(k->max_chunks);
-            nb = k->api->scratch_bytes(g, k->max_chunks, k->pool);
+            const size_t nc = k->api->scratch_bytes(g, k->max_chunks, k->pool);
+            nb = nc > nb ? nc : nb;
         }
         if (k->scan) {
             k->scan_mc = scan_max_chunks(desc->capacity);
@@ -644,8 +652,15 @@ int insitu_append_seq(insitu_cache *k, int32_t seq, const int32_t *kr, const int
 static bool use_scan(const insitu_cache *k, int32_t mode) {
     if (mode == INSITU_SERIAL || mode == INSITU_TWO_PASS || !k->scan) return false;
     if (k->path == 1) return true;
-    if (k->path == 2) return false;
+    if (k->path == 2 || k->path == 3) return false;
     return !k->chunked;
+}
+
+// The fused decode step's own kernel (attend_step.hip), sequential and split mode, where it
+// handles the format: pinned by the test hook (3) while it is being brought up to speed.
+static bool use_step_kernel(const insitu_cache *k, int32_t mode) {
+    if ((mode != INSITU_SEQUENTIAL && mode != INSITU_SPLIT) || !k->step) return false;
+    return k->path == 3;
 }
 
 // q_staged: the chunked path's fp64 query staging already holds q (the step's
@@ -669,6 +684,17 @@ static int attend_impl(insitu_cache *k, const int32_t *q, int32_t *out, int32_t 
         HIP_TRY(launch_attend_scan(k->ctx->stream, k->g, k->tabs, q, out, len, k->scr, ep, k->scan_mc, chunks,
                                    step, ev, k->stats),
                 "scan attend launch");
+        return INSITU_OK;
+    }
+    if (step && use_step_kernel(k, mode)) {
+        // the fused step's own kernel, its grid sized by the longest sequence
+        if (!ep) HIP_TRY(scratch_begin(k->ctx->stream, k->scr, &ep), "scratch clear");
+        k->scr.spin_limit = k->spin_limit;
+        int64_t longest = 0;
+        for (int64_t n : k->len_host) longest = n > longest ? n : longest;
+        HIP_TRY(launch_step(k->ctx->stream, k->g, k->tabs, out, len, k->scr, ep, k->step_mc,
+                            step_max_chunks(longest + 1), *step, ev, k->stats),
+                "step launch");
         return INSITU_OK;
     }
     if (mode != INSITU_SERIAL && k->chunked) {
@@ -900,7 +926,8 @@ int insitu_step(insitu_cache *k, const int32_t *q, const int32_t *kw, const int3
     // (which also stages the rotated queries for a chunked attend) and the attend.
     const bool scan = use_scan(k, mode);
     const bool chunked = !scan && mode != INSITU_SERIAL && k->chunked;
-    const bool fused = scan || (mode != INSITU_TWO_PASS && chunked && chunked_fused_step(g));
+    const bool fused = scan || use_step_kernel(k, mode) ||
+                       (mode != INSITU_TWO_PASS && chunked && chunked_fused_step(g));
     if (fused) {
         StepIn si;
         si.qw = q;
@@ -952,7 +979,9 @@ int insitu_cache_debug(insitu_cache *k, int32_t what, int64_t value) {
     case INSITU_DEBUG_PATH:
         if (value == 1 && !k->scan) return fail(INSITU_EINVAL, "the scan attend does not handle this cache");
         if (value == 2 && !k->chunked) return fail(INSITU_EINVAL, "the chunked attend does not handle this cache");
-        if (value < 0 || value > 2) return fail(INSITU_EINVAL, "path is 0 (auto), 1 (scan) or 2 (chunked)");
+        if (value == 3 && !k->step) return fail(INSITU_EINVAL, "the step kernel does not handle this cache");
+        if (value < 0 || value > 3)
+            return fail(INSITU_EINVAL, "path is 0 (auto), 1 (scan), 2 (chunked) or 3 (step kernel)");
         k->path = (int32_t)value;
         return INSITU_OK;
     default:

@@ -1,0 +1,1115 @@
+// The fused decode step (kernel.py:271-345): rotate q/k/v, encode and append the
+// token's k/v row, then attend_online (ops/attention.py:451-513) and the finalize
+// (:873-880) over every cached row, bit-exact, in one launch of 16-wave workgroups,
+// one per (1,024-token chunk, sequence, KV head) at d = 64, 4 query heads per KV head.
+//
+// The arithmetic is the chunked attend's (attend_chunked.hip): a chunk knows the
+// running maximum before it (M_in, by a decoupled look-back over its predecessors'
+// chunk maxima), so every token's p = LUT(m_t - s_t) and every rescale event
+// (s_t > m_{t-1}, factor f = LUT(s_t - m_{t-1})) are known locally; between two
+// events the terms floor(v_norm * p * c_v[code] / 2^23) only add, so the chunk
+// hands over per query head one int32 sum per run and the factor opening it, and
+//     acc = floor(acc * f / 2^15) + S,   l = floor(l * f / 2^15) + L
+// replayed over the runs in order is the reference recurrence whenever the
+// per-token int32 clamp never fires. That is certified per run from the exact acc
+// where the run starts and B, the sum of its |term| bounds; a head that fails is
+// recomputed token by token (serial_head.h).
+//
+// What this kernel does differently, so that the chain of dependent steps inside a
+// workgroup stays short:
+//   - 16 waves, one token per thread, 4 waves per SIMD to hide the plane loads;
+//   - the group's rotated query rows are staged by the workgroup in global memory
+//     and read back by scalar loads, entering the fp64 score FMAs as scalar
+//     operands: the LDS then carries only the centroid reads;
+//   - candidates, p, the factors and each token's term for every value code are
+//     computed with lane = token for the 4 heads at once; the run sums are then
+//     walked by every wave over its own 64 tokens (lane = channel) and merged by
+//     LDS atomics into per-run accumulators (integer adds commute, and their
+//     wrapping sum is exact whenever the result fits);
+//   - a chunk publishes everything before it counts itself done, so the last
+//     workgroup of a sequence's KV head reads all headers in one batch, stages the
+//     runs' sums in LDS with all its waves, and walks them in blocks of 8.
+// A sequence of one chunk (context <= 1,024) never publishes, counts or replays.
+#include "query.h"
+#include "row_codec.h"
+#include "serial_head.h"
+#include "wave.h"
+
+#ifdef INSITU_STEP_STAMPS
+// Phase stamps (s_memrealtime) of every wave, for timing studies only, in a build
+// that defines INSITU_STEP_STAMPS: [workgroup][wave][stamp], read back by the host.
+__device__ unsigned long long insitu_step_stamps[8192 * 16 * 16];
+extern "C" int insitu_step_stamps_read(unsigned long long *host, long n) {
+    return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(insitu_step_stamps), (size_t)n * 8, 0, hipMemcpyDeviceToHost);
+}
+extern "C" int insitu_step_stamps_clear() {
+    void *p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(insitu_step_stamps)) != hipSuccess) return 1;
+    return (int)hipMemset(p, 0, sizeof(unsigned long long) * 8192 * 16 * 16);
+}
+#define STAMP(k)                                                                                \
+    do {                                                                                        \
+        const unsigned long long _t = __builtin_amdgcn_s_memrealtime();                         \
+        if ((threadIdx.x & 63) == 0 && blockIdx.x < 8192)                                       \
+            insitu_step_stamps[((size_t)blockIdx.x * 16 + (threadIdx.x >> 6)) * 16 + (k)] = _t; \
+    } while (0)
+#else
+#define STAMP(k) \
+    do {         \
+    } while (0)
+#endif
+
+namespace insitu {
+namespace stepk {
+
+constexpr int NT = 1024;          // threads per workgroup: 16 waves, 4 per SIMD
+constexpr int NW = NT / 64;
+constexpr int CHUNK = NT;         // tokens per workgroup, one per thread
+constexpr int D = 64;
+constexpr int G = GF;             // query heads per KV head
+constexpr int RMAX = 32;          // runs per head a chunk sums in LDS
+constexpr int SLOTS = 16;         // runs per head a chunk after chunk 0 publishes
+constexpr int HMAX = 512;         // chunks per sequence
+constexpr int NSEG = 2048;        // runs per head the replay lists
+constexpr uint16_t RUN_EVENT = 0x8000;
+static_assert(1 + (HMAX - 1) * SLOTS + 1 < RUN_EVENT, "run slots fit 15 bits");
+// Per-head flags in a chunk header: the head is recomputed serially.
+constexpr int FL_POOL = 1;        // more runs than the chunk can hold
+constexpr int FL_LB = 2;          // a look-back gave up waiting
+constexpr int FL_Q = 4;           // the query rows fail the fp64 exactness bound
+constexpr int FL_CERT = 8;        // chunk 0's own clamp certificate failed
+// Look-back words: flag (bits 62-63) | call epoch (bits 48-61) | score - SCORE_LO.
+constexpr unsigned long long ST_AGG = 1ull << 62, ST_INC = 2ull << 62, ST_FLAGS = 3ull << 62;
+constexpr unsigned EPOCH_MASK = (1u << 14) - 1u;
+constexpr double MAGIC = 6755399441055744.0;   // 1.5 * 2^52
+constexpr int64_t MAGIC_BITS = 0x4338000000000000LL;
+
+__device__ __forceinline__ void pub64(void *p, uint64_t v) {
+    __hip_atomic_store((uint64_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void pub32(void *p, uint32_t v) {
+    __hip_atomic_store((uint32_t *)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t get64(const void *p) {
+    return __hip_atomic_load((uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t get32(const void *p) {
+    return __hip_atomic_load((uint32_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until this thread's stores (the relaxed atomics above, and plain stores) have completed.
+__device__ __forceinline__ void stores_done() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0x0F70);          // vmcnt(0)
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+__device__ __forceinline__ unsigned long long st_pack(unsigned long long flag, unsigned ep, int64_t v) {
+    return flag | (unsigned long long)ep << 48 | (unsigned long long)(v - SCORE_LO);
+}
+__device__ __forceinline__ unsigned long long st_flag(unsigned long long w, unsigned ep) {
+    return ((unsigned)(w >> 48) & EPOCH_MASK) == ep ? w & ST_FLAGS : 0ull;
+}
+__device__ __forceinline__ int64_t st_val(unsigned long long w) {
+    return (int64_t)(w & ((1ull << 48) - 1)) + SCORE_LO;
+}
+__device__ __forceinline__ int64_t dbl_to_i64(double x) {
+    // x is an integer with |x| <= 2^51: adding 1.5 * 2^52 puts it in the low mantissa bits.
+    return (int64_t)__double_as_longlong(x + MAGIC) - MAGIC_BITS;
+}
+// |acc| + B <= 2^31 - 1: no prefix sum of a run whose |terms| sum to at most B can
+// take acc out of int32 (B >= 0).
+__device__ __forceinline__ bool fits(int32_t acc, int64_t bound) {
+    const int64_t a = acc < 0 ? -(int64_t)acc : (int64_t)acc;
+    return a + bound <= ACC_HI;
+}
+struct OpOr64 {
+    __device__ static int64_t f(int64_t a, int64_t b) { return a | b; }
+};
+__device__ __forceinline__ int slot_base(int chunk) { return chunk == 0 ? 0 : 1 + (chunk - 1) * SLOTS; }
+
+// Chunk scratch: look-back words, headers and counters first (the epoch-checked front,
+// zeroed when a launch lays the buffer out differently), then the runs and the query staging.
+struct Sck {
+    unsigned long long *status;   // [chain][G][2][mc]: inclusive, aggregate
+    uint64_t *hdr;                // [chain][mc][G][2]: w0, w1
+    unsigned int *done;           // [chain]: chunks done with their runs
+    uint64_t *meta;               // [chain][G][pool][2]: L | f << 32, B
+    int32_t *segS;                // [chain][G][pool][D]
+    double *qst;                  // [workgroup][D][G]: the rotated query rows, fp64
+    int32_t mc, pool;
+    uint32_t ep;                  // this call's epoch, 1 .. 2^14 - 1
+    int32_t spin_limit;
+};
+
+template <int KB, int VB>
+struct StepLds {
+    static constexpr int NV = 1 << VB;
+    static constexpr int VWORDS = D * VB / 32;
+    static constexpr int RS = (D * KB / 8 + D * VB / 8 + 4 + 3) / 4 * 4;
+    // the small tables first: their reads then take the LDS address from an immediate offset
+    double kcf[16];
+    int32_t vc32[8];
+    int32_t expt[256];
+    union {
+        struct {
+            int4 tt[CHUNK][NV];             // each token's term for every value code, the 4 heads
+            uint32_t vw[CHUNK][VWORDS];     // each token's value codes
+        } ph;
+        struct {
+            uint16_t rl[G][NSEG];           // the runs of chunks 1.. in order: slot | RUN_EVENT
+            uint64_t rlf[G][RMAX], rbb[G][RMAX];
+        } rp;
+        SerialLds<RS> fb[G];
+    } u;
+    int32_t runS[G][RMAX][D];               // run sums; the replay's staged runs
+    unsigned long long runB[G][RMAX];
+    uint32_t runL[G][RMAX];
+    int32_t runf[G][RMAX];
+    int32_t qi[G][D];                       // the rotated query rows, for the serial path
+    uint8_t codes[2][MAX_D];                // the new token's key and value codes
+    uint32_t nk[D * 4 / 32 + 1], nv[D * 2 / 32 + 1], nn;   // the new row: key words, value words, norms
+    int64_t wmax[NW][G];
+    int64_t wt[G][NW];
+    int32_t evc[G][NW];
+    int64_t min_[G], lmax[G];
+    int32_t total[G];
+    int qbad[G];
+    int lbfail, last;
+    uint64_t qaddr;                         // the query staging's address, handed over the barrier
+    unsigned long long ovf, mabs;
+    unsigned long long sev, samax;          // the chain's merged statistics (replay)
+    int32_t sdone;
+};
+
+template <int KB, int VB>
+__global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__restrict__ tabs, int32_t *out,
+                                                     const int64_t *__restrict__ len, Sck ck, DevStats *st,
+                                                     StepIn si) {
+    using L = StepLds<KB, VB>;
+    constexpr int NV = 1 << VB, NK = 1 << KB;
+    constexpr int KWORDS = D * KB / 32, VWORDS = D * VB / 32;
+    constexpr int KBYTES = D * KB / 8;
+    constexpr int NFULL = KBYTES / 16, HALF = (KBYTES % 16) / 8;
+    constexpr int KPL = NFULL + HALF;         // key planes; the value plane follows, then the norms
+    static_assert(VB == 1 || VB == 2, "one value plane of 8 or 16 bytes");
+    static_assert(32 % KB == 0 && 32 % VB == 0, "the new row's codes never straddle a word");
+    static_assert(KWORDS <= D * 4 / 32 && VWORDS <= D * 2 / 32, "new-row staging sizes");
+    __shared__ L S;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n_chains = g.batch * g.n_kv;
+    // chunk-major: every predecessor of a chunk has a smaller workgroup number
+    const int chunk = (int)(blockIdx.x / (unsigned)n_chains);
+    const int chain = (int)(blockIdx.x % (unsigned)n_chains);
+    const int b = chain / g.n_kv, kvh = chain % g.n_kv;
+    const int64_t T = len[b] + 1;
+    const int nch = (int)((T + CHUNK - 1) / CHUNK);
+    if (chunk >= nch) return;
+    STAMP(0);
+    const bool newrow = chunk == nch - 1;     // this chunk holds the step's new token
+    const int64_t t0 = (int64_t)chunk * CHUNK;
+    const int tln = (int)(T - 1 - t0);
+    const bool live = t0 + tid < T;
+    const bool fresh = newrow && tid == tln;
+    const bool own = chunk == 0;
+    if (own && kvh == 0 && tid == 0) si.len_out[b] = T;
+    const int score_shift = CENT_FRAC + g.norm_frac;
+    const int acc_shift = CENT_FRAC + g.norm_frac + PROB_FRAC - ACC_FRAC;
+    const uint8_t *hb = plane_ptr(g, b, kvh, 0);
+
+    // -- P0: loads, rotations, the new row ---------------------------------------
+    // The small loads first (wire rows, tables), then the chunk's planes: the vector
+    // memory counter drains in order, so the rotations wait only for their rows.
+    int32_t xv = 0;
+    if (wv < G)
+        xv = si.qw[((int64_t)b * g.n_q + kvh * G + wv) * D + lane];
+    else if (newrow && wv < G + 2)
+        xv = (wv == G ? si.kw : si.vw)[((int64_t)b * g.n_kv + kvh) * D + lane];
+    // the new token's encoder: lane i < 2^bits - 1 of wave G (keys) and G + 1 (values) holds
+    // boundary i (quantize.py:183-196)
+    int64_t bl = 0;
+    if (newrow && wv == G && lane < NK - 1)
+        bl = tabs->kbnd[lane];
+    else if (newrow && wv == G + 1 && lane < NV - 1)
+        bl = tabs->vbnd[lane];
+    int64_t tab = 0;
+    int32_t ex = 0;
+    if (tid < NK)
+        tab = tabs->kc[tid];
+    else if (tid >= 64 && tid < 64 + NV)
+        tab = tabs->vc[tid - 64];
+    if (tid >= 384 && tid < 384 + 256) ex = tabs->exp_table[tid - 384];
+    uint32_t kw[KWORDS + 1];
+    uint32_t vwd[VWORDS];
+    uint32_t nw = 0;
+#pragma unroll
+    for (int i = 0; i <= KWORDS; ++i) kw[i] = 0;
+#pragma unroll
+    for (int i = 0; i < VWORDS; ++i) vwd[i] = 0;
+    if (live && !fresh) {
+        const int64_t t = t0 + tid;
+#pragma unroll
+        for (int p = 0; p < NFULL; ++p) {
+            const uint4 v = *(const uint4 *)(hb + p * g.span + t * 16);
+            kw[4 * p] = v.x;
+            kw[4 * p + 1] = v.y;
+            kw[4 * p + 2] = v.z;
+            kw[4 * p + 3] = v.w;
+        }
+        if (HALF) {
+            const uint2 v = *(const uint2 *)(hb + NFULL * g.span + t * 8);
+            kw[4 * NFULL] = v.x;
+            kw[4 * NFULL + 1] = v.y;
+        }
+        if (VB == 2) {
+            const uint4 v = *(const uint4 *)(hb + KPL * g.span + t * 16);
+            vwd[0] = v.x;
+            vwd[1] = v.y;
+            vwd[2 % VWORDS] = v.z;
+            vwd[3 % VWORDS] = v.w;
+        } else {
+            const uint2 v = *(const uint2 *)(hb + KPL * g.span + t * 8);
+            vwd[0] = v.x;
+            vwd[1 % VWORDS] = v.y;
+        }
+        nw = *(const uint32_t *)(hb + (KPL + 1) * g.span + t * 4);
+    }
+    // zero the run accumulators (LDS atomics add into them)
+    for (int i = tid; i < G * RMAX * D; i += NT) (&S.runS[0][0][0])[i] = 0;
+    if (tid < G * RMAX) {
+        (&S.runB[0][0])[tid] = 0;
+        (&S.runL[0][0])[tid] = 0;
+        (&S.runf[0][0])[tid] = 0;
+    }
+    if (tid == 0) {
+        S.ovf = S.mabs = 0;
+        S.lbfail = 0;
+        S.sev = S.samax = 0;
+        S.sdone = 0;
+    }
+    if (tid < NK) S.kcf[tid] = (double)tab;
+    if (tid >= 64 && tid < 64 + NV) S.vc32[tid - 64] = (int32_t)tab;   // |centroid| < 2^18 (Q1.15)
+    if (tid >= 384 && tid < 384 + 256) S.expt[tid - 384] = ex;
+    double *qst = ck.qst + (size_t)blockIdx.x * (D * G);
+    if (wv < G) {
+        // Chunk 0 counts the queries' range errors, once per call: values beyond int32
+        // after the rotation, and rotated values beyond the 24-bit seam's +-2^27.
+        int32_t r[1];
+        const int32_t in[1] = {xv};
+        rotate_loaded<1>(in, D, si.rounds, si.sg, r, own ? &st->range_errors : nullptr);
+        S.qi[wv][lane] = r[0];
+        // The staging [head][channel]: this wave's 512 bytes are its own, so that it can warm
+        // the scalar cache with them as soon as its stores are done. Scores stay exact fp64
+        // integers when ||q||_1 * max|c| < 2^51 (attention.py:333-359 computes them in int64);
+        // rotated values beyond the 24-bit seam's +-2^27 count as range errors.
+        const int64_t xq = r[0];
+        qst[wv * D + lane] = (double)xq;
+        const int64_t aq = xq < 0 ? -xq : xq;
+        const int64_t l1 = wave_sum_i64(aq);                 // < 2^38: exact as a double below
+        const int64_t bad = wave_sum_i64(aq >= Q_ROT_LIMIT ? 1 : 0);
+        if (own && lane == 0 && bad) atomicAdd(&st->range_errors, (unsigned long long)bad);
+        const bool okh = (double)l1 * tabs->kc_absmax < DOT_LIMIT;
+        if (lane == 0) S.qbad[wv] = okh ? 0 : 1;
+        if (wv == 0 && lane == 0) S.qaddr = (uint64_t)(uintptr_t)qst;
+        stores_done();             // the staging is in L2 before the barrier: the score reads it by scalar loads
+        // Warm the scalar cache with this wave's staging (written by this wave alone, and
+        // complete): its 512 bytes, one load per 64-byte line, all in flight together, so that
+        // the score loop's scalar loads hit.
+        {
+            uint64_t d0, d1, d2, d3, d4, d5, d6, d7;
+            asm volatile(
+                "s_load_dwordx2 %0, %8, 0x0\n\t"
+                "s_load_dwordx2 %1, %8, 0x40\n\t"
+                "s_load_dwordx2 %2, %8, 0x80\n\t"
+                "s_load_dwordx2 %3, %8, 0xc0\n\t"
+                "s_load_dwordx2 %4, %8, 0x100\n\t"
+                "s_load_dwordx2 %5, %8, 0x140\n\t"
+                "s_load_dwordx2 %6, %8, 0x180\n\t"
+                "s_load_dwordx2 %7, %8, 0x1c0\n\t"
+                "s_waitcnt lgkmcnt(0)"
+                : "=&s"(d0), "=&s"(d1), "=&s"(d2), "=&s"(d3), "=&s"(d4), "=&s"(d5), "=&s"(d6), "=&s"(d7)
+                : "s"(qst + 64 * wv)
+                : "memory");
+        }
+    } else if (newrow && wv < G + 2) {
+        // the new token: rotate, norm, codes (quantize.py:164-212), pack (:237-252), store
+        const int f = wv - G;      // 0: key, 1: value
+        int32_t r[1];
+        const int32_t in[1] = {xv};
+        rotate_loaded<1>(in, D, si.rounds, si.sg, r, &st->range_errors);
+        const int64_t x[1] = {r[0]};
+        const int64_t n = norm_wire<1>(x, D, g.norm_frac);
+        // code = #{i : (x << 8) > norm * b_i}, the products norm * b_i broadcast from their lanes
+        const int64_t xs = x[0] << (CENT_FRAC + g.norm_frac - QK_FRAC);
+        const int64_t thr = n * bl;
+        const int nb = f == 0 ? NK - 1 : NV - 1;
+        int code = 0;
+#pragma unroll
+        for (int i = 0; i < NK - 1; ++i)
+            if (i < nb) code += xs > readlane64(thr, i) ? 1 : 0;
+        // Pack: a word holds 32 / bits consecutive codes, LSB first (quantize.py:271-289): each
+        // lane shifts its code into place, an OR over its group of lanes (lane xor 1, 2, ...)
+        // gives the word in every lane of the group, and the group's first lane stores it.
+        const int bits = f == 0 ? KB : VB;
+        const int per = 32 / bits;                                  // codes per word
+        uint32_t wword = (uint32_t)code << (bits * (lane & (per - 1)));
+        wword |= xor_lane32<1>(wword, lane);
+        wword |= xor_lane32<2>(wword, lane);
+        if (per > 4) wword |= xor_lane32<4>(wword, lane);
+        if (per > 8) wword |= xor_lane32<8>(wword, lane);
+        if (per > 16) wword |= xor_lane32<16>(wword, lane);
+        const int wi = lane / per;                                  // the word of the field
+        uint8_t *const rowb = plane_ptr(g, b, kvh, 0);            // writable
+        uint16_t *nword = (uint16_t *)(rowb + (KPL + 1) * g.span + (T - 1) * 4);
+        if ((lane & (per - 1)) == 0) {
+            if (f == 0) {
+                // key word wi: plane wi / 4, word wi % 4 of the token's 16 bytes (8 in a half plane)
+                const int pw = wi / 4 < NFULL ? 16 : 8;
+                pub32(rowb + (wi / 4) * g.span + (T - 1) * pw + 4 * (wi % 4), wword);
+                S.nk[wi] = wword;
+            } else {
+                pub32(rowb + KPL * g.span + (T - 1) * (VWORDS * 4) + 4 * wi, wword);
+                S.nv[wi] = wword;
+            }
+        }
+        if (lane == 0) {
+            __hip_atomic_store(nword + f, (uint16_t)(n & 0xFFFF), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ((uint16_t *)&S.nn)[f] = (uint16_t)(n & 0xFFFF);
+        }
+    }
+    STAMP(1);
+    __syncthreads();                                               // B1
+    STAMP(2);
+    const bool ok = !(S.qbad[0] | S.qbad[1] | S.qbad[2] | S.qbad[3]);
+    if (fresh) {
+#pragma unroll
+        for (int i = 0; i < KWORDS; ++i) kw[i] = S.nk[i];
+#pragma unroll
+        for (int i = 0; i < VWORDS; ++i) vwd[i] = S.nv[i];
+        nw = S.nn;
+    }
+
+    // -- P1: scores (attention.py:333-359), lane = token, the 4 heads at once ------
+    // sum_ch q[ch] * c[code_ch] in fp64 FMA is exact: every partial sum is an integer
+    // below 2^51 (the query check). Then the int64 norm multiply, >> 24, clamp to 48 bits.
+    int64_t s[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) s[h] = SCORE_LO;
+    unsigned long long ovf = 0;
+    int64_t mabs = 0;
+    if (ok && t0 + 64 * wv < T) {
+        double acc[G];
+#pragma unroll
+        for (int h = 0; h < G; ++h) acc[h] = 0.0;
+        // Two channels a step, software-pipelined by hand: wait for this step's centroids
+        // (LDS) and query values (scalar loads), request the next step's, then this step's
+        // FMAs, which hide the latency. The loads are issued from inline asm, so that the
+        // compiler neither hoists them (the query staging is read-only to it) nor inserts a
+        // wait of its own (scalar and LDS loads share one counter and scalar loads return
+        // out of order, so any wait of its own would be a wait for everything); the asm that
+        // requests the next step also takes the accumulators, so the FMAs follow it.
+        auto caddr = [&](int ch) __attribute__((always_inline)) {
+            const int bo = KB * ch, wi = bo >> 5, sh = bo & 31;
+            const uint32_t win = sh == 0 ? kw[wi] : __builtin_amdgcn_alignbit(kw[wi + 1], kw[wi], sh);
+            return (uint32_t)(uintptr_t)&S.kcf[win & (NK - 1)];
+        };
+        const uint64_t qa = (uint64_t)uni64((int64_t)S.qaddr);
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        double c0, c1;
+        u32x4 q0, q1, q2, q3;              // head h: the step's two channels' fp64 values
+        asm volatile("ds_read_b64 %0, %1" : "=v"(c0) : "v"(caddr(0)));
+        asm volatile("ds_read_b64 %0, %1" : "=v"(c1) : "v"(caddr(1)));
+        asm volatile(
+            "s_load_dwordx4 %0, %4, 0x0\n\t"
+            "s_load_dwordx4 %1, %4, 0x200\n\t"
+            "s_load_dwordx4 %2, %4, 0x400\n\t"
+            "s_load_dwordx4 %3, %4, 0x600"
+            : "=s"(q0), "=s"(q1), "=s"(q2), "=s"(q3)
+            : "s"(qa));
+#pragma unroll
+        for (int st2 = 0; st2 < D / 2; ++st2) {
+            asm volatile("s_waitcnt lgkmcnt(0)"
+                         : "+v"(c0), "+v"(c1), "+s"(q0), "+s"(q1), "+s"(q2), "+s"(q3), "+v"(acc[0]),
+                           "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
+            double n0 = 0.0, n1 = 0.0;
+            u32x4 m0 = q0, m1 = q1, m2 = q2, m3 = q3;
+            if (st2 + 1 < D / 2) {
+                asm volatile("ds_read_b64 %0, %1" : "=v"(n0) : "v"(caddr(2 * st2 + 2)));
+                asm volatile("ds_read_b64 %0, %1" : "=v"(n1) : "v"(caddr(2 * st2 + 3)));
+                asm volatile(
+                    "s_load_dwordx4 %0, %8, %9\n\t"
+                    "s_load_dwordx4 %1, %8, %10\n\t"
+                    "s_load_dwordx4 %2, %8, %11\n\t"
+                    "s_load_dwordx4 %3, %8, %12"
+                    : "=s"(m0), "=s"(m1), "=s"(m2), "=s"(m3), "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]),
+                      "+v"(acc[3])
+                    : "s"(qa), "i"(16 * (st2 + 1)), "i"(512 + 16 * (st2 + 1)), "i"(1024 + 16 * (st2 + 1)),
+                      "i"(1536 + 16 * (st2 + 1)));
+            }
+            const u32x4 qh[G] = {q0, q1, q2, q3};
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                const double qa0 = __builtin_bit_cast(double, (uint64_t)qh[h][0] | ((uint64_t)qh[h][1] << 32));
+                const double qa1 = __builtin_bit_cast(double, (uint64_t)qh[h][2] | ((uint64_t)qh[h][3] << 32));
+                acc[h] = fma(qa0, c0, acc[h]);
+                acc[h] = fma(qa1, c1, acc[h]);
+            }
+            c0 = n0;
+            c1 = n1;
+            q0 = m0;
+            q1 = m1;
+            q2 = m2;
+            q3 = m3;
+        }
+        if (live) {
+            const int64_t kn = sext16(nw);
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                int64_t v = wmul(dbl_to_i64(acc[h]), kn) >> score_shift;
+                if (v < SCORE_LO || v > SCORE_HI) {
+                    ++ovf;
+                    v = v < SCORE_LO ? SCORE_LO : SCORE_HI;
+                }
+                const int64_t a = v < 0 ? -v : v;
+                mabs = a > mabs ? a : mabs;
+                s[h] = v;
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < VWORDS; ++i) S.u.ph.vw[tid][i] = vwd[i];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        const int64_t m = wave_max_i64(s[h]);
+        if (lane == 0) S.wmax[wv][h] = m;
+    }
+    if (ok) {
+        ovf = (unsigned long long)wave_sum_i64((int64_t)ovf);
+        mabs = wave_max_i64(mabs);
+        if (lane == 0) {
+            if (ovf) atomicAdd(&S.ovf, ovf);
+            if (mabs) atomicMax(&S.mabs, (unsigned long long)mabs);
+        }
+    }
+    STAMP(3);
+    __syncthreads();                                               // B2
+    STAMP(4);
+
+    // -- P2: the maximum before this chunk, by look-back --------------------------
+    // Two words per (chunk, head): the inclusive maximum and this chunk's own
+    // (aggregate). Wave G + h publishes head h's aggregate (chunk 0: its inclusive
+    // maximum) while wave h looks back, so that the polling wave has no store in
+    // flight. A sequence of one chunk needs neither. The query check fails alike in
+    // every chunk of a sequence, and then nothing is scored or waited for.
+    if (ok && wv < 2 * G) {
+        const int h = wv & (G - 1);
+        int64_t local = S.wmax[0][h];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) local = S.wmax[w][h] > local ? S.wmax[w][h] : local;
+        int64_t run = SCORE_LO;
+        if (nch > 1) {
+            unsigned long long *wi0 = ck.status + ((int64_t)chain * G + h) * 2 * ck.mc;
+            unsigned long long *wa0 = wi0 + ck.mc;
+            if (wv >= G) {
+                if (lane == 0)
+                    __hip_atomic_store((own ? wi0 : wa0) + chunk, st_pack(own ? ST_INC : ST_AGG, ck.ep, local),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            } else if (!own) {
+                int64_t base = chunk - 1;       // the predecessor lane 0 reads
+                int spins = 0;
+                bool fail = ck.spin_limit == 0;
+                while (!fail) {
+                    const int64_t pc = base - lane;
+                    unsigned long long flag = ST_INC;
+                    int64_t val = SCORE_LO;
+                    if (pc >= 0) {
+                        const unsigned long long w1 = __hip_atomic_load(wi0 + pc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        const unsigned long long w2 = __hip_atomic_load(wa0 + pc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        const bool has_inc = st_flag(w1, ck.ep) == ST_INC;
+                        flag = has_inc ? ST_INC : st_flag(w2, ck.ep);
+                        val = st_val(has_inc ? w1 : w2);
+                    }
+                    const unsigned long long inc = __ballot(flag == ST_INC);
+                    const int nearest = inc ? __ffsll((long long)inc) - 1 : 64;
+                    const unsigned long long wait = __ballot(flag == 0 && lane <= nearest);
+                    if (wait) {
+                        if (++spins > ck.spin_limit) {
+                            fail = true;
+                            break;
+                        }
+                        __builtin_amdgcn_s_sleep(2);
+                        continue;
+                    }
+                    const int64_t v = wave_max_i64(lane <= nearest ? val : SCORE_LO);
+                    run = v > run ? v : run;
+                    if (nearest < 64) break;
+                    base -= 64;
+                }
+                const int64_t incl = run > local ? run : local;
+                if (lane == 0)
+                    __hip_atomic_store(wi0 + chunk, st_pack(ST_INC, ck.ep, incl), __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                if (fail && lane == 0) S.lbfail = 1;
+            }
+        }
+        if (wv < G && lane == 0) {
+            S.min_[h] = run;
+            S.lmax[h] = local;
+        }
+    }
+    __syncthreads();                                               // B3
+    STAMP(5);
+    const bool lbfail = S.lbfail != 0;
+    const bool work = ok && !lbfail;
+
+    // -- P3: events, p, factors and terms, lane = token --------------------------
+    // A head whose chunk maximum does not exceed M_in has no event here, and then
+    // every token's running maximum is M_in. Otherwise the running maximum comes from
+    // a block-wide prefix-max scan. A token at or below m - delta_max has p = 0; the
+    // others are candidates, and only waves that hold one do the rest: each
+    // candidate's terms floor(v_norm * p * c_v[c] / 2^23) for every value code c go to
+    // LDS; run r of a head is the tokens from its r-th event of the chunk on (run 0:
+    // before the first), and its L = sum p, its bound B = sum ((|w| * max|c_v|) >> 23) + 1
+    // over w = v_norm * p != 0, and its opening factor go to the run accumulators.
+    uint64_t evb[G], cb[G];
+    uint64_t candb = 0;
+    int rb[G];
+    int nruns[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        evb[h] = cb[h] = 0;
+        rb[h] = 0;
+        nruns[h] = 1;
+    }
+    if (work) {
+        const int64_t dm = tabs->delta_max;
+        int64_t Min[G], incl[G];
+        bool evh[G];
+        bool any_ev = false;
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            Min[h] = S.min_[h];
+            evh[h] = S.lmax[h] > Min[h];
+            any_ev = any_ev || evh[h];
+            incl[h] = SCORE_LO;
+            if (evh[h]) {
+                incl[h] = wave_scan64<OpMax64>(s[h], SCORE_LO);
+                if (lane == 63) S.wt[h][wv] = incl[h];
+            }
+        }
+        if (any_ev) __syncthreads();                               // B4 (uniform)
+        STAMP(11);
+        int64_t pm[G], dd[G];
+        bool ev[G], cand[G];
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            pm[h] = Min[h];
+            if (evh[h]) {
+#pragma unroll
+                for (int w = 0; w < NW - 1; ++w) {
+                    const int64_t m = S.wt[h][w];
+                    pm[h] = w < wv && m > pm[h] ? m : pm[h];
+                }
+                const int64_t ex1 = wave_shr1_64(incl[h], SCORE_LO);
+                pm[h] = ex1 > pm[h] ? ex1 : pm[h];
+            }
+            ev[h] = evh[h] && live && s[h] > pm[h];
+            dd[h] = (ev[h] ? s[h] : pm[h]) - s[h];                   // m - s >= 0; 0 at an event
+            cand[h] = live && dd[h] < dm;
+            evb[h] = __ballot(ev[h]);
+            cb[h] = __ballot(cand[h]);
+            candb |= cb[h];
+        }
+        int32_t pv[G], fv[G], bw[G];
+#pragma unroll
+        for (int h = 0; h < G; ++h) pv[h] = fv[h] = bw[h] = 0;
+        if (candb) {
+            const int32_t vn = (int32_t)(int16_t)(nw >> 16);
+            int64_t vcmax = 0;
+#pragma unroll
+            for (int c = 0; c < NV; ++c) {
+                const int64_t a = S.vc32[c] < 0 ? -(int64_t)S.vc32[c] : (int64_t)S.vc32[c];
+                vcmax = a > vcmax ? a : vcmax;
+            }
+            int32_t tv[NV][G];
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+#pragma unroll
+                for (int c = 0; c < NV; ++c) tv[c][h] = 0;
+                if (!cb[h]) continue;
+                const int32_t p = cand[h] ? exp_lut(dd[h], S.expt, dm) : 0;   // LUT(0) = 2^15 at an event
+                const int32_t w = vn * p;                                  // |w| <= 2^30
+                const uint32_t aw = (uint32_t)(w < 0 ? -w : w);
+                pv[h] = p;
+                // |w| * max|c_v| < 2^48; the bound of one term fits 32 bits
+                bw[h] = w != 0 ? (int32_t)(((uint64_t)aw * (uint64_t)vcmax) >> acc_shift) + 1 : 0;
+#pragma unroll
+                for (int c = 0; c < NV; ++c) tv[c][h] = (int32_t)(((int64_t)w * S.vc32[c]) >> acc_shift);
+                if (evb[h]) fv[h] = ev[h] ? exp_lut(s[h] - pm[h], S.expt, dm) : 0;
+            }
+            if ((candb >> lane) & 1ull) {
+#pragma unroll
+                for (int c = 0; c < NV; ++c) S.u.ph.tt[tid][c] = make_int4(tv[c][0], tv[c][1], tv[c][2], tv[c][3]);
+            }
+        }
+        STAMP(12);
+        if (any_ev) {
+            if (lane == 0) {
+#pragma unroll
+                for (int h = 0; h < G; ++h) S.evc[h][wv] = (int32_t)__popcll(evb[h]);
+            }
+            __syncthreads();                                       // B5 (uniform)
+            STAMP(13);
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                if (!evh[h]) continue;
+                int before = 0, all = 0;
+#pragma unroll
+                for (int w = 0; w < NW; ++w) {
+                    const int c = S.evc[h][w];
+                    before += w < wv ? c : 0;
+                    all += c;
+                }
+                rb[h] = before;
+                nruns[h] = 1 + all;
+            }
+        }
+        // Per-run L and B: the wave's tokens lie in run rb[h] up to its first event, then in
+        // one run per event. Lane prefix sums (p <= 2^15 and a term bound < 2^25, so 64 of
+        // them fit 32 bits) give every segment's sums: the segment's last lane adds its
+        // inclusive sum less the one before the segment's first lane into its run.
+        const uint64_t le = lane == 63 ? ~0ull : (2ull << lane) - 1ull;       // lanes 0 .. lane
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            if (!cb[h]) continue;
+            const uint32_t sl = wave_scan_add32((uint32_t)pv[h]);
+            const uint32_t sb = wave_scan_add32((uint32_t)bw[h]);
+            const uint64_t mine = evb[h] & le;                     // events at or before this lane
+            const int ri = rb[h] + (int)__popcll(mine);           // this lane's run
+            const int first = mine ? 63 - __clzll((long long)mine) : 0;   // the first lane of its segment
+            const bool last = lane == 63 || ((evb[h] >> (lane + 1)) & 1ull);
+            const uint32_t pl = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (first - 1), (int)sl);
+            const uint32_t pb = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (first - 1), (int)sb);
+            const uint32_t L = sl - (first ? pl : 0u), B = sb - (first ? pb : 0u);
+            if (last && ri < RMAX && (L || B)) {
+                atomicAdd(&S.runL[h][ri], L);
+                atomicAdd(&S.runB[h][ri], (unsigned long long)B);
+            }
+            if (((evb[h] >> lane) & 1ull) && ri < RMAX) S.runf[h][ri] = fv[h];   // the factor opening run ri
+        }
+    }
+    __syncthreads();                                               // B6
+    STAMP(6);
+
+    // -- P4: run sums, lane = channel ---------------------------------------------
+    // Every wave walks the candidates among its own 64 tokens in order, for the 4
+    // heads at once, 8 at a time: the tokens' value words and then the terms their
+    // codes of this lane's channel pick are read first, then added in order; an event
+    // of a head closes that head's open run, whose partial sum goes to its
+    // accumulator with an LDS atomic add.
+    if (work && candb) {
+        int32_t P[G];
+        int rr[G];
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            P[h] = 0;
+            rr[h] = rb[h];
+        }
+        const int wi = (lane * VB) >> 5, sh = (lane * VB) & 31;
+        const uint64_t anyev = evb[0] | evb[1] | evb[2] | evb[3];
+        const int tb = 64 * wv;
+        uint64_t cm = candb;
+        while (cm) {
+            int js[8];
+            uint64_t taken = 0;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int j = cm ? __builtin_ctzll(cm) : (k ? js[k - 1] : 0);
+                js[k] = j;
+                if (cm) {
+                    taken |= 1ull << j;
+                    cm &= cm - 1;
+                }
+            }
+            const int nt = __popcll(taken);
+            uint32_t wd[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) wd[k] = S.u.ph.vw[tb + js[k]][wi];
+            int4 t4[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                t4[k] = S.u.ph.tt[tb + js[k]][__builtin_amdgcn_ubfe(wd[k], (uint32_t)sh, (uint32_t)VB)];
+            if (!(anyev & taken)) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    if (k < nt) {
+                        P[0] += t4[k].x;
+                        P[1] += t4[k].y;
+                        P[2] += t4[k].z;
+                        P[3] += t4[k].w;
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    if (k < nt) {
+                        const int j = js[k];
+                        if ((anyev >> j) & 1ull) {
+#pragma unroll
+                            for (int h = 0; h < G; ++h) {
+                                if ((evb[h] >> j) & 1ull) {
+                                    if (rr[h] < RMAX) atomicAdd(&S.runS[h][rr[h]][lane], P[h]);
+                                    P[h] = 0;
+                                    ++rr[h];
+                                }
+                            }
+                        }
+                        P[0] += t4[k].x;
+                        P[1] += t4[k].y;
+                        P[2] += t4[k].z;
+                        P[3] += t4[k].w;
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int h = 0; h < G; ++h)
+            if (rr[h] < RMAX && P[h]) atomicAdd(&S.runS[h][rr[h]][lane], P[h]);
+    }
+    __syncthreads();                                               // B7
+    STAMP(7);
+
+    // -- P5: chunk 0 folds its runs; the others publish theirs ---------------------
+    int flags = (ok ? 0 : FL_Q) | (lbfail ? FL_LB : 0);
+    int32_t acc0 = 0;
+    int64_t l0 = 0;
+    int nev0 = 0;
+    const bool hw = wv < G;        // wave h < G: query head h, lane = channel
+    const int h = hw ? wv : 0;
+    if (hw && work) {
+        const int nr = nruns[h];
+        if (nr > RMAX || (!own && nr > SLOTS)) flags |= FL_POOL;
+        if (own && !(flags & FL_POOL)) {
+            // acc = floor(acc * f / 2^15) + S per run (run 0 has no rescale), certified
+            bool unsafe = false;
+            for (int r = 0; r < nr; ++r) {
+                if (r > 0) {
+                    const int64_t f = S.runf[h][r];
+                    acc0 = (int32_t)(((int64_t)acc0 * f) >> PROB_FRAC);
+                    l0 = (l0 * f) >> PROB_FRAC;
+                }
+                if (!fits(acc0, (int64_t)S.runB[h][r])) unsafe = true;
+                acc0 += S.runS[h][r][lane];
+                l0 += S.runL[h][r];
+            }
+            if (__ballot(unsafe)) flags |= FL_CERT;
+            nev0 = nr - 1;
+        }
+    }
+    bool last = nch == 1;
+    if (!last) {
+        if (hw) {
+            uint64_t *hp = ck.hdr + (((int64_t)chain * ck.mc + chunk) * G + h) * 2;
+            const int64_t hbase = ((int64_t)chain * G + h) * ck.pool;
+            int npub = 0;
+            if (own) {
+                pub32(&ck.segS[hbase * D + lane], (uint32_t)acc0);
+                if (lane == 0) pub64(&ck.meta[hbase * 2], (uint64_t)(uint32_t)l0 | ((uint64_t)(uint32_t)nev0 << 32));
+                npub = 1;
+            } else if (work && !(flags & FL_POOL)) {
+                const int nr = nruns[h];
+                const bool empty = nr == 1 && S.runL[h][0] == 0 && S.runB[h][0] == 0;
+                npub = empty ? 0 : nr;
+                for (int r = 0; r < npub; ++r) {
+                    const int64_t slot = hbase + slot_base(chunk) + r;
+                    pub32(&ck.segS[slot * D + lane], (uint32_t)S.runS[h][r][lane]);
+                    if (lane == 0) {
+                        pub64(&ck.meta[slot * 2], (uint64_t)S.runL[h][r] | ((uint64_t)(uint32_t)S.runf[h][r] << 32));
+                        pub64(&ck.meta[slot * 2 + 1], (uint64_t)S.runB[h][r]);
+                    }
+                }
+            }
+            if (lane == 0) {
+                pub64(hp + 1, ok ? S.mabs : 0ull);
+                pub64(hp, (uint64_t)(uint32_t)npub | ((uint64_t)(uint32_t)flags << 16) |
+                              ((uint64_t)(ok ? S.ovf & 0xFFFF : 0) << 24) | ((uint64_t)ck.ep << 40));
+            }
+            stores_done();
+        }
+        if (newrow && (wv == G || wv == G + 1)) stores_done();     // the new row, for a serial path elsewhere
+        __syncthreads();
+        if (tid == 0) {
+            const unsigned prior = __hip_atomic_fetch_add(&ck.done[chain], 1u, __ATOMIC_RELAXED,
+                                                          __HIP_MEMORY_SCOPE_AGENT);
+            S.last = prior == (unsigned)(nch - 1);
+        }
+        __syncthreads();
+        last = S.last != 0;
+    }
+    STAMP(8);
+    if (!last) return;
+
+    // -- P6: the last workgroup of the sequence's KV head replays ------------------
+    int32_t aw = acc0;
+    int64_t l = l0;
+    unsigned long long events = (unsigned long long)nev0;
+    int hflags = flags;            // this head's flags over every chunk
+    unsigned long long tovf = ok ? S.ovf : 0, tmabs = ok ? S.mabs : 0;
+    int total = 0;
+    if (nch > 1 && hw) {
+        const uint64_t *hdr = ck.hdr + ((int64_t)chain * ck.mc * G + h) * 2;    // chunk c: hdr[c * G * 2]
+        const int64_t hbase = ((int64_t)chain * G + h) * ck.pool;
+        const uint32_t ep = ck.ep;
+        if (!own) {
+            const uint64_t h0 = get64(&hdr[0]);
+            aw = (int32_t)get32(&ck.segS[hbase * D + lane]);
+            const uint64_t lf = get64(&ck.meta[hbase * 2]);
+            l = (int64_t)(uint32_t)lf;
+            events = lf >> 32;
+            hflags = (int)((h0 >> 16) & 0xFF);
+            if ((uint32_t)(h0 >> 40) != ep) {                      // cannot happen: it counted itself done
+                hflags |= FL_POOL;
+                atomicOr((unsigned long long *)&st->fault, 1ull);
+            }
+            tovf = (h0 >> 24) & 0xFFFF;
+            tmabs = get64(&hdr[1]);
+        }
+        // the runs of chunks 1 .. nch-1 in order, one header per lane and 64 chunks
+        uint16_t *rl = S.u.rp.rl[h];
+        for (int c0 = 1; c0 < nch; c0 += 64) {
+            const int c = c0 + lane;
+            const bool in = c < nch;
+            uint64_t w0 = 0, w1 = 0;
+            if (in) {
+                w0 = get64(&hdr[(int64_t)c * G * 2]);
+                w1 = get64(&hdr[(int64_t)c * G * 2 + 1]);
+            }
+            // A header is current (every chunk published before it counted itself done) and
+            // lists at most SLOTS runs; anything else would be an internal error, which sends
+            // the head to the serial path and raises the fault flag instead of reading past
+            // the run pool.
+            const bool cur = in && (uint32_t)(w0 >> 40) == ep && (int)(w0 & 0xFFFF) <= SLOTS;
+            const int n = cur ? (int)(w0 & 0xFFFF) : 0;
+            int fl = cur ? (int)((w0 >> 16) & 0xFF) : 0;
+            if (in && !cur) {
+                fl |= FL_POOL;
+                atomicOr((unsigned long long *)&st->fault, 1ull);
+            }
+            const int incl = (int)wave_scan_add32((uint32_t)n);
+            const int start = total + incl - n;
+            for (int j = 0; j < n && start + j < NSEG; ++j)
+                rl[start + j] = (uint16_t)((slot_base(c) + j) | (j ? RUN_EVENT : 0));
+            total += __builtin_amdgcn_readlane(incl, 63);
+            hflags |= (int)wave_reduce64<OpOr64>((int64_t)fl);
+            tovf += (unsigned long long)wave_sum_i64(in ? (int64_t)((w0 >> 24) & 0xFFFF) : 0);
+            const int64_t mm = wave_max_i64(in ? (int64_t)w1 : 0);
+            tmabs = (unsigned long long)mm > tmabs ? (unsigned long long)mm : tmabs;
+        }
+        STAMP(14);
+        if (total > NSEG) hflags |= FL_POOL;
+        if (lane == 0) S.total[h] = hflags ? 0 : total;
+    } else if (hw && lane == 0) {
+        S.total[h] = 0;
+    }
+    __syncthreads();
+    int tmax = 0;
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) tmax = S.total[hh] > tmax ? S.total[hh] : tmax;
+    const int tot_h = hw ? S.total[h] : 0;
+    bool unsafe = false;
+    for (int g0 = 0; g0 < tmax; g0 += RMAX) {
+        // Stage up to RMAX runs per head in LDS: wave w loads runs w / G, w / G + 4, ... of head
+        // w % G (lane = channel), every slot read, then every load, then every store.
+        {
+            constexpr int PER = RMAX / (NW / G);
+            const int hh = wv & (G - 1), part = wv / G;
+            const int th = S.total[hh];
+            const int64_t hbase = ((int64_t)chain * G + hh) * ck.pool;
+            int slot[PER];
+#pragma unroll
+            for (int k = 0; k < PER; ++k) {
+                const int i = g0 + part + (NW / G) * k;
+                slot[k] = i < th ? (S.u.rp.rl[hh][i] & (RUN_EVENT - 1)) : -1;
+            }
+            int32_t v[PER];
+#pragma unroll
+            for (int k = 0; k < PER; ++k) v[k] = slot[k] >= 0 ? (int32_t)get32(&ck.segS[(hbase + slot[k]) * D + lane]) : 0;
+#pragma unroll
+            for (int k = 0; k < PER; ++k)
+                if (slot[k] >= 0) S.runS[hh][part + (NW / G) * k][lane] = v[k];
+            if (wv < G) {
+                const int i = g0 + lane;
+                if (lane < RMAX && i < th) {
+                    const int sl = S.u.rp.rl[hh][i] & (RUN_EVENT - 1);
+                    const uint64_t lf = get64(&ck.meta[(hbase + sl) * 2]);
+                    const uint64_t bb = get64(&ck.meta[(hbase + sl) * 2 + 1]);
+                    S.u.rp.rlf[hh][lane] = lf;
+                    S.u.rp.rbb[hh][lane] = bb;
+                }
+            }
+        }
+        __syncthreads();
+        STAMP(15);
+        if (hw && g0 < tot_h) {
+            // The walk. Lane k < nb holds run k's list entry, L, f and bound B; prefix sums over
+            // the lanes give each block's sums. |acc| only shrinks at a rescale and grows by at
+            // most a run's B per run, so |acc at a block's start| + the block's B certifies 8
+            // event-free runs at once; elsewhere the walk goes run by run.
+            const int nb = tot_h - g0 < RMAX ? tot_h - g0 : RMAX;
+            const bool mine = lane < nb;
+            const uint32_t ent = mine ? (uint32_t)S.u.rp.rl[h][g0 + lane] : 0u;
+            const uint64_t lf = mine ? S.u.rp.rlf[h][lane] : 0ull;
+            const int64_t bb = mine ? (int64_t)S.u.rp.rbb[h][lane] : 0;
+            const uint64_t evm = __ballot(mine && (ent & RUN_EVENT));
+            const int64_t PB = wave_scan64<OpAdd64>(bb, 0);
+            const int64_t PL = wave_scan64<OpAdd64>((int64_t)(uint32_t)lf, 0);
+            for (int k0 = 0; k0 < nb; k0 += 8) {
+                const int kn = nb - k0 < 8 ? nb - k0 : 8;
+                const uint32_t bev = (uint32_t)(evm >> k0) & ((1u << kn) - 1u);
+                const int64_t before_b = k0 ? readlane64(PB, k0 - 1) : 0;
+                const int64_t before_l = k0 ? readlane64(PL, k0 - 1) : 0;
+                const int64_t bsum = readlane64(PB, k0 + kn - 1) - before_b;
+                const int64_t a = aw < 0 ? -(int64_t)aw : (int64_t)aw;
+                int32_t v[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) v[k] = k < kn ? S.runS[h][k0 + k][lane] : 0;
+                if (!bev && !__ballot(a + bsum > ACC_HI)) {
+                    aw += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+                    l += readlane64(PL, k0 + kn - 1) - before_l;
+                    continue;
+                }
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    if (k < kn) {
+                        if ((bev >> k) & 1u) {
+                            const int64_t f = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(lf >> 32), k0 + k);
+                            aw = (int32_t)(((int64_t)aw * f) >> PROB_FRAC);
+                            l = (l * f) >> PROB_FRAC;
+                            ++events;
+                        }
+                        if (!fits(aw, readlane64(bb, k0 + k))) unsafe = true;
+                        aw += v[k];
+                        l += (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)lf, k0 + k);
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    if (hw && __ballot(unsafe)) hflags |= FL_CERT;
+    STAMP(9);
+    __syncthreads();               // the replay's lists are dead: the serial path reuses the LDS
+    if (hw) {
+        const int qh = kvh * G + h;
+        int32_t *orow = out + ((int64_t)b * g.n_q + qh) * D;
+        if (hflags) {
+            // The serial path counts score statistics only when no chunk did (the query
+            // check failed). The new row came from another workgroup: acquire it.
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            serial_head<1, L::RS>(g, tabs, tabs->kc, tabs->vc, &S.qi[h][0], b, kvh, T, 0, !ok, S.u.fb[h], orow, st);
+            if (lane == 0) atomicAdd(&st->serial_fallbacks, 1ull);
+        } else {
+            const Recip rc = reciprocal(l);
+            const int64_t acc = aw;
+            orow[lane] = (int32_t)(wmul(acc, rc.r) >> rc.shift);
+            const int64_t amax = wave_max_i64(acc < 0 ? -acc : acc);
+            if (lane == 0) {
+                if (events) atomicAdd(&S.sev, events);
+                atomicMax(&S.samax, (unsigned long long)amax);
+                atomicOr((unsigned int *)&S.sdone, 2u);
+            }
+        }
+        if (h == 0 && lane == 0) {
+            S.ovf = tovf;
+            S.mabs = tmabs;
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        // the chain's statistics, once: the heads' merged, and the score statistics of
+        // every chunk (when the query check passed; the serial path counted them otherwise)
+        if (S.sdone & 2) {
+            atomicMax(&st->n_tokens, (unsigned long long)T);
+            if (S.sev) atomicAdd(&st->rescale_events, S.sev);
+            atomicMax(&st->max_abs_acc, S.samax);
+        }
+        if (ok) {
+            if (S.ovf) atomicAdd(&st->score_overflows, S.ovf);
+            atomicMax(&st->max_abs_score, S.mabs);
+        }
+        if (nch > 1) ck.done[chain] = 0;    // every workgroup of the chain has counted itself
+    }
+    STAMP(10);
+}
+
+static void carve(const Geom &g, int64_t mc, int64_t pool, uint8_t *p, Sck *ck, size_t *total, size_t *front) {
+    const int64_t chains = (int64_t)g.batch * g.n_kv;
+    size_t o = 0;
+    auto take = [&](size_t n) {
+        const size_t at = o;
+        o += (n + 255) / 256 * 256;
+        return p ? p + at : nullptr;
+    };
+    Sck c{};
+    c.status = (unsigned long long *)take(chains * G * 2 * mc * sizeof(unsigned long long));
+    c.hdr = (uint64_t *)take(chains * mc * G * 2 * sizeof(uint64_t));
+    c.done = (unsigned int *)take(chains * sizeof(unsigned int));
+    if (front) *front = o;
+    c.meta = (uint64_t *)take(chains * G * pool * 2 * sizeof(uint64_t));
+    c.segS = (int32_t *)take(chains * G * pool * D * sizeof(int32_t));
+    c.qst = (double *)take(chains * mc * D * G * sizeof(double));
+    c.mc = (int32_t)mc;
+    c.pool = (int32_t)pool;
+    if (ck) *ck = c;
+    if (total) *total = o;
+}
+
+}  // namespace stepk
+
+bool step_supported(const Geom &g, int64_t capacity) {
+    using namespace stepk;
+    const int kbytes = g.d * g.kb / 8;
+    const int kpl = kbytes / 16 + (kbytes % 16) / 8;
+    return g.d == D && g.G == G && g.kb == 4 && g.vb == 2 && g.n_planes == kpl + 2 &&
+           (capacity + CHUNK - 1) / CHUNK <= HMAX && g.norm_frac == 9;
+}
+
+int64_t step_max_chunks(int64_t capacity) { return (capacity + stepk::CHUNK - 1) / stepk::CHUNK; }
+
+static int64_t step_pool(int64_t mc) { return 1 + (mc - 1) * stepk::SLOTS + 1; }
+
+size_t step_scratch_bytes(const Geom &g, int64_t mc) {
+    size_t n = 0;
+    stepk::carve(g, mc, step_pool(mc), nullptr, nullptr, &n, nullptr);
+    return n;
+}
+
+hipError_t launch_step(hipStream_t s, const Geom &g, const Tables *t, int32_t *out, const int64_t *len,
+                       ChunkScratch &cs, uint32_t ep, int64_t mc, int64_t grid_chunks, const StepIn &si,
+                       LaunchEv ev, DevStats *st) {
+    using namespace stepk;
+    const int64_t chains = (int64_t)g.batch * g.n_kv;
+    if (mc > HMAX || chains > 65535 || mc * chains > 0x7fffffff) return hipErrorInvalidValue;
+    if (grid_chunks < 1 || grid_chunks > mc) grid_chunks = mc;
+    const int64_t pool = step_pool(mc);
+    Sck ck;
+    size_t bytes = 0, front = 0;
+    carve(g, mc, pool, (uint8_t *)cs.p, &ck, &bytes, &front);
+    if (bytes > cs.bytes || ep == 0 || ep > EPOCH_MASK) return hipErrorInvalidValue;
+    ck.ep = ep;
+    ck.spin_limit = cs.spin_limit;
+    const uint64_t layout = ((uint64_t)mc << 48) ^ ((uint64_t)pool << 24) ^ ((uint64_t)g.batch << 8) ^
+                            (uint64_t)g.n_kv ^ (1ull << 61);
+    {
+        const hipError_t e = scratch_layout(s, cs, layout, front);
+        if (e != hipSuccess) return e;
+    }
+    dim3 grid((unsigned)(grid_chunks * chains)), block(NT);
+    if (g.kb == 4 && g.vb == 2)
+        hipExtLaunchKernelGGL((step_kernel<4, 2>), grid, block, 0, s, ev.start, ev.stop, 0, g, t, out, len, ck, st,
+                              si);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+}  // namespace insitu

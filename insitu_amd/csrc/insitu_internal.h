@@ -285,6 +285,15 @@ struct ChunkedApi {
                          const int64_t *, ChunkScratch &, uint32_t, int64_t, int64_t, int, bool,
                          const StepIn *, LaunchEv, DevStats *, int64_t, int64_t);
 };
+// The fused decode step's own kernel (attend_step.hip): sequential mode at d = 64, 4 query
+// heads per KV head, 4-bit keys and 2-bit values, 1,024-token chunks of 16 waves. It lays the
+// chunk scratch out its own way (scratch_layout clears the front when the layout changes).
+bool step_supported(const Geom &g, int64_t capacity);
+int64_t step_max_chunks(int64_t capacity);
+size_t step_scratch_bytes(const Geom &g, int64_t mc);
+hipError_t launch_step(hipStream_t s, const Geom &g, const Tables *t, int32_t *out, const int64_t *len,
+                       ChunkScratch &cs, uint32_t ep, int64_t mc, int64_t grid_chunks, const StepIn &si,
+                       LaunchEv ev, DevStats *st);
 hipError_t launch_step_write(hipStream_t s, const Geom &g, const Tables *t, const int32_t *qw,
                              const int32_t *kw, const int32_t *vw, int rounds,
                              const uint64_t (*signs)[2], int32_t *qr, double *qd, int32_t *qok,
