@@ -74,6 +74,9 @@ def _args():
     ap.add_argument("--mode", default="online", choices=["online", "two_pass", "split", "serial"])
     ap.add_argument("--chunk-tokens", type=int, default=0, choices=[0, 512, 1024],
                     help="tokens per chunk of the chunked attend for C2/C3/C4 (0: the cache default, 1,024)")
+    ap.add_argument("--kernel", default="auto", choices=["auto", "step", "chunked"],
+                    help="the decode step's kernel (C2, short): the automatic choice, the step kernel "
+                         "(attend_step.hip) or the chunked attend's fused step")
     ap.add_argument("--caches", type=int, default=40)
     ap.add_argument("--ctx", type=int, default=CTX)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -464,6 +467,8 @@ def bench_short(a) -> int:
     for cap in (131072, 256):
         c = CompressedCache(N_KV, D, cap, quant, n_q_heads=N_Q, ctx=ctx)
         c.append_rotated(kr, vr)
+        if a.kernel != "auto":
+            c.pin_kernel(a.kernel)
 
         def launch(i, c=c):
             _lib.check(lib.insitu_step(c.handle, ptr(q[i]), ptr(kw[i]), ptr(vw[i]), ptr(out),
@@ -792,6 +797,8 @@ def main() -> int:
     for _ in range(n_caches):
         c = CompressedCache(N_KV, D, a.ctx, quant, batch=1, n_q_heads=N_Q, chunk_tokens=a.chunk_tokens, ctx=ctx)
         c.append_rotated(kr, vr)
+        if a.kernel != "auto":
+            c.pin_kernel(a.kernel)
         caches.append(c)
     qs_d = ctx.to_device(qs[0], torch.int32)
     ks_d = ctx.to_device(ks[0], torch.int32)

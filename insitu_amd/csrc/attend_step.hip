@@ -148,15 +148,19 @@ struct StepLds {
     // the small tables first: their reads then take the LDS address from an immediate offset
     double kcf[16];
     int32_t vc32[8];
+    int32_t vc9[8];                         // the value centroids << 9 (|c| < 2^18)
     int32_t expt[256];
     union {
         struct {
             int4 tt[CHUNK][NV];             // each token's term for every value code, the 4 heads
             uint32_t vw[CHUNK][VWORDS];     // each token's value codes
+            uint32_t rix[CHUNK];            // each token's run, a byte per head
+            uint16_t clist[CHUNK];          // the chunk's candidates (any head) in token order
         } ph;
         struct {
             uint16_t rl[G][NSEG];           // the runs of chunks 1.. in order: slot | RUN_EVENT
             uint64_t rlf[G][RMAX], rbb[G][RMAX];
+            int32_t rs[G][RMAX][D];         // their sums, RMAX runs per head at a time
         } rp;
         SerialLds<RS> fb[G];
     } u;
@@ -170,6 +174,7 @@ struct StepLds {
     int64_t wmax[NW][G];
     int64_t wt[G][NW];
     int32_t evc[G][NW];
+    int32_t ccnt[NW];                       // candidates per wave
     int64_t min_[G], lmax[G];
     int32_t total[G];
     int qbad[G];
@@ -245,7 +250,10 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     for (int i = 0; i <= KWORDS; ++i) kw[i] = 0;
 #pragma unroll
     for (int i = 0; i < VWORDS; ++i) vwd[i] = 0;
-    if (live && !fresh) {
+    // The token's planes: key words, value words, norms. The waves that stage the query rows
+    // request them after the staging, whose store wait would otherwise wait for them too.
+    auto load_planes = [&]() __attribute__((always_inline)) {
+        if (!live || fresh) return;
         const int64_t t = t0 + tid;
 #pragma unroll
         for (int p = 0; p < NFULL; ++p) {
@@ -272,7 +280,8 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             vwd[1 % VWORDS] = v.y;
         }
         nw = *(const uint32_t *)(hb + (KPL + 1) * g.span + t * 4);
-    }
+    };
+    if (wv >= G) load_planes();
     // zero the run accumulators (LDS atomics add into them)
     for (int i = tid; i < G * RMAX * D; i += NT) (&S.runS[0][0][0])[i] = 0;
     if (tid < G * RMAX) {
@@ -287,7 +296,10 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         S.sdone = 0;
     }
     if (tid < NK) S.kcf[tid] = (double)tab;
-    if (tid >= 64 && tid < 64 + NV) S.vc32[tid - 64] = (int32_t)tab;   // |centroid| < 2^18 (Q1.15)
+    if (tid >= 64 && tid < 64 + NV) {
+        S.vc32[tid - 64] = (int32_t)tab;   // |centroid| < 2^18 (Q1.15)
+        S.vc9[tid - 64] = (int32_t)tab * 512;
+    }
     if (tid >= 384 && tid < 384 + 256) S.expt[tid - 384] = ex;
     double *qst = ck.qst + (size_t)blockIdx.x * (D * G);
     if (wv < G) {
@@ -330,6 +342,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
                 : "s"(qst + 64 * wv)
                 : "memory");
         }
+        load_planes();
     } else if (newrow && wv < G + 2) {
         // the new token: rotate, norm, codes (quantize.py:164-212), pack (:237-252), store
         const int f = wv - G;      // 0: key, 1: value
@@ -502,9 +515,8 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     // every chunk of a sequence, and then nothing is scored or waited for.
     if (ok && wv < 2 * G) {
         const int h = wv & (G - 1);
-        int64_t local = S.wmax[0][h];
-#pragma unroll
-        for (int w = 1; w < NW; ++w) local = S.wmax[w][h] > local ? S.wmax[w][h] : local;
+        // the chunk's maximum: lanes 0..15 hold the waves' maxima
+        const int64_t local = wave_max_i64(lane < NW ? S.wmax[lane & (NW - 1)][h] : SCORE_LO);
         int64_t run = SCORE_LO;
         if (nch > 1) {
             unsigned long long *wi0 = ck.status + ((int64_t)chain * G + h) * 2 * ck.mc;
@@ -570,6 +582,8 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     // LDS; run r of a head is the tokens from its r-th event of the chunk on (run 0:
     // before the first), and its L = sum p, its bound B = sum ((|w| * max|c_v|) >> 23) + 1
     // over w = v_norm * p != 0, and its opening factor go to the run accumulators.
+    // The reference's int64 floors are taken as 32-bit high products: for |a * b| < 2^63,
+    // floor(a * b / 2^k) = mulhi(a, b * 2^(32 - k)) whenever b * 2^(32 - k) fits 32 bits.
     uint64_t evb[G], cb[G];
     uint64_t candb = 0;
     int rb[G];
@@ -598,17 +612,28 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         }
         if (any_ev) __syncthreads();                               // B4 (uniform)
         STAMP(11);
+        // u = floor(min(d, delta_max) * log2e / 2^24) (attention.py:153-159), then the table
+        auto lut = [&](int64_t d) __attribute__((always_inline)) {
+            const uint32_t dc = (uint32_t)(d < dm ? d : dm);                     // < 2^20
+            const uint32_t u = __umulhi(dc << 8, (uint32_t)LOG2E_Q16);
+            const int32_t v = S.expt[u & 255] >> (u >> LUT_BITS);
+            return u < (uint32_t)LUT_SPAN ? v : 0;
+        };
         int64_t pm[G], dd[G];
         bool ev[G], cand[G];
 #pragma unroll
         for (int h = 0; h < G; ++h) {
             pm[h] = Min[h];
             if (evh[h]) {
-#pragma unroll
-                for (int w = 0; w < NW - 1; ++w) {
-                    const int64_t m = S.wt[h][w];
-                    pm[h] = w < wv && m > pm[h] ? m : pm[h];
-                }
+                // the maxima of the waves before this one: lanes 0..15 hold the waves' maxima,
+                // a 16-lane inclusive max-scan, read at wave - 1
+                int64_t wmx = lane < NW ? S.wt[h][lane & (NW - 1)] : SCORE_LO;
+                wmx = OpMax64::f(wmx, dpp64<DPP_ROW_SHR1>(SCORE_LO, wmx));
+                wmx = OpMax64::f(wmx, dpp64<DPP_ROW_SHR2>(SCORE_LO, wmx));
+                wmx = OpMax64::f(wmx, dpp64<DPP_ROW_SHR4>(SCORE_LO, wmx));
+                wmx = OpMax64::f(wmx, dpp64<DPP_ROW_SHR8>(SCORE_LO, wmx));
+                const int64_t before = wv ? readlane64(wmx, wv - 1) : SCORE_LO;
+                pm[h] = before > pm[h] ? before : pm[h];
                 const int64_t ex1 = wave_shr1_64(incl[h], SCORE_LO);
                 pm[h] = ex1 > pm[h] ? ex1 : pm[h];
             }
@@ -624,11 +649,11 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         for (int h = 0; h < G; ++h) pv[h] = fv[h] = bw[h] = 0;
         if (candb) {
             const int32_t vn = (int32_t)(int16_t)(nw >> 16);
-            int64_t vcmax = 0;
+            uint32_t vcmax9 = 0;
 #pragma unroll
             for (int c = 0; c < NV; ++c) {
-                const int64_t a = S.vc32[c] < 0 ? -(int64_t)S.vc32[c] : (int64_t)S.vc32[c];
-                vcmax = a > vcmax ? a : vcmax;
+                const uint32_t a = (uint32_t)(S.vc9[c] < 0 ? -S.vc9[c] : S.vc9[c]);
+                vcmax9 = a > vcmax9 ? a : vcmax9;
             }
             int32_t tv[NV][G];
 #pragma unroll
@@ -636,22 +661,21 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
 #pragma unroll
                 for (int c = 0; c < NV; ++c) tv[c][h] = 0;
                 if (!cb[h]) continue;
-                const int32_t p = cand[h] ? exp_lut(dd[h], S.expt, dm) : 0;   // LUT(0) = 2^15 at an event
-                const int32_t w = vn * p;                                  // |w| <= 2^30
+                const int32_t p = cand[h] ? lut(dd[h]) : 0;           // LUT(0) = 2^15 at an event
+                const int32_t w = vn * p;                              // |w| <= 2^30
                 const uint32_t aw = (uint32_t)(w < 0 ? -w : w);
                 pv[h] = p;
-                // |w| * max|c_v| < 2^48; the bound of one term fits 32 bits
-                bw[h] = w != 0 ? (int32_t)(((uint64_t)aw * (uint64_t)vcmax) >> acc_shift) + 1 : 0;
+                // (|w| * max|c_v|) >> 23 < 2^25; the term floor(w * c / 2^23) < 2^25 in magnitude
+                bw[h] = w != 0 ? (int32_t)__umulhi(aw, vcmax9) + 1 : 0;
 #pragma unroll
-                for (int c = 0; c < NV; ++c) tv[c][h] = (int32_t)(((int64_t)w * S.vc32[c]) >> acc_shift);
-                if (evb[h]) fv[h] = ev[h] ? exp_lut(s[h] - pm[h], S.expt, dm) : 0;
+                for (int c = 0; c < NV; ++c) tv[c][h] = __mulhi(w, S.vc9[c]);
+                if (evb[h]) fv[h] = ev[h] ? lut(s[h] - pm[h]) : 0;
             }
             if ((candb >> lane) & 1ull) {
 #pragma unroll
                 for (int c = 0; c < NV; ++c) S.u.ph.tt[tid][c] = make_int4(tv[c][0], tv[c][1], tv[c][2], tv[c][3]);
             }
         }
-        STAMP(12);
         if (any_ev) {
             if (lane == 0) {
 #pragma unroll
@@ -659,32 +683,35 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             }
             __syncthreads();                                       // B5 (uniform)
             STAMP(13);
+            // the events of the waves before this one, and of all: lanes 0..15 hold the waves'
+            // counts, a 16-lane prefix sum read at wave - 1 and at 15
 #pragma unroll
             for (int h = 0; h < G; ++h) {
                 if (!evh[h]) continue;
-                int before = 0, all = 0;
-#pragma unroll
-                for (int w = 0; w < NW; ++w) {
-                    const int c = S.evc[h][w];
-                    before += w < wv ? c : 0;
-                    all += c;
-                }
-                rb[h] = before;
-                nruns[h] = 1 + all;
+                uint32_t c = lane < NW ? (uint32_t)S.evc[h][lane & (NW - 1)] : 0u;
+                c += dpp32<DPP_ROW_SHR1>(0u, c);
+                c += dpp32<DPP_ROW_SHR2>(0u, c);
+                c += dpp32<DPP_ROW_SHR4>(0u, c);
+                c += dpp32<DPP_ROW_SHR8>(0u, c);
+                rb[h] = wv ? __builtin_amdgcn_readlane((int)c, wv - 1) : 0;
+                nruns[h] = 1 + __builtin_amdgcn_readlane((int)c, NW - 1);
             }
         }
         // Per-run L and B: the wave's tokens lie in run rb[h] up to its first event, then in
         // one run per event. Lane prefix sums (p <= 2^15 and a term bound < 2^25, so 64 of
         // them fit 32 bits) give every segment's sums: the segment's last lane adds its
-        // inclusive sum less the one before the segment's first lane into its run.
+        // inclusive sum less the one before the segment's first lane into its run. Each
+        // candidate also records its run for the walk, a byte per head (runs < RMAX count).
         const uint64_t le = lane == 63 ? ~0ull : (2ull << lane) - 1ull;       // lanes 0 .. lane
+        uint32_t rix = 0;
 #pragma unroll
         for (int h = 0; h < G; ++h) {
+            const uint64_t mine = evb[h] & le;                     // events at or before this lane
+            const int ri = rb[h] + (int)__popcll(mine);           // this lane's run
+            rix |= (uint32_t)(ri < 255 ? ri : 255) << (8 * h);
             if (!cb[h]) continue;
             const uint32_t sl = wave_scan_add32((uint32_t)pv[h]);
             const uint32_t sb = wave_scan_add32((uint32_t)bw[h]);
-            const uint64_t mine = evb[h] & le;                     // events at or before this lane
-            const int ri = rb[h] + (int)__popcll(mine);           // this lane's run
             const int first = mine ? 63 - __clzll((long long)mine) : 0;   // the first lane of its segment
             const bool last = lane == 63 || ((evb[h] >> (lane + 1)) & 1ull);
             const uint32_t pl = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (first - 1), (int)sl);
@@ -696,84 +723,84 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             }
             if (((evb[h] >> lane) & 1ull) && ri < RMAX) S.runf[h][ri] = fv[h];   // the factor opening run ri
         }
+        if ((candb >> lane) & 1ull) S.u.ph.rix[tid] = rix;
     }
+    if (lane == 0) S.ccnt[wv] = work ? (int32_t)__popcll(candb) : 0;
     __syncthreads();                                               // B6
+    // The chunk's candidates listed in token order (16-lane prefix sum of the waves' counts):
+    // the walk then gives every wave an equal share, wherever the candidates crowd.
+    int n_all = 0;
+    if (work) {
+        uint32_t c = lane < NW ? (uint32_t)S.ccnt[lane & (NW - 1)] : 0u;
+        c += dpp32<DPP_ROW_SHR1>(0u, c);
+        c += dpp32<DPP_ROW_SHR2>(0u, c);
+        c += dpp32<DPP_ROW_SHR4>(0u, c);
+        c += dpp32<DPP_ROW_SHR8>(0u, c);
+        n_all = __builtin_amdgcn_readlane((int)c, NW - 1);
+        const int off = wv ? __builtin_amdgcn_readlane((int)c, wv - 1) : 0;
+        if ((candb >> lane) & 1ull) {
+            const int at = off + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(candb >> 32),
+                                                                __builtin_amdgcn_mbcnt_lo((uint32_t)candb, 0u));
+            S.u.ph.clist[at] = (uint16_t)tid;
+        }
+        __syncthreads();                                           // B6b (uniform)
+    }
     STAMP(6);
 
     // -- P4: run sums, lane = channel ---------------------------------------------
-    // Every wave walks the candidates among its own 64 tokens in order, for the 4
-    // heads at once, 8 at a time: the tokens' value words and then the terms their
-    // codes of this lane's channel pick are read first, then added in order; an event
-    // of a head closes that head's open run, whose partial sum goes to its
-    // accumulator with an LDS atomic add.
-    if (work && candb) {
+    // Wave w walks candidates [w n / 16, (w + 1) n / 16) of the list in order, for the 4
+    // heads at once, 8 at a time: the tokens' value words, then the terms their codes of
+    // this lane's channel pick, then the adds; where a head's run changes (at its events,
+    // and at the wave's first candidate) the partial sum goes to that run's accumulator with
+    // an LDS atomic add.
+    const int i0 = (int)((int64_t)wv * n_all / NW), i1 = (int)((int64_t)(wv + 1) * n_all / NW);
+    if (work && i1 > i0) {
+        const int myn = i1 - i0;                                   // <= 64: n_all <= 1,024
+        const uint32_t tokl = lane < myn ? (uint32_t)S.u.ph.clist[i0 + lane] : 0u;
+        const uint32_t rixl = S.u.ph.rix[tokl];
         int32_t P[G];
-        int rr[G];
 #pragma unroll
-        for (int h = 0; h < G; ++h) {
-            P[h] = 0;
-            rr[h] = rb[h];
-        }
+        for (int h = 0; h < G; ++h) P[h] = 0;
+        uint32_t cur = (uint32_t)__builtin_amdgcn_readlane((int)rixl, 0);   // the open run of each head
         const int wi = (lane * VB) >> 5, sh = (lane * VB) & 31;
-        const uint64_t anyev = evb[0] | evb[1] | evb[2] | evb[3];
-        const int tb = 64 * wv;
-        uint64_t cm = candb;
-        while (cm) {
-            int js[8];
-            uint64_t taken = 0;
+        for (int k0 = 0; k0 < myn; k0 += 8) {
+            const int nt = myn - k0 < 8 ? myn - k0 : 8;
+            int tk[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                const int j = cm ? __builtin_ctzll(cm) : (k ? js[k - 1] : 0);
-                js[k] = j;
-                if (cm) {
-                    taken |= 1ull << j;
-                    cm &= cm - 1;
-                }
-            }
-            const int nt = __popcll(taken);
+            for (int k = 0; k < 8; ++k) tk[k] = __builtin_amdgcn_readlane((int)tokl, k0 + (k < nt ? k : 0));
             uint32_t wd[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) wd[k] = S.u.ph.vw[tb + js[k]][wi];
+            for (int k = 0; k < 8; ++k) wd[k] = S.u.ph.vw[tk[k]][wi];
             int4 t4[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k)
-                t4[k] = S.u.ph.tt[tb + js[k]][__builtin_amdgcn_ubfe(wd[k], (uint32_t)sh, (uint32_t)VB)];
-            if (!(anyev & taken)) {
+            for (int k = 0; k < 8; ++k) t4[k] = S.u.ph.tt[tk[k]][__builtin_amdgcn_ubfe(wd[k], (uint32_t)sh, (uint32_t)VB)];
 #pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    if (k < nt) {
-                        P[0] += t4[k].x;
-                        P[1] += t4[k].y;
-                        P[2] += t4[k].z;
-                        P[3] += t4[k].w;
-                    }
-                }
-            } else {
+            for (int k = 0; k < 8; ++k) {
+                if (k < nt) {
+                    const uint32_t rx = (uint32_t)__builtin_amdgcn_readlane((int)rixl, k0 + k);
+                    if (rx != cur) {
 #pragma unroll
-                for (int k = 0; k < 8; ++k) {
-                    if (k < nt) {
-                        const int j = js[k];
-                        if ((anyev >> j) & 1ull) {
-#pragma unroll
-                            for (int h = 0; h < G; ++h) {
-                                if ((evb[h] >> j) & 1ull) {
-                                    if (rr[h] < RMAX) atomicAdd(&S.runS[h][rr[h]][lane], P[h]);
-                                    P[h] = 0;
-                                    ++rr[h];
-                                }
+                        for (int h = 0; h < G; ++h) {
+                            const uint32_t ro = (cur >> (8 * h)) & 255u, rn = (rx >> (8 * h)) & 255u;
+                            if (ro != rn) {
+                                if (ro < RMAX && P[h]) atomicAdd(&S.runS[h][ro][lane], P[h]);
+                                P[h] = 0;
                             }
                         }
-                        P[0] += t4[k].x;
-                        P[1] += t4[k].y;
-                        P[2] += t4[k].z;
-                        P[3] += t4[k].w;
+                        cur = rx;
                     }
+                    P[0] += t4[k].x;
+                    P[1] += t4[k].y;
+                    P[2] += t4[k].z;
+                    P[3] += t4[k].w;
                 }
             }
         }
 #pragma unroll
-        for (int h = 0; h < G; ++h)
-            if (rr[h] < RMAX && P[h]) atomicAdd(&S.runS[h][rr[h]][lane], P[h]);
+        for (int h = 0; h < G; ++h) {
+            const uint32_t ro = (cur >> (8 * h)) & 255u;
+            if (ro < RMAX && P[h]) atomicAdd(&S.runS[h][ro][lane], P[h]);
+        }
     }
     __syncthreads();                                               // B7
     STAMP(7);
@@ -785,9 +812,13 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     int nev0 = 0;
     const bool hw = wv < G;        // wave h < G: query head h, lane = channel
     const int h = hw ? wv : 0;
+    // The last chunk of the sequence replays (it holds the new token, and its look-back is the
+    // longest); every other chunk publishes its runs (chunk 0: its state), waits until they
+    // are complete, then publishes its header, and is done. The replayer's runs stay in LDS.
+    const bool replayer = chunk == nch - 1;
     if (hw && work) {
         const int nr = nruns[h];
-        if (nr > RMAX || (!own && nr > SLOTS)) flags |= FL_POOL;
+        if (nr > RMAX || (!own && !replayer && nr > SLOTS)) flags |= FL_POOL;
         if (own && !(flags & FL_POOL)) {
             // acc = floor(acc * f / 2^15) + S per run (run 0 has no rescale), certified
             bool unsafe = false;
@@ -805,8 +836,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             nev0 = nr - 1;
         }
     }
-    bool last = nch == 1;
-    if (!last) {
+    if (!replayer) {
         if (hw) {
             uint64_t *hp = ck.hdr + (((int64_t)chain * ck.mc + chunk) * G + h) * 2;
             const int64_t hbase = ((int64_t)chain * G + h) * ck.pool;
@@ -828,27 +858,24 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
                     }
                 }
             }
+            stores_done();
             if (lane == 0) {
                 pub64(hp + 1, ok ? S.mabs : 0ull);
                 pub64(hp, (uint64_t)(uint32_t)npub | ((uint64_t)(uint32_t)flags << 16) |
                               ((uint64_t)(ok ? S.ovf & 0xFFFF : 0) << 24) | ((uint64_t)ck.ep << 40));
             }
-            stores_done();
         }
-        if (newrow && (wv == G || wv == G + 1)) stores_done();     // the new row, for a serial path elsewhere
-        __syncthreads();
-        if (tid == 0) {
-            const unsigned prior = __hip_atomic_fetch_add(&ck.done[chain], 1u, __ATOMIC_RELAXED,
-                                                          __HIP_MEMORY_SCOPE_AGENT);
-            S.last = prior == (unsigned)(nch - 1);
-        }
-        __syncthreads();
-        last = S.last != 0;
+        return;
     }
+    if (newrow && (wv == G || wv == G + 1)) stores_done();         // the new row, for the serial path
     STAMP(8);
-    if (!last) return;
 
-    // -- P6: the last workgroup of the sequence's KV head replays ------------------
+    // -- P6: the replay --------------------------------------------------------------
+    // Wave h < G polls the headers of chunks 0 .. nch - 2 (one per lane and 64 at a time;
+    // the wait is bounded, and a head whose wait gives up goes to the serial path), takes
+    // their statistics and flags, and lists the runs of chunks 1 .. nch - 2 in order. Then
+    // every wave stages runs (lane = channel) in LDS, and wave h walks chunk 0's state
+    // through them and through this chunk's own runs.
     int32_t aw = acc0;
     int64_t l = l0;
     unsigned long long events = (unsigned long long)nev0;
@@ -857,52 +884,45 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     int total = 0;
     if (nch > 1 && hw) {
         const uint64_t *hdr = ck.hdr + ((int64_t)chain * ck.mc * G + h) * 2;    // chunk c: hdr[c * G * 2]
-        const int64_t hbase = ((int64_t)chain * G + h) * ck.pool;
         const uint32_t ep = ck.ep;
-        if (!own) {
-            const uint64_t h0 = get64(&hdr[0]);
-            aw = (int32_t)get32(&ck.segS[hbase * D + lane]);
-            const uint64_t lf = get64(&ck.meta[hbase * 2]);
-            l = (int64_t)(uint32_t)lf;
-            events = lf >> 32;
-            hflags = (int)((h0 >> 16) & 0xFF);
-            if ((uint32_t)(h0 >> 40) != ep) {                      // cannot happen: it counted itself done
-                hflags |= FL_POOL;
-                atomicOr((unsigned long long *)&st->fault, 1ull);
-            }
-            tovf = (h0 >> 24) & 0xFFFF;
-            tmabs = get64(&hdr[1]);
-        }
-        // the runs of chunks 1 .. nch-1 in order, one header per lane and 64 chunks
         uint16_t *rl = S.u.rp.rl[h];
-        for (int c0 = 1; c0 < nch; c0 += 64) {
+        int spins = 0;
+        bool gaveup = ck.spin_limit == 0;
+        for (int c0 = 0; c0 < nch - 1; c0 += 64) {
             const int c = c0 + lane;
-            const bool in = c < nch;
+            const bool in = c < nch - 1;
             uint64_t w0 = 0, w1 = 0;
-            if (in) {
-                w0 = get64(&hdr[(int64_t)c * G * 2]);
-                w1 = get64(&hdr[(int64_t)c * G * 2 + 1]);
+            while (true) {
+                if (in) {
+                    w0 = get64(&hdr[(int64_t)c * G * 2]);
+                    w1 = get64(&hdr[(int64_t)c * G * 2 + 1]);
+                }
+                if (!__ballot(in && (uint32_t)(w0 >> 40) != ep)) break;
+                if (gaveup || ++spins > ck.spin_limit) {
+                    gaveup = true;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
             }
-            // A header is current (every chunk published before it counted itself done) and
-            // lists at most SLOTS runs; anything else would be an internal error, which sends
-            // the head to the serial path and raises the fault flag instead of reading past
-            // the run pool.
+            // a current header lists at most SLOTS runs (chunk 0: its state, one)
             const bool cur = in && (uint32_t)(w0 >> 40) == ep && (int)(w0 & 0xFFFF) <= SLOTS;
-            const int n = cur ? (int)(w0 & 0xFFFF) : 0;
+            const int n = cur && c > 0 ? (int)(w0 & 0xFFFF) : 0;
             int fl = cur ? (int)((w0 >> 16) & 0xFF) : 0;
-            if (in && !cur) {
-                fl |= FL_POOL;
-                atomicOr((unsigned long long *)&st->fault, 1ull);
-            }
+            if (in && !cur) fl |= FL_LB;
             const int incl = (int)wave_scan_add32((uint32_t)n);
             const int start = total + incl - n;
             for (int j = 0; j < n && start + j < NSEG; ++j)
                 rl[start + j] = (uint16_t)((slot_base(c) + j) | (j ? RUN_EVENT : 0));
             total += __builtin_amdgcn_readlane(incl, 63);
-            hflags |= (int)wave_reduce64<OpOr64>((int64_t)fl);
-            tovf += (unsigned long long)wave_sum_i64(in ? (int64_t)((w0 >> 24) & 0xFFFF) : 0);
-            const int64_t mm = wave_max_i64(in ? (int64_t)w1 : 0);
-            tmabs = (unsigned long long)mm > tmabs ? (unsigned long long)mm : tmabs;
+#pragma unroll
+            for (int bit = 0; bit < 4; ++bit) hflags |= __ballot((fl >> bit) & 1) ? 1 << bit : 0;
+            if (h == 0) {
+                // the score statistics, once per chain: counts below 2^16 per chunk
+                tovf += (uint32_t)__builtin_amdgcn_readlane(
+                    (int)wave_scan_add32(cur ? (uint32_t)((w0 >> 24) & 0xFFFF) : 0u), 63);
+                const int64_t mm = wave_max_i64(cur ? (int64_t)w1 : 0);
+                tmabs = (unsigned long long)mm > tmabs ? (unsigned long long)mm : tmabs;
+            }
         }
         STAMP(14);
         if (total > NSEG) hflags |= FL_POOL;
@@ -916,6 +936,14 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     for (int hh = 0; hh < G; ++hh) tmax = S.total[hh] > tmax ? S.total[hh] : tmax;
     const int tot_h = hw ? S.total[h] : 0;
     bool unsafe = false;
+    if (nch > 1 && hw) {
+        // chunk 0's state: acc (lane = channel), l | events << 32 (its header is current)
+        const int64_t hbase = ((int64_t)chain * G + h) * ck.pool;
+        aw = (int32_t)get32(&ck.segS[hbase * D + lane]);
+        const uint64_t lf = get64(&ck.meta[hbase * 2]);
+        l = (int64_t)(uint32_t)lf;
+        events = lf >> 32;
+    }
     for (int g0 = 0; g0 < tmax; g0 += RMAX) {
         // Stage up to RMAX runs per head in LDS: wave w loads runs w / G, w / G + 4, ... of head
         // w % G (lane = channel), every slot read, then every load, then every store.
@@ -935,7 +963,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             for (int k = 0; k < PER; ++k) v[k] = slot[k] >= 0 ? (int32_t)get32(&ck.segS[(hbase + slot[k]) * D + lane]) : 0;
 #pragma unroll
             for (int k = 0; k < PER; ++k)
-                if (slot[k] >= 0) S.runS[hh][part + (NW / G) * k][lane] = v[k];
+                if (slot[k] >= 0) S.u.rp.rs[hh][part + (NW / G) * k][lane] = v[k];
             if (wv < G) {
                 const int i = g0 + lane;
                 if (lane < RMAX && i < th) {
@@ -960,21 +988,25 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             const uint64_t lf = mine ? S.u.rp.rlf[h][lane] : 0ull;
             const int64_t bb = mine ? (int64_t)S.u.rp.rbb[h][lane] : 0;
             const uint64_t evm = __ballot(mine && (ent & RUN_EVENT));
-            const int64_t PB = wave_scan64<OpAdd64>(bb, 0);
-            const int64_t PL = wave_scan64<OpAdd64>((int64_t)(uint32_t)lf, 0);
+            // 32-bit prefix sums: L < 2^26 per run, and bounds below 2^27 (a run with a larger
+            // one is checked on its own, by the walk run by run)
+            const uint64_t bigm = __ballot(mine && bb >= (1ll << 27));
+            const uint32_t PB = wave_scan_add32(bb < (1ll << 27) ? (uint32_t)bb : 0u);
+            const uint32_t PL = wave_scan_add32((uint32_t)lf);
             for (int k0 = 0; k0 < nb; k0 += 8) {
                 const int kn = nb - k0 < 8 ? nb - k0 : 8;
-                const uint32_t bev = (uint32_t)(evm >> k0) & ((1u << kn) - 1u);
-                const int64_t before_b = k0 ? readlane64(PB, k0 - 1) : 0;
-                const int64_t before_l = k0 ? readlane64(PL, k0 - 1) : 0;
-                const int64_t bsum = readlane64(PB, k0 + kn - 1) - before_b;
+                const uint32_t bmask = (1u << kn) - 1u;
+                const uint32_t bev = (uint32_t)(evm >> k0) & bmask;
+                const uint32_t before_b = k0 ? (uint32_t)__builtin_amdgcn_readlane((int)PB, k0 - 1) : 0u;
+                const uint32_t before_l = k0 ? (uint32_t)__builtin_amdgcn_readlane((int)PL, k0 - 1) : 0u;
+                const int64_t bsum = (uint32_t)__builtin_amdgcn_readlane((int)PB, k0 + kn - 1) - before_b;
                 const int64_t a = aw < 0 ? -(int64_t)aw : (int64_t)aw;
                 int32_t v[8];
 #pragma unroll
-                for (int k = 0; k < 8; ++k) v[k] = k < kn ? S.runS[h][k0 + k][lane] : 0;
-                if (!bev && !__ballot(a + bsum > ACC_HI)) {
+                for (int k = 0; k < 8; ++k) v[k] = k < kn ? S.u.rp.rs[h][k0 + k][lane] : 0;
+                if (!bev && !((uint32_t)(bigm >> k0) & bmask) && !__ballot(a + bsum > ACC_HI)) {
                     aw += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-                    l += readlane64(PL, k0 + kn - 1) - before_l;
+                    l += (uint32_t)__builtin_amdgcn_readlane((int)PL, k0 + kn - 1) - before_l;
                     continue;
                 }
 #pragma unroll
@@ -995,6 +1027,21 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         }
         __syncthreads();
     }
+    if (nch > 1 && hw && work && !hflags) {
+        // this chunk's own runs, last (run 0 continues the run open before it)
+        const int nr = nruns[h];
+        for (int r = 0; r < nr; ++r) {
+            if (r > 0) {
+                const int64_t f = S.runf[h][r];
+                aw = (int32_t)(((int64_t)aw * f) >> PROB_FRAC);
+                l = (l * f) >> PROB_FRAC;
+                ++events;
+            }
+            if (!fits(aw, (int64_t)S.runB[h][r])) unsafe = true;
+            aw += S.runS[h][r][lane];
+            l += S.runL[h][r];
+        }
+    }
     if (hw && __ballot(unsafe)) hflags |= FL_CERT;
     STAMP(9);
     __syncthreads();               // the replay's lists are dead: the serial path reuses the LDS
@@ -1003,7 +1050,8 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         int32_t *orow = out + ((int64_t)b * g.n_q + qh) * D;
         if (hflags) {
             // The serial path counts score statistics only when no chunk did (the query
-            // check failed). The new row came from another workgroup: acquire it.
+            // check failed). The new row came from this workgroup's waves G, G + 1, whose
+            // stores are complete; the fence orders this wave's loads after them.
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
             serial_head<1, L::RS>(g, tabs, tabs->kc, tabs->vc, &S.qi[h][0], b, kvh, T, 0, !ok, S.u.fb[h], orow, st);
             if (lane == 0) atomicAdd(&st->serial_fallbacks, 1ull);
@@ -1036,7 +1084,6 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             if (S.ovf) atomicAdd(&st->score_overflows, S.ovf);
             atomicMax(&st->max_abs_score, S.mabs);
         }
-        if (nch > 1) ck.done[chain] = 0;    // every workgroup of the chain has counted itself
     }
     STAMP(10);
 }
