@@ -656,11 +656,12 @@ static bool use_scan(const insitu_cache *k, int32_t mode) {
     return !k->chunked;
 }
 
-// The fused decode step's own kernel (attend_step.hip), sequential and split mode, where it
-// handles the format: pinned by the test hook (3) while it is being brought up to speed.
+// The fused decode step's own kernel (attend_step.hip), sequential and split mode, wherever
+// it handles the format (d = 64, 4 query heads per KV head, 4-bit keys, 2-bit values, up to
+// 512 chunks of 1,024 tokens); the test hook can pin the chunked (2) or scan (1) attend.
 static bool use_step_kernel(const insitu_cache *k, int32_t mode) {
     if ((mode != INSITU_SEQUENTIAL && mode != INSITU_SPLIT) || !k->step) return false;
-    return k->path == 3;
+    return k->path == 0 || k->path == 3;
 }
 
 // q_staged: the chunked path's fp64 query staging already holds q (the step's

@@ -35,6 +35,8 @@
 #include "serial_head.h"
 #include "wave.h"
 
+#include <type_traits>
+
 #ifdef INSITU_STEP_STAMPS
 // Phase stamps (s_memrealtime) of every wave, for timing studies only, in a build
 // that defines INSITU_STEP_STAMPS: [workgroup][wave][stamp], read back by the host.
@@ -196,6 +198,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     constexpr int NFULL = KBYTES / 16, HALF = (KBYTES % 16) / 8;
     constexpr int KPL = NFULL + HALF;         // key planes; the value plane follows, then the norms
     static_assert(VB == 1 || VB == 2, "one value plane of 8 or 16 bytes");
+    static_assert(KB == 4, "the score's channel slices take 8 codes a word, 2 planes a row");
     static_assert(32 % KB == 0 && 32 % VB == 0, "the new row's codes never straddle a word");
     static_assert(KWORDS <= D * 4 / 32 && VWORDS <= D * 2 / 32, "new-row staging sizes");
     __shared__ L S;
@@ -216,6 +219,23 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     const bool live = t0 + tid < T;
     const bool fresh = newrow && tid == tln;
     const bool own = chunk == 0;
+    // The score's waves: a chunk of ntw token waves (lane = token) splits its channels over
+    // sp = 16 / ntw waves when it has few tokens (sp a power of two): wave wv scores channel
+    // slice wv / ntw of token wave wv % ntw; slice 0 is the token wave itself, which adds the
+    // other slices' partial sums (exact: integers below 2^51 in fp64).
+    const int ntok = (int)(T - t0 < CHUNK ? T - t0 : CHUNK);
+    const int ntw = (ntok + 63) >> 6;
+    const int sp = ntw > 8 ? 1 : ntw > 4 ? 2 : ntw > 2 ? 4 : ntw > 1 ? 8 : 16;
+    const bool scorer = wv < ntw * sp;
+    const int slice = wv / ntw, tw = wv - slice * ntw;
+    const int cps = D / sp;                   // channels per slice
+    const int hidx = 64 * tw + lane;          // a helper's token, within the chunk
+    const bool hlive = slice > 0 && scorer && t0 + hidx < T;
+    const bool hfresh = hlive && newrow && hidx == tln;
+    // A wave with no token of the chunk skips the per-token work (its reductions and scans
+    // would only take issue slots from the waves that share its SIMD) and leaves neutral
+    // entries in LDS; it still takes every barrier and its share of the walk.
+    const bool wlive = t0 + 64 * wv < T;
     if (own && kvh == 0 && tid == 0) si.len_out[b] = T;
     const int score_shift = CENT_FRAC + g.norm_frac;
     const int acc_shift = CENT_FRAC + g.norm_frac + PROB_FRAC - ACC_FRAC;
@@ -253,6 +273,19 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     // The token's planes: key words, value words, norms. The waves that stage the query rows
     // request them after the staging, whose store wait would otherwise wait for them too.
     auto load_planes = [&]() __attribute__((always_inline)) {
+        if (slice > 0) {
+            // a helper: the key words of its slice of token hidx, from word 0 on
+            if (!hlive || hfresh) return;
+            const int w0 = cps >= 8 ? slice * cps / 8 : slice / 2;     // the slice's first word
+            const uint4 v = *(const uint4 *)(hb + (w0 >> 2) * g.span + (t0 + hidx) * 16);
+            // slices of 4 words start at a plane, of 2 at an even word, of 1 or half anywhere
+            const uint32_t x0 = (w0 & 2) ? v.z : v.x, x1 = (w0 & 2) ? v.w : v.y;
+            kw[0] = ((w0 & 1) ? x1 : x0) >> (cps >= 8 ? 0 : 16 * (slice & 1));
+            kw[1] = x1;
+            kw[2] = v.z;
+            kw[3] = v.w;
+            return;
+        }
         if (!live || fresh) return;
         const int64_t t = t0 + tid;
 #pragma unroll
@@ -400,6 +433,13 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         for (int i = 0; i < VWORDS; ++i) vwd[i] = S.nv[i];
         nw = S.nn;
     }
+    if (hfresh) {
+        const int w0 = cps >= 8 ? slice * cps / 8 : slice / 2;
+        const uint32_t x = S.nk[w0];
+        kw[0] = x >> (cps >= 8 ? 0 : 16 * (slice & 1));
+#pragma unroll
+        for (int i = 1; i < 4; ++i) kw[i] = S.nk[(w0 + i) & (KWORDS - 1)];
+    }
 
     // -- P1: scores (attention.py:333-359), lane = token, the 4 heads at once ------
     // sum_ch q[ch] * c[code_ch] in fp64 FMA is exact: every partial sum is an integer
@@ -409,10 +449,13 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     for (int h = 0; h < G; ++h) s[h] = SCORE_LO;
     unsigned long long ovf = 0;
     int64_t mabs = 0;
-    if (ok && t0 + 64 * wv < T) {
-        double acc[G];
+    double acc[G];
 #pragma unroll
-        for (int h = 0; h < G; ++h) acc[h] = 0.0;
+    for (int h = 0; h < G; ++h) acc[h] = 0.0;
+    // The loop for NS steps of two channels: straight-line code, so that no copy of a register
+    // that a load still fills sits between a load and its wait.
+    auto score_steps = [&](auto ns) __attribute__((always_inline)) {
+        constexpr int NS = decltype(ns)::value;
         // Two channels a step, software-pipelined by hand: wait for this step's centroids
         // (LDS) and query values (scalar loads), request the next step's, then this step's
         // FMAs, which hide the latency. The loads are issued from inline asm, so that the
@@ -425,7 +468,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             const uint32_t win = sh == 0 ? kw[wi] : __builtin_amdgcn_alignbit(kw[wi + 1], kw[wi], sh);
             return (uint32_t)(uintptr_t)&S.kcf[win & (NK - 1)];
         };
-        const uint64_t qa = (uint64_t)uni64((int64_t)S.qaddr);
+        const uint64_t qa = (uint64_t)uni64((int64_t)S.qaddr) + (uint64_t)(slice * cps * 8);
         typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
         double c0, c1;
         u32x4 q0, q1, q2, q3;              // head h: the step's two channels' fp64 values
@@ -440,39 +483,67 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             : "s"(qa));
 #pragma unroll
         for (int st2 = 0; st2 < D / 2; ++st2) {
-            asm volatile("s_waitcnt lgkmcnt(0)"
-                         : "+v"(c0), "+v"(c1), "+s"(q0), "+s"(q1), "+s"(q2), "+s"(q3), "+v"(acc[0]),
-                           "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
-            double n0 = 0.0, n1 = 0.0;
-            u32x4 m0 = q0, m1 = q1, m2 = q2, m3 = q3;
-            if (st2 + 1 < D / 2) {
-                asm volatile("ds_read_b64 %0, %1" : "=v"(n0) : "v"(caddr(2 * st2 + 2)));
-                asm volatile("ds_read_b64 %0, %1" : "=v"(n1) : "v"(caddr(2 * st2 + 3)));
-                asm volatile(
-                    "s_load_dwordx4 %0, %8, %9\n\t"
-                    "s_load_dwordx4 %1, %8, %10\n\t"
-                    "s_load_dwordx4 %2, %8, %11\n\t"
-                    "s_load_dwordx4 %3, %8, %12"
-                    : "=s"(m0), "=s"(m1), "=s"(m2), "=s"(m3), "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]),
-                      "+v"(acc[3])
-                    : "s"(qa), "i"(16 * (st2 + 1)), "i"(512 + 16 * (st2 + 1)), "i"(1024 + 16 * (st2 + 1)),
-                      "i"(1536 + 16 * (st2 + 1)));
-            }
-            const u32x4 qh[G] = {q0, q1, q2, q3};
+            if (st2 < NS) {
+                asm volatile("s_waitcnt lgkmcnt(0)"
+                             : "+v"(c0), "+v"(c1), "+s"(q0), "+s"(q1), "+s"(q2), "+s"(q3), "+v"(acc[0]),
+                               "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
+                double n0 = 0.0, n1 = 0.0;
+                u32x4 m0 = q0, m1 = q1, m2 = q2, m3 = q3;
+                if (st2 + 1 < NS) {
+                    asm volatile("ds_read_b64 %0, %1" : "=v"(n0) : "v"(caddr(2 * st2 + 2)));
+                    asm volatile("ds_read_b64 %0, %1" : "=v"(n1) : "v"(caddr(2 * st2 + 3)));
+                    asm volatile(
+                        "s_load_dwordx4 %0, %8, %9\n\t"
+                        "s_load_dwordx4 %1, %8, %10\n\t"
+                        "s_load_dwordx4 %2, %8, %11\n\t"
+                        "s_load_dwordx4 %3, %8, %12"
+                        : "=s"(m0), "=s"(m1), "=s"(m2), "=s"(m3), "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]),
+                          "+v"(acc[3])
+                        : "s"(qa), "i"(16 * (st2 + 1)), "i"(512 + 16 * (st2 + 1)), "i"(1024 + 16 * (st2 + 1)),
+                          "i"(1536 + 16 * (st2 + 1)));
+                }
+                const u32x4 qh[G] = {q0, q1, q2, q3};
 #pragma unroll
-            for (int h = 0; h < G; ++h) {
-                const double qa0 = __builtin_bit_cast(double, (uint64_t)qh[h][0] | ((uint64_t)qh[h][1] << 32));
-                const double qa1 = __builtin_bit_cast(double, (uint64_t)qh[h][2] | ((uint64_t)qh[h][3] << 32));
-                acc[h] = fma(qa0, c0, acc[h]);
-                acc[h] = fma(qa1, c1, acc[h]);
+                for (int h = 0; h < G; ++h) {
+                    const double qa0 = __builtin_bit_cast(double, (uint64_t)qh[h][0] | ((uint64_t)qh[h][1] << 32));
+                    const double qa1 = __builtin_bit_cast(double, (uint64_t)qh[h][2] | ((uint64_t)qh[h][3] << 32));
+                    acc[h] = fma(qa0, c0, acc[h]);
+                    acc[h] = fma(qa1, c1, acc[h]);
+                }
+                c0 = n0;
+                c1 = n1;
+                q0 = m0;
+                q1 = m1;
+                q2 = m2;
+                q3 = m3;
             }
-            c0 = n0;
-            c1 = n1;
-            q0 = m0;
-            q1 = m1;
-            q2 = m2;
-            q3 = m3;
         }
+    };
+    if (ok && scorer) {
+        switch (sp) {
+        case 1: score_steps(std::integral_constant<int, 32>{}); break;
+        case 2: score_steps(std::integral_constant<int, 16>{}); break;
+        case 4: score_steps(std::integral_constant<int, 8>{}); break;
+        case 8: score_steps(std::integral_constant<int, 4>{}); break;
+        default: score_steps(std::integral_constant<int, 2>{}); break;
+        }
+    }
+    if (sp > 1) {
+        // the slices' partial sums to their token wave, through the (not yet used) tt area
+        double *part = (double *)&S.u.ph.tt[0][0];
+        if (ok && scorer && slice > 0) {
+#pragma unroll
+            for (int h = 0; h < G; ++h) part[(((slice - 1) * ntw + tw) * G + h) * 64 + lane] = acc[h];
+        }
+        __syncthreads();
+        if (ok && slice == 0 && scorer) {
+            for (int j = 1; j < sp; ++j) {
+#pragma unroll
+                for (int h = 0; h < G; ++h) acc[h] += part[(((j - 1) * ntw + tw) * G + h) * 64 + lane];
+            }
+        }
+    }
+    if (ok && slice == 0 && scorer) {
         if (live) {
             const int64_t kn = sext16(nw);
 #pragma unroll
@@ -492,10 +563,10 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     for (int i = 0; i < VWORDS; ++i) S.u.ph.vw[tid][i] = vwd[i];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-        const int64_t m = wave_max_i64(s[h]);
+        const int64_t m = wlive ? wave_max_i64(s[h]) : SCORE_LO;
         if (lane == 0) S.wmax[wv][h] = m;
     }
-    if (ok) {
+    if (ok && wlive) {
         ovf = (unsigned long long)wave_sum_i64((int64_t)ovf);
         mabs = wave_max_i64(mabs);
         if (lane == 0) {
@@ -606,7 +677,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             any_ev = any_ev || evh[h];
             incl[h] = SCORE_LO;
             if (evh[h]) {
-                incl[h] = wave_scan64<OpMax64>(s[h], SCORE_LO);
+                if (wlive) incl[h] = wave_scan64<OpMax64>(s[h], SCORE_LO);
                 if (lane == 63) S.wt[h][wv] = incl[h];
             }
         }
@@ -624,6 +695,9 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
 #pragma unroll
         for (int h = 0; h < G; ++h) {
             pm[h] = Min[h];
+            ev[h] = cand[h] = false;
+            dd[h] = 0;
+            if (!wlive) continue;
             if (evh[h]) {
                 // the maxima of the waves before this one: lanes 0..15 hold the waves' maxima,
                 // a 16-lane inclusive max-scan, read at wave - 1
