@@ -8,11 +8,13 @@ q/k/v, append the token's compressed k/v row (row 32,767), attend over all
 32,768 rows, Q16 out. The scan bytes are the compressed-cache bytes the attend
 reads: 8 KV heads x 32,768 rows x 52 B = 13,631,488 B.
 
-Defeating the 256 MB Infinity Cache: a pass of K timed steps uses K distinct
-caches (at least 40 of ~13.6 MB, more than twice the Infinity Cache in total),
-and between passes each cache is rewound to 32,767 rows (a length reset,
-outside the timed region), so every timed step is at ctx 32,768 and no step
-reads a cache that is still resident from the step before.
+Defeating the 256 MB Infinity Cache: the steps of the whole run (warmup, the
+K steps of `value`, the 64 event-timed steps of the roofline, the two-pass line)
+take caches in one rotation over 64 caches of ~13.6 MB: step i reads cache
+i % 64, so between two reads of a cache the other 63 are read (a reuse distance
+of ~1 GB, four times the Infinity Cache). Before each pass every cache is rewound
+to 32,767 rows (a length reset, outside the timed region), so every timed step is
+at ctx 32,768.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--mode online]
     python bench.py --copy-calibration      # a plain copy kernel of known size
@@ -64,6 +66,13 @@ HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, published
 CTX = 32768
 N_Q, N_KV, D = 32, 8, 64
 ROW = 52
+N_CU = 256                 # MI355X compute units
+
+
+def rotate_q(q_wire):
+    """The query row rotated as the step rotates it (rotate.py:170-197), for the oracle."""
+    from oracle.rotate import rotate, signs_from_seed
+    return rotate(np.asarray(q_wire).astype(np.int64), signs_from_seed(D, 0, 1))
 
 
 def _args():
@@ -77,7 +86,7 @@ def _args():
     ap.add_argument("--kernel", default="auto", choices=["auto", "step", "chunked"],
                     help="the decode step's kernel (C2, short): the automatic choice, the step kernel "
                          "(attend_step.hip) or the chunked attend's fused step")
-    ap.add_argument("--caches", type=int, default=40)
+    ap.add_argument("--caches", type=int, default=64)
     ap.add_argument("--ctx", type=int, default=CTX)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
@@ -89,18 +98,21 @@ def _args():
     return ap.parse_args()
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "chunk_kernel_c2_traffic.json")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "step_kernel_c2_traffic.json")
 
 
 # The kernels insitu_step launches for one decode step, per mode, at C2's format
 # (d = 64, 4-bit keys, 2-bit values, 4 query heads per KV head): online and split
-# mode are the one fused chunk_kernel launch.
+# mode are one launch of the step kernel (attend_step.hip), or of the chunked
+# attend's fused step when --kernel chunked pins it.
 STEP_KERNEL = {
-    "online": "insitu::chunk_kernel<64, 4, true, false, true>",
-    "split": "insitu::chunk_kernel<64, 4, true, false, true>",
+    "online": "insitu::stepk::step_kernel<4, 2>",
+    "split": "insitu::stepk::step_kernel<4, 2>",
     "two_pass": "insitu::step_write_kernel + insitu::chunk_max_kernel + insitu::chunk_kernel",
     "serial": "insitu::step_write_kernel + insitu::attend_serial_kernel",
 }
+CHUNKED_STEP_KERNEL = "insitu::chunk_kernel<64, 4, true, false, true>"
+TIMED_LAUNCHES = 64        # event-timed attends behind the roofline median (at least 50)
 
 
 def measured_traffic(kernel: str, ctx: int):
@@ -779,12 +791,17 @@ def main() -> int:
     quant = QuantConfig(key_bits=4, value_bits=2)
     rot = Rotation.for_quant(quant, D)
     # Every timed step is the configuration's one decode step: the cache holds
-    # ctx - 1 rows, the step appends row ctx - 1 and attends over all ctx. A pass
-    # of K steps uses K distinct caches (at least --caches of them, whose total is
-    # more than twice the Infinity Cache); between passes every cache is rewound
-    # to ctx - 1 rows (a length reset, outside the timed region).
-    n_caches = max(a.caches, a.steps, a.warmup, 1)
-    n_steps_total = a.warmup + 2 * a.steps
+    # ctx - 1 rows, the step appends row ctx - 1 and attends over all ctx. Steps
+    # cycle through n_caches caches (--caches, at least as many as any pass has
+    # steps) in one rotation that runs on across the warmup and every pass: step i
+    # of the run uses cache i % n_caches, so between two uses of a cache the other
+    # n_caches - 1 are read (more than twice the 256 MB Infinity Cache). Before a
+    # pass every cache is rewound to ctx - 1 rows (a length reset, outside the timed
+    # region). The roofline pass times TIMED_LAUNCHES attends with HIP events.
+    n_ev = max(TIMED_LAUNCHES, a.steps)
+    n_caches = max(a.caches, a.steps, a.warmup, n_ev, 1)
+    n_tp = a.steps if a.mode == "online" else 0        # the two-pass line's steps
+    n_steps_total = a.warmup + a.steps + n_ev + n_tp
 
     # Prefill data: ctx-1 tokens of seeded wire k/v, rotated and appended on the GPU.
     wl = Workload(seed=0)
@@ -815,58 +832,79 @@ def main() -> int:
     mode = _lib.MODES[a.mode]
     step_bytes = float(N_KV * ROW * a.ctx)      # the rows one attend scans
 
-    def step(i, j):
+    def step(i, md=None):
         # One decode step from the wire, CMD_STEP (kernel.py:271-345): rotate q/k/v,
-        # append the k/v row, attend -- one launch in online mode.
-        _lib.check(lib.insitu_step(caches[j].handle, ptr(qs_d[i]), ptr(ks_d[i]), ptr(vs_d[i]),
-                                   ptr(outs[i]), mode, None))
+        # append the k/v row, attend -- one launch in online mode. Step i of the run
+        # takes cache i % n_caches.
+        _lib.check(lib.insitu_step(caches[i % n_caches].handle, ptr(qs_d[i]), ptr(ks_d[i]), ptr(vs_d[i]),
+                                   ptr(outs[i]), mode if md is None else md, None))
 
     def rewind():
         for c in caches:
             c.set_length(a.ctx - 1)
         torch.cuda.synchronize()
 
-    def timed_pass(i0, timing):
+    def timed_pass(i0, n, timing, md=None):
         rewind()
         _lib.check(lib.insitu_ctx_timing(ctx.handle, 1 if timing else 0))
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for j in range(a.steps):
-            step(i0 + j, j)
+        for j in range(n):
+            step(i0 + j, md)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
-        ms = (ctypes.c_double * a.steps)()
+        ms = (ctypes.c_double * n)()
         n_att = ctypes.c_int64()
-        _lib.check(lib.insitu_ctx_timing_read_each(ctx.handle, ms, a.steps, ctypes.byref(n_att)))
+        _lib.check(lib.insitu_ctx_timing_read_each(ctx.handle, ms, n, ctypes.byref(n_att)))
         _lib.check(lib.insitu_ctx_timing(ctx.handle, 0))
-        if n_att.value != (a.steps if timing else 0):
-            raise RuntimeError(f"timed {n_att.value} attends for {a.steps} steps")
+        if n_att.value != (n if timing else 0):
+            raise RuntimeError(f"timed {n_att.value} attends for {n} steps")
         return wall, np.array(ms[:n_att.value]) * 1e3
 
     for i in range(a.warmup):
-        step(i, i)
+        step(i)
     torch.cuda.synchronize()
-    # value: the steps with nothing attached; roofline: the attend kernel's own
-    # time, from HIP events attached to its dispatches on the stream it runs on
-    # (insitu_ctx_timing), over a second pass of as many steps (the events
-    # themselves cost the step a few microseconds, so that pass is not `value`)
-    wall, _ = timed_pass(a.warmup, False)
-    wall_ev, us_each = timed_pass(a.warmup + a.steps, True)
+    # value: K steps with nothing attached; roofline: the attend kernel's own time,
+    # from HIP events attached to its dispatches on the stream it runs on
+    # (insitu_ctx_timing), over a pass of TIMED_LAUNCHES steps (the events themselves
+    # cost the step a few microseconds, so that pass is not `value`)
+    wall, _ = timed_pass(a.warmup, a.steps, False)
+    wall_ev, us_each = timed_pass(a.warmup + a.steps, n_ev, True)
     us_med = float(np.median(us_each))
     us_mean = float(us_each.mean())
     kernel_gbs = step_bytes / (us_med * 1e-6) / 1e9
     whole_gbs = step_bytes * a.steps / wall / 1e9
 
-    # Correctness of the timed work: the last step against the oracle (and the CPU baseline).
-    last = n_steps_total - 1
+    # Correctness of the timed work: the roofline pass's last step against the oracle
+    # (and the CPU baseline).
+    last = a.warmup + a.steps + n_ev - 1
     out_last = outs[last].cpu().numpy()[0].astype(np.int64)
-    cache_last = caches[a.steps - 1]
+    cache_last = caches[last % n_caches]
     if cache_last.length != a.ctx:
         raise RuntimeError(f"the last step's cache holds {cache_last.length} rows, not {a.ctx}")
+    # The adapter's default softmax is two-pass (three launches a step): its line, K steps
+    # on the same rotation, checked against the oracle's attend_two_pass.
+    two_pass = None
+    if n_tp:
+        i0 = last + 1
+        wall_tp, _ = timed_pass(i0, n_tp, False, _lib.MODES["two_pass"])
+        i_tp = i0 + n_tp - 1
+        q_tp = rotate_q(qs[0, i_tp])
+        c_tp = caches[i_tp % n_caches]
+        from oracle import native as _nat
+        from oracle.quantize import Format as _Fmt
+        want_tp = np.concatenate([_nat.attend_two_pass(q_tp[4 * h:4 * h + 4], c_tp.view(h), _Fmt())[0]
+                                  for h in range(N_KV)])
+        if not np.array_equal(want_tp, outs[i_tp].cpu().numpy()[0].astype(np.int64)):
+            raise AssertionError("the two-pass line's last step disagrees with the oracle")
+        two_pass = {"mode": "two_pass", "steps": n_tp,
+                    "kernels": STEP_KERNEL["two_pass"],
+                    "us_per_decode_step": round(wall_tp / n_tp * 1e6, 2),
+                    "GB/s": round(step_bytes * n_tp / wall_tp / 1e9, 3),
+                    "checked": "the last step equal to oracle/c attend_two_pass"}
     from oracle import native
     from oracle.quantize import Format
-    from oracle.rotate import rotate, signs_from_seed
-    q_rot_last = rotate(qs[0, last].astype(np.int64), signs_from_seed(D, 0, 1))
+    q_rot_last = rotate_q(qs[0, last])
     want = np.concatenate([native.attend_online(q_rot_last[4 * h:4 * h + 4], cache_last.view(h), Format())[0]
                            for h in range(N_KV)]) if a.mode != "two_pass" else None
     if want is not None and not np.array_equal(want, out_last):
@@ -875,7 +913,10 @@ def main() -> int:
     if not a.no_cpu_baseline:
         cpu = cpu_baseline(cache_last, q_rot_last, out_last, (qs[0, last], ks[0, last], vs[0, last]))
     kernel = STEP_KERNEL.get(a.mode, a.mode)
+    if a.kernel == "chunked" and a.mode in ("online", "split"):
+        kernel = CHUNKED_STEP_KERNEL
     traffic, traffic_src = measured_traffic(kernel, a.ctx)
+    cache_mb = total_mb / n_caches
 
     res = {
         "metric": "compressed-KV scan GB/s (% HBM peak) + us/decode-step at ctx 32k, 1 GPU",
@@ -894,9 +935,11 @@ def main() -> int:
         "data": "synthetic (seeded N(0,1) q/k/v with 4 outlier channels x8 per head, Q8.16)",
         "config": {"workload": "C2: Llama-3.2-1B-shape single layer, batch 1, ctx 32768, "
                                "4b K / 2b V, decode step = insitu_step: rotate + append + attend",
-                   "mode": a.mode, "chunk_tokens": a.chunk_tokens or 1024, "ctx": a.ctx, "rotating_caches": n_caches,
-                   "rotating_mb": round(total_mb, 1), "kv_heads": N_KV, "q_heads": N_Q,
-                   "head_dim": D, "row_bytes": ROW},
+                   "mode": a.mode, "kernel": a.kernel, "chunk_tokens": a.chunk_tokens or 1024, "ctx": a.ctx,
+                   "rotating_caches": n_caches, "rotating_mb": round(total_mb, 1),
+                   "caches_per_timed_pass": min(a.steps, n_caches),
+                   "reuse_distance_mb": round(cache_mb * (n_caches - 1), 1),
+                   "kv_heads": N_KV, "q_heads": N_Q, "head_dim": D, "row_bytes": ROW},
         "roofline": {"bound": "hbm", "achieved": round(kernel_gbs, 3), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(kernel_gbs / HBM_PEAK_GBS, 5),
                      "traffic": traffic, "traffic_source": traffic_src,
@@ -906,9 +949,13 @@ def main() -> int:
                      "attend_us_mean": round(us_mean, 3),
                      "attend_us_min": round(float(us_each.min()), 3),
                      "attend_us_max": round(float(us_each.max()), 3),
+                     "event_timed_launches": int(us_each.size),
                      "cycles_per_row_gpu_wide_2p4ghz": round(
-                         us_med * 1e-6 * 2.4e9 / (step_bytes / ROW), 4)},
+                         us_med * 1e-6 * 2.4e9 / (step_bytes / ROW), 4),
+                     "cycles_per_row_per_cu_2p4ghz": round(
+                         us_med * 1e-6 * 2.4e9 * N_CU / (step_bytes / ROW), 2)},
         "checked": "the last timed step equal to oracle/c attend_online" if want is not None else None,
+        "two_pass_line": two_pass,
         "cpu_baseline": cpu,
     }
     print(json.dumps(res))

@@ -1,9 +1,11 @@
 """Build libinsitu_hip.so in-tree for gfx950 with hipcc (no JIT cache, no torch extension).
 
-    python -m insitu_amd.build
+    python -m insitu_amd.build [--stamps]
 
 Each .hip file compiles to an object in parallel, then one shared library is
-linked next to this file so it travels with the source tree.
+linked next to this file so it travels with the source tree. --stamps also links
+libinsitu_hip_stamps.so, the decode step kernel with its phase stamps compiled in
+(timing studies: python -m insitu_amd.phases).
 """
 
 from __future__ import annotations
@@ -65,6 +67,31 @@ def build(verbose: bool = False) -> str:
     return OUT
 
 
+STAMPS_OUT = os.path.join(HERE, "libinsitu_hip_stamps.so")
+
+
+def build_stamps(verbose: bool = False) -> str:
+    """libinsitu_hip_stamps.so: the library with the decode step kernel's phase stamps
+    compiled in (attend_step.hip with INSITU_STEP_STAMPS), for insitu_amd.phases only.
+    It reuses build()'s other objects, so build() runs first."""
+    if not os.path.exists(OUT):
+        build(verbose)
+    obj = _compile((os.path.join(CSRC, "attend_step.hip"), "stamps", ["-DINSITU_STEP_STAMPS"]))
+    others = [o for o in sorted(glob.glob(os.path.join(BUILD, "*.o")))
+              if not os.path.basename(o).startswith("attend_step.hip")]
+    tmp = STAMPS_OUT + ".tmp"
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, obj, *others, "-lrocblas"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode:
+        raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, STAMPS_OUT)
+    if verbose:
+        print(f"built {STAMPS_OUT}")
+    return STAMPS_OUT
+
+
 if __name__ == "__main__":
     build(verbose=True)
+    if "--stamps" in sys.argv:
+        build_stamps(verbose=True)
     sys.exit(0)
