@@ -189,14 +189,16 @@ int insitu_attend_causal_head(insitu_cache *cache, int32_t seq, int32_t kv_head,
                               insitu_stats *stats_host);
 
 /* insitu_attend_causal without allocating: no counterpart in the reference; for callers
- * that cannot call hipMalloc (code under HIP graph capture, tight serving loops). The same
+ * that cannot call hipMalloc (tight serving loops, harnesses that forbid it). The same
  * launches and results as insitu_attend_causal, but the chunk scratch and the lengths of
  * the virtual batch live in a fixed device array of the library (64 MiB, one per device,
  * set up by insitu_ctx_create) instead of buffers the cache allocates. A launch takes as
  * many queries as fit it; EBADLEN when a single query's scratch does not (its size is in
  * the message). No statistics (nothing is copied back) and no timing events. Every call on
  * a device shares that device's array: calls that overlap on one device (two streams, two
- * threads) race and must not. Stream-ordered on the cache's context. */
+ * threads) race and must not. Stream-ordered on the cache's context. Not for HIP graph
+ * capture: each call takes its scratch epoch from a host counter into the launch's
+ * arguments, so a replayed graph would run every replay under the captured epoch. */
 int insitu_attend_causal_static(insitu_cache *cache, int32_t seq, int64_t base, int64_t n_q,
                                 const int32_t *q_rot_dev, int32_t *out_dev, int32_t mode);
 
@@ -278,6 +280,16 @@ enum {
                                         INSITU_EINVAL if the kernel does not handle the cache   */
 };
 int insitu_cache_debug(insitu_cache *cache, int32_t what, int64_t value);
+/* The invariants of a scratch layout, computed on the host without a GPU: kernel 0 the
+ * chunked attend (1,024-token chunks), 1 the chunked attend (512), 2 the decode step's own
+ * kernel (d = 64), for a cache of `capacity` tokens, batch sequences and n_kv KV heads of
+ * dimension d, 4 query heads per KV head. facts (n >= 11): chunks per sequence, run slots
+ * per head, slots per chunk after chunk 0, one past the last chunk's slots, runs the replay
+ * lists per head, most chunks per sequence, scratch bytes, bytes of the epoch-checked front,
+ * 1 when every area is 256-aligned and ends before the next begins, tokens per chunk, the
+ * slot id limit. */
+int insitu_debug_scratch_layout(int32_t kernel, int64_t capacity, int32_t batch, int32_t n_kv, int32_t d,
+                                int64_t *facts, int32_t n);
 
 /* Message of the last failing call on this thread. */
 const char *insitu_last_error(void);

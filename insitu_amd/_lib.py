@@ -31,7 +31,7 @@ EXPORTS = (
     "insitu_attend", "insitu_attend_causal", "insitu_attend_causal_head", "insitu_attend_causal_static", "insitu_step", "insitu_project", "insitu_seam_wire",
     "insitu_output_projection", "insitu_read_rows", "insitu_load_rows", "insitu_read_image",
     "insitu_load_image", "insitu_probe_read", "insitu_probe_empty", "insitu_cache_debug",
-    "insitu_last_error",
+    "insitu_debug_scratch_layout", "insitu_last_error",
 )
 
 
@@ -132,6 +132,7 @@ def load(path: str | None = None):
         "insitu_probe_read": (i32, [vp, vp, i64, i32, i32, vp]),
         "insitu_probe_empty": (i32, [vp, i32, vp]),
         "insitu_cache_debug": (i32, [vp, i32, i64]),
+        "insitu_debug_scratch_layout": (i32, [i32, i64, i32, i32, i32, P(i64), i32]),
         "insitu_last_error": (ctypes.c_char_p, []),
     }
     for name, (res, args) in sig.items():

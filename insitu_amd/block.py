@@ -32,6 +32,24 @@ from .config import FixedFormat, ModelConfig, QuantConfig
 from .runtime import default_context, ptr
 
 
+# The chunked attend takes at most this many chunks per sequence (attend_chunked.hip, HMAX).
+CHUNKED_MAX_CHUNKS = 512
+
+
+def default_chunk_tokens(softmax: str, capacity: int) -> int:
+    """Tokens per chunk of the chunked attend (prefill, and attends outside the decode step)
+    for a block's cache. 512 for the online softmax: a model's queries (projections of
+    unit-scale hidden states) give a flat softmax, whose run-sum walk 512-token chunks split
+    over twice the workgroups; but only while the capacity fits the chunked attend's 512
+    chunks of 512 tokens, since past that the chunked attend would refuse the cache and the
+    format's attends would fall to slower kernels, while 1,024-token chunks still fit. Two-pass
+    keeps 1,024 (its chunk-max launch and the prefill's query batches favour fewer chunks: a
+    4,096-token two-pass prefill takes 10.1 ms on 1,024- and 17.0 ms on 512-token chunks)."""
+    if softmax == "two_pass":
+        return 1024
+    return 512 if -(-capacity // 512) <= CHUNKED_MAX_CHUNKS else 1024
+
+
 @dataclass
 class StepReport:
     """kernel.py:49-67: what one forward did. `saturated` counts the fp -> fixed
@@ -64,13 +82,8 @@ class AttentionBlock:
         self.quant = quant or QuantConfig()
         self.fmt = fmt or FixedFormat()
         self.ctx = ctx or default_context()
-        # 512-token chunks for the online softmax: a model's queries (projections of unit-scale
-        # hidden states) give a flat softmax, whose run-sum walk they split over twice the
-        # workgroups. Two-pass keeps 1,024 (its chunk-max launch and the prefill's query
-        # batches favour fewer chunks: a 4,096-token two-pass prefill takes 10.1 ms on 1,024-
-        # and 17.0 ms on 512-token chunks).
         if chunk_tokens is None:
-            chunk_tokens = 1024 if softmax == "two_pass" else 512
+            chunk_tokens = default_chunk_tokens(softmax, capacity)
         self.cache = CompressedCache(model.num_kv_heads, model.head_dim, capacity, self.quant,
                                      self.fmt, batch=batch, n_q_heads=model.num_heads,
                                      chunk_tokens=chunk_tokens, ctx=self.ctx)

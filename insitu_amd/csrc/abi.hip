@@ -7,6 +7,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -112,7 +113,9 @@ namespace {
 
 constexpr int MAX_DEVICES = 64;
 struct StaticScratch {
-    uint8_t *ptr = nullptr;     // the device's copy of `scratch`
+    // the device's copy of `scratch`: published last (release), after cs and len, so that a
+    // reader that sees it (acquire) sees them too
+    std::atomic<uint8_t *> ptr{nullptr};
     ChunkScratch cs;            // its chunk-scratch part and attend count
     int64_t *len = nullptr;     // its lengths part
 };
@@ -129,7 +132,7 @@ hipError_t static_scratch_setup(int device, hipStream_t stream) {
     std::lock_guard<std::mutex> lock(g_static_mu);
     if (device < 0 || device >= MAX_DEVICES) return hipErrorInvalidDevice;
     StaticScratch &ss = g_static[device];
-    if (ss.ptr) return hipSuccess;
+    if (ss.ptr.load(std::memory_order_acquire)) return hipSuccess;
     void *p = nullptr;
     hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess) return e;
@@ -138,10 +141,10 @@ hipError_t static_scratch_setup(int device, hipStream_t stream) {
     e = hipGetLastError();
     if (e == hipSuccess) e = hipStreamSynchronize(stream);
     if (e != hipSuccess) return e;
-    ss.ptr = (uint8_t *)p;
     ss.cs.p = p;
     ss.cs.bytes = STATIC_SCRATCH_BYTES - STATIC_LEN_BYTES;
     ss.len = (int64_t *)((uint8_t *)p + ss.cs.bytes);
+    ss.ptr.store((uint8_t *)p, std::memory_order_release);
     return hipSuccess;
 }
 
@@ -881,7 +884,7 @@ int insitu_attend_causal_static(insitu_cache *k, int32_t seq, int64_t base, int6
     if (rc) return rc;
     if (n_q == 0) return INSITU_OK;
     const int dev = k->ctx->device;
-    if (dev < 0 || dev >= MAX_DEVICES || !g_static[dev].ptr)
+    if (dev < 0 || dev >= MAX_DEVICES || !g_static[dev].ptr.load(std::memory_order_acquire))
         return fail(INSITU_EINVAL, "the device's static scratch is not set up (insitu_ctx_create)");
     StaticScratch &ss = g_static[dev];
     HIP_TRY(hipSetDevice(dev), "hipSetDevice");
@@ -960,6 +963,28 @@ int insitu_step(insitu_cache *k, const int32_t *q, const int32_t *kw, const int3
     rc = attend_impl(k, qr, out, mode, chunked, nullptr, ep);
     if (rc) return rc;
     return copy_stats(k, stats);
+}
+
+// Test hook: the invariants of a scratch layout, computed on the host (no GPU call).
+int insitu_debug_scratch_layout(int32_t kernel, int64_t capacity, int32_t batch, int32_t n_kv, int32_t d,
+                                int64_t *facts, int32_t n) {
+    if (!facts || n < 11 || capacity < 1 || batch < 1 || n_kv < 1 || (d != 64 && d != 128))
+        return fail(INSITU_EINVAL, "bad argument");
+    Geom g{};
+    g.batch = batch;
+    g.n_kv = n_kv;
+    g.d = d;
+    g.G = 4;
+    g.n_q = 4 * n_kv;
+    if (kernel == 0)
+        insitu::chunked_layout_facts(g, insitu::chunked_max_chunks(capacity), facts);
+    else if (kernel == 1)
+        insitu::c512::chunked_layout_facts(g, insitu::c512::chunked_max_chunks(capacity), facts);
+    else if (kernel == 2 && d == 64)
+        insitu::step_layout_facts(g, insitu::step_max_chunks(capacity), facts);
+    else
+        return fail(INSITU_EINVAL, "kernel: 0 chunked (1,024-token chunks), 1 chunked (512), 2 step (d = 64)");
+    return INSITU_OK;
 }
 
 int insitu_cache_debug(insitu_cache *k, int32_t what, int64_t value) {

@@ -254,7 +254,7 @@ struct ChunkLds {
 };
 
 // Run slots: chunk 0 owns slot 0 (its replayed state), chunk c > 0 owns SLOTS after it.
-__device__ __forceinline__ int slot_base(int chunk) { return chunk == 0 ? 0 : 1 + (chunk - 1) * SLOTS; }
+__host__ __device__ __forceinline__ int slot_base(int chunk) { return chunk == 0 ? 0 : 1 + (chunk - 1) * SLOTS; }
 static_assert(1 + (HMAX - 1) * SLOTS < RUN_EVENT, "run slots of the chunked path fit 15 bits");
 
 // The key codes and norm words of this thread's TPT consecutive tokens
@@ -1442,7 +1442,15 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     const int c = 1 + lane + 64 * i;
                     const bool in = c < nch;
                     if (in && !cur(w0[i])) flags |= FLAG_POOL;     // cannot happen: it counted itself done
-                    const int n = in ? (int)(w0[i] & 0xFFFF) : 0;
+                    // A header lists more than SLOTS runs only with FLAG_POOL (its runs did not
+                    // fit and were not published); one without it would send the walk past the
+                    // chunk's slots: a fault. Either way the chain takes the serial path.
+                    const bool over = in && (int)(w0[i] & 0xFFFF) > SLOTS;
+                    if (over) {
+                        if (!((w0[i] >> 16) & FLAG_POOL)) st->fault = 1;
+                        flags |= FLAG_POOL;
+                    }
+                    const int n = in && !over ? (int)(w0[i] & 0xFFFF) : 0;
                     flags |= in ? (int)((w0[i] >> 16) & 0xFF) : 0;
                     ovf += in ? (int64_t)((w0[i] >> 24) & 0xFFFF) : 0;
                     mabs = (int64_t)w1[i] > mabs ? (int64_t)w1[i] : mabs;
@@ -1475,7 +1483,15 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     const int nb = total - g0 < SB ? total - g0 : SB;     // uniform
                     const int nblk = (nb + 7) >> 3;                        // blocks of 8 runs
                     const bool mine = lane < nb;
-                    const uint32_t ent = mine ? (uint32_t)sl[g0 + lane] : (uint32_t)zslot;
+                    uint32_t ent = mine ? (uint32_t)sl[g0 + lane] : (uint32_t)zslot;
+                    // Every slot index is checked against the pool before its row is read: one
+                    // past it (a fault: the list is built from checked headers) is not loaded,
+                    // and the chain takes the serial path.
+                    if (__ballot((int)(ent & (RUN_EVENT - 1)) >= ck.pool)) {
+                        if (lane == 0) st->fault = 1;
+                        fb = true;
+                        break;
+                    }
                     // lane i: the byte offset of run i's row (lanes past the batch: the spare
                     // slot, whose contents are read but never added)
                     const uint32_t roff = (ent & (RUN_EVENT - 1)) * (uint32_t)(D * 4);
@@ -1771,6 +1787,37 @@ static void carve(const Geom &g, int64_t max_chunks, int64_t pool, uint8_t *p, C
     c.pool = (int32_t)pool;
     if (ck) *ck = c;
     if (total) *total = o;
+}
+
+void chunked_layout_facts(const Geom &g, int64_t max_chunks, int64_t *f) {
+    // carved at a stand-in base address (never dereferenced): the areas' offsets
+    uint8_t *const base = (uint8_t *)((uintptr_t)1 << 40);
+    const int64_t pool = chunked_pool_slots(max_chunks);
+    const int64_t chains = (int64_t)g.batch * g.n_kv;
+    Chunked c;
+    size_t total = 0;
+    carve(g, max_chunks, pool, base, &c, &total);
+    auto off = [&](const void *q) { return (int64_t)((const uint8_t *)q - base); };
+    // every area 256-aligned, in carve order, each ending at or before the next one's start
+    const int64_t at[] = {off(c.cmax), off(c.status), off(c.hdr), off(c.done), off(c.chain_fb),
+                          off(c.meta), off(c.segS), off(c.qd), off(c.qok), (int64_t)total};
+    const int64_t sz[] = {chains * max_chunks * GF * 8, chains * max_chunks * GF * 2 * 8,
+                          chains * max_chunks * GF * (int64_t)sizeof(ChunkHdr), chains * 4, chains * 4,
+                          chains * GF * pool * (int64_t)sizeof(SegMeta), chains * GF * pool * g.d * 4,
+                          chains * g.d * GF * 8, chains * 4};
+    bool ok = true;
+    for (int i = 0; i < 9; ++i) ok = ok && at[i] % 256 == 0 && at[i] + sz[i] <= at[i + 1];
+    f[0] = max_chunks;
+    f[1] = pool;
+    f[2] = SLOTS;
+    f[3] = max_chunks > 1 ? slot_base((int)max_chunks - 1) + SLOTS : 1;    // chunk 0: one state slot
+    f[4] = NSEG;
+    f[5] = HMAX;
+    f[6] = (int64_t)total;
+    f[7] = off(c.meta);
+    f[8] = ok ? 1 : 0;
+    f[9] = CHUNK;
+    f[10] = RUN_EVENT;
 }
 
 size_t chunked_scratch_bytes(const Geom &g, int64_t max_chunks, int64_t pool) {

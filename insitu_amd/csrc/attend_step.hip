@@ -126,7 +126,7 @@ __device__ __forceinline__ bool fits(int32_t acc, int64_t bound) {
 struct OpOr64 {
     __device__ static int64_t f(int64_t a, int64_t b) { return a | b; }
 };
-__device__ __forceinline__ int slot_base(int chunk) { return chunk == 0 ? 0 : 1 + (chunk - 1) * SLOTS; }
+__host__ __device__ __forceinline__ int slot_base(int chunk) { return chunk == 0 ? 0 : 1 + (chunk - 1) * SLOTS; }
 
 // Chunk scratch: look-back words, headers and counters first (the epoch-checked front,
 // zeroed when a launch lays the buffer out differently), then the runs and the query staging.
@@ -180,6 +180,7 @@ struct StepLds {
     int64_t min_[G], lmax[G];
     int32_t total[G];
     int qbad[G];
+    int sbad[G];                            // a replay slot index past the pool (a fault)
     int lbfail, last;
     uint64_t qaddr;                         // the query staging's address, handed over the barrier
     unsigned long long ovf, mabs;
@@ -322,6 +323,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         (&S.runL[0][0])[tid] = 0;
         (&S.runf[0][0])[tid] = 0;
     }
+    if (tid < G) S.sbad[tid] = 0;
     if (tid == 0) {
         S.ovf = S.mabs = 0;
         S.lbfail = 0;
@@ -978,11 +980,17 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
                 }
                 __builtin_amdgcn_s_sleep(2);
             }
-            // a current header lists at most SLOTS runs (chunk 0: its state, one)
-            const bool cur = in && (uint32_t)(w0 >> 40) == ep && (int)(w0 & 0xFFFF) <= SLOTS;
+            // A current header lists at most SLOTS runs (chunk 0: its state, one; a chunk whose
+            // runs did not fit publishes none, with FL_POOL); one that lists more would send the
+            // staging past the chunk's slots: a fault, and the head takes the serial path.
+            const bool cep = in && (uint32_t)(w0 >> 40) == ep;
+            const bool over = cep && (int)(w0 & 0xFFFF) > SLOTS;
+            if (over && !((w0 >> 16) & FL_POOL)) st->fault = 1;
+            const bool cur = cep && !over;
             const int n = cur && c > 0 ? (int)(w0 & 0xFFFF) : 0;
             int fl = cur ? (int)((w0 >> 16) & 0xFF) : 0;
-            if (in && !cur) fl |= FL_LB;
+            if (over) fl |= FL_POOL;
+            if (in && !cep) fl |= FL_LB;
             const int incl = (int)wave_scan_add32((uint32_t)n);
             const int start = total + incl - n;
             for (int j = 0; j < n && start + j < NSEG; ++j)
@@ -1026,11 +1034,19 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             const int hh = wv & (G - 1), part = wv / G;
             const int th = S.total[hh];
             const int64_t hbase = ((int64_t)chain * G + hh) * ck.pool;
+            // every slot index is checked against the pool before it is read: one past it
+            // (a fault: the list is built from checked headers) is not loaded, and sends the
+            // head to the serial path
             int slot[PER];
 #pragma unroll
             for (int k = 0; k < PER; ++k) {
                 const int i = g0 + part + (NW / G) * k;
                 slot[k] = i < th ? (S.u.rp.rl[hh][i] & (RUN_EVENT - 1)) : -1;
+                if (slot[k] >= ck.pool) {
+                    slot[k] = -1;
+                    st->fault = 1;
+                    S.sbad[hh] = 1;
+                }
             }
             int32_t v[PER];
 #pragma unroll
@@ -1040,8 +1056,8 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
                 if (slot[k] >= 0) S.u.rp.rs[hh][part + (NW / G) * k][lane] = v[k];
             if (wv < G) {
                 const int i = g0 + lane;
-                if (lane < RMAX && i < th) {
-                    const int sl = S.u.rp.rl[hh][i] & (RUN_EVENT - 1);
+                const int sl = lane < RMAX && i < th ? S.u.rp.rl[hh][i] & (RUN_EVENT - 1) : 0;
+                if (lane < RMAX && i < th && sl < ck.pool) {
                     const uint64_t lf = get64(&ck.meta[(hbase + sl) * 2]);
                     const uint64_t bb = get64(&ck.meta[(hbase + sl) * 2 + 1]);
                     S.u.rp.rlf[hh][lane] = lf;
@@ -1051,7 +1067,8 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         }
         __syncthreads();
         STAMP(15);
-        if (hw && g0 < tot_h) {
+        if (hw && S.sbad[h]) hflags |= FL_POOL;
+        if (hw && g0 < tot_h && !hflags) {
             // The walk. Lane k < nb holds run k's list entry, L, f and bound B; prefix sums over
             // the lanes give each block's sums. |acc| only shrinks at a rescale and grows by at
             // most a run's B per run, so |acc at a block's start| + the block's B certifies 8
@@ -1197,6 +1214,36 @@ bool step_supported(const Geom &g, int64_t capacity) {
 int64_t step_max_chunks(int64_t capacity) { return (capacity + stepk::CHUNK - 1) / stepk::CHUNK; }
 
 static int64_t step_pool(int64_t mc) { return 1 + (mc - 1) * stepk::SLOTS + 1; }
+
+void step_layout_facts(const Geom &g, int64_t mc, int64_t *f) {
+    using namespace stepk;
+    // carved at a stand-in base address (never dereferenced): the areas' offsets
+    uint8_t *const base = (uint8_t *)((uintptr_t)1 << 40);
+    const int64_t pool = step_pool(mc);
+    const int64_t chains = (int64_t)g.batch * g.n_kv;
+    Sck c;
+    size_t total = 0, front = 0;
+    carve(g, mc, pool, base, &c, &total, &front);
+    auto off = [&](const void *q) { return (int64_t)((const uint8_t *)q - base); };
+    const int64_t at[] = {off(c.status), off(c.hdr), off(c.done), off(c.meta), off(c.segS), off(c.qst),
+                          (int64_t)total};
+    const int64_t sz[] = {chains * G * 2 * mc * 8, chains * mc * G * 2 * 8, chains * 4, chains * G * pool * 2 * 8,
+                          chains * G * pool * D * 4, chains * mc * D * G * 8};
+    bool ok = true;
+    for (int i = 0; i < 6; ++i) ok = ok && at[i] % 256 == 0 && at[i] + sz[i] <= at[i + 1];
+    ok = ok && (int64_t)front == off(c.meta);
+    f[0] = mc;
+    f[1] = pool;
+    f[2] = SLOTS;
+    f[3] = mc > 1 ? slot_base((int)mc - 1) + SLOTS : 1;    // chunk 0: one state slot
+    f[4] = NSEG;
+    f[5] = HMAX;
+    f[6] = (int64_t)total;
+    f[7] = (int64_t)front;
+    f[8] = ok ? 1 : 0;
+    f[9] = CHUNK;
+    f[10] = RUN_EVENT;
+}
 
 size_t step_scratch_bytes(const Geom &g, int64_t mc) {
     size_t n = 0;

@@ -288,6 +288,17 @@ struct ChunkedApi {
 // The fused decode step's own kernel (attend_step.hip): sequential mode at d = 64, 4 query
 // heads per KV head, 4-bit keys and 2-bit values, 1,024-token chunks of 16 waves. It lays the
 // chunk scratch out its own way (scratch_layout clears the front when the layout changes).
+// The scratch layouts' invariants, for a host-side test (insitu_debug_scratch_layout):
+// f[0] chunks the layout is for, f[1] run slots per head (pool), f[2] slots per chunk after
+// chunk 0, f[3] one past the last chunk's slots, f[4] runs the replay lists per head, f[5]
+// most chunks per sequence, f[6] bytes, f[7] bytes of the epoch-checked front, f[8] 1 when
+// every area is 256-aligned and ends before the next begins, f[9] tokens per chunk, f[10]
+// the slot id limit (15 bits).
+void chunked_layout_facts(const Geom &g, int64_t max_chunks, int64_t *f);
+namespace c512 {
+void chunked_layout_facts(const Geom &g, int64_t max_chunks, int64_t *f);
+}
+void step_layout_facts(const Geom &g, int64_t mc, int64_t *f);
 bool step_supported(const Geom &g, int64_t capacity);
 int64_t step_max_chunks(int64_t capacity);
 size_t step_scratch_bytes(const Geom &g, int64_t mc);

@@ -246,3 +246,61 @@ def test_checkpoint_tensors_convert_for_the_weights():
     assert got.dtype == np.float32 and got.shape == (4, 3)
     np.testing.assert_array_equal(got.astype(np.float16), w.detach().numpy())
     assert _host_array(None) is None
+
+
+def _layout(lib, kernel, capacity, batch=1, n_kv=8, d=64):
+    f = (ctypes.c_int64 * 11)()
+    rc = lib.insitu_debug_scratch_layout(kernel, capacity, batch, n_kv, d, f, 11)
+    assert rc == 0, lib.insitu_last_error()
+    return dict(zip(["chunks", "pool", "slots", "last_end", "nseg", "hmax", "bytes", "front", "areas_ok",
+                     "chunk_tokens", "slot_limit"], list(f)))
+
+
+@pytest.mark.parametrize("kernel", [0, 1, 2])
+def test_scratch_layout_invariants(kernel):
+    """The replay's indices stay inside the carve (computed on the host, no GPU call): every
+    chunk's run slots fit the pool with the spare slot after them, slot ids fit 15 bits, the
+    areas are aligned and disjoint, and the epoch-checked front comes first."""
+    from insitu_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.skip("library not built")
+    lib = _lib.load()
+    for d in ([64, 128] if kernel < 2 else [64]):
+        for batch in (1, 3):
+            for cap in (1, 1023, 1024, 1025, 32768, 262144, 300000, 524288):
+                f = _layout(lib, kernel, cap, batch, 8, d)
+                assert f["chunks"] == -(-cap // f["chunk_tokens"])
+                if f["chunks"] > f["hmax"]:
+                    continue                  # a capacity the kernel refuses
+                assert f["areas_ok"] == 1, f
+                # the last chunk's slots end at pool - 1: the spare slot is never written
+                assert f["last_end"] == f["pool"] - 1, f
+                assert f["pool"] < f["slot_limit"], f
+                assert 0 < f["front"] <= f["bytes"], f
+    # The replay lists at most NSEG runs per head, fewer than the most a sequence can publish
+    # (HMAX - 1 chunks x SLOTS): the list's length is checked before the walk, and a head past
+    # it takes the serial path.
+    f = _layout(lib, kernel, 1024 * 512)
+    assert f["nseg"] < (f["hmax"] - 1) * f["slots"]
+    src = open(os.path.join(ROOT, "insitu_amd", "csrc",
+                            "attend_step.hip" if kernel == 2 else "attend_chunked.hip")).read()
+    assert "total > NSEG" in src
+
+
+def test_block_chunk_size_follows_capacity():
+    """A block's cache takes 512-token chunks only while the chunked attend's chunk limit
+    holds them; past 262,144 tokens it keeps 1,024-token chunks (and the chunked path)."""
+    from insitu_amd import _lib
+    from insitu_amd.block import CHUNKED_MAX_CHUNKS, default_chunk_tokens
+    src = open(os.path.join(ROOT, "insitu_amd", "csrc", "attend_chunked.hip")).read()
+    assert re.search(r"constexpr int HMAX = (\d+);", src).group(1) == str(CHUNKED_MAX_CHUNKS)
+    assert default_chunk_tokens("online", 262144) == 512
+    assert default_chunk_tokens("online", 300000) == 1024
+    assert default_chunk_tokens("split", 300000) == 1024
+    assert default_chunk_tokens("two_pass", 1000) == 1024
+    if os.path.exists(_lib.LIB_PATH):
+        lib = _lib.load()
+        for cap in (262144, 300000, 524288):
+            kernel = 1 if default_chunk_tokens("online", cap) == 512 else 0
+            f = _layout(lib, kernel, cap)
+            assert f["chunks"] <= f["hmax"], (cap, f)
