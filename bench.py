@@ -24,6 +24,7 @@ at ctx 32,768.
     python bench.py --config block          # hidden states in, hidden states out, ctx 32k
     python bench.py --config probe          # bytes-only read of the C2 scan size: the launch ceiling
     python bench.py --config short          # ctx 100 in a 131,072-token cache vs a 256-token one
+    python bench.py --config append         # the write path: 32,767 wire rows into an empty cache
 
 C3: batch 64, one layer, per-sequence contexts uniform in
 [1024, 8192] from seed 3, each sequence its own seeded k/v and query, one
@@ -91,7 +92,7 @@ def _args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--config", default="c2",
-                    choices=["c1", "c2", "c3", "c4", "prefill", "block", "probe", "short"])
+                    choices=["c1", "c2", "c3", "c4", "prefill", "block", "probe", "short", "append"])
     ap.add_argument("--prompt", type=int, default=4096)
     ap.add_argument("--c1-layers", type=int, default=16)
     ap.add_argument("--c1-steps", type=int, default=4096)
@@ -452,6 +453,70 @@ def bench_scale(a) -> int:
     return 0 if not bad else 1
 
 
+def bench_append(a) -> int:
+    """The write path at C2's shape: 32,767 wire rows (8 KV heads, d=64, 4b/2b) into an empty
+    cache, (1) rotated by two rotate launches then appended (append_rotated), (2) rotated and
+    appended in one launch (append_wire, kernel.py:271-272 + :283-284). Times from HIP events
+    on the library's stream around each call, median of the repetitions; the two paths' rows
+    are compared byte for byte."""
+    import torch
+
+    from insitu_amd import QuantConfig
+    from insitu_amd.cache import CompressedCache
+    from insitu_amd.rotate import Rotation
+    from insitu_amd.runtime import default_context
+    from insitu_amd.workload import Workload
+
+    ctx = default_context(0)
+    quant = QuantConfig(key_bits=4, value_bits=2)
+    rot = Rotation.for_quant(quant, D)
+    n = CTX - 1
+    wl = Workload(seed=0)
+    _, k, v = wl.steps(n)
+    kd = ctx.to_device(k[0], torch.int32)
+    vd = ctx.to_device(v[0], torch.int32)
+    sp = ctx.lib.insitu_ctx_stream(ctx.handle)          # None: the null stream
+    stream = torch.cuda.ExternalStream(int(sp)) if sp else torch.cuda.default_stream()
+    reps = max(a.steps, 20)
+
+    def timed(c, fn):
+        us = []
+        for i in range(reps + 2):
+            c.set_length(0)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            fn()
+            e1.record(stream)
+            e1.synchronize()
+            if i >= 2:
+                us.append(e0.elapsed_time(e1) * 1e3)
+        return np.array(us)
+
+    a_c = CompressedCache(N_KV, D, CTX, quant, n_q_heads=N_Q, ctx=ctx)
+    b_c = CompressedCache(N_KV, D, CTX, quant, n_q_heads=N_Q, ctx=ctx)
+    us_two = timed(a_c, lambda: a_c.append_rotated(rot.apply(kd, ctx), rot.apply(vd, ctx)))
+    us_one = timed(b_c, lambda: b_c.append_wire(kd, vd))
+    for h in (0, N_KV - 1):
+        if not np.array_equal(a_c.read_rows(h, 0, n), b_c.read_rows(h, 0, n)):
+            raise AssertionError("append_wire and rotate + append_rotated wrote different rows")
+    moved = n * N_KV * (2 * D * 4 + ROW)         # int32 k and v in, packed rows out
+    res = {
+        "metric": "write path: rows appended per second, C2 shape",
+        "value": round(n * N_KV / (np.median(us_one) * 1e-6) / 1e6, 2), "unit": "M rows/s",
+        "n_gpus": 1, "steps": reps, "higher_is_better": True, "dtype": "int64",
+        "data": "synthetic (seeded N(0,1) k/v with 4 outlier channels x8 per head, Q8.16)",
+        "config": {"workload": f"{n} tokens x {N_KV} KV heads, d={D}, 4b K / 2b V, into an empty cache"},
+        "append_wire_us_median": round(float(np.median(us_one)), 2),
+        "append_wire_us_min": round(float(us_one.min()), 2),
+        "rotate_then_append_us_median": round(float(np.median(us_two)), 2),
+        "append_wire_GBps": round(moved / (np.median(us_one) * 1e-6) / 1e9, 1),
+        "checked": "append_wire rows equal rotate + append_rotated rows (KV heads 0 and 7)",
+    }
+    print(json.dumps(res))
+    return 0
+
+
 def bench_short(a) -> int:
     """Decode at a short context in a large cache: ctx 100 (C2's format) in caches sized for
     131,072 tokens and for 256, the same steps on each, per-launch event times. The attend
@@ -776,6 +841,8 @@ def main() -> int:
         return bench_probe(a)
     if a.config == "short":
         return bench_short(a)
+    if a.config == "append":
+        return bench_append(a)
     if a.config != "c2":
         return bench_scale(a)
     import torch

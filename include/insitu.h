@@ -158,6 +158,13 @@ int insitu_append(insitu_cache *cache, const int32_t *k_rot_dev, const int32_t *
 /* The same for one sequence: k/v_rot_dev int32 (n_tok, n_kv_heads, d). */
 int insitu_append_seq(insitu_cache *cache, int32_t seq, const int32_t *k_rot_dev,
                       const int32_t *v_rot_dev, int32_t n_tok);
+/* kernel.py:271-272 + :283-284 in one pass: rotate wire k/v rows (Rotation.apply,
+ * rotate.py:170-197, with the cache format's rotation) and append them as insitu_append
+ * does, without the rotated copies. seq = -1: every sequence, k/v_wire_dev int32 (batch,
+ * n_tok, n_kv_heads, d); else that sequence, (n_tok, n_kv_heads, d). Rotated values beyond
+ * int32 count as range errors. */
+int insitu_append_wire(insitu_cache *cache, int32_t seq, const int32_t *k_wire_dev,
+                       const int32_t *v_wire_dev, int32_t n_tok);
 
 /* attend_online / attend_two_pass over every sequence's cache (kernel.py:337-345,
  * attention.py:429-513). q_rot_dev int32 (batch, n_q_heads, d) rotated;

@@ -28,7 +28,7 @@ EXPORTS = (
     "insitu_rotate", "insitu_encode", "insitu_qtab", "insitu_exp_lut", "insitu_finalize",
     "insitu_cache_create", "insitu_cache_destroy", "insitu_cache_reset", "insitu_cache_length",
     "insitu_cache_set_length", "insitu_cache_layout", "insitu_append", "insitu_append_seq",
-    "insitu_attend", "insitu_attend_causal", "insitu_attend_causal_head", "insitu_attend_causal_static", "insitu_step", "insitu_project", "insitu_seam_wire",
+    "insitu_append_wire", "insitu_attend", "insitu_attend_causal", "insitu_attend_causal_head", "insitu_attend_causal_static", "insitu_step", "insitu_project", "insitu_seam_wire",
     "insitu_output_projection", "insitu_read_rows", "insitu_load_rows", "insitu_read_image",
     "insitu_load_image", "insitu_probe_read", "insitu_probe_empty", "insitu_cache_debug",
     "insitu_debug_scratch_layout", "insitu_last_error",
@@ -116,6 +116,7 @@ def load(path: str | None = None):
         "insitu_cache_layout": (i32, [vp, P(Layout)]),
         "insitu_append": (i32, [vp, vp, vp, i32]),
         "insitu_append_seq": (i32, [vp, i32, vp, vp, i32]),
+        "insitu_append_wire": (i32, [vp, i32, vp, vp, i32]),
         "insitu_attend": (i32, [vp, vp, vp, i32, P(Stats)]),
         "insitu_attend_causal": (i32, [vp, i32, i64, i64, vp, vp, i32, P(Stats)]),
         "insitu_attend_causal_head": (i32, [vp, i32, i32, i64, i64, vp, vp, i32, P(Stats)]),

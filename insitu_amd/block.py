@@ -142,7 +142,7 @@ class AttentionBlock:
         v = self.ctx.to_device(vi, torch.int32).reshape(n, m.num_kv_heads, m.head_dim)
         base = self.cache.length
         qr = self.rotation.apply(q, self.ctx)
-        self.cache.append_rotated(self.rotation.apply(k, self.ctx), self.rotation.apply(v, self.ctx))
+        self.cache.append_wire(k, v)            # rotate and append in one launch
         out, st = self.attn.attend_prefill(qr, base, self.softmax, stats=stats)
         self.last_stats = st
         return out.reshape(n, m.num_heads * m.head_dim)

@@ -38,6 +38,35 @@ class KVCache(abc.ABC):
         """One token, all KV heads."""
 
     @abc.abstractmethod
+    def append_wire(self, k_wire, v_wire, *, seq: int | None = None) -> None:
+        """kernel.py:271-272 + :283-284 in one launch: rotate wire k/v rows with the
+        cache's rotation and append them (as append_rotated after Rotation.apply).
+
+        batch == 1 (or `seq` given): (tokens, n_kv_heads, d); otherwise (batch, tokens,
+        n_kv_heads, d). Raises ValueError past capacity.
+        """
+        import torch
+        k = self.ctx.to_device(k_wire, torch.int32)
+        v = self.ctx.to_device(v_wire, torch.int32)
+        if k.shape != v.shape:
+            raise ValueError(f"k {tuple(k.shape)} and v {tuple(v.shape)} differ")
+        if seq is None and self.batch == 1 and k.dim() == 3:
+            seq = 0
+        if seq is not None:
+            if k.dim() != 3 or k.shape[1:] != (self.n_kv_heads, self.head_dim):
+                raise ValueError(f"expected (tokens, {self.n_kv_heads}, {self.head_dim}), "
+                                 f"got {tuple(k.shape)}")
+            n = int(k.shape[0])
+        else:
+            if k.dim() != 4 or k.shape[0] != self.batch or \
+                    k.shape[2:] != (self.n_kv_heads, self.head_dim):
+                raise ValueError(f"expected ({self.batch}, tokens, {self.n_kv_heads}, "
+                                 f"{self.head_dim}), got {tuple(k.shape)}")
+            n = int(k.shape[1])
+        _lib.check(self.ctx.lib.insitu_append_wire(self.handle, -1 if seq is None else seq,
+                                                   ptr(k), ptr(v), n))
+        self._keep = (k, v)     # keep inputs alive until the stream has consumed them
+
     def append(self, k, v, positions, trace=None) -> None:
         """Store (tokens, n_kv_heads, head_dim) of post-RoPE K and V."""
 
@@ -280,6 +309,35 @@ class CompressedCache(KVCache):
                 raise ValueError(f"expected ({self.batch}, tokens, {self.n_kv_heads}, "
                                  f"{self.head_dim}), got {tuple(k.shape)}")
             _lib.check(self.ctx.lib.insitu_append(self.handle, ptr(k), ptr(v), int(k.shape[1])))
+        self._keep = (k, v)     # keep inputs alive until the stream has consumed them
+
+    def append_wire(self, k_wire, v_wire, *, seq: int | None = None) -> None:
+        """kernel.py:271-272 + :283-284 in one launch: rotate wire k/v rows with the
+        cache's rotation and append them (as append_rotated after Rotation.apply).
+
+        batch == 1 (or `seq` given): (tokens, n_kv_heads, d); otherwise (batch, tokens,
+        n_kv_heads, d). Raises ValueError past capacity.
+        """
+        import torch
+        k = self.ctx.to_device(k_wire, torch.int32)
+        v = self.ctx.to_device(v_wire, torch.int32)
+        if k.shape != v.shape:
+            raise ValueError(f"k {tuple(k.shape)} and v {tuple(v.shape)} differ")
+        if seq is None and self.batch == 1 and k.dim() == 3:
+            seq = 0
+        if seq is not None:
+            if k.dim() != 3 or k.shape[1:] != (self.n_kv_heads, self.head_dim):
+                raise ValueError(f"expected (tokens, {self.n_kv_heads}, {self.head_dim}), "
+                                 f"got {tuple(k.shape)}")
+            n = int(k.shape[0])
+        else:
+            if k.dim() != 4 or k.shape[0] != self.batch or \
+                    k.shape[2:] != (self.n_kv_heads, self.head_dim):
+                raise ValueError(f"expected ({self.batch}, tokens, {self.n_kv_heads}, "
+                                 f"{self.head_dim}), got {tuple(k.shape)}")
+            n = int(k.shape[1])
+        _lib.check(self.ctx.lib.insitu_append_wire(self.handle, -1 if seq is None else seq,
+                                                   ptr(k), ptr(v), n))
         self._keep = (k, v)     # keep inputs alive until the stream has consumed them
 
     def append(self, k, v, positions, trace=None) -> None:

@@ -497,6 +497,9 @@ int insitu_cache_create(insitu_ctx *c, const insitu_cache_desc *desc, insitu_cac
     for (int i = 0; i + 1 < nk; ++i) t.kbnd[i] = desc->key_bounds_host[i];
     for (int i = 0; i < nv; ++i) t.vc[i] = desc->value_centroids_host[i];
     for (int i = 0; i + 1 < nv; ++i) t.vbnd[i] = desc->value_bounds_host[i];
+    t.bnd_sorted = 1;
+    for (int i = 0; i + 2 < nk; ++i) t.bnd_sorted &= t.kbnd[i] <= t.kbnd[i + 1] ? 1 : 0;
+    for (int i = 0; i + 2 < nv; ++i) t.bnd_sorted &= t.vbnd[i] <= t.vbnd[i + 1] ? 1 : 0;
 
     hipError_t e = hipMalloc(&k->base, k->total_bytes);
     if (e == hipSuccess) e = hipMemsetAsync(k->base, 0, k->total_bytes, c->stream);
@@ -614,7 +617,7 @@ int insitu_cache_layout(const insitu_cache *k, insitu_layout *o) {
 }
 
 static int append_impl(insitu_cache *k, int seq_lo, int seq_hi, const int32_t *kr,
-                       const int32_t *vr, int32_t n_tok) {
+                       const int32_t *vr, int32_t n_tok, bool wire = false) {
     if (!k || !kr || !vr) return fail(INSITU_EINVAL, "null argument");
     if (n_tok < 0) return fail(INSITU_EBADLEN, "n_tok < 0");
     if (n_tok == 0) return INSITU_OK;
@@ -628,7 +631,8 @@ static int append_impl(insitu_cache *k, int seq_lo, int seq_hi, const int32_t *k
         }
     HIP_TRY(hipSetDevice(k->ctx->device), "hipSetDevice");
     HIP_TRY(launch_append(k->ctx->stream, k->g, k->tabs, kr, vr, n_tok, seq_lo, seq_hi,
-                          k->len_dev[k->cur], k->len_dev[k->cur ^ 1], k->stats),
+                          k->len_dev[k->cur], k->len_dev[k->cur ^ 1], k->stats,
+                          wire ? k->desc.fmt.rot_rounds : 0, wire ? k->desc.fmt.rot_signs : nullptr),
             "append launch");
     k->cur ^= 1;
     for (int b = seq_lo; b < seq_hi; ++b) k->len_host[b] += n_tok;
@@ -645,6 +649,15 @@ int insitu_append_seq(insitu_cache *k, int32_t seq, const int32_t *kr, const int
     if (!k) return fail(INSITU_EINVAL, "cache is NULL");
     if (seq < 0 || seq >= k->g.batch) return fail(INSITU_EINVAL, "no such sequence");
     return append_impl(k, seq, seq + 1, kr, vr, n_tok);
+}
+
+int insitu_append_wire(insitu_cache *k, int32_t seq, const int32_t *kw, const int32_t *vw, int32_t n_tok) {
+    if (!k) return fail(INSITU_EINVAL, "cache is NULL");
+    if (seq < -1 || seq >= k->g.batch) return fail(INSITU_EINVAL, "no such sequence");
+    if (k->desc.fmt.rot_rounds < 1 || k->desc.fmt.rot_rounds > 2)
+        return fail(INSITU_EINVAL, "the cache's format has no rotation of one or two rounds");
+    return seq < 0 ? append_impl(k, 0, k->g.batch, kw, vw, n_tok, true)
+                   : append_impl(k, seq, seq + 1, kw, vw, n_tok, true);
 }
 
 

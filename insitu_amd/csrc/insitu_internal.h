@@ -55,6 +55,7 @@ struct Tables {
     int32_t exp_table[256];   // rint(2^(-i/256) * 2^15), attention.py:106-108
     int64_t delta_max;        // attention.py:145-146
     double kc_absmax;         // max |kc[i]|, for the exactness bound of the fp64 scores
+    int32_t bnd_sorted;       // 1: both boundary lists non-decreasing (the encoder may bisect)
 };
 
 // The sign diagonals of up to two rotation rounds, one 64-bit word per 64 channels.
@@ -191,9 +192,12 @@ hipError_t launch_exp_lut(hipStream_t s, const Tables *t, const int64_t *delta, 
                           int32_t *p);
 hipError_t launch_finalize(hipStream_t s, const int64_t *acc, const int64_t *l, int rows, int d,
                            int64_t *out, int64_t *recip, int32_t *shift);
+// Append n_tok rows of k/v ([seq][tok][kv head][d], int32) to sequences [seq_lo, seq_hi);
+// rounds > 0 rotates them first (wire rows, rotate.py:170-197, `signs` as launch_rotate's).
 hipError_t launch_append(hipStream_t s, const Geom &g, const Tables *t, const int32_t *k,
                          const int32_t *v, int n_tok, int seq_lo, int seq_hi, const int64_t *len_in,
-                         int64_t *len_out, DevStats *st);
+                         int64_t *len_out, DevStats *st, int rounds = 0,
+                         const uint64_t (*signs)[2] = nullptr);
 bool chunked_supported(const Geom &g, int64_t capacity);
 int64_t chunked_max_chunks(int64_t capacity);
 int64_t chunked_pool_slots(int64_t max_chunks);

@@ -164,7 +164,16 @@ __device__ __forceinline__ int64_t norm_wire(const int64_t (&x)[CPL], int d, int
 #pragma unroll
     for (int k = 0; k < CPL; ++k) sq += x[k] * x[k];
     sq = wave_sum_i64(sq);
-    int64_t mean = sq >= 0 ? sq / d : -((-sq + d - 1) / d);   // floor division
+    // floor(sq / d), sq >= 0: a shift for the power-of-two widths (no 64-bit division)
+    int64_t mean;
+    if (d == 64)
+        mean = sq >> 6;
+    else if (d == 128)
+        mean = sq >> 7;
+    else if (d == 32)
+        mean = sq >> 5;
+    else
+        mean = sq >= 0 ? sq / d : -((-sq + d - 1) / d);
     int64_t n = isqrt64(mean);
     int64_t w = rshift_even(n, QK_FRAC - norm_frac);
     if (w > 32767) w = 32767;
@@ -246,6 +255,76 @@ __device__ __forceinline__ uint32_t *row_word_ptr(const Geom &g, int b, int h, i
     int p = 0;
     while (p + 1 < g.n_planes && byte >= g.plane_lo[p + 1]) ++p;
     return (uint32_t *)(plane_ptr(g, b, h, p) + pos * g.plane_w[p] + (byte - g.plane_lo[p]));
+}
+
+// Where dword w of a row lives, relative to its (sequence, KV head) base: plane offset plus
+// the byte within the token's plane entry, and the plane's width (the stride per token).
+// The plane search reads the layout's arrays by a computed index, so a kernel does it once,
+// before its loop over rows, and keeps the result in registers.
+struct WordLoc {
+    int64_t off;
+    int32_t stride;
+};
+__device__ __forceinline__ WordLoc word_loc(const Geom &g, int w) {
+    const int byte = 4 * w;
+    int p = 0;
+    while (p + 1 < g.n_planes && byte >= g.plane_lo[p + 1]) ++p;
+    return WordLoc{(int64_t)p * g.span + (byte - g.plane_lo[p]), g.plane_w[p]};
+}
+__device__ __forceinline__ uint32_t *word_ptr(const Geom &g, const WordLoc &l, int b, int h, int64_t pos) {
+    return (uint32_t *)(g.base + (int64_t)b * g.seq_stride + (int64_t)h * g.head_stride + l.off + pos * l.stride);
+}
+
+// The words a lane stores under pack_store_row_regs: its key and value words (channel
+// lane + 64 q leads its word's group) and, lane 0, the norms' word.
+template <int CPL>
+struct RegPackLocs {
+    WordLoc k[CPL], v[CPL], n;
+};
+template <int CPL>
+__device__ __forceinline__ RegPackLocs<CPL> reg_pack_locs(const Geom &g) {
+    const int lane = threadIdx.x & 63;
+    const int kwords = g.key_bytes / 4, vwords = g.value_bytes / 4;
+    const int kper = 32 / g.kb, vper = 32 / g.vb;
+    RegPackLocs<CPL> L;
+#pragma unroll
+    for (int q = 0; q < CPL; ++q) {
+        const int ch = lane + 64 * q;
+        L.k[q] = word_loc(g, ch / kper < kwords ? ch / kper : 0);
+        L.v[q] = word_loc(g, kwords + (ch / vper < vwords ? ch / vper : 0));
+    }
+    L.n = word_loc(g, kwords + vwords);
+    return L;
+}
+
+// One wave packs and stores the row of (sequence b, KV head h) at token pos from codes in
+// registers (lane = channel, lane + 64), for widths that divide 32: a word holds 32 / bits
+// codes, LSB first (quantize.py:271-289); each lane shifts its code into place, an OR over
+// its group of lanes (lane xor 1, 2, ...) gives the word in every lane of the group, and
+// the group's first lane stores it.
+template <int CPL>
+__device__ __forceinline__ void pack_store_row_regs(const Geom &g, const RegPackLocs<CPL> &L, const int (&kc)[CPL],
+                                                    const int (&vc)[CPL], int64_t nk, int64_t nv, int b, int h,
+                                                    int64_t pos) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+        const int bits = f == 0 ? g.kb : g.vb;
+        const int per = 32 / bits;
+#pragma unroll
+        for (int q = 0; q < CPL; ++q) {
+            const int ch = lane + 64 * q;
+            const int code = f == 0 ? kc[q] : vc[q];
+            uint32_t w = ch < g.d ? (uint32_t)code << (bits * (ch & (per - 1))) : 0u;
+            w |= xor_lane32<1>(w, lane);
+            w |= xor_lane32<2>(w, lane);
+            if (per > 4) w |= xor_lane32<4>(w, lane);
+            if (per > 8) w |= xor_lane32<8>(w, lane);
+            if (per > 16) w |= xor_lane32<16>(w, lane);
+            if (ch < g.d && (ch & (per - 1)) == 0) *word_ptr(g, f == 0 ? L.k[q] : L.v[q], b, h, pos) = w;
+        }
+    }
+    if (lane == 0) *word_ptr(g, L.n, b, h, pos) = (uint32_t)(nk & 0xFFFF) | ((uint32_t)(nv & 0xFFFF) << 16);
 }
 
 // One wave packs the row of (sequence b, KV head h) at token pos and stores it.

@@ -87,61 +87,139 @@ hipError_t launch_encode(hipStream_t s, const int32_t *x, int64_t n_vec, int d, 
 }
 
 // ---------------------------------------------------------------------------
-// append: one wave per (sequence, token, kv head) -> one packed row
+// append: every wave packs rows in turn, lane = channel
 // ---------------------------------------------------------------------------
 
-template <int CPL>
-__global__ void __launch_bounds__(64) append_kernel(Geom g, const Tables *__restrict__ tabs,
-                                                    const int32_t *__restrict__ k,
-                                                    const int32_t *__restrict__ v, int n_tok,
-                                                    int seq_lo, const int64_t *__restrict__ len_in,
-                                                    int64_t *len_out, int seq_hi,
-                                                    DevStats *st) {
-    __shared__ uint8_t codes[2][MAX_D];
-    __shared__ int64_t bnd[2][255];
-    const int lane = threadIdx.x;
-    const int h = blockIdx.x % g.n_kv;
-    stage_bounds(tabs, g, bnd);
-    const int t = (blockIdx.x / g.n_kv) % n_tok;
-    const int b = seq_lo + blockIdx.x / (g.n_kv * n_tok);
-    const int d = g.d;
+// The code of x under the boundaries bnd[0 .. n_b), #{i : (x << s) > norm * bnd[i]}
+// (quantize.py:183-196). With the boundaries non-decreasing and norm >= 0 the compare is
+// true for a prefix of i, so the count is found by bisection: log2(n_b + 1) compares.
+__device__ __forceinline__ int encode_bisect(int64_t x, int64_t norm, const int64_t *bnd, int bits,
+                                             int norm_frac) {
+    const int64_t xs = x << (CENT_FRAC + norm_frac - QK_FRAC);
+    const int n_b = (1 << bits) - 1;
+    int c = 0;
+    for (int step = 1 << (bits - 1); step > 0; step >>= 1) {
+        const int i = c + step - 1;
+        if (i < n_b && xs > norm * bnd[i]) c += step;
+    }
+    return c;
+}
 
-    // The length bookkeeping rides on block 0: len_out = len_in + n_tok for the
+// One wave: the norm and codes of a field in registers (lane = channel): the codes into
+// c (registers) and codes[0 .. d) (LDS, for the widths the register packer does not take).
+template <int CPL>
+__device__ __forceinline__ int64_t encode_field_fast(const int64_t (&x)[CPL], int d, int norm_frac,
+                                                     const int64_t *__restrict__ bnd, int bits, bool bisect,
+                                                     int (&c)[CPL], uint8_t *codes, bool to_lds) {
+    const int lane = threadIdx.x & 63;
+    const int64_t n = norm_wire<CPL>(x, d, norm_frac);
+#pragma unroll
+    for (int q = 0; q < CPL; ++q) {
+        const int ch = lane + 64 * q;
+        c[q] = bisect ? encode_bisect(x[q], n, bnd, bits, norm_frac)
+                      : encode_one(x[q], n, bnd, (1 << bits) - 1, norm_frac);
+        if (to_lds && ch < d) codes[ch] = (uint8_t)c[q];
+    }
+    return n;
+}
+
+// Rows in (sequence, KV head, token) order, token fastest, so that the waves of a
+// workgroup write neighbouring rows of each plane. Each wave takes rows wave, wave + W,
+// ... (W waves in the grid) and loads its next row's k and v while it encodes the current
+// one. ROT: the rows are wire values and are rotated first (the decode step's rotation,
+// rotate.py:170-197), so that a prompt's k/v go from the wire to the cache in one pass.
+constexpr int APPEND_WAVES = 4;
+
+template <int CPL, bool ROT>
+__global__ void __launch_bounds__(64 * APPEND_WAVES) append_kernel(
+        Geom g, const Tables *__restrict__ tabs, const int32_t *__restrict__ k, const int32_t *__restrict__ v,
+        int n_tok, int seq_lo, const int64_t *__restrict__ len_in, int64_t *len_out, int seq_hi, int rounds,
+        RotSigns sg, DevStats *st) {
+    __shared__ uint8_t codes[APPEND_WAVES][2][MAX_D];
+    __shared__ int64_t bnd[2][255];
+    // wv is uniform in the wave: the row indices below are then scalar
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    stage_bounds(tabs, g, bnd);
+    // The length bookkeeping rides on workgroup 0: len_out = len_in + n_tok for the
     // sequences this call appends to, len_in elsewhere (double-buffered so no
-    // block can observe a half-updated length).
+    // workgroup can observe a half-updated length).
     if (blockIdx.x == 0) {
-        for (int i = lane; i < g.batch; i += 64)
+        for (int i = threadIdx.x; i < g.batch; i += blockDim.x)
             len_out[i] = len_in[i] + ((i >= seq_lo && i < seq_hi) ? n_tok : 0);
     }
-
-    const int64_t pos = len_in[b] + t;
-    if (pos >= g.capacity) {     // the host checks capacity first; this only guards memory
-        if (lane == 0) atomicAdd(&st->fault, 1ull);
-        return;
-    }
-    const int64_t src = (((int64_t)(b - seq_lo) * n_tok + t) * g.n_kv + h) * d;
+    const bool bisect = tabs->bnd_sorted != 0;
+    const bool regpack = (32 % g.kb) == 0 && (32 % g.vb) == 0;   // widths 1, 2, 4, 8
+    // where this lane's stores go, relative to a row's (sequence, KV head) and token
+    const RegPackLocs<CPL> locs = reg_pack_locs<CPL>(g);
+    const WordLoc myloc = word_loc(g, lane < g.row_bytes / 4 ? lane : 0);
     __syncthreads();
-    int64_t nk, nv;
-    {
-        int64_t x[CPL];
+    const int d = g.d;
+    // Wave w takes the contiguous rows [w R, (w + 1) R) of the (sequence, KV head, token)
+    // order: its first row's indices by division, then token by token.
+    const int64_t rows = (int64_t)(seq_hi - seq_lo) * g.n_kv * n_tok;
+    const int64_t nwaves = (int64_t)gridDim.x * APPEND_WAVES;
+    const int64_t per = (rows + nwaves - 1) / nwaves;
+    const int64_t r0 = ((int64_t)blockIdx.x * APPEND_WAVES + wv) * per;
+    const int64_t r1 = r0 + per < rows ? r0 + per : rows;
+    if (r0 >= r1) return;
+    int t = (int)(r0 % n_tok);
+    int h = (int)((r0 / n_tok) % g.n_kv);
+    int bb = (int)(r0 / ((int64_t)n_tok * g.n_kv));          // sequence - seq_lo
+    auto src_of = [&](int b_, int t_, int h_) { return (((int64_t)b_ * n_tok + t_) * g.n_kv + h_) * d; };
+    int32_t kn[CPL], vn[CPL];
+    load_vec<CPL>(k + src_of(bb, t, h), d, kn);
+    load_vec<CPL>(v + src_of(bb, t, h), d, vn);
+    int64_t base_len = len_in[seq_lo + bb];
+    for (int64_t r = r0; r < r1; ++r) {
+        int32_t kc[CPL], vc[CPL];
 #pragma unroll
         for (int q = 0; q < CPL; ++q) {
-            int ch = lane + 64 * q;
-            x[q] = ch < d ? (int64_t)k[src + ch] : 0;
+            kc[q] = kn[q];
+            vc[q] = vn[q];
         }
-        nk = encode_field<CPL>(x, d, g.norm_frac, bnd[0], (1 << g.kb) - 1, codes[0]);
-    }
-    {
-        int64_t x[CPL];
+        const int b = seq_lo + bb;
+        const int hh = h;
+        const int64_t pos = base_len + t;
+        // the next row's indices, and its k and v in flight while this one is encoded
+        if (++t == n_tok) {
+            t = 0;
+            if (++h == g.n_kv) {
+                h = 0;
+                ++bb;
+            }
+        }
+        if (r + 1 < r1) {
+            load_vec<CPL>(k + src_of(bb, t, h), d, kn);
+            load_vec<CPL>(v + src_of(bb, t, h), d, vn);
+        }
+        if (pos >= g.capacity) {     // the host checks capacity first; this only guards memory
+            if (lane == 0) atomicAdd(&st->fault, 1ull);
+        } else {
+            if (ROT) {
+                rotate_loaded<CPL>(kc, d, rounds, sg, kc, &st->range_errors);
+                rotate_loaded<CPL>(vc, d, rounds, sg, vc, &st->range_errors);
+            }
+            int64_t xk[CPL], xv[CPL];
 #pragma unroll
-        for (int q = 0; q < CPL; ++q) {
-            int ch = lane + 64 * q;
-            x[q] = ch < d ? (int64_t)v[src + ch] : 0;
+            for (int q = 0; q < CPL; ++q) {
+                xk[q] = kc[q];
+                xv[q] = vc[q];
+            }
+            int ck[CPL], cv[CPL];
+            const int64_t nk = encode_field_fast<CPL>(xk, d, g.norm_frac, bnd[0], g.kb, bisect, ck, codes[wv][0], !regpack);
+            const int64_t nv = encode_field_fast<CPL>(xv, d, g.norm_frac, bnd[1], g.vb, bisect, cv, codes[wv][1], !regpack);
+            if (regpack) {
+                pack_store_row_regs<CPL>(g, locs, ck, cv, nk, nv, b, hh, pos);
+            } else {
+                __builtin_amdgcn_wave_barrier();         // the wave's codes, written above, read below
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                if (lane < g.row_bytes / 4) *word_ptr(g, myloc, b, hh, pos) = pack_row_word(g, codes[wv], nk, nv, lane);
+                __builtin_amdgcn_wave_barrier();         // the codes are read before the next row's
+            }
         }
-        nv = encode_field<CPL>(x, d, g.norm_frac, bnd[1], (1 << g.vb) - 1, codes[1]);
+        if (seq_lo + bb != b && r + 1 < r1) base_len = len_in[seq_lo + bb];
     }
-    __syncthreads();
-    pack_store_row(g, codes, nk, nv, b, h, pos);
 }
 
 // ---------------------------------------------------------------------------
@@ -235,17 +313,32 @@ hipError_t launch_step_write(hipStream_t s, const Geom &g, const Tables *t, cons
 
 hipError_t launch_append(hipStream_t s, const Geom &g, const Tables *t, const int32_t *k,
                          const int32_t *v, int n_tok, int seq_lo, int seq_hi, const int64_t *len_in,
-                         int64_t *len_out, DevStats *st) {
-    const int64_t blocks = (int64_t)(seq_hi - seq_lo) * n_tok * g.n_kv;
-    if (blocks <= 0) return hipSuccess;
-    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
-    dim3 grid((unsigned)blocks), block(64);
-    if (g.d <= 64)
-        hipLaunchKernelGGL(append_kernel<1>, grid, block, 0, s, g, t, k, v, n_tok, seq_lo, len_in,
-                           len_out, seq_hi, st);
-    else
-        hipLaunchKernelGGL(append_kernel<2>, grid, block, 0, s, g, t, k, v, n_tok, seq_lo, len_in,
-                           len_out, seq_hi, st);
+                         int64_t *len_out, DevStats *st, int rounds, const uint64_t (*signs)[2]) {
+    const int64_t rows = (int64_t)(seq_hi - seq_lo) * n_tok * g.n_kv;
+    if (rows <= 0) return hipSuccess;
+    if (rounds < 0 || rounds > 2 || (rounds && !signs)) return hipErrorInvalidValue;
+    const RotSigns sg = rounds ? rot_signs(rounds, signs) : RotSigns{};
+    // about 8 rows a wave at the most, 4 waves a workgroup, up to 8 workgroups a CU
+    int64_t blocks = (rows + 8 * APPEND_WAVES - 1) / (8 * APPEND_WAVES);
+    if (blocks > 2048) blocks = 2048;
+    if (blocks < 1) blocks = 1;
+    dim3 grid((unsigned)blocks), block(64 * APPEND_WAVES);
+    const bool rot = rounds > 0;
+    if (g.d <= 64) {
+        if (rot)
+            hipLaunchKernelGGL((append_kernel<1, true>), grid, block, 0, s, g, t, k, v, n_tok, seq_lo, len_in,
+                               len_out, seq_hi, rounds, sg, st);
+        else
+            hipLaunchKernelGGL((append_kernel<1, false>), grid, block, 0, s, g, t, k, v, n_tok, seq_lo, len_in,
+                               len_out, seq_hi, rounds, sg, st);
+    } else {
+        if (rot)
+            hipLaunchKernelGGL((append_kernel<2, true>), grid, block, 0, s, g, t, k, v, n_tok, seq_lo, len_in,
+                               len_out, seq_hi, rounds, sg, st);
+        else
+            hipLaunchKernelGGL((append_kernel<2, false>), grid, block, 0, s, g, t, k, v, n_tok, seq_lo, len_in,
+                               len_out, seq_hi, rounds, sg, st);
+    }
     return hipGetLastError();
 }
 
