@@ -25,6 +25,7 @@ at ctx 32,768.
     python bench.py --config probe          # bytes-only read of the C2 scan size: the launch ceiling
     python bench.py --config short          # ctx 100 in a 131,072-token cache vs a 256-token one
     python bench.py --config append         # the write path: 32,767 wire rows into an empty cache
+    python bench.py --config formats        # decode steps with 8 query heads 3b/2b and 2 query heads 4b/2b
 
 C3: batch 64, one layer, per-sequence contexts uniform in
 [1024, 8192] from seed 3, each sequence its own seeded k/v and query, one
@@ -92,7 +93,7 @@ def _args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
     ap.add_argument("--config", default="c2",
-                    choices=["c1", "c2", "c3", "c4", "prefill", "block", "probe", "short", "append"])
+                    choices=["c1", "c2", "c3", "c4", "prefill", "block", "probe", "short", "append", "formats"])
     ap.add_argument("--prompt", type=int, default=4096)
     ap.add_argument("--c1-layers", type=int, default=16)
     ap.add_argument("--c1-steps", type=int, default=4096)
@@ -517,6 +518,74 @@ def bench_append(a) -> int:
     return 0
 
 
+def bench_formats(a) -> int:
+    """Decode steps in formats outside C2's: the reference's default 3-bit keys with 8 query
+    heads a KV head (TinyLlama's group, config.py:122-125, 141), and 2 query heads a KV head
+    with 4-bit keys, each at ctx 9,000 (8 KV heads, d=64, 2-bit values): per-launch event
+    times of the attend over 50 steps, the statistics' serial fallbacks (0: every head on
+    the fast path), and the last step checked against the oracle."""
+    import torch
+
+    from insitu_amd import QuantConfig, _lib
+    from insitu_amd.cache import CompressedCache
+    from insitu_amd.runtime import default_context, ptr
+    from oracle import native
+    from oracle.quantize import Cache, Format
+
+    ctx = default_context(0)
+    lib = ctx.lib
+    rng = np.random.default_rng(9)
+    T0, reps = 9000, max(a.steps, 50)
+    lines = {}
+    for name, G, kb in (("G8_3b2b", 8, 3), ("G2_4b2b", 2, 4)):
+        quant = QuantConfig(key_bits=kb, value_bits=2)
+        f = Format(key_bits=kb, value_bits=2)
+        n_q = N_KV * G
+        # N(0, 1) rows in Q8.16, the wire's format (the prompt's rows rotated as a step would)
+        def wire(*shape):
+            return np.rint(rng.standard_normal(shape) * 65536.0).astype(np.int64)
+        sg = __import__("oracle.rotate", fromlist=["signs_from_seed"]).signs_from_seed(D, 0, 1)
+        rot = __import__("oracle.rotate", fromlist=["rotate"]).rotate
+        kr = rot(wire(T0 * N_KV, D), sg).reshape(T0, N_KV, D)
+        vr = rot(wire(T0 * N_KV, D), sg).reshape(T0, N_KV, D)
+        c = CompressedCache(N_KV, D, T0 + reps + a.warmup, quant, n_q_heads=n_q, ctx=ctx)
+        c.append_rotated(kr, vr)
+        qw = ctx.to_device(wire(reps + a.warmup, n_q, D), torch.int32)
+        kw = ctx.to_device(wire(reps + a.warmup, N_KV, D), torch.int32)
+        vw = ctx.to_device(wire(reps + a.warmup, N_KV, D), torch.int32)
+        out = torch.empty((n_q, D), dtype=torch.int32, device=ctx.torch_device)
+        st = _lib.Stats()
+        serial = 0
+
+        def launch(i):
+            nonlocal serial
+            _lib.check(lib.insitu_step(c.handle, ptr(qw[i]), ptr(kw[i]), ptr(vw[i]), ptr(out), 0, st))
+            serial += st.serial_fallbacks
+
+        for i in range(a.warmup):
+            launch(i)
+        c.set_length(T0)
+        us = _timed_each(ctx, lambda i: launch(a.warmup + i), reps)
+        # the last step against the oracle over the cache's rows
+        q_last = rotate_q(qw[a.warmup + reps - 1].cpu().numpy())
+        want = np.concatenate([native.attend_online(q_last[G * h:G * h + G], c.view(h), f)[0]
+                               for h in range(N_KV)])
+        if not np.array_equal(want, out.cpu().numpy().astype(np.int64).reshape(-1, D)):
+            raise AssertionError(f"{name}: the last step disagrees with the oracle")
+        lines[name] = {"query_heads_per_kv_head": G, "key_bits": kb, "value_bits": 2,
+                       "ctx_first": T0 + 1, "attend_us_median": round(float(np.median(us)), 3),
+                       "attend_us_min": round(float(us.min()), 3), "serial_fallbacks": int(serial),
+                       "GB/s": round(N_KV * c.layout()["row_bytes"] * (T0 + reps // 2) /
+                                     (np.median(us) * 1e-6) / 1e9, 1)}
+    res = {"metric": "decode step (rotate + append + attend) in other formats: attend us",
+           "value": lines["G8_3b2b"]["attend_us_median"], "unit": "us", "n_gpus": 1, "steps": reps,
+           "higher_is_better": False, "dtype": "int64", "data": "synthetic (seeded N(0,1) q/k/v, Q8.16)",
+           "config": {"workload": "8 KV heads, d=64, ctx 9,000 on, batch 1"}, "formats": lines,
+           "checked": "the last step of each format equal to oracle/c attend_online"}
+    print(json.dumps(res))
+    return 0
+
+
 def bench_short(a) -> int:
     """Decode at a short context in a large cache: ctx 100 (C2's format) in caches sized for
     131,072 tokens and for 256, the same steps on each, per-launch event times. The attend
@@ -843,6 +912,8 @@ def main() -> int:
         return bench_short(a)
     if a.config == "append":
         return bench_append(a)
+    if a.config == "formats":
+        return bench_formats(a)
     if a.config != "c2":
         return bench_scale(a)
     import torch

@@ -178,6 +178,8 @@ struct insitu_cache {
     int32_t *wire_scratch = nullptr;      // insitu_step: the rotated queries
     const ChunkedApi *api = nullptr;      // the chunked attend's build: 1,024- or 512-token chunks
     bool chunked = false;                 // the chunked attend handles this format and capacity
+    bool vsplit = false;                  // ... seeing each KV head's 8 query heads as two chains of 4
+    bool gpad = false;                    // ... computing fewer than 4 query heads a KV head in 4 slots
     bool scan = false;                    // the scan attend does (sequential mode)
     bool step = false;                    // the fused step's own kernel does (sequential mode)
     int64_t step_mc = 0;                  // its layout: chunks per sequence
@@ -409,6 +411,22 @@ int insitu_finalize(insitu_ctx *c, const int64_t *acc, const int64_t *l, int32_t
     return INSITU_OK;
 }
 
+// The geometry the chunked attend sees: the cache's, or with every KV head as two chains of
+// 4 query heads (vsplit; planes from KV head h >> 1).
+static Geom chunk_geom(const insitu_cache *k, Geom g) {
+    if (k->vsplit) {
+        g.n_kv *= 2;
+        g.G = 4;
+        g.kv_shift = 1;
+    } else if (k->gpad) {
+        // 1 to 3 query heads a KV head: the chain's 4 slots compute head h % G (the slots
+        // past G duplicate; their outputs and statistics are dropped)
+        g.gq = g.G;
+        g.G = 4;
+    }
+    return g;
+}
+
 int insitu_cache_create(insitu_ctx *c, const insitu_cache_desc *desc, insitu_cache **out) {
     if (!c || !desc || !out) return fail(INSITU_EINVAL, "null argument");
     *out = nullptr;
@@ -519,6 +537,18 @@ int insitu_cache_create(insitu_ctx *c, const insitu_cache_desc *desc, insitu_cac
     k->chunked = k->api->supported(g, desc->capacity);
     k->scan = scan_supported(g, desc->capacity);
     k->step = step_supported(g, desc->capacity);
+    if (!k->chunked && !k->scan && g.G == 8) {
+        // 8 query heads a KV head, in a format only the chunked attend takes: as two chains of
+        // 4 query heads over the same rows (the rows are read twice, the recurrence is each
+        // head's own either way)
+        k->vsplit = true;
+        k->chunked = k->api->supported(chunk_geom(k, g), desc->capacity);
+        k->vsplit = k->chunked;
+    } else if (!k->chunked && g.G >= 1 && g.G < 4) {
+        k->gpad = true;
+        k->chunked = k->api->supported(chunk_geom(k, g), desc->capacity);
+        k->gpad = k->chunked;
+    }
     if (e == hipSuccess && (k->chunked || k->scan || k->step)) {
         size_t nb = 0;
         if (k->step) {
@@ -528,7 +558,7 @@ int insitu_cache_create(insitu_ctx *c, const insitu_cache_desc *desc, insitu_cac
         if (k->chunked) {
             k->max_chunks = k->api->max_chunks(desc->capacity);
             k->pool = k->api->pool_slots(k->max_chunks);
-            const size_t nc = k->api->scratch_bytes(g, k->max_chunks, k->pool);
+            const size_t nc = k->api->scratch_bytes(chunk_geom(k, g), k->max_chunks, k->pool);
             nb = nc > nb ? nc : nb;
         }
         if (k->scan) {
@@ -719,7 +749,7 @@ static int attend_impl(insitu_cache *k, const int32_t *q, int32_t *out, int32_t 
         k->scr.spin_limit = k->spin_limit;
         int64_t longest = 0;
         for (int64_t n : k->len_host) longest = n > longest ? n : longest;
-        HIP_TRY(k->api->launch(k->ctx->stream, k->g, k->tabs, q, out, len, k->scr, ep,
+        HIP_TRY(k->api->launch(k->ctx->stream, chunk_geom(k, k->g), k->tabs, q, out, len, k->scr, ep,
                                k->max_chunks, k->pool, two_pass, q_staged, step, ev, k->stats, 0,
                                k->api->max_chunks(longest + (step ? 1 : 0))),
                 "chunked attend launch");
@@ -771,6 +801,7 @@ struct PrefillPlan {
     size_t bytes;
 };
 PrefillPlan prefill_plan(const ChunkedApi &api, const Geom &gv, int64_t base, int64_t n_q, size_t budget) {
+    // gv: the geometry the chunked attend sees (chunk_geom)
     PrefillPlan pl{};
     pl.max_chunks = api.max_chunks(base + n_q);
     pl.pool = api.pool_slots(pl.max_chunks);
@@ -811,7 +842,7 @@ static int prefill_launches(insitu_cache *k, const Geom &gv, const PrefillPlan &
             uint32_t ep = 0;
             HIP_TRY(scratch_begin(k->ctx->stream, scr, &ep), "scratch clear");
             scr.spin_limit = k->spin_limit;
-            HIP_TRY(k->api->launch(k->ctx->stream, gb, k->tabs, q + i0 * row, out + i0 * row, len_dev,
+            HIP_TRY(k->api->launch(k->ctx->stream, chunk_geom(k, gb), k->tabs, q + i0 * row, out + i0 * row, len_dev,
                                    scr, ep, pl.max_chunks, pl.pool, mode == INSITU_TWO_PASS ? 1 : 0,
                                    false, nullptr, ev, k->stats, pl.qb, 0),
                     "prefill attend launch");
@@ -848,7 +879,7 @@ static int causal_impl(insitu_cache *k, const Geom &gv, int64_t base, int64_t n_
     int rc = stats ? zero_stats(k) : INSITU_OK;
     if (rc) return rc;
     if (n_q == 0) return copy_stats(k, stats);
-    const PrefillPlan pl = prefill_plan(*k->api, gv, base, n_q, PREFILL_SCRATCH_BUDGET);
+    const PrefillPlan pl = prefill_plan(*k->api, chunk_geom(k, gv), base, n_q, PREFILL_SCRATCH_BUDGET);
     if (!k->prefill_len) HIP_TRY(hipMalloc(&k->prefill_len, PREFILL_QB * sizeof(int64_t)), "hipMalloc");
     if (mode != INSITU_SERIAL && k->chunked && k->prefill_scr.bytes < pl.bytes) {
         // grow: the old buffer may still be in use by queued launches
@@ -907,9 +938,9 @@ int insitu_attend_causal_static(insitu_cache *k, int32_t seq, int64_t base, int6
     gv.seq_stride = 0;
     PrefillPlan pl{};
     if (mode != INSITU_SERIAL && k->chunked) {
-        pl = prefill_plan(*k->api, gv, base, n_q, ss.cs.bytes);
+        pl = prefill_plan(*k->api, chunk_geom(k, gv), base, n_q, ss.cs.bytes);
         if (pl.qb < 1) {
-            Geom one = gv;
+            Geom one = chunk_geom(k, gv);
             one.batch = 1;
             char buf[240];
             snprintf(buf, sizeof buf, "one query over %lld rows needs %zu B of chunk scratch; the static "
@@ -943,8 +974,10 @@ int insitu_step(insitu_cache *k, const int32_t *q, const int32_t *kw, const int3
     // (which also stages the rotated queries for a chunked attend) and the attend.
     const bool scan = use_scan(k, mode);
     const bool chunked = !scan && mode != INSITU_SERIAL && k->chunked;
+    // (a KV head seen as two chains would write its new row twice, and duplicate query slots
+    // would count the rotation's range errors twice: two launches then)
     const bool fused = scan || use_step_kernel(k, mode) ||
-                       (mode != INSITU_TWO_PASS && chunked && chunked_fused_step(g));
+                       (mode != INSITU_TWO_PASS && chunked && !k->vsplit && !k->gpad && chunked_fused_step(g));
     if (fused) {
         StepIn si;
         si.qw = q;
@@ -962,7 +995,10 @@ int insitu_step(insitu_cache *k, const int32_t *q, const int32_t *kw, const int3
     double *qd = nullptr;
     int32_t *qok = nullptr;
     uint32_t ep = 0;
-    if (chunked) {
+    // the chunked attend's query staging (4 query heads a KV head, as the write kernel stages
+    // them; a KV head seen as two chains reads the rotated queries instead)
+    const bool staged = chunked && !k->vsplit && !k->gpad;
+    if (staged) {
         // the epoch (and the wrap's clear) before the write kernel stages the queries
         HIP_TRY(scratch_begin(k->ctx->stream, k->scr, &ep), "scratch clear");
         k->api->query_area(g, k->max_chunks, k->pool, k->scr.p, &qd, &qok);
@@ -973,7 +1009,7 @@ int insitu_step(insitu_cache *k, const int32_t *q, const int32_t *kw, const int3
             "step write launch");
     k->cur ^= 1;
     for (int b = 0; b < g.batch; ++b) k->len_host[b] += 1;
-    rc = attend_impl(k, qr, out, mode, chunked, nullptr, ep);
+    rc = attend_impl(k, qr, out, mode, staged, nullptr, ep);
     if (rc) return rc;
     return copy_stats(k, stats);
 }

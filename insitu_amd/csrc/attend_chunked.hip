@@ -254,6 +254,13 @@ struct ChunkLds {
 };
 
 // Run slots: chunk 0 owns slot 0 (its replayed state), chunk c > 0 owns SLOTS after it.
+// The query head that slot h of KV head kvh's chain computes: its own (GF a KV head), or
+// with g.gq query heads a KV head (fewer than GF) head h % gq: the slots from gq on compute
+// duplicates of the first gq, whose outputs and statistics are dropped.
+__device__ __forceinline__ int qhead(const Geom &g, int kvh, int h) {
+    return g.gq ? kvh * g.gq + h % g.gq : kvh * GF + h;
+}
+__device__ __forceinline__ bool real_head(const Geom &g, int h) { return g.gq == 0 || h < g.gq; }
 __host__ __device__ __forceinline__ int slot_base(int chunk) { return chunk == 0 ? 0 : 1 + (chunk - 1) * SLOTS; }
 static_assert(1 + (HMAX - 1) * SLOTS < RUN_EVENT, "run slots of the chunked path fit 15 bits");
 
@@ -380,7 +387,7 @@ __global__ void __launch_bounds__(CT) chunk_max_kernel(Geom g, const Tables *__r
     // centroid table while they land
     int32_t q_t[D / 64];
     if (!QS && wv < GF) {
-        const int32_t *qrow = q + ((int64_t)b * g.n_q + kvh * GF + wv) * D;
+        const int32_t *qrow = q + ((int64_t)b * g.n_q + qhead(g, kvh, wv)) * D;
 #pragma unroll
         for (int k = 0; k < D / 64; ++k) q_t[k] = qrow[lane + 64 * k];
     }
@@ -401,7 +408,7 @@ __global__ void __launch_bounds__(CT) chunk_max_kernel(Geom g, const Tables *__r
             double cmax = 0.0;
             for (int i = 0; i < (1 << g.kb); ++i) cmax = fmax(cmax, fabs(kcf[i]));
             const bool okh = stage_query_head<D / 64>(q_t, D, wv, qf, cmax,
-                                                      chunk == 0 ? &st->range_errors : nullptr);
+                                                      chunk == 0 && real_head(g, wv) ? &st->range_errors : nullptr);
             if (lane == 0 && !okh) atomicAnd(&qok_s, 0);
         }
         __syncthreads();
@@ -427,7 +434,7 @@ __global__ void __launch_bounds__(CT) chunk_max_kernel(Geom g, const Tables *__r
             for (int h = 0; h < GF; ++h) {
                 int64_t v = s[j][h];
                 if (v < SCORE_LO || v > SCORE_HI) {
-                    ++ovf;
+                    if (real_head(g, h)) ++ovf;
                     v = v < SCORE_LO ? SCORE_LO : SCORE_HI;
                 }
                 const int64_t a = v < 0 ? -v : v;
@@ -518,11 +525,11 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
         int32_t kv_t[D / 64];          // STEP: the new token's key (wave GF) or value (GF + 1)
         if (STEP) {
             if (wv < GF)
-                load_vec<D / 64>(si.qw + ((int64_t)b * g.n_q + kvh * GF + wv) * D, D, q_t);
+                load_vec<D / 64>(si.qw + ((int64_t)b * g.n_q + qhead(g, kvh, wv)) * D, D, q_t);
             else if (new_row && wv < GF + 2)
                 load_vec<D / 64>((wv == GF ? si.kw : si.vw) + ((int64_t)b * g.n_kv + kvh) * D, D, kv_t);
         } else if (!QS && wv < GF) {
-            const int32_t *qrow = q + ((int64_t)b * g.n_q + kvh * GF + wv) * D;
+            const int32_t *qrow = q + ((int64_t)b * g.n_q + qhead(g, kvh, wv)) * D;
 #pragma unroll
             for (int k = 0; k < D / 64; ++k) q_t[k] = qrow[lane + 64 * k];
         }
@@ -591,7 +598,8 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
             // Chunk 0 counts the range errors of the rotated queries, once per call.
             if (wv < GF) {
                 const bool okh = stage_query_head<D / 64>(q_t, D, wv, S.qt.qf, tabs->kc_absmax,
-                                                          chunk == 0 ? &st->range_errors : nullptr);
+                                                          chunk == 0 && real_head(g, wv) ? &st->range_errors
+                                                                                         : nullptr);
                 if (lane == 0 && !okh) atomicAnd(&S.qok, 0);
                 if constexpr (STEP) {
 #pragma unroll
@@ -696,7 +704,7 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
                     for (int h = 0; h < GF; ++h) {
                         int64_t v = s[j][h];
                         if (v < SCORE_LO || v > SCORE_HI) {
-                            ++ovf;
+                            if (real_head(g, h)) ++ovf;
                             v = v < SCORE_LO ? SCORE_LO : SCORE_HI;
                         }
                         const int64_t a = v < 0 ? -v : v;
@@ -1590,9 +1598,10 @@ __global__ void __launch_bounds__(CT, 2) chunk_kernel(Geom g, const Tables *__re
 #pragma unroll
             for (int k = 0; k < CPL; ++k) acc[k] = (int64_t)aw[k];
             __syncthreads();   // the replay buffers are dead; the serial path reuses the LDS
-            const int qh = kvh * GF + h;
+            const int qh = qhead(g, kvh, h);
             int32_t *orow = out + ((int64_t)b * g.n_q + qh) * D;
-            if (!hw) {
+            if (!hw || !real_head(g, h)) {
+                // (a duplicate slot: no output, no statistics)
             } else if (fb) {
                 // The serial path counts score statistics only when the headers did not.
                 // The fused step's new row came from another workgroup: acquire it.
@@ -1686,9 +1695,9 @@ __global__ void __launch_bounds__(GF * 64) qprep_kernel(Geom g, const Tables *__
     if (threadIdx.x == 0) ok_s = 1;
     __syncthreads();
     int32_t v[CPL];
-    load_vec<CPL>(q + ((int64_t)b * g.n_q + kvh * GF + h) * g.d, g.d, v);
+    load_vec<CPL>(q + ((int64_t)b * g.n_q + qhead(g, kvh, h)) * g.d, g.d, v);
     const bool ok = stage_query_head<CPL>(v, g.d, h, qd + (int64_t)chain * g.d * GF, tabs->kc_absmax,
-                                          &st->range_errors);
+                                          real_head(g, h) ? &st->range_errors : nullptr);
     if (lane == 0 && !ok) atomicAnd(&ok_s, 0);
     __syncthreads();
     if (threadIdx.x == 0) qok[chain] = ok_s;

@@ -44,6 +44,12 @@ struct Geom {
     int32_t row_bytes, key_bytes, value_bytes;   // norms follow the value field, 4 B
     int32_t d, kb, vb, norm_frac;
     int32_t n_kv, n_q, G, batch;
+    // KV head h's planes are those of h >> kv_shift: an attend may see each KV head as
+    // 2^kv_shift chains of G query heads (8 query heads a KV head as two chains of 4)
+    int32_t kv_shift;
+    // 0, or the query heads a KV head has when fewer than an attend's chains hold: chain
+    // slot h then computes query head h % gq (the slots past gq duplicate, and are dropped)
+    int32_t gq;
 };
 
 // Device-resident constants of a cache: codebooks and the exp table.
@@ -150,7 +156,7 @@ __device__ __forceinline__ Recip reciprocal(int64_t l) {
 }
 
 __device__ __forceinline__ uint8_t *plane_ptr(const Geom &g, int b, int h, int p) {
-    return g.base + (int64_t)b * g.seq_stride + (int64_t)h * g.head_stride + (int64_t)p * g.span;
+    return g.base + (int64_t)b * g.seq_stride + (int64_t)(h >> g.kv_shift) * g.head_stride + (int64_t)p * g.span;
 }
 
 // Code of channel c in an LSB-first bitstream of `bits`-wide codes (quantize.py:271-283).
