@@ -54,7 +54,9 @@ __global__ void add_bias_kernel(float *__restrict__ y, const float *__restrict__
 // one rounding, kernel.py:354 to_float). Wave = GEMV_RPW rows, lane = 8
 // consecutive columns per 16-byte load; DPP row steps and readlane sum the lanes.
 // One row per wave (twice the workgroups of two) measured 8.8 -> 7.2 us for the
-// 3,072 x 2,048 projection.
+// 3,072 x 2,048 projection; two rows a wave, or 8 waves a workgroup, were no faster than
+// one row and 4 waves; staging the inputs before the weight loads are issued was 4 %
+// faster than after.
 constexpr int GEMV_N = 4, GEMV_RPW = 1, GEMV_WAVES = 4, GEMV_UNR = 4;
 
 // The sum of a float over the wave's 64 lanes (in lane 0; a fixed order): within each
@@ -83,7 +85,7 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_f16_kernel(
     const int lane = threadIdx.x & 63;
     const int row0 = (blockIdx.x * GEMV_WAVES + (threadIdx.x >> 6)) * GEMV_RPW;
     // GEMV_UNR 16-byte chunks of each row per batch: for in_f <= 2,048 one batch, all of the
-    // wave's weight loads in flight before the inputs are staged
+    // wave's weight loads in flight at once
     uint4 wv[GEMV_UNR][GEMV_RPW];
     auto load = [&](int cb) __attribute__((always_inline)) {
 #pragma unroll
@@ -96,9 +98,8 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_f16_kernel(
             }
         }
     };
-    load(lane * 8);
-    // the inputs, 4 values per 16-byte load and 4 loads per thread in flight (n * in_f is a
-    // multiple of 8)
+    // the inputs first, 4 values per 16-byte load and 4 loads per thread in flight (n * in_f
+    // is a multiple of 8), then the weights
     const int total = n * in_f;
     for (int i0 = threadIdx.x * 4; i0 < total; i0 += 64 * GEMV_WAVES * 16) {
         uint4 xv[4];
@@ -124,6 +125,7 @@ __global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_f16_kernel(
             }
         }
     }
+    load(lane * 8);
     __syncthreads();
     float acc[GEMV_RPW][GEMV_N];
 #pragma unroll
