@@ -563,14 +563,17 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     }
 #pragma unroll
     for (int i = 0; i < VWORDS; ++i) S.u.ph.vw[tid][i] = vwd[i];
+    // the wave's maxima (scores lie in [SCORE_LO, SCORE_HI], within +-2^47: 32-bit steps),
+    // its overflow count (at most 4 a lane: three ballots) and its largest |score|
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-        const int64_t m = wlive ? wave_max_i64(s[h]) : SCORE_LO;
+        const int64_t m = wlive ? wave_max_s48(s[h]) : SCORE_LO;
         if (lane == 0) S.wmax[wv][h] = m;
     }
     if (ok && wlive) {
-        ovf = (unsigned long long)wave_sum_i64((int64_t)ovf);
-        mabs = wave_max_i64(mabs);
+        ovf = (unsigned long long)(__popcll(__ballot(ovf & 1)) + 2 * __popcll(__ballot(ovf & 2)) +
+                                   4 * __popcll(__ballot(ovf & 4)));
+        mabs = wave_max_s48(mabs - (int64_t(1) << 47)) + (int64_t(1) << 47);    // |score| <= 2^47
         if (lane == 0) {
             if (ovf) atomicAdd(&S.ovf, ovf);
             if (mabs) atomicMax(&S.mabs, (unsigned long long)mabs);

@@ -95,6 +95,27 @@ __device__ __forceinline__ int64_t wave_shr1_64(int64_t v, int64_t id) {
     return dpp64<DPP_WAVE_SHR1>(id, v);
 }
 
+// The maximum of a signed 32-bit value over the wave, wave-uniform: DPP steps within each
+// row of 16 lanes (32-bit ops, one instruction each), then readlane combines the rows.
+__device__ __forceinline__ int32_t wave_max_i32(int32_t v) {
+    auto mx = [](int32_t a, int32_t b) { return a > b ? a : b; };
+    v = mx(v, (int32_t)dpp32<DPP_QUAD_1032>((uint32_t)v, (uint32_t)v));
+    v = mx(v, (int32_t)dpp32<DPP_QUAD_2301>((uint32_t)v, (uint32_t)v));
+    v = mx(v, (int32_t)dpp32<DPP_ROW_HALF_MIRROR>((uint32_t)v, (uint32_t)v));
+    v = mx(v, (int32_t)dpp32<DPP_ROW_MIRROR>((uint32_t)v, (uint32_t)v));
+    const int32_t r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+    const int32_t r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+    return mx(mx(r0, r1), mx(r2, r3));
+}
+// The maximum of a value in [-2^47, 2^47) over the wave, wave-uniform and exact, in 32-bit
+// steps: the largest v >> 16 first, then the largest low 16 bits among the lanes that hold it.
+__device__ __forceinline__ int64_t wave_max_s48(int64_t v) {
+    const int32_t hi = (int32_t)(v >> 16);
+    const int32_t mhi = wave_max_i32(hi);
+    const int32_t lo = hi == mhi ? (int32_t)(v & 0xFFFF) : 0;
+    return (int64_t)mhi * 65536 + wave_max_i32(lo);
+}
+
 // 32-bit inclusive prefix sum in lane order.
 __device__ __forceinline__ uint32_t wave_scan_add32(uint32_t v) {
     v += dpp32<DPP_ROW_SHR1>(0u, v);
