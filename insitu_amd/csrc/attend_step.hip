@@ -40,20 +40,20 @@
 #ifdef INSITU_STEP_STAMPS
 // Phase stamps (s_memrealtime) of every wave, for timing studies only, in a build
 // that defines INSITU_STEP_STAMPS: [workgroup][wave][stamp], read back by the host.
-__device__ unsigned long long insitu_step_stamps[8192 * 16 * 16];
+__device__ unsigned long long insitu_step_stamps[8192 * 16 * 32];
 extern "C" int insitu_step_stamps_read(unsigned long long *host, long n) {
     return (int)hipMemcpyFromSymbol(host, HIP_SYMBOL(insitu_step_stamps), (size_t)n * 8, 0, hipMemcpyDeviceToHost);
 }
 extern "C" int insitu_step_stamps_clear() {
     void *p = nullptr;
     if (hipGetSymbolAddress(&p, HIP_SYMBOL(insitu_step_stamps)) != hipSuccess) return 1;
-    return (int)hipMemset(p, 0, sizeof(unsigned long long) * 8192 * 16 * 16);
+    return (int)hipMemset(p, 0, sizeof(unsigned long long) * 8192 * 16 * 32);
 }
 #define STAMP(k)                                                                                \
     do {                                                                                        \
         const unsigned long long _t = __builtin_amdgcn_s_memrealtime();                         \
         if ((threadIdx.x & 63) == 0 && blockIdx.x < 8192)                                       \
-            insitu_step_stamps[((size_t)blockIdx.x * 16 + (threadIdx.x >> 6)) * 16 + (k)] = _t; \
+            insitu_step_stamps[((size_t)blockIdx.x * 16 + (threadIdx.x >> 6)) * 32 + (k)] = _t; \
     } while (0)
 #else
 #define STAMP(k) \
@@ -73,6 +73,7 @@ constexpr int RMAX = 32;          // runs per head a chunk sums in LDS
 constexpr int SLOTS = 16;         // runs per head a chunk after chunk 0 publishes
 constexpr int HMAX = 512;         // chunks per sequence
 constexpr int NSEG = 2048;        // runs per head the replay lists
+constexpr int LPOOL = 256;        // chunk 0's candidate list (every head): at most this many
 constexpr uint16_t RUN_EVENT = 0x8000;
 static_assert(1 + (HMAX - 1) * SLOTS + 1 < RUN_EVENT, "run slots fit 15 bits");
 // Per-head flags in a chunk header: the head is recomputed serially.
@@ -154,7 +155,18 @@ struct StepLds {
     int32_t expt[256];
     union {
         struct {
-            int4 tt[CHUNK][NV];             // each token's term for every value code, the 4 heads
+            union {
+                int4 tt[CHUNK][NV];         // each token's term for every value code, the 4 heads
+                // chunk 0's list: (score - SCORE_LO) | token << 48 and v_norm, head h at
+                // [loff[h], ...); per head its tokens of weight: token | event << 31, p | f << 16,
+                // and the token's term floor(v_norm * p * c_v[c] / 2^23) for each value code c
+                struct {
+                    uint64_t e[LPOOL];
+                    int32_t vn[LPOOL];
+                    uint32_t itk[G][LPOOL], ipf[G][LPOOL];
+                    int4 it4[G][LPOOL];
+                } ol;
+            } tu;
             uint32_t vw[CHUNK][VWORDS];     // each token's value codes
             uint32_t rix[CHUNK];            // each token's run, a byte per head
             uint16_t clist[CHUNK];          // the chunk's candidates (any head) in token order
@@ -177,6 +189,8 @@ struct StepLds {
     int64_t wt[G][NW];
     int32_t evc[G][NW];
     int32_t ccnt[NW];                       // candidates per wave
+    int32_t lcnt[G][NW];                    // chunk 0's list: candidates per head and wave
+    int32_t onseg[G];                       // chunk 0's list: segments per head
     int64_t min_[G], lmax[G];
     int32_t total[G];
     int qbad[G];
@@ -187,6 +201,41 @@ struct StepLds {
     unsigned long long sev, samax;          // the chain's merged statistics (replay)
     int32_t sdone;
 };
+
+// Applies a chunk's runs 0 .. nr - 1 of head h (its LDS run accumulators; run r > 0 opens
+// with a rescale by its factor) to the state (acc, l), lane = channel. A rescale never grows
+// |acc| (|floor(acc * f / 2^15)| <= |acc| for 0 <= f <= 2^15), so |acc| + the sum of the runs'
+// bounds B certifies every run at once; then only the rescales and adds remain, eight runs'
+// sums read at a time. Returns false (nothing applied) when the bound does not certify them,
+// and the caller goes run by run.
+template <class L>
+__device__ __forceinline__ bool fold_runs_certified(const L &S, int h, int nr, int lane, int32_t &acc, int64_t &l) {
+    constexpr int RM = sizeof(S.runL[0]) / sizeof(S.runL[0][0]);
+    const bool in = lane < nr && lane < RM;
+    const uint32_t Lr = in ? S.runL[h][lane] : 0u;
+    const int32_t fr = in ? S.runf[h][lane] : 0;
+    const int64_t bsum = wave_sum_i64(in ? (int64_t)S.runB[h][lane] : 0);
+    const int64_t a = acc < 0 ? -(int64_t)acc : (int64_t)acc;
+    if (__ballot(a + bsum > ACC_HI)) return false;
+    for (int r0 = 0; r0 < nr; r0 += 8) {
+        int32_t v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = r0 + k < nr ? S.runS[h][r0 + k][lane] : 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            if (r0 + k < nr) {
+                if (r0 + k > 0) {
+                    const int64_t f = __builtin_amdgcn_readlane(fr, r0 + k);
+                    acc = (int32_t)(((int64_t)acc * f) >> PROB_FRAC);
+                    l = (l * f) >> PROB_FRAC;
+                }
+                acc += v[k];
+                l += (uint32_t)__builtin_amdgcn_readlane((int)Lr, r0 + k);
+            }
+        }
+    }
+    return true;
+}
 
 template <int KB, int VB>
 __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__restrict__ tabs, int32_t *out,
@@ -239,7 +288,6 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     const bool wlive = t0 + 64 * wv < T;
     if (own && kvh == 0 && tid == 0) si.len_out[b] = T;
     const int score_shift = CENT_FRAC + g.norm_frac;
-    const int acc_shift = CENT_FRAC + g.norm_frac + PROB_FRAC - ACC_FRAC;
     const uint8_t *hb = plane_ptr(g, b, kvh, 0);
 
     // -- P0: loads, rotations, the new row ---------------------------------------
@@ -532,7 +580,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     }
     if (sp > 1) {
         // the slices' partial sums to their token wave, through the (not yet used) tt area
-        double *part = (double *)&S.u.ph.tt[0][0];
+        double *part = (double *)&S.u.ph.tu.tt[0][0];
         if (ok && scorer && slice > 0) {
 #pragma unroll
             for (int h = 0; h < G; ++h) part[(((slice - 1) * ntw + tw) * G + h) * 64 + lane] = acc[h];
@@ -647,7 +695,160 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     __syncthreads();                                               // B3
     STAMP(5);
     const bool lbfail = S.lbfail != 0;
-    const bool work = ok && !lbfail;
+    int flags = (ok ? 0 : FL_Q) | (lbfail ? FL_LB : 0);
+    int32_t acc0 = 0;
+    int64_t l0 = 0;
+    int nev0 = 0;
+    const int64_t dm = tabs->delta_max;
+    // u = floor(min(d, delta_max) * log2e / 2^24) (attention.py:153-159), then the table
+    auto lut = [&](int64_t d) __attribute__((always_inline)) {
+        const uint32_t dc = (uint32_t)(d < dm ? d : dm);                     // < 2^20
+        const uint32_t u = __umulhi(dc << 8, (uint32_t)LOG2E_Q16);
+        const int32_t v = S.expt[u & 255] >> (u >> LUT_BITS);
+        return u < (uint32_t)LUT_SPAN ? v : 0;
+    };
+
+    // -- P3 of chunk 0, from a list of its candidates ------------------------------
+    // Chunk 0 has no running maximum before it, so its candidates (a token of weight or an
+    // event has s > m_t - delta_max, m_t its running maximum) are all real, its events many,
+    // and the lane-per-token phases below would make it the last chunk to finish. When they
+    // fit LPOOL it lists them instead (a superset, in 32-bit steps: with hi the running
+    // maximum of floor(s / 2^16) up to the token, s > m - delta_max implies floor(s / 2^16)
+    // >= hi - ceil(delta_max / 2^16)), and per head one pass over the list (lane = entry) gives
+    // every listed token its running maximum, hence its event, p and factor
+    // (ops/attention.py:451-513 over the listed tokens is the recurrence over all: the others
+    // add nothing). Its tokens of weight form segments that open at an event (or every SEGMAX
+    // tokens); four waves per head sum each segment's terms floor(v_norm * p * c_v / 2^23)
+    // (lane = channel), and the head's wave folds the segments, certified by one bound.
+    bool olist = false;
+    if (own && ok && !lbfail) {
+        const int64_t dmh = (dm + 65535) >> 16;
+        uint64_t lb[G];
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            uint32_t wmx = lane < NW ? (uint32_t)(int32_t)(S.wmax[lane & (NW - 1)][h] >> 16) : 0x80000000u;
+            wmx = (uint32_t)max((int32_t)wmx, (int32_t)dpp32<DPP_ROW_SHR1>(0x80000000u, wmx));
+            wmx = (uint32_t)max((int32_t)wmx, (int32_t)dpp32<DPP_ROW_SHR2>(0x80000000u, wmx));
+            wmx = (uint32_t)max((int32_t)wmx, (int32_t)dpp32<DPP_ROW_SHR4>(0x80000000u, wmx));
+            wmx = (uint32_t)max((int32_t)wmx, (int32_t)dpp32<DPP_ROW_SHR8>(0x80000000u, wmx));
+            const int32_t before = wv ? __builtin_amdgcn_readlane((int)wmx, wv - 1) : INT32_MIN;
+            const int32_t hs = (int32_t)(s[h] >> 16);     // scores lie in [-2^47, 2^47)
+            const int32_t hi = max(wave_scan_max32(hs), before);
+            lb[h] = __ballot(live && (int64_t)hs + dmh >= (int64_t)hi);
+            if (lane == 0) S.lcnt[h][wv] = (int32_t)__popcll(lb[h]);
+        }
+        STAMP(17);
+        __syncthreads();                                           // L1
+        STAMP(18);
+        int lnum[G], loff[G], lwoff[G], lsum = 0;
+#pragma unroll
+        for (int h = 0; h < G; ++h) {
+            uint32_t c = lane < NW ? (uint32_t)S.lcnt[h][lane & (NW - 1)] : 0u;
+            c += dpp32<DPP_ROW_SHR1>(0u, c);
+            c += dpp32<DPP_ROW_SHR2>(0u, c);
+            c += dpp32<DPP_ROW_SHR4>(0u, c);
+            c += dpp32<DPP_ROW_SHR8>(0u, c);
+            lnum[h] = __builtin_amdgcn_readlane((int)c, NW - 1);
+            lwoff[h] = wv ? __builtin_amdgcn_readlane((int)c, wv - 1) : 0;
+            loff[h] = lsum;
+            lsum += lnum[h];
+        }
+        olist = lsum <= LPOOL;
+        if (olist) {
+            auto &ol = S.u.ph.tu.ol;
+#pragma unroll
+            for (int h = 0; h < G; ++h) {
+                if ((lb[h] >> lane) & 1ull) {
+                    const int at = loff[h] + lwoff[h] +
+                                   (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(lb[h] >> 32),
+                                                                  __builtin_amdgcn_mbcnt_lo((uint32_t)lb[h], 0u));
+                    ol.e[at] = (uint64_t)(s[h] - SCORE_LO) | ((uint64_t)tid << 48);
+                    ol.vn[at] = (int32_t)(int16_t)(nw >> 16);
+                }
+            }
+            STAMP(19);
+            __syncthreads();                                       // L2
+            if (wv < G) {
+                // Head h's wave alone (the heads' waves sit on the four SIMDs): one pass over the
+                // list gives the tokens of weight, their four terms and the bound B, then the
+                // fold walks them in order: a rescale at an event, then the term of this lane's
+                // code. |acc| + the sum of B certifies every step (a rescale never grows |acc|).
+                const int h = wv, n = lnum[h], o = loff[h];
+                int32_t vcs[4];
+#pragma unroll
+                for (int c = 0; c < 4; ++c) vcs[c] = uni32(S.vc9[c < L::NV ? c : 0]);
+                uint32_t vcmax9 = 0;
+#pragma unroll
+                for (int c = 0; c < L::NV; ++c) {
+                    const uint32_t a = (uint32_t)(vcs[c] < 0 ? -vcs[c] : vcs[c]);
+                    vcmax9 = a > vcmax9 ? a : vcmax9;
+                }
+                int64_t smax = SCORE_LO;
+                int nitem = 0, nev = 0;
+                uint64_t bsum = 0;
+                for (int j0 = 0; j0 < n; j0 += 64) {
+                    const int j = j0 + lane;
+                    const bool in = j < n;
+                    const uint64_t e = in ? ol.e[o + j] : 0ull;
+                    const int64_t sc = in ? (int64_t)(e & ((1ull << 48) - 1)) + SCORE_LO : SCORE_LO;
+                    const int64_t inc = wave_scan64<OpMax64>(sc, SCORE_LO);
+                    int64_t mb = wave_shr1_64(inc, SCORE_LO);
+                    mb = mb > smax ? mb : smax;                    // the running maximum before
+                    smax = OpMax64::f(smax, readlane64(inc, 63));
+                    const bool ev = in && sc > mb;
+                    const int32_t p = in ? lut(ev ? 0 : mb - sc) : 0;
+                    const int32_t f = ev ? lut(sc - mb) : 0;
+                    const bool useful = in && (ev || p > 0);
+                    const uint64_t ub = __ballot(useful);
+                    const int32_t w = useful ? ol.vn[o + j] * p : 0;          // |w| <= 2^30
+                    const uint32_t aw = (uint32_t)(w < 0 ? -w : w);
+                    bsum += (uint32_t)__builtin_amdgcn_readlane(
+                        (int)wave_scan_add32(w != 0 ? __umulhi(aw, vcmax9) + 1 : 0u), 63);   // < 2^31
+                    if (useful) {
+                        const int ipos = nitem + (int)__builtin_amdgcn_mbcnt_hi(
+                                                     (uint32_t)(ub >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)ub, 0u));
+                        ol.itk[h][ipos] = (uint32_t)(e >> 48) | (ev ? 0x80000000u : 0u);
+                        ol.ipf[h][ipos] = (uint32_t)p | ((uint32_t)f << 16);
+                        ol.it4[h][ipos] = make_int4(__mulhi(w, vcs[0]), __mulhi(w, vcs[1]), __mulhi(w, vcs[2]),
+                                                    __mulhi(w, vcs[3]));
+                    }
+                    nitem += (int)__popcll(ub);
+                    nev += (int)__popcll(__ballot(ev));
+                }
+                nev0 = nev;
+                if (bsum > (uint64_t)ACC_HI) {
+                    flags |= FL_CERT;
+                } else {
+                    const int wsel = (lane * VB) >> 5, wsh = (lane * VB) & 31;
+                    for (int i0 = 0; i0 < nitem; i0 += 8) {
+                        uint32_t tk[8], wd[8];
+#pragma unroll
+                        for (int q = 0; q < 8; ++q) tk[q] = uni32((int32_t)ol.itk[h][(i0 + q) & (LPOOL - 1)]);
+#pragma unroll
+                        for (int q = 0; q < 8; ++q) wd[q] = S.u.ph.vw[tk[q] & (CHUNK - 1)][wsel];
+#pragma unroll
+                        for (int q = 0; q < 8; ++q) {
+                            if (i0 + q < nitem) {
+                                const uint32_t pf = (uint32_t)uni32((int32_t)ol.ipf[h][i0 + q]);
+                                if (tk[q] >> 31) {
+                                    const int64_t fq = pf >> 16;
+                                    acc0 = (int32_t)(((int64_t)acc0 * fq) >> PROB_FRAC);
+                                    l0 = (l0 * fq) >> PROB_FRAC;
+                                }
+                                const int4 t = ol.it4[h][i0 + q];
+                                const uint32_t code = __builtin_amdgcn_ubfe(wd[q], (uint32_t)wsh, (uint32_t)VB);
+                                const int32_t t01 = code & 1 ? t.y : t.x, t23 = code & 1 ? t.w : t.z;
+                                acc0 += code & 2 ? t23 : t01;
+                                l0 += pf & 0xFFFF;
+                            }
+                        }
+                    }
+                }
+            }
+        }
+    }
+    const bool work = ok && !lbfail && !olist;
+    if (olist) STAMP(16);
 
     // -- P3: events, p, factors and terms, lane = token --------------------------
     // A head whose chunk maximum does not exceed M_in has no event here, and then
@@ -671,7 +872,6 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         nruns[h] = 1;
     }
     if (work) {
-        const int64_t dm = tabs->delta_max;
         int64_t Min[G], incl[G];
         bool evh[G];
         bool any_ev = false;
@@ -688,13 +888,6 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         }
         if (any_ev) __syncthreads();                               // B4 (uniform)
         STAMP(11);
-        // u = floor(min(d, delta_max) * log2e / 2^24) (attention.py:153-159), then the table
-        auto lut = [&](int64_t d) __attribute__((always_inline)) {
-            const uint32_t dc = (uint32_t)(d < dm ? d : dm);                     // < 2^20
-            const uint32_t u = __umulhi(dc << 8, (uint32_t)LOG2E_Q16);
-            const int32_t v = S.expt[u & 255] >> (u >> LUT_BITS);
-            return u < (uint32_t)LUT_SPAN ? v : 0;
-        };
         int64_t pm[G], dd[G];
         bool ev[G], cand[G];
 #pragma unroll
@@ -752,7 +945,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             }
             if ((candb >> lane) & 1ull) {
 #pragma unroll
-                for (int c = 0; c < NV; ++c) S.u.ph.tt[tid][c] = make_int4(tv[c][0], tv[c][1], tv[c][2], tv[c][3]);
+                for (int c = 0; c < NV; ++c) S.u.ph.tu.tt[tid][c] = make_int4(tv[c][0], tv[c][1], tv[c][2], tv[c][3]);
             }
         }
         if (any_ev) {
@@ -852,7 +1045,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             for (int k = 0; k < 8; ++k) wd[k] = S.u.ph.vw[tk[k]][wi];
             int4 t4[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) t4[k] = S.u.ph.tt[tk[k]][__builtin_amdgcn_ubfe(wd[k], (uint32_t)sh, (uint32_t)VB)];
+            for (int k = 0; k < 8; ++k) t4[k] = S.u.ph.tu.tt[tk[k]][__builtin_amdgcn_ubfe(wd[k], (uint32_t)sh, (uint32_t)VB)];
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
                 if (k < nt) {
@@ -885,10 +1078,6 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     STAMP(7);
 
     // -- P5: chunk 0 folds its runs; the others publish theirs ---------------------
-    int flags = (ok ? 0 : FL_Q) | (lbfail ? FL_LB : 0);
-    int32_t acc0 = 0;
-    int64_t l0 = 0;
-    int nev0 = 0;
     const bool hw = wv < G;        // wave h < G: query head h, lane = channel
     const int h = hw ? wv : 0;
     // The last chunk of the sequence replays (it holds the new token, and its look-back is the
@@ -898,8 +1087,10 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     if (hw && work) {
         const int nr = nruns[h];
         if (nr > RMAX || (!own && !replayer && nr > SLOTS)) flags |= FL_POOL;
-        if (own && !(flags & FL_POOL)) {
-            // acc = floor(acc * f / 2^15) + S per run (run 0 has no rescale), certified
+        if (own && !(flags & FL_POOL) && fold_runs_certified(S, h, nr, lane, acc0, l0)) {
+            nev0 = nr - 1;
+        } else if (own && !(flags & FL_POOL)) {
+            // acc = floor(acc * f / 2^15) + S per run (run 0 has no rescale), each run certified
             bool unsafe = false;
             for (int r = 0; r < nr; ++r) {
                 if (r > 0) {
@@ -944,6 +1135,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
                               ((uint64_t)(ok ? S.ovf & 0xFFFF : 0) << 24) | ((uint64_t)ck.ep << 40));
             }
         }
+        STAMP(12);
         return;
     }
     if (newrow && (wv == G || wv == G + 1)) stores_done();         // the new row, for the serial path
@@ -1098,9 +1290,26 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
                 int32_t v[8];
 #pragma unroll
                 for (int k = 0; k < 8; ++k) v[k] = k < kn ? S.u.rp.rs[h][k0 + k][lane] : 0;
-                if (!bev && !((uint32_t)(bigm >> k0) & bmask) && !__ballot(a + bsum > ACC_HI)) {
+                // A rescale never grows |acc|, so the block's bound certifies blocks with events
+                // too: then only their rescales are applied in turn, with no check per run.
+                const bool cert = !((uint32_t)(bigm >> k0) & bmask) && !__ballot(a + bsum > ACC_HI);
+                if (cert && !bev) {
                     aw += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
                     l += (uint32_t)__builtin_amdgcn_readlane((int)PL, k0 + kn - 1) - before_l;
+                    continue;
+                }
+                if (cert) {
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        if ((bev >> k) & 1u) {
+                            const int64_t f = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(lf >> 32), k0 + k);
+                            aw = (int32_t)(((int64_t)aw * f) >> PROB_FRAC);
+                            l = (l * f) >> PROB_FRAC;
+                            ++events;
+                        }
+                        aw += v[k];                    // (0 past kn)
+                        if (k < kn) l += (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)lf, k0 + k);
+                    }
                     continue;
                 }
 #pragma unroll
@@ -1124,7 +1333,9 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     if (nch > 1 && hw && work && !hflags) {
         // this chunk's own runs, last (run 0 continues the run open before it)
         const int nr = nruns[h];
-        for (int r = 0; r < nr; ++r) {
+        const bool cert = fold_runs_certified(S, h, nr, lane, aw, l);
+        if (cert) events += (unsigned long long)(nr - 1);
+        for (int r = 0; r < nr && !cert; ++r) {
             if (r > 0) {
                 const int64_t f = S.runf[h][r];
                 aw = (int32_t)(((int64_t)aw * f) >> PROB_FRAC);

@@ -116,6 +116,19 @@ __device__ __forceinline__ int64_t wave_max_s48(int64_t v) {
     return (int64_t)mhi * 65536 + wave_max_i32(lo);
 }
 
+// 32-bit inclusive running maximum (signed) in lane order.
+__device__ __forceinline__ int32_t wave_scan_max32(int32_t v) {
+    auto mx = [](int32_t a, int32_t b) { return a > b ? a : b; };
+    const uint32_t lo = 0x80000000u;
+    v = mx(v, (int32_t)dpp32<DPP_ROW_SHR1>(lo, (uint32_t)v));
+    v = mx(v, (int32_t)dpp32<DPP_ROW_SHR2>(lo, (uint32_t)v));
+    v = mx(v, (int32_t)dpp32<DPP_ROW_SHR4>(lo, (uint32_t)v));
+    v = mx(v, (int32_t)dpp32<DPP_ROW_SHR8>(lo, (uint32_t)v));
+    v = mx(v, (int32_t)dpp32<DPP_ROW_BCAST15, 0xA>(lo, (uint32_t)v));
+    v = mx(v, (int32_t)dpp32<DPP_ROW_BCAST31, 0xC>(lo, (uint32_t)v));
+    return v;
+}
+
 // 32-bit inclusive prefix sum in lane order.
 __device__ __forceinline__ uint32_t wave_scan_add32(uint32_t v) {
     v += dpp32<DPP_ROW_SHR1>(0u, v);

@@ -26,7 +26,7 @@ import sys
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-NWAVES, NSTAMPS, MAXBLK = 16, 16, 8192
+NWAVES, NSTAMPS, MAXBLK = 16, 32, 8192
 
 # stamp index -> the point of the kernel it marks
 PHASES = [
@@ -36,10 +36,15 @@ PHASES = [
     (3, "P1 scores and wave maxima"),
     (4, "barrier B2"),
     (5, "P2 look-back (barrier B3)"),
+    (17, "P3 chunk 0: list test"),
+    (18, "P3 chunk 0: barrier L1"),
+    (19, "P3 chunk 0: list compacted"),
+    (16, "P3 chunk 0 folded from its list"),
     (11, "P3 event scan (barrier B4)"),
     (13, "P3 candidates, terms (barrier B5)"),
     (6, "P3 run sums, candidate list (B6)"),
     (7, "P4 walk (barrier B7)"),
+    (12, "P5 runs and header published (other chunks)"),
     (8, "P5 own fold or publish"),
     (14, "P6 headers read"),
     (15, "P6 runs staged"),
@@ -111,6 +116,11 @@ def run(ctx_len: int, n_caches: int, reps: int, flat: bool = False) -> dict:
         per_blk = np.nanmedian(np.nanmax(R, axis=2), axis=0)     # (block, stamp)
         rep_blk = (nch - 1) * 8                                  # chain 0's last chunk
         w0 = np.nanmedian(R[:, rep_blk, 0], axis=0)               # (stamp,)
+    pub = per_blk[:, 12]
+    if nch > 1 and not np.all(np.isnan(pub)):
+        order = np.argsort(np.nan_to_num(pub, nan=-1.0))[::-1][:6]
+        print("last chunks to publish (chunk, KV head, us): " +
+              ", ".join(f"({b // 8}, {b % 8}, {pub[b]:.2f})" for b in order))
     return {"ctx": ctx_len, "flat": flat, "reps": reps, "blocks": nblk, "per_blk": per_blk, "replayer_w0": w0}
 
 
@@ -120,16 +130,17 @@ def table(res: dict) -> str:
     lines = [f"ctx {res['ctx']}{' (flat softmax)' if res['flat'] else ''}: {res['blocks']} workgroups, "
              f"median of {res['reps']} steps, us from the launch's first wave",
              "",
-             "| stamp | point | workgroups: median | min | max | replaying workgroup, wave 0 |",
-             "|---|---|---|---|---|---|"]
+             "| stamp | point | workgroups: median | min | max | replaying workgroup, wave 0 | chunk 0 (median over KV heads) |",
+             "|---|---|---|---|---|---|---|"]
     for k, name in PHASES:
         col = res["per_blk"][:, k]
         if np.all(np.isnan(col)) and np.isnan(res["replayer_w0"][k]):
             continue
         with np.errstate(all="ignore"), __import__("warnings").catch_warnings():
             __import__("warnings").simplefilter("ignore")
+            c0 = np.nanmedian(col[:8]) if res["blocks"] > 8 else np.nan
             lines.append(f"| {k} | {name} | {f(np.nanmedian(col))} | {f(np.nanmin(col))} | "
-                         f"{f(np.nanmax(col))} | {f(res['replayer_w0'][k])} |")
+                         f"{f(np.nanmax(col))} | {f(res['replayer_w0'][k])} | {f(c0)} |")
     return "\n".join(lines)
 
 
