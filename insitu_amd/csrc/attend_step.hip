@@ -157,13 +157,14 @@ struct StepLds {
         struct {
             union {
                 int4 tt[CHUNK][NV];         // each token's term for every value code, the 4 heads
-                // chunk 0's list: (score - SCORE_LO) | token << 48 and v_norm, head h at
+                // the chunk's list: (score - SCORE_LO) | token << 48 and v_norm, head h at
                 // [loff[h], ...); per head its tokens of weight: token | event << 31, p | f << 16,
-                // and the token's term floor(v_norm * p * c_v[c] / 2^23) for each value code c
+                // the bound of its term, and its term floor(v_norm * p * c_v[c] / 2^23) for each
+                // value code c
                 struct {
                     uint64_t e[LPOOL];
                     int32_t vn[LPOOL];
-                    uint32_t itk[G][LPOOL], ipf[G][LPOOL];
+                    uint32_t itk[G][LPOOL], ipf[G][LPOOL], ib[G][LPOOL];
                     int4 it4[G][LPOOL];
                 } ol;
             } tu;
@@ -708,20 +709,33 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         return u < (uint32_t)LUT_SPAN ? v : 0;
     };
 
-    // -- P3 of chunk 0, from a list of its candidates ------------------------------
-    // Chunk 0 has no running maximum before it, so its candidates (a token of weight or an
-    // event has s > m_t - delta_max, m_t its running maximum) are all real, its events many,
-    // and the lane-per-token phases below would make it the last chunk to finish. When they
-    // fit LPOOL it lists them instead (a superset, in 32-bit steps: with hi the running
-    // maximum of floor(s / 2^16) up to the token, s > m - delta_max implies floor(s / 2^16)
-    // >= hi - ceil(delta_max / 2^16)), and per head one pass over the list (lane = entry) gives
-    // every listed token its running maximum, hence its event, p and factor
+    // -- P3 from a list of the chunk's candidates -------------------------------------
+    // A token of weight or an event has s > m_t - delta_max, m_t its running maximum, which is
+    // at least M_in and at least the chunk's own running maximum. The chunk lists the tokens
+    // that pass both tests (a superset; the second in 32-bit steps: with hi the running
+    // maximum of floor(s / 2^16) up to the token, s > m - delta_max implies floor(s / 2^16) >=
+    // hi - ceil(delta_max / 2^16)). When they fit LPOOL, per head one pass over the list (lane
+    // = entry) gives every listed token its running maximum (the larger of M_in and the listed
+    // scores before it: every event is listed), hence its event, p and factor
     // (ops/attention.py:451-513 over the listed tokens is the recurrence over all: the others
-    // add nothing). Its tokens of weight form segments that open at an event (or every SEGMAX
-    // tokens); four waves per head sum each segment's terms floor(v_norm * p * c_v / 2^23)
-    // (lane = channel), and the head's wave folds the segments, certified by one bound.
+    // add nothing), and the head's wave then walks its tokens of weight in order (lane =
+    // channel): chunk 0 folds them into its state (a rescale at an event, then the term of this
+    // lane's code, certified by one bound: a rescale never grows |acc|), the other chunks cut
+    // them into runs at their events. The lane-per-token phases below, which scan every token,
+    // remain for a chunk whose list does not fit (a flat softmax).
+    uint64_t evb[G], cb[G];
+    uint64_t candb = 0;
+    int rb[G];
+    int nruns[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        evb[h] = cb[h] = 0;
+        rb[h] = 0;
+        nruns[h] = 1;
+    }
+    const bool replayer = chunk == nch - 1;      // the sequence's last chunk replays the others
     bool olist = false;
-    if (own && ok && !lbfail) {
+    if (ok && !lbfail) {
         const int64_t dmh = (dm + 65535) >> 16;
         uint64_t lb[G];
 #pragma unroll
@@ -734,7 +748,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             const int32_t before = wv ? __builtin_amdgcn_readlane((int)wmx, wv - 1) : INT32_MIN;
             const int32_t hs = (int32_t)(s[h] >> 16);     // scores lie in [-2^47, 2^47)
             const int32_t hi = max(wave_scan_max32(hs), before);
-            lb[h] = __ballot(live && (int64_t)hs + dmh >= (int64_t)hi);
+            lb[h] = __ballot(live && (int64_t)hs + dmh >= (int64_t)hi && s[h] > S.min_[h] - dm);
             if (lane == 0) S.lcnt[h][wv] = (int32_t)__popcll(lb[h]);
         }
         STAMP(17);
@@ -783,7 +797,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
                     const uint32_t a = (uint32_t)(vcs[c] < 0 ? -vcs[c] : vcs[c]);
                     vcmax9 = a > vcmax9 ? a : vcmax9;
                 }
-                int64_t smax = SCORE_LO;
+                int64_t smax = S.min_[h];                          // M_in
                 int nitem = 0, nev = 0;
                 uint64_t bsum = 0;
                 for (int j0 = 0; j0 < n; j0 += 64) {
@@ -809,17 +823,68 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
                                                      (uint32_t)(ub >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)ub, 0u));
                         ol.itk[h][ipos] = (uint32_t)(e >> 48) | (ev ? 0x80000000u : 0u);
                         ol.ipf[h][ipos] = (uint32_t)p | ((uint32_t)f << 16);
+                        ol.ib[h][ipos] = w != 0 ? __umulhi(aw, vcmax9) + 1 : 0u;
                         ol.it4[h][ipos] = make_int4(__mulhi(w, vcs[0]), __mulhi(w, vcs[1]), __mulhi(w, vcs[2]),
                                                     __mulhi(w, vcs[3]));
                     }
                     nitem += (int)__popcll(ub);
                     nev += (int)__popcll(__ballot(ev));
                 }
-                nev0 = nev;
-                if (bsum > (uint64_t)ACC_HI) {
+                const int wsel = (lane * VB) >> 5, wsh = (lane * VB) & 31;
+                if (!own) {
+                    // runs: run r holds the tokens from the chunk's r-th event on (run 0: those
+                    // before its first), with its sum, L, bound and opening factor
+                    int r = 0;
+                    int32_t sacc = 0;
+                    uint32_t sL = 0;
+                    uint64_t sB = 0;
+                    for (int i0 = 0; i0 < nitem; i0 += 8) {
+                        uint32_t tk[8], wd[8];
+#pragma unroll
+                        for (int q = 0; q < 8; ++q) tk[q] = uni32((int32_t)ol.itk[h][(i0 + q) & (LPOOL - 1)]);
+#pragma unroll
+                        for (int q = 0; q < 8; ++q) wd[q] = S.u.ph.vw[tk[q] & (CHUNK - 1)][wsel];
+#pragma unroll
+                        for (int q = 0; q < 8; ++q) {
+                            if (i0 + q < nitem) {
+                                const uint32_t pf = (uint32_t)uni32((int32_t)ol.ipf[h][i0 + q]);
+                                if (tk[q] >> 31) {
+                                    if (r < RMAX) {
+                                        S.runS[h][r][lane] = sacc;
+                                        if (lane == 0) {
+                                            S.runL[h][r] = sL;
+                                            S.runB[h][r] = sB;
+                                        }
+                                    }
+                                    ++r;
+                                    if (r < RMAX && lane == 0) S.runf[h][r] = (int32_t)(pf >> 16);
+                                    sacc = 0;
+                                    sL = 0;
+                                    sB = 0;
+                                }
+                                const int4 t = ol.it4[h][i0 + q];
+                                const uint32_t code = __builtin_amdgcn_ubfe(wd[q], (uint32_t)wsh, (uint32_t)VB);
+                                const int32_t t01 = code & 1 ? t.y : t.x, t23 = code & 1 ? t.w : t.z;
+                                sacc += code & 2 ? t23 : t01;
+                                sL += pf & 0xFFFF;
+                                sB += (uint32_t)uni32((int32_t)ol.ib[h][i0 + q]);
+                            }
+                        }
+                    }
+                    if (r < RMAX) {
+                        S.runS[h][r][lane] = sacc;
+                        if (lane == 0) {
+                            S.runL[h][r] = sL;
+                            S.runB[h][r] = sB;
+                        }
+                    }
+                    nruns[h] = r + 1;
+                    if (r + 1 > RMAX || (!replayer && r + 1 > SLOTS)) flags |= FL_POOL;
+                } else if (bsum > (uint64_t)ACC_HI) {
+                    nev0 = nev;
                     flags |= FL_CERT;
                 } else {
-                    const int wsel = (lane * VB) >> 5, wsh = (lane * VB) & 31;
+                    nev0 = nev;
                     for (int i0 = 0; i0 < nitem; i0 += 8) {
                         uint32_t tk[8], wd[8];
 #pragma unroll
@@ -847,7 +912,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             }
         }
     }
-    const bool work = ok && !lbfail && !olist;
+    const bool work = ok && !lbfail && !olist;     // the lane-per-token phases
     if (olist) STAMP(16);
 
     // -- P3: events, p, factors and terms, lane = token --------------------------
@@ -861,16 +926,6 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     // over w = v_norm * p != 0, and its opening factor go to the run accumulators.
     // The reference's int64 floors are taken as 32-bit high products: for |a * b| < 2^63,
     // floor(a * b / 2^k) = mulhi(a, b * 2^(32 - k)) whenever b * 2^(32 - k) fits 32 bits.
-    uint64_t evb[G], cb[G];
-    uint64_t candb = 0;
-    int rb[G];
-    int nruns[G];
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-        evb[h] = cb[h] = 0;
-        rb[h] = 0;
-        nruns[h] = 1;
-    }
     if (work) {
         int64_t Min[G], incl[G];
         bool evh[G];
@@ -1083,7 +1138,6 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     // The last chunk of the sequence replays (it holds the new token, and its look-back is the
     // longest); every other chunk publishes its runs (chunk 0: its state), waits until they
     // are complete, then publishes its header, and is done. The replayer's runs stay in LDS.
-    const bool replayer = chunk == nch - 1;
     if (hw && work) {
         const int nr = nruns[h];
         if (nr > RMAX || (!own && !replayer && nr > SLOTS)) flags |= FL_POOL;
@@ -1115,7 +1169,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
                 pub32(&ck.segS[hbase * D + lane], (uint32_t)acc0);
                 if (lane == 0) pub64(&ck.meta[hbase * 2], (uint64_t)(uint32_t)l0 | ((uint64_t)(uint32_t)nev0 << 32));
                 npub = 1;
-            } else if (work && !(flags & FL_POOL)) {
+            } else if ((work || olist) && !(flags & FL_POOL)) {
                 const int nr = nruns[h];
                 const bool empty = nr == 1 && S.runL[h][0] == 0 && S.runB[h][0] == 0;
                 npub = empty ? 0 : nr;
@@ -1330,7 +1384,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         }
         __syncthreads();
     }
-    if (nch > 1 && hw && work && !hflags) {
+    if (nch > 1 && hw && (work || olist) && !hflags) {
         // this chunk's own runs, last (run 0 continues the run open before it)
         const int nr = nruns[h];
         const bool cert = fold_runs_certified(S, h, nr, lane, aw, l);
