@@ -632,6 +632,24 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     __syncthreads();                                               // B2
     STAMP(4);
 
+    // The list test's half that needs no M_in (its 32-bit running maxima), done here so that
+    // it overlaps the look-back's wait: k32[h] holds the tokens with floor(s / 2^16) >= hi -
+    // ceil(delta_max / 2^16), hi the running maximum of floor(s / 2^16) up to the token.
+    const int64_t dmh = (tabs->delta_max + 65535) >> 16;
+    uint64_t k32[G];
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+        uint32_t wmx = lane < NW ? (uint32_t)(int32_t)(S.wmax[lane & (NW - 1)][h] >> 16) : 0x80000000u;
+        wmx = (uint32_t)max((int32_t)wmx, (int32_t)dpp32<DPP_ROW_SHR1>(0x80000000u, wmx));
+        wmx = (uint32_t)max((int32_t)wmx, (int32_t)dpp32<DPP_ROW_SHR2>(0x80000000u, wmx));
+        wmx = (uint32_t)max((int32_t)wmx, (int32_t)dpp32<DPP_ROW_SHR4>(0x80000000u, wmx));
+        wmx = (uint32_t)max((int32_t)wmx, (int32_t)dpp32<DPP_ROW_SHR8>(0x80000000u, wmx));
+        const int32_t before = wv ? __builtin_amdgcn_readlane((int)wmx, wv - 1) : INT32_MIN;
+        const int32_t hs = (int32_t)(s[h] >> 16);         // scores lie in [-2^47, 2^47)
+        const int32_t hi = max(wave_scan_max32(hs), before);
+        k32[h] = __ballot(ok && live && (int64_t)hs + dmh >= (int64_t)hi);
+    }
+
     // -- P2: the maximum before this chunk, by look-back --------------------------
     // Two words per (chunk, head): the inclusive maximum and this chunk's own
     // (aggregate). Wave G + h publishes head h's aggregate (chunk 0: its inclusive
@@ -736,19 +754,10 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     const bool replayer = chunk == nch - 1;      // the sequence's last chunk replays the others
     bool olist = false;
     if (ok && !lbfail) {
-        const int64_t dmh = (dm + 65535) >> 16;
         uint64_t lb[G];
 #pragma unroll
         for (int h = 0; h < G; ++h) {
-            uint32_t wmx = lane < NW ? (uint32_t)(int32_t)(S.wmax[lane & (NW - 1)][h] >> 16) : 0x80000000u;
-            wmx = (uint32_t)max((int32_t)wmx, (int32_t)dpp32<DPP_ROW_SHR1>(0x80000000u, wmx));
-            wmx = (uint32_t)max((int32_t)wmx, (int32_t)dpp32<DPP_ROW_SHR2>(0x80000000u, wmx));
-            wmx = (uint32_t)max((int32_t)wmx, (int32_t)dpp32<DPP_ROW_SHR4>(0x80000000u, wmx));
-            wmx = (uint32_t)max((int32_t)wmx, (int32_t)dpp32<DPP_ROW_SHR8>(0x80000000u, wmx));
-            const int32_t before = wv ? __builtin_amdgcn_readlane((int)wmx, wv - 1) : INT32_MIN;
-            const int32_t hs = (int32_t)(s[h] >> 16);     // scores lie in [-2^47, 2^47)
-            const int32_t hi = max(wave_scan_max32(hs), before);
-            lb[h] = __ballot(live && (int64_t)hs + dmh >= (int64_t)hi && s[h] > S.min_[h] - dm);
+            lb[h] = k32[h] & __ballot(s[h] > S.min_[h] - dm);
             if (lane == 0) S.lcnt[h][wv] = (int32_t)__popcll(lb[h]);
         }
         STAMP(17);
@@ -1261,79 +1270,56 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     } else if (hw && lane == 0) {
         S.total[h] = 0;
     }
-    __syncthreads();
-    int tmax = 0;
-#pragma unroll
-    for (int hh = 0; hh < G; ++hh) tmax = S.total[hh] > tmax ? S.total[hh] : tmax;
-    const int tot_h = hw ? S.total[h] : 0;
+    // Each head's wave walks its own runs, RMAX at a time: their sums (lane = channel), L, f
+    // and bounds (lane = run) loaded into registers together, one round trip, then the walk.
     bool unsafe = false;
-    if (nch > 1 && hw) {
-        // chunk 0's state: acc (lane = channel), l | events << 32 (its header is current)
+    if (hw) {
         const int64_t hbase = ((int64_t)chain * G + h) * ck.pool;
-        aw = (int32_t)get32(&ck.segS[hbase * D + lane]);
-        const uint64_t lf = get64(&ck.meta[hbase * 2]);
-        l = (int64_t)(uint32_t)lf;
-        events = lf >> 32;
-    }
-    for (int g0 = 0; g0 < tmax; g0 += RMAX) {
-        // Stage up to RMAX runs per head in LDS: wave w loads runs w / G, w / G + 4, ... of head
-        // w % G (lane = channel), every slot read, then every load, then every store.
-        {
-            constexpr int PER = RMAX / (NW / G);
-            const int hh = wv & (G - 1), part = wv / G;
-            const int th = S.total[hh];
-            const int64_t hbase = ((int64_t)chain * G + hh) * ck.pool;
-            // every slot index is checked against the pool before it is read: one past it
-            // (a fault: the list is built from checked headers) is not loaded, and sends the
-            // head to the serial path
-            int slot[PER];
-#pragma unroll
-            for (int k = 0; k < PER; ++k) {
-                const int i = g0 + part + (NW / G) * k;
-                slot[k] = i < th ? (S.u.rp.rl[hh][i] & (RUN_EVENT - 1)) : -1;
-                if (slot[k] >= ck.pool) {
-                    slot[k] = -1;
-                    st->fault = 1;
-                    S.sbad[hh] = 1;
-                }
-            }
-            int32_t v[PER];
-#pragma unroll
-            for (int k = 0; k < PER; ++k) v[k] = slot[k] >= 0 ? (int32_t)get32(&ck.segS[(hbase + slot[k]) * D + lane]) : 0;
-#pragma unroll
-            for (int k = 0; k < PER; ++k)
-                if (slot[k] >= 0) S.u.rp.rs[hh][part + (NW / G) * k][lane] = v[k];
-            if (wv < G) {
-                const int i = g0 + lane;
-                const int sl = lane < RMAX && i < th ? S.u.rp.rl[hh][i] & (RUN_EVENT - 1) : 0;
-                if (lane < RMAX && i < th && sl < ck.pool) {
-                    const uint64_t lf = get64(&ck.meta[(hbase + sl) * 2]);
-                    const uint64_t bb = get64(&ck.meta[(hbase + sl) * 2 + 1]);
-                    S.u.rp.rlf[hh][lane] = lf;
-                    S.u.rp.rbb[hh][lane] = bb;
-                }
-            }
+        if (nch > 1) {
+            // chunk 0's state: acc (lane = channel), l | events << 32 (its header is current)
+            aw = (int32_t)get32(&ck.segS[hbase * D + lane]);
+            const uint64_t lf = get64(&ck.meta[hbase * 2]);
+            l = (int64_t)(uint32_t)lf;
+            events = lf >> 32;
         }
-        __syncthreads();
-        STAMP(15);
-        if (hw && S.sbad[h]) hflags |= FL_POOL;
-        if (hw && g0 < tot_h && !hflags) {
-            // The walk. Lane k < nb holds run k's list entry, L, f and bound B; prefix sums over
-            // the lanes give each block's sums. |acc| only shrinks at a rescale and grows by at
-            // most a run's B per run, so |acc at a block's start| + the block's B certifies 8
-            // event-free runs at once; elsewhere the walk goes run by run.
+        const int tot_h = S.total[h];
+        for (int g0 = 0; g0 < tot_h && !hflags; g0 += RMAX) {
             const int nb = tot_h - g0 < RMAX ? tot_h - g0 : RMAX;
             const bool mine = lane < nb;
             const uint32_t ent = mine ? (uint32_t)S.u.rp.rl[h][g0 + lane] : 0u;
-            const uint64_t lf = mine ? S.u.rp.rlf[h][lane] : 0ull;
-            const int64_t bb = mine ? (int64_t)S.u.rp.rbb[h][lane] : 0;
+            // every slot index is checked against the pool before it is read: one past it (a
+            // fault: the list is built from checked headers) is not loaded, and sends the head
+            // to the serial path
+            const int slot = (int)(ent & (RUN_EVENT - 1));
+            const bool bad = mine && slot >= ck.pool;
+            const bool ld = mine && !bad;
+            const uint64_t lf = ld ? get64(&ck.meta[(hbase + slot) * 2]) : 0ull;
+            const int64_t bb = ld ? (int64_t)get64(&ck.meta[(hbase + slot) * 2 + 1]) : 0;
+            int32_t v[RMAX];
+#pragma unroll
+            for (int k = 0; k < RMAX; ++k) {
+                const int sk = __builtin_amdgcn_readlane(ld ? slot : -1, k);
+                v[k] = k < nb && sk >= 0 ? (int32_t)get32(&ck.segS[(hbase + sk) * D + lane]) : 0;
+            }
+            if (__ballot(bad)) {
+                st->fault = 1;
+                hflags |= FL_POOL;
+                break;
+            }
+            STAMP(15);
+            // The walk. Lane k < nb holds run k's list entry, L, f and bound B; prefix sums over
+            // the lanes give each block's sums. |acc| only shrinks at a rescale and grows by at
+            // most a run's B per run, so |acc at a block's start| + the block's B certifies 8
+            // runs at once; elsewhere the walk goes run by run.
             const uint64_t evm = __ballot(mine && (ent & RUN_EVENT));
             // 32-bit prefix sums: L < 2^26 per run, and bounds below 2^27 (a run with a larger
             // one is checked on its own, by the walk run by run)
             const uint64_t bigm = __ballot(mine && bb >= (1ll << 27));
             const uint32_t PB = wave_scan_add32(bb < (1ll << 27) ? (uint32_t)bb : 0u);
             const uint32_t PL = wave_scan_add32((uint32_t)lf);
-            for (int k0 = 0; k0 < nb; k0 += 8) {
+#pragma unroll
+            for (int k0 = 0; k0 < RMAX; k0 += 8) {
+                if (k0 >= nb) break;
                 const int kn = nb - k0 < 8 ? nb - k0 : 8;
                 const uint32_t bmask = (1u << kn) - 1u;
                 const uint32_t bev = (uint32_t)(evm >> k0) & bmask;
@@ -1341,29 +1327,12 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
                 const uint32_t before_l = k0 ? (uint32_t)__builtin_amdgcn_readlane((int)PL, k0 - 1) : 0u;
                 const int64_t bsum = (uint32_t)__builtin_amdgcn_readlane((int)PB, k0 + kn - 1) - before_b;
                 const int64_t a = aw < 0 ? -(int64_t)aw : (int64_t)aw;
-                int32_t v[8];
-#pragma unroll
-                for (int k = 0; k < 8; ++k) v[k] = k < kn ? S.u.rp.rs[h][k0 + k][lane] : 0;
                 // A rescale never grows |acc|, so the block's bound certifies blocks with events
                 // too: then only their rescales are applied in turn, with no check per run.
                 const bool cert = !((uint32_t)(bigm >> k0) & bmask) && !__ballot(a + bsum > ACC_HI);
                 if (cert && !bev) {
-                    aw += ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+                    aw += ((v[k0] + v[k0 + 1]) + (v[k0 + 2] + v[k0 + 3])) + ((v[k0 + 4] + v[k0 + 5]) + (v[k0 + 6] + v[k0 + 7]));
                     l += (uint32_t)__builtin_amdgcn_readlane((int)PL, k0 + kn - 1) - before_l;
-                    continue;
-                }
-                if (cert) {
-#pragma unroll
-                    for (int k = 0; k < 8; ++k) {
-                        if ((bev >> k) & 1u) {
-                            const int64_t f = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(lf >> 32), k0 + k);
-                            aw = (int32_t)(((int64_t)aw * f) >> PROB_FRAC);
-                            l = (l * f) >> PROB_FRAC;
-                            ++events;
-                        }
-                        aw += v[k];                    // (0 past kn)
-                        if (k < kn) l += (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)lf, k0 + k);
-                    }
                     continue;
                 }
 #pragma unroll
@@ -1375,14 +1344,13 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
                             l = (l * f) >> PROB_FRAC;
                             ++events;
                         }
-                        if (!fits(aw, readlane64(bb, k0 + k))) unsafe = true;
-                        aw += v[k];
+                        if (!cert && !fits(aw, readlane64(bb, k0 + k))) unsafe = true;
+                        aw += v[k0 + k];
                         l += (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)lf, k0 + k);
                     }
                 }
             }
         }
-        __syncthreads();
     }
     if (nch > 1 && hw && (work || olist) && !hflags) {
         // this chunk's own runs, last (run 0 continues the run open before it)
