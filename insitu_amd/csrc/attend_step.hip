@@ -177,7 +177,10 @@ struct StepLds {
             uint64_t rlf[G][RMAX], rbb[G][RMAX];
             int32_t rs[G][RMAX][D];         // their sums, RMAX runs per head at a time
         } rp;
-        SerialLds<RS> fb[G];
+        struct {
+            uint16_t rl_[G][NSEG];          // (the replay's list, left intact: no barrier between)
+            SerialLds<RS> fb[G];            // the serial path, per head
+        } sr;
     } u;
     int32_t runS[G][RMAX][D];               // run sums; the replay's staged runs
     unsigned long long runB[G][RMAX];
@@ -201,6 +204,7 @@ struct StepLds {
     unsigned long long ovf, mabs;
     unsigned long long sev, samax;          // the chain's merged statistics (replay)
     int32_t sdone;
+    int32_t hfin;                           // head waves done with the finalize
 };
 
 // Applies a chunk's runs 0 .. nr - 1 of head h (its LDS run accumulators; run r > 0 opens
@@ -378,6 +382,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         S.lbfail = 0;
         S.sev = S.samax = 0;
         S.sdone = 0;
+        S.hfin = 0;
     }
     if (tid < NK) S.kcf[tid] = (double)tab;
     if (tid >= 64 && tid < 64 + NV) {
@@ -1371,7 +1376,8 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     }
     if (hw && __ballot(unsafe)) hflags |= FL_CERT;
     STAMP(9);
-    __syncthreads();               // the replay's lists are dead: the serial path reuses the LDS
+    // The head waves finish alone: the serial path's LDS lies past the replay's list, and the
+    // last head wave to finish posts the chain's statistics.
     if (hw) {
         const int qh = kvh * G + h;
         int32_t *orow = out + ((int64_t)b * g.n_q + qh) * D;
@@ -1380,7 +1386,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             // check failed). The new row came from this workgroup's waves G, G + 1, whose
             // stores are complete; the fence orders this wave's loads after them.
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-            serial_head<1, L::RS>(g, tabs, tabs->kc, tabs->vc, &S.qi[h][0], b, kvh, T, 0, !ok, S.u.fb[h], orow, st);
+            serial_head<1, L::RS>(g, tabs, tabs->kc, tabs->vc, &S.qi[h][0], b, kvh, T, 0, !ok, S.u.sr.fb[h], orow, st);
             if (lane == 0) atomicAdd(&st->serial_fallbacks, 1ull);
         } else {
             const Recip rc = reciprocal(l);
@@ -1397,19 +1403,24 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             S.ovf = tovf;
             S.mabs = tmabs;
         }
-    }
-    __syncthreads();
-    if (tid == 0) {
-        // the chain's statistics, once: the heads' merged, and the score statistics of
-        // every chunk (when the query check passed; the serial path counted them otherwise)
-        if (S.sdone & 2) {
-            atomicMax(&st->n_tokens, (unsigned long long)T);
-            if (S.sev) atomicAdd(&st->rescale_events, S.sev);
-            atomicMax(&st->max_abs_acc, S.samax);
+        int last = 0;
+        if (lane == 0) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            last = atomicAdd(&S.hfin, 1) == G - 1;
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
         }
-        if (ok) {
-            if (S.ovf) atomicAdd(&st->score_overflows, S.ovf);
-            atomicMax(&st->max_abs_score, S.mabs);
+        if (__builtin_amdgcn_readfirstlane(last) && lane == 0) {
+            // the chain's statistics, once: the heads' merged, and the score statistics of
+            // every chunk (when the query check passed; the serial path counted them otherwise)
+            if (S.sdone & 2) {
+                atomicMax(&st->n_tokens, (unsigned long long)T);
+                if (S.sev) atomicAdd(&st->rescale_events, S.sev);
+                atomicMax(&st->max_abs_acc, S.samax);
+            }
+            if (ok) {
+                if (S.ovf) atomicAdd(&st->score_overflows, S.ovf);
+                atomicMax(&st->max_abs_score, S.mabs);
+            }
         }
     }
     STAMP(10);
