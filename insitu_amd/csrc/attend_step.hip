@@ -637,6 +637,24 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     __syncthreads();                                               // B2
     STAMP(4);
 
+    // This chunk's maxima go out first (wave G + h: head h's aggregate; chunk 0: its inclusive
+    // maximum), and wave h issues the look-back's first poll (the nearest 64 predecessors'
+    // words), whose round trip the list test's scans below then overlap.
+    int64_t local0 = SCORE_LO;
+    unsigned long long pw1 = 0, pw2 = 0;
+    if (ok && wv < 2 * G && nch > 1) {
+        const int h = wv & (G - 1);
+        unsigned long long *wi0 = ck.status + ((int64_t)chain * G + h) * 2 * ck.mc;
+        if (wv >= G) {
+            local0 = wave_max_i64(lane < NW ? S.wmax[lane & (NW - 1)][h] : SCORE_LO);
+            if (lane == 0)
+                __hip_atomic_store((own ? wi0 : wi0 + ck.mc) + chunk, st_pack(own ? ST_INC : ST_AGG, ck.ep, local0),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else if (!own && (int64_t)chunk - 1 - lane >= 0) {
+            pw1 = __hip_atomic_load(wi0 + chunk - 1 - lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            pw2 = __hip_atomic_load(wi0 + ck.mc + chunk - 1 - lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
     // The list test's half that needs no M_in (its 32-bit running maxima), done here so that
     // it overlaps the look-back's wait: k32[h] holds the tokens with floor(s / 2^16) >= hi -
     // ceil(delta_max / 2^16), hi the running maximum of floor(s / 2^16) up to the token.
@@ -670,24 +688,26 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             unsigned long long *wi0 = ck.status + ((int64_t)chain * G + h) * 2 * ck.mc;
             unsigned long long *wa0 = wi0 + ck.mc;
             if (wv >= G) {
-                if (lane == 0)
-                    __hip_atomic_store((own ? wi0 : wa0) + chunk, st_pack(own ? ST_INC : ST_AGG, ck.ep, local),
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                // (published above)
             } else if (!own) {
                 int64_t base = chunk - 1;       // the predecessor lane 0 reads
                 int spins = 0;
                 bool fail = ck.spin_limit == 0;
+                bool first = true;              // the first poll's words were loaded above
                 while (!fail) {
                     const int64_t pc = base - lane;
                     unsigned long long flag = ST_INC;
                     int64_t val = SCORE_LO;
                     if (pc >= 0) {
-                        const unsigned long long w1 = __hip_atomic_load(wi0 + pc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        const unsigned long long w2 = __hip_atomic_load(wa0 + pc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        const unsigned long long w1 =
+                            first ? pw1 : __hip_atomic_load(wi0 + pc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        const unsigned long long w2 =
+                            first ? pw2 : __hip_atomic_load(wa0 + pc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                         const bool has_inc = st_flag(w1, ck.ep) == ST_INC;
                         flag = has_inc ? ST_INC : st_flag(w2, ck.ep);
                         val = st_val(has_inc ? w1 : w2);
                     }
+                    first = false;
                     const unsigned long long inc = __ballot(flag == ST_INC);
                     const int nearest = inc ? __ffsll((long long)inc) - 1 : 64;
                     const unsigned long long wait = __ballot(flag == 0 && lane <= nearest);
