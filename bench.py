@@ -1020,6 +1020,17 @@ def main() -> int:
     cache_last = caches[last % n_caches]
     if cache_last.length != a.ctx:
         raise RuntimeError(f"the last step's cache holds {cache_last.length} rows, not {a.ctx}")
+    from oracle import native
+    from oracle.quantize import Format
+    q_rot_last = rotate_q(qs[0, last])
+    want = np.concatenate([native.attend_online(q_rot_last[4 * h:4 * h + 4], cache_last.view(h), Format())[0]
+                           for h in range(N_KV)]) if a.mode != "two_pass" else None
+    if want is not None and not np.array_equal(want, out_last):
+        raise AssertionError("the last timed step disagrees with the oracle")
+    # (before the two-pass line below, whose pass rewinds every cache to ctx - 1 rows)
+    cpu = None
+    if not a.no_cpu_baseline:
+        cpu = cpu_baseline(cache_last, q_rot_last, out_last, (qs[0, last], ks[0, last], vs[0, last]))
     # The adapter's default softmax is two-pass (three launches a step): its line, K steps
     # on the same rotation, checked against the oracle's attend_two_pass.
     two_pass = None
@@ -1029,9 +1040,7 @@ def main() -> int:
         i_tp = i0 + n_tp - 1
         q_tp = rotate_q(qs[0, i_tp])
         c_tp = caches[i_tp % n_caches]
-        from oracle import native as _nat
-        from oracle.quantize import Format as _Fmt
-        want_tp = np.concatenate([_nat.attend_two_pass(q_tp[4 * h:4 * h + 4], c_tp.view(h), _Fmt())[0]
+        want_tp = np.concatenate([native.attend_two_pass(q_tp[4 * h:4 * h + 4], c_tp.view(h), Format())[0]
                                   for h in range(N_KV)])
         if not np.array_equal(want_tp, outs[i_tp].cpu().numpy()[0].astype(np.int64)):
             raise AssertionError("the two-pass line's last step disagrees with the oracle")
@@ -1040,16 +1049,6 @@ def main() -> int:
                     "us_per_decode_step": round(wall_tp / n_tp * 1e6, 2),
                     "GB/s": round(step_bytes * n_tp / wall_tp / 1e9, 3),
                     "checked": "the last step equal to oracle/c attend_two_pass"}
-    from oracle import native
-    from oracle.quantize import Format
-    q_rot_last = rotate_q(qs[0, last])
-    want = np.concatenate([native.attend_online(q_rot_last[4 * h:4 * h + 4], cache_last.view(h), Format())[0]
-                           for h in range(N_KV)]) if a.mode != "two_pass" else None
-    if want is not None and not np.array_equal(want, out_last):
-        raise AssertionError("the last timed step disagrees with the oracle")
-    cpu = None
-    if not a.no_cpu_baseline:
-        cpu = cpu_baseline(cache_last, q_rot_last, out_last, (qs[0, last], ks[0, last], vs[0, last]))
     kernel = STEP_KERNEL.get(a.mode, a.mode)
     if a.kernel == "chunked" and a.mode in ("online", "split"):
         kernel = CHUNKED_STEP_KERNEL

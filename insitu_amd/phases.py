@@ -116,11 +116,6 @@ def run(ctx_len: int, n_caches: int, reps: int, flat: bool = False) -> dict:
         per_blk = np.nanmedian(np.nanmax(R, axis=2), axis=0)     # (block, stamp)
         rep_blk = (nch - 1) * 8                                  # chain 0's last chunk
         w0 = np.nanmedian(R[:, rep_blk, 0], axis=0)               # (stamp,)
-    pub = per_blk[:, 12]
-    if nch > 1 and not np.all(np.isnan(pub)):
-        order = np.argsort(np.nan_to_num(pub, nan=-1.0))[::-1][:6]
-        print("last chunks to publish (chunk, KV head, us): " +
-              ", ".join(f"({b // 8}, {b % 8}, {pub[b]:.2f})" for b in order))
     return {"ctx": ctx_len, "flat": flat, "reps": reps, "blocks": nblk, "per_blk": per_blk, "replayer_w0": w0}
 
 
@@ -141,6 +136,11 @@ def table(res: dict) -> str:
             c0 = np.nanmedian(col[:8]) if res["blocks"] > 8 else np.nan
             lines.append(f"| {k} | {name} | {f(np.nanmedian(col))} | {f(np.nanmin(col))} | "
                          f"{f(np.nanmax(col))} | {f(res['replayer_w0'][k])} | {f(c0)} |")
+    pub = res["per_blk"][:, 12]
+    if res["blocks"] > 8 and not np.all(np.isnan(pub)):
+        order = np.argsort(np.nan_to_num(pub, nan=-1.0))[::-1][:6]
+        lines += ["", "last chunks to publish (chunk, KV head, us): " +
+                  ", ".join(f"({b // 8}, {b % 8}, {pub[b]:.2f})" for b in order)]
     return "\n".join(lines)
 
 
