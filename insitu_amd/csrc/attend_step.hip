@@ -55,7 +55,17 @@ extern "C" int insitu_step_stamps_clear() {
         if ((threadIdx.x & 63) == 0 && blockIdx.x < 8192)                                       \
             insitu_step_stamps[((size_t)blockIdx.x * 16 + (threadIdx.x >> 6)) * 32 + (k)] = _t; \
     } while (0)
+// a count instead of a time, in slots 24 and up
+#define STAMPV(k, v)                                                                            \
+    do {                                                                                        \
+        if ((threadIdx.x & 63) == 0 && blockIdx.x < 8192)                                       \
+            insitu_step_stamps[((size_t)blockIdx.x * 16 + (threadIdx.x >> 6)) * 32 + (k)] =      \
+                (unsigned long long)(v);                                                        \
+    } while (0)
 #else
+#define STAMPV(k, v) \
+    do {             \
+    } while (0)
 #define STAMP(k) \
     do {         \
     } while (0)
@@ -158,14 +168,15 @@ struct StepLds {
             union {
                 int4 tt[CHUNK][NV];         // each token's term for every value code, the 4 heads
                 // the chunk's list: (score - SCORE_LO) | token << 48 and v_norm, head h at
-                // [loff[h], ...); per head its tokens of weight: token | event << 31, p | f << 16,
-                // the bound of its term, and its term floor(v_norm * p * c_v[c] / 2^23) for each
-                // value code c
+                // [loff[h], ...); per head its tokens of weight: p | f << 16, the bound of its
+                // term | event << 31 (bounds lie below 2^25), its term
+                // floor(v_norm * p * c_v[c] / 2^23) for each value code c, and its value codes
                 struct {
                     uint64_t e[LPOOL];
                     int32_t vn[LPOOL];
-                    uint32_t itk[G][LPOOL], ipf[G][LPOOL], ib[G][LPOOL];
+                    uint32_t ipf[G][LPOOL], ib[G][LPOOL];
                     int4 it4[G][LPOOL];
+                    uint32_t iw[G][LPOOL][VWORDS];
                 } ol;
             } tu;
             uint32_t vw[CHUNK][VWORDS];     // each token's value codes
@@ -816,6 +827,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             }
             STAMP(19);
             __syncthreads();                                       // L2
+            STAMP(21);
             if (wv < G) {
                 // Head h's wave alone (the heads' waves sit on the four SIMDs): one pass over the
                 // list gives the tokens of weight, their four terms and the bound B, then the
@@ -855,16 +867,51 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
                     if (useful) {
                         const int ipos = nitem + (int)__builtin_amdgcn_mbcnt_hi(
                                                      (uint32_t)(ub >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)ub, 0u));
-                        ol.itk[h][ipos] = (uint32_t)(e >> 48) | (ev ? 0x80000000u : 0u);
-                        ol.ipf[h][ipos] = (uint32_t)p | ((uint32_t)f << 16);
+                        const int tk = (int)(e >> 48) & (CHUNK - 1);
+                        ol.ipf[h][ipos] = ev ? 0x80000000u | (uint32_t)f : (uint32_t)p;
                         ol.ib[h][ipos] = w != 0 ? __umulhi(aw, vcmax9) + 1 : 0u;
                         ol.it4[h][ipos] = make_int4(__mulhi(w, vcs[0]), __mulhi(w, vcs[1]), __mulhi(w, vcs[2]),
                                                     __mulhi(w, vcs[3]));
+#pragma unroll
+                        for (int k = 0; k < L::VWORDS; ++k) ol.iw[h][ipos][k] = S.u.ph.vw[tk][k];
                     }
                     nitem += (int)__popcll(ub);
                     nev += (int)__popcll(__ballot(ev));
                 }
+                // up to a multiple of 8 with tokens that change nothing (no event, p 0, terms and
+                // bound 0): the walks below then take whole batches of 8 with no mask
+                if (nitem + lane < ((nitem + 7) & ~7)) {
+                    ol.ipf[h][nitem + lane] = 0u;
+                    ol.ib[h][nitem + lane] = 0u;
+                    ol.it4[h][nitem + lane] = make_int4(0, 0, 0, 0);
+                }
+                STAMP(20);
+                STAMPV(24, n);
+                STAMPV(25, nitem);
+                STAMPV(26, nev);
                 const int wsel = (lane * VB) >> 5, wsh = (lane * VB) & 31;
+                const uint32_t pev = (uint32_t)uni32(S.expt[0]);   // an event's p: LUT(0)
+                // The walk, lane = channel, 8 tokens at a time: every value the 8 need (event | f
+                // or p, the bound, the four terms, this lane's value-code word) is read from the
+                // list by position, all loads issued before the first is used.
+                uint32_t pfv[8], ibv[8], wd[8];
+                int4 t4[8];
+                auto batch = [&](int i0, bool bounds) __attribute__((always_inline)) {
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) {
+                        const int i = (i0 + q) & (LPOOL - 1);
+                        pfv[q] = ol.ipf[h][i];
+                        if (bounds) ibv[q] = ol.ib[h][i];
+                        t4[q] = ol.it4[h][i];
+                        wd[q] = ol.iw[h][i][wsel];
+                    }
+                    __builtin_amdgcn_sched_barrier(0);     // every load issued before any use
+                };
+                auto term = [&](int q) __attribute__((always_inline)) {
+                    const uint32_t code = __builtin_amdgcn_ubfe(wd[q], (uint32_t)wsh, (uint32_t)VB);
+                    const int32_t t01 = code & 1 ? t4[q].y : t4[q].x, t23 = code & 1 ? t4[q].w : t4[q].z;
+                    return code & 2 ? t23 : t01;
+                };
                 if (!own) {
                     // runs: run r holds the tokens from the chunk's r-th event on (run 0: those
                     // before its first), with its sum, L, bound and opening factor
@@ -873,36 +920,44 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
                     uint32_t sL = 0;
                     uint64_t sB = 0;
                     for (int i0 = 0; i0 < nitem; i0 += 8) {
-                        uint32_t tk[8], wd[8];
+                        batch(i0, true);
+                        uint32_t any = 0;
 #pragma unroll
-                        for (int q = 0; q < 8; ++q) tk[q] = uni32((int32_t)ol.itk[h][(i0 + q) & (LPOOL - 1)]);
+                        for (int q = 0; q < 8; ++q) any |= pfv[q];
+                        if (!((uint32_t)uni32((int32_t)any) >> 31)) {
+                            // no event among them: one tree of adds (int32: the same bits in any order)
+                            int32_t t[8];
 #pragma unroll
-                        for (int q = 0; q < 8; ++q) wd[q] = S.u.ph.vw[tk[q] & (CHUNK - 1)][wsel];
+                            for (int q = 0; q < 8; ++q) t[q] = term(q);
+                            sacc += ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+#pragma unroll
+                            for (int q = 0; q < 8; ++q) {
+                                sL += (uint32_t)uni32((int32_t)pfv[q]);
+                                sB += (uint32_t)uni32((int32_t)ibv[q]);
+                            }
+                            continue;
+                        }
 #pragma unroll
                         for (int q = 0; q < 8; ++q) {
-                            if (i0 + q < nitem) {
-                                const uint32_t pf = (uint32_t)uni32((int32_t)ol.ipf[h][i0 + q]);
-                                if (tk[q] >> 31) {
-                                    if (r < RMAX) {
-                                        S.runS[h][r][lane] = sacc;
-                                        if (lane == 0) {
-                                            S.runL[h][r] = sL;
-                                            S.runB[h][r] = sB;
-                                        }
+                            const uint32_t pw = (uint32_t)uni32((int32_t)pfv[q]);
+                            const uint32_t bq = (uint32_t)uni32((int32_t)ibv[q]);
+                            if (pw >> 31) {
+                                if (r < RMAX) {
+                                    S.runS[h][r][lane] = sacc;
+                                    if (lane == 0) {
+                                        S.runL[h][r] = sL;
+                                        S.runB[h][r] = sB;
                                     }
-                                    ++r;
-                                    if (r < RMAX && lane == 0) S.runf[h][r] = (int32_t)(pf >> 16);
-                                    sacc = 0;
-                                    sL = 0;
-                                    sB = 0;
                                 }
-                                const int4 t = ol.it4[h][i0 + q];
-                                const uint32_t code = __builtin_amdgcn_ubfe(wd[q], (uint32_t)wsh, (uint32_t)VB);
-                                const int32_t t01 = code & 1 ? t.y : t.x, t23 = code & 1 ? t.w : t.z;
-                                sacc += code & 2 ? t23 : t01;
-                                sL += pf & 0xFFFF;
-                                sB += (uint32_t)uni32((int32_t)ol.ib[h][i0 + q]);
+                                ++r;
+                                if (r < RMAX && lane == 0) S.runf[h][r] = (int32_t)(pw & 0xFFFF);
+                                sacc = 0;
+                                sL = 0;
+                                sB = 0;
                             }
+                            sacc += term(q);
+                            sL += pw >> 31 ? pev : pw;
+                            sB += bq;
                         }
                     }
                     if (r < RMAX) {
@@ -919,27 +974,29 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
                     flags |= FL_CERT;
                 } else {
                     nev0 = nev;
+                    // Chunk 0's events are dense (its running maximum starts low), so every token
+                    // takes the same steps, with no branch: a factor of 2^15 where there is no
+                    // event (floor(acc * 2^15 / 2^15) = acc). The batch's factors, p and terms
+                    // first (none depends on acc), then the chain of rescales and adds alone, so
+                    // that the in-order wave does not stall on them token by token.
                     for (int i0 = 0; i0 < nitem; i0 += 8) {
-                        uint32_t tk[8], wd[8];
-#pragma unroll
-                        for (int q = 0; q < 8; ++q) tk[q] = uni32((int32_t)ol.itk[h][(i0 + q) & (LPOOL - 1)]);
-#pragma unroll
-                        for (int q = 0; q < 8; ++q) wd[q] = S.u.ph.vw[tk[q] & (CHUNK - 1)][wsel];
+                        batch(i0, false);
+                        int64_t fq[8];
+                        uint32_t pq[8];
+                        int32_t tq[8];
 #pragma unroll
                         for (int q = 0; q < 8; ++q) {
-                            if (i0 + q < nitem) {
-                                const uint32_t pf = (uint32_t)uni32((int32_t)ol.ipf[h][i0 + q]);
-                                if (tk[q] >> 31) {
-                                    const int64_t fq = pf >> 16;
-                                    acc0 = (int32_t)(((int64_t)acc0 * fq) >> PROB_FRAC);
-                                    l0 = (l0 * fq) >> PROB_FRAC;
-                                }
-                                const int4 t = ol.it4[h][i0 + q];
-                                const uint32_t code = __builtin_amdgcn_ubfe(wd[q], (uint32_t)wsh, (uint32_t)VB);
-                                const int32_t t01 = code & 1 ? t.y : t.x, t23 = code & 1 ? t.w : t.z;
-                                acc0 += code & 2 ? t23 : t01;
-                                l0 += pf & 0xFFFF;
-                            }
+                            const uint32_t pw = (uint32_t)uni32((int32_t)pfv[q]);
+                            const bool ev = (pw >> 31) != 0;
+                            fq[q] = ev ? (int64_t)(pw & 0xFFFF) : (int64_t)1 << PROB_FRAC;
+                            pq[q] = ev ? pev : pw;
+                            tq[q] = term(q);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                        for (int q = 0; q < 8; ++q) {
+                            acc0 = (int32_t)(((int64_t)acc0 * fq[q]) >> PROB_FRAC) + tq[q];
+                            l0 = ((l0 * fq[q]) >> PROB_FRAC) + pq[q];
                         }
                     }
                 }
@@ -1086,12 +1143,13 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         }
         if ((candb >> lane) & 1ull) S.u.ph.rix[tid] = rix;
     }
-    if (lane == 0) S.ccnt[wv] = work ? (int32_t)__popcll(candb) : 0;
-    __syncthreads();                                               // B6
     // The chunk's candidates listed in token order (16-lane prefix sum of the waves' counts):
-    // the walk then gives every wave an equal share, wherever the candidates crowd.
+    // the walk then gives every wave an equal share, wherever the candidates crowd. (work is
+    // uniform in the workgroup: a chunk that took the list path passes none of these barriers.)
     int n_all = 0;
     if (work) {
+        if (lane == 0) S.ccnt[wv] = (int32_t)__popcll(candb);
+        __syncthreads();                                           // B6 (uniform)
         uint32_t c = lane < NW ? (uint32_t)S.ccnt[lane & (NW - 1)] : 0u;
         c += dpp32<DPP_ROW_SHR1>(0u, c);
         c += dpp32<DPP_ROW_SHR2>(0u, c);
@@ -1163,7 +1221,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             if (ro < RMAX && P[h]) atomicAdd(&S.runS[h][ro][lane], P[h]);
         }
     }
-    __syncthreads();                                               // B7
+    if (work) __syncthreads();                                     // B7 (uniform)
     STAMP(7);
 
     // -- P5: chunk 0 folds its runs; the others publish theirs ---------------------
@@ -1227,6 +1285,8 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         return;
     }
     if (newrow && (wv == G || wv == G + 1)) stores_done();         // the new row, for the serial path
+    // the replay's list lies over the chunk list, which the other head waves may still read
+    if (!work) __syncthreads();                                    // (uniform)
     STAMP(8);
 
     // -- P6: the replay --------------------------------------------------------------
@@ -1300,13 +1360,10 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     bool unsafe = false;
     if (hw) {
         const int64_t hbase = ((int64_t)chain * G + h) * ck.pool;
-        if (nch > 1) {
-            // chunk 0's state: acc (lane = channel), l | events << 32 (its header is current)
-            aw = (int32_t)get32(&ck.segS[hbase * D + lane]);
-            const uint64_t lf = get64(&ck.meta[hbase * 2]);
-            l = (int64_t)(uint32_t)lf;
-            events = lf >> 32;
-        }
+        // this head's slot 0 (chunk 0's state), lane = channel, and its meta words
+        const int32_t *segh = ck.segS + hbase * D + lane;
+        const uint64_t *metah = ck.meta + hbase * 2;
+        bool take_c0 = nch > 1;
         const int tot_h = S.total[h];
         for (int g0 = 0; g0 < tot_h && !hflags; g0 += RMAX) {
             const int nb = tot_h - g0 < RMAX ? tot_h - g0 : RMAX;
@@ -1318,13 +1375,26 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             const int slot = (int)(ent & (RUN_EVENT - 1));
             const bool bad = mine && slot >= ck.pool;
             const bool ld = mine && !bad;
-            const uint64_t lf = ld ? get64(&ck.meta[(hbase + slot) * 2]) : 0ull;
-            const int64_t bb = ld ? (int64_t)get64(&ck.meta[(hbase + slot) * 2 + 1]) : 0;
+            // Every load first, none of them conditional, so that all are in flight together
+            // and the first use waits once: chunk 0's state (its header is current: acc, and
+            // l | events << 32 in lane 63's meta word), each run's L | f << 32 and bound (lane
+            // = run) and its sums (lane = channel). A lane past nb, or one whose slot failed
+            // the check, reads slot 0, which lies in the pool, and its values count 0.
+            const int sl = ld ? slot : 0;
+            const uint32_t acc_c0 = get32(segh);
+            const uint64_t lfr = get64(metah + (lane == 63 ? 0 : 2 * sl));
+            const uint64_t bbr = get64(metah + 2 * sl + 1);
             int32_t v[RMAX];
 #pragma unroll
-            for (int k = 0; k < RMAX; ++k) {
-                const int sk = __builtin_amdgcn_readlane(ld ? slot : -1, k);
-                v[k] = k < nb && sk >= 0 ? (int32_t)get32(&ck.segS[(hbase + sk) * D + lane]) : 0;
+            for (int k = 0; k < RMAX; ++k) v[k] = (int32_t)get32(segh + (int64_t)__builtin_amdgcn_readlane(sl, k) * D);
+            const uint64_t lf = ld ? lfr : 0ull;
+            const int64_t bb = ld ? (int64_t)bbr : 0;
+            if (take_c0) {
+                const uint64_t lf0 = readlane64((int64_t)lfr, 63);
+                aw = (int32_t)acc_c0;
+                l = (int64_t)(uint32_t)lf0;
+                events = lf0 >> 32;
+                take_c0 = false;
             }
             if (__ballot(bad)) {
                 st->fault = 1;
@@ -1355,6 +1425,10 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
                 // A rescale never grows |acc|, so the block's bound certifies blocks with events
                 // too: then only their rescales are applied in turn, with no check per run.
                 const bool cert = !((uint32_t)(bigm >> k0) & bmask) && !__ballot(a + bsum > ACC_HI);
+                if (kn < 8) {
+#pragma unroll
+                    for (int k = 1; k < 8; ++k) v[k0 + k] = k < kn ? v[k0 + k] : 0;
+                }
                 if (cert && !bev) {
                     aw += ((v[k0] + v[k0 + 1]) + (v[k0 + 2] + v[k0 + 3])) + ((v[k0 + 4] + v[k0 + 5]) + (v[k0 + 6] + v[k0 + 7]));
                     l += (uint32_t)__builtin_amdgcn_readlane((int)PL, k0 + kn - 1) - before_l;
@@ -1375,6 +1449,13 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
                     }
                 }
             }
+        }
+        if (take_c0) {
+            // no runs to walk (or the flags sent the head to the serial path)
+            const uint64_t lf0 = get64(metah);
+            aw = (int32_t)get32(segh);
+            l = (int64_t)(uint32_t)lf0;
+            events = lf0 >> 32;
         }
     }
     if (nch > 1 && hw && (work || olist) && !hflags) {

@@ -39,6 +39,8 @@ PHASES = [
     (17, "P3 chunk 0: list test"),
     (18, "P3 chunk 0: barrier L1"),
     (19, "P3 chunk 0: list compacted"),
+    (21, "P3 list: barrier L2"),
+    (20, "P3 list: pass (events, p, terms)"),
     (16, "P3 chunk 0 folded from its list"),
     (11, "P3 event scan (barrier B4)"),
     (13, "P3 candidates, terms (barrier B5)"),
@@ -95,7 +97,7 @@ def run(ctx_len: int, n_caches: int, reps: int, flat: bool = False) -> dict:
     nch = (ctx_len + 1023) // 1024
     nblk = nch * 8
     buf = np.zeros(MAXBLK * NWAVES * NSTAMPS, dtype=np.uint64)
-    runs = []
+    runs, counts = [], []
     for i in range(reps + 4):
         c = caches[i % n_caches]
         c.set_length(ctx_len - 1)
@@ -108,6 +110,8 @@ def run(ctx_len: int, n_caches: int, reps: int, flat: bool = False) -> dict:
         if i < 4:
             continue                                   # warmup
         st = buf[:nblk * NWAVES * NSTAMPS].reshape(nblk, NWAVES, NSTAMPS).astype(np.int64)
+        counts.append(st[:, :4, 24:27].copy())          # head waves: list entries, tokens of weight, events
+        st[:, :, 24:] = 0
         t0 = st[:, :, 0][st[:, :, 0] > 0].min()
         runs.append(np.where(st > 0, (st - t0) * 0.01, np.nan))
     R = np.stack(runs)                                  # (reps, block, wave, stamp), us
@@ -116,7 +120,9 @@ def run(ctx_len: int, n_caches: int, reps: int, flat: bool = False) -> dict:
         per_blk = np.nanmedian(np.nanmax(R, axis=2), axis=0)     # (block, stamp)
         rep_blk = (nch - 1) * 8                                  # chain 0's last chunk
         w0 = np.nanmedian(R[:, rep_blk, 0], axis=0)               # (stamp,)
-    return {"ctx": ctx_len, "flat": flat, "reps": reps, "blocks": nblk, "per_blk": per_blk, "replayer_w0": w0}
+    C = np.stack(counts[4:]) if len(counts) > 4 else None          # (reps, block, head, 3)
+    return {"ctx": ctx_len, "flat": flat, "reps": reps, "blocks": nblk, "per_blk": per_blk, "replayer_w0": w0,
+            "counts": C}
 
 
 def table(res: dict) -> str:
@@ -136,6 +142,14 @@ def table(res: dict) -> str:
             c0 = np.nanmedian(col[:8]) if res["blocks"] > 8 else np.nan
             lines.append(f"| {k} | {name} | {f(np.nanmedian(col))} | {f(np.nanmin(col))} | "
                          f"{f(np.nanmax(col))} | {f(res['replayer_w0'][k])} | {f(c0)} |")
+    C = res.get("counts")
+    if C is not None and C.any():
+        c0, rest = C[:, :8], C[:, 8:]
+        lines += ["", "chunk list per head (median over steps; chunk 0 / other chunks): "
+                  f"entries {np.median(c0[..., 0]):.0f} (max {c0[..., 0].max()}) / {np.median(rest[..., 0]) if rest.size else 0:.1f} "
+                  f"(max {rest[..., 0].max() if rest.size else 0}), tokens of weight {np.median(c0[..., 1]):.0f} "
+                  f"(max {c0[..., 1].max()}) / {np.median(rest[..., 1]) if rest.size else 0:.1f}, "
+                  f"events {np.median(c0[..., 2]):.0f} (max {c0[..., 2].max()})"]
     pub = res["per_blk"][:, 12]
     if res["blocks"] > 8 and not np.all(np.isnan(pub)):
         order = np.argsort(np.nan_to_num(pub, nan=-1.0))[::-1][:6]
