@@ -147,7 +147,6 @@ struct Sck {
     unsigned int *done;           // [chain]: chunks done with their runs
     uint64_t *meta;               // [chain][G][pool][2]: L | f << 32, B
     int32_t *segS;                // [chain][G][pool][D]
-    double *qst;                  // [workgroup][D][G]: the rotated query rows, fp64
     int32_t mc, pool;
     uint32_t ep;                  // this call's epoch, 1 .. 2^14 - 1
     int32_t spin_limit;
@@ -159,8 +158,7 @@ struct StepLds {
     static constexpr int VWORDS = D * VB / 32;
     static constexpr int RS = (D * KB / 8 + D * VB / 8 + 4 + 3) / 4 * 4;
     // the small tables first: their reads then take the LDS address from an immediate offset
-    double kcf[16];
-    int32_t vc32[8];
+    double kcd[256][2];                     // a key-code byte's two centroids (low nibble first)
     int32_t vc9[8];                         // the value centroids << 9 (|c| < 2^18)
     int32_t expt[256];
     union {
@@ -197,7 +195,10 @@ struct StepLds {
     unsigned long long runB[G][RMAX];
     uint32_t runL[G][RMAX];
     int32_t runf[G][RMAX];
-    int32_t qi[G][D];                       // the rotated query rows, for the serial path
+    int32_t qi[G][D];                       // the rotated query rows (the score, the serial path)
+    // the head waves' planes (key words, value words, norm word a lane), loaded for them by
+    // waves G .. 2G - 1, so that a head wave's first load is its query row
+    uint32_t hpl[G][D * KB / 32 + D * VB / 32 + 1][64];
     uint8_t codes[2][MAX_D];                // the new token's key and value codes
     uint32_t nk[D * 4 / 32 + 1], nv[D * 2 / 32 + 1], nn;   // the new row: key words, value words, norms
     int64_t wmax[NW][G];
@@ -211,7 +212,6 @@ struct StepLds {
     int qbad[G];
     int sbad[G];                            // a replay slot index past the pool (a fault)
     int lbfail, last;
-    uint64_t qaddr;                         // the query staging's address, handed over the barrier
     unsigned long long ovf, mabs;
     unsigned long long sev, samax;          // the chain's merged statistics (replay)
     int32_t sdone;
@@ -321,13 +321,14 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         bl = tabs->kbnd[lane];
     else if (newrow && wv == G + 1 && lane < NV - 1)
         bl = tabs->vbnd[lane];
-    int64_t tab = 0;
-    int32_t ex = 0;
-    if (tid < NK)
-        tab = tabs->kc[tid];
-    else if (tid >= 64 && tid < 64 + NV)
-        tab = tabs->vc[tid - 64];
-    if (tid >= 384 && tid < 384 + 256) ex = tabs->exp_table[tid - 384];
+    const double kc_absmax = tabs->kc_absmax;
+    // The score's table by code byte (two channels' key centroids in one LDS read), loaded by
+    // waves past the head waves, whose one load before the rotation is their query row.
+    int64_t kp0 = 0, kp1 = 0;
+    if (tid >= 512 && tid < 512 + 256) {
+        kp0 = tabs->kc[(tid - 512) & 15];
+        kp1 = tabs->kc[(tid - 512) >> 4];
+    }
     uint32_t kw[KWORDS + 1];
     uint32_t vwd[VWORDS];
     uint32_t nw = 0;
@@ -335,51 +336,70 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     for (int i = 0; i <= KWORDS; ++i) kw[i] = 0;
 #pragma unroll
     for (int i = 0; i < VWORDS; ++i) vwd[i] = 0;
-    // The token's planes: key words, value words, norms. The waves that stage the query rows
-    // request them after the staging, whose store wait would otherwise wait for them too.
-    auto load_planes = [&]() __attribute__((always_inline)) {
-        if (slice > 0) {
-            // a helper: the key words of its slice of token hidx, from word 0 on
-            if (!hlive || hfresh) return;
-            const int w0 = cps >= 8 ? slice * cps / 8 : slice / 2;     // the slice's first word
-            const uint4 v = *(const uint4 *)(hb + (w0 >> 2) * g.span + (t0 + hidx) * 16);
+    // Wave w's planes (key words, value words, norm word) into (k, v, n): a token wave's own
+    // token, or a helper's slice of its token wave's token; nothing for a token past the
+    // context or the step's new one (its row arrives through LDS).
+    auto load_planes = [&](int w, uint32_t(&k)[KWORDS + 1], uint32_t(&v)[VWORDS], uint32_t &n)
+        __attribute__((always_inline)) {
+        const int sl = w / ntw, tww = w - sl * ntw;
+        if (sl > 0) {
+            // a helper: the key words of its slice of token hx, from word 0 on
+            const int hx = 64 * tww + lane;
+            if (!(w < ntw * sp && t0 + hx < T) || (newrow && hx == tln)) return;
+            const int w0 = cps >= 8 ? sl * cps / 8 : sl / 2;       // the slice's first word
+            const uint4 x = *(const uint4 *)(hb + (w0 >> 2) * g.span + (t0 + hx) * 16);
             // slices of 4 words start at a plane, of 2 at an even word, of 1 or half anywhere
-            const uint32_t x0 = (w0 & 2) ? v.z : v.x, x1 = (w0 & 2) ? v.w : v.y;
-            kw[0] = ((w0 & 1) ? x1 : x0) >> (cps >= 8 ? 0 : 16 * (slice & 1));
-            kw[1] = x1;
-            kw[2] = v.z;
-            kw[3] = v.w;
+            const uint32_t x0 = (w0 & 2) ? x.z : x.x, x1 = (w0 & 2) ? x.w : x.y;
+            k[0] = ((w0 & 1) ? x1 : x0) >> (cps >= 8 ? 0 : 16 * (sl & 1));
+            k[1] = x1;
+            k[2] = x.z;
+            k[3] = x.w;
             return;
         }
-        if (!live || fresh) return;
-        const int64_t t = t0 + tid;
+        const int lt = 64 * w + lane;
+        if (!(t0 + lt < T) || (newrow && lt == tln)) return;
+        const int64_t t = t0 + lt;
 #pragma unroll
         for (int p = 0; p < NFULL; ++p) {
-            const uint4 v = *(const uint4 *)(hb + p * g.span + t * 16);
-            kw[4 * p] = v.x;
-            kw[4 * p + 1] = v.y;
-            kw[4 * p + 2] = v.z;
-            kw[4 * p + 3] = v.w;
+            const uint4 x = *(const uint4 *)(hb + p * g.span + t * 16);
+            k[4 * p] = x.x;
+            k[4 * p + 1] = x.y;
+            k[4 * p + 2] = x.z;
+            k[4 * p + 3] = x.w;
         }
         if (HALF) {
-            const uint2 v = *(const uint2 *)(hb + NFULL * g.span + t * 8);
-            kw[4 * NFULL] = v.x;
-            kw[4 * NFULL + 1] = v.y;
+            const uint2 x = *(const uint2 *)(hb + NFULL * g.span + t * 8);
+            k[4 * NFULL] = x.x;
+            k[4 * NFULL + 1] = x.y;
         }
         if (VB == 2) {
-            const uint4 v = *(const uint4 *)(hb + KPL * g.span + t * 16);
-            vwd[0] = v.x;
-            vwd[1] = v.y;
-            vwd[2 % VWORDS] = v.z;
-            vwd[3 % VWORDS] = v.w;
+            const uint4 x = *(const uint4 *)(hb + KPL * g.span + t * 16);
+            v[0] = x.x;
+            v[1] = x.y;
+            v[2 % VWORDS] = x.z;
+            v[3 % VWORDS] = x.w;
         } else {
-            const uint2 v = *(const uint2 *)(hb + KPL * g.span + t * 8);
-            vwd[0] = v.x;
-            vwd[1 % VWORDS] = v.y;
+            const uint2 x = *(const uint2 *)(hb + KPL * g.span + t * 8);
+            v[0] = x.x;
+            v[1 % VWORDS] = x.y;
         }
-        nw = *(const uint32_t *)(hb + (KPL + 1) * g.span + t * 4);
+        n = *(const uint32_t *)(hb + (KPL + 1) * g.span + t * 4);
     };
-    if (wv >= G) load_planes();
+    if (wv >= G) load_planes(wv, kw, vwd, nw);
+    if (wv >= G && wv < 2 * G) {
+        // head wave wv - G's planes, handed over in LDS
+        uint32_t k2[KWORDS + 1], v2[VWORDS], n2 = 0;
+#pragma unroll
+        for (int i = 0; i <= KWORDS; ++i) k2[i] = 0;
+#pragma unroll
+        for (int i = 0; i < VWORDS; ++i) v2[i] = 0;
+        load_planes(wv - G, k2, v2, n2);
+#pragma unroll
+        for (int i = 0; i < KWORDS; ++i) S.hpl[wv - G][i][lane] = k2[i];
+#pragma unroll
+        for (int i = 0; i < VWORDS; ++i) S.hpl[wv - G][KWORDS + i][lane] = v2[i];
+        S.hpl[wv - G][KWORDS + VWORDS][lane] = n2;
+    }
     // zero the run accumulators (LDS atomics add into them)
     for (int i = tid; i < G * RMAX * D; i += NT) (&S.runS[0][0][0])[i] = 0;
     if (tid < G * RMAX) {
@@ -395,54 +415,38 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         S.sdone = 0;
         S.hfin = 0;
     }
-    if (tid < NK) S.kcf[tid] = (double)tab;
-    if (tid >= 64 && tid < 64 + NV) {
-        S.vc32[tid - 64] = (int32_t)tab;   // |centroid| < 2^18 (Q1.15)
-        S.vc9[tid - 64] = (int32_t)tab * 512;
+    if (tid >= 512 && tid < 512 + 256) {
+        S.kcd[tid - 512][0] = (double)kp0;          // |centroid| < 2^18: exact
+        S.kcd[tid - 512][1] = (double)kp1;
     }
-    if (tid >= 384 && tid < 384 + 256) S.expt[tid - 384] = ex;
-    double *qst = ck.qst + (size_t)blockIdx.x * (D * G);
     if (wv < G) {
         // Chunk 0 counts the queries' range errors, once per call: values beyond int32
         // after the rotation, and rotated values beyond the 24-bit seam's +-2^27.
         int32_t r[1];
+#ifdef INSITU_STEP_STAMPS
+        asm volatile("" ::"v"(xv));
+        STAMP(29);
+#endif
         const int32_t in[1] = {xv};
         rotate_loaded<1>(in, D, si.rounds, si.sg, r, own ? &st->range_errors : nullptr);
+        STAMP(27);
+        // The rotated row, for every wave's score (which reads it from LDS after the barrier)
+        // and the serial path. Scores stay exact fp64 integers when ||q||_1 * max|c| < 2^51
+        // (attention.py:333-359 computes them in int64); rotated values beyond the 24-bit
+        // seam's +-2^27 count as range errors.
         S.qi[wv][lane] = r[0];
-        // The staging [head][channel]: this wave's 512 bytes are its own, so that it can warm
-        // the scalar cache with them as soon as its stores are done. Scores stay exact fp64
-        // integers when ||q||_1 * max|c| < 2^51 (attention.py:333-359 computes them in int64);
-        // rotated values beyond the 24-bit seam's +-2^27 count as range errors.
         const int64_t xq = r[0];
-        qst[wv * D + lane] = (double)xq;
-        const int64_t aq = xq < 0 ? -xq : xq;
-        const int64_t l1 = wave_sum_i64(aq);                 // < 2^38: exact as a double below
-        const int64_t bad = wave_sum_i64(aq >= Q_ROT_LIMIT ? 1 : 0);
+        const uint32_t aq = (uint32_t)(xq < 0 ? -xq : xq);  // <= 2^31
+        // ||q||_1 from the sums of |q|'s 16-bit halves (each below 2^22 over 64 lanes)
+        const uint32_t halves[2] = {aq >> 16, aq & 0xFFFFu};
+        uint32_t hs[2];
+        wave_sum_u32_n<2>(halves, hs);
+        const int64_t l1 = (int64_t)hs[0] * 65536 + hs[1];   // < 2^38: exact as a double below
+        const int bad = __popcll(__ballot(aq >= (uint32_t)Q_ROT_LIMIT));
         if (own && lane == 0 && bad) atomicAdd(&st->range_errors, (unsigned long long)bad);
-        const bool okh = (double)l1 * tabs->kc_absmax < DOT_LIMIT;
+        const bool okh = (double)l1 * kc_absmax < DOT_LIMIT;
         if (lane == 0) S.qbad[wv] = okh ? 0 : 1;
-        if (wv == 0 && lane == 0) S.qaddr = (uint64_t)(uintptr_t)qst;
-        stores_done();             // the staging is in L2 before the barrier: the score reads it by scalar loads
-        // Warm the scalar cache with this wave's staging (written by this wave alone, and
-        // complete): its 512 bytes, one load per 64-byte line, all in flight together, so that
-        // the score loop's scalar loads hit.
-        {
-            uint64_t d0, d1, d2, d3, d4, d5, d6, d7;
-            asm volatile(
-                "s_load_dwordx2 %0, %8, 0x0\n\t"
-                "s_load_dwordx2 %1, %8, 0x40\n\t"
-                "s_load_dwordx2 %2, %8, 0x80\n\t"
-                "s_load_dwordx2 %3, %8, 0xc0\n\t"
-                "s_load_dwordx2 %4, %8, 0x100\n\t"
-                "s_load_dwordx2 %5, %8, 0x140\n\t"
-                "s_load_dwordx2 %6, %8, 0x180\n\t"
-                "s_load_dwordx2 %7, %8, 0x1c0\n\t"
-                "s_waitcnt lgkmcnt(0)"
-                : "=&s"(d0), "=&s"(d1), "=&s"(d2), "=&s"(d3), "=&s"(d4), "=&s"(d5), "=&s"(d6), "=&s"(d7)
-                : "s"(qst + 64 * wv)
-                : "memory");
-        }
-        load_planes();
+        STAMP(28);
     } else if (newrow && wv < G + 2) {
         // the new token: rotate, norm, codes (quantize.py:164-212), pack (:237-252), store
         const int f = wv - G;      // 0: key, 1: value
@@ -493,6 +497,19 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     __syncthreads();                                               // B1
     STAMP(2);
     const bool ok = !(S.qbad[0] | S.qbad[1] | S.qbad[2] | S.qbad[3]);
+    // the value centroids and the exp table, first read after barrier B2: requested here and
+    // stored before B2, so that neither barrier waits for them
+    int64_t tab = 0;
+    int32_t ex = 0;
+    if (tid >= 320 && tid < 320 + NV) tab = tabs->vc[tid - 320];
+    if (tid >= 384 && tid < 384 + 256) ex = tabs->exp_table[tid - 384];
+    if (wv < G) {
+#pragma unroll
+        for (int i = 0; i < KWORDS; ++i) kw[i] = S.hpl[wv][i][lane];
+#pragma unroll
+        for (int i = 0; i < VWORDS; ++i) vwd[i] = S.hpl[wv][KWORDS + i][lane];
+        nw = S.hpl[wv][KWORDS + VWORDS][lane];
+    }
     if (fresh) {
 #pragma unroll
         for (int i = 0; i < KWORDS; ++i) kw[i] = S.nk[i];
@@ -519,71 +536,52 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     double acc[G];
 #pragma unroll
     for (int h = 0; h < G; ++h) acc[h] = 0.0;
-    // The loop for NS steps of two channels: straight-line code, so that no copy of a register
-    // that a load still fills sits between a load and its wait.
+    // The loop for NS steps of two channels. The query values come from VGPRs by row broadcast:
+    // register j holds, in every row of 16 lanes, channels 4j .. 4j + 3 (of this slice) of the 4
+    // heads, lane 4 c + h: channel 4j + c of head h, and the FMA's DPP operand row_newbcast:n
+    // hands lane n of the row to all 16 (the same value in every row, so in every lane). The
+    // centroids of a step's two channels come from one LDS read, by the token's code byte.
     auto score_steps = [&](auto ns) __attribute__((always_inline)) {
         constexpr int NS = decltype(ns)::value;
-        // Two channels a step, software-pipelined by hand: wait for this step's centroids
-        // (LDS) and query values (scalar loads), request the next step's, then this step's
-        // FMAs, which hide the latency. The loads are issued from inline asm, so that the
-        // compiler neither hoists them (the query staging is read-only to it) nor inserts a
-        // wait of its own (scalar and LDS loads share one counter and scalar loads return
-        // out of order, so any wait of its own would be a wait for everything); the asm that
-        // requests the next step also takes the accumulators, so the FMAs follow it.
-        auto caddr = [&](int ch) __attribute__((always_inline)) {
-            const int bo = KB * ch, wi = bo >> 5, sh = bo & 31;
-            const uint32_t win = sh == 0 ? kw[wi] : __builtin_amdgcn_alignbit(kw[wi + 1], kw[wi], sh);
-            return (uint32_t)(uintptr_t)&S.kcf[win & (NK - 1)];
-        };
-        const uint64_t qa = (uint64_t)uni64((int64_t)S.qaddr) + (uint64_t)(slice * cps * 8);
-        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-        double c0, c1;
-        u32x4 q0, q1, q2, q3;              // head h: the step's two channels' fp64 values
-        asm volatile("ds_read_b64 %0, %1" : "=v"(c0) : "v"(caddr(0)));
-        asm volatile("ds_read_b64 %0, %1" : "=v"(c1) : "v"(caddr(1)));
-        asm volatile(
-            "s_load_dwordx4 %0, %4, 0x0\n\t"
-            "s_load_dwordx4 %1, %4, 0x200\n\t"
-            "s_load_dwordx4 %2, %4, 0x400\n\t"
-            "s_load_dwordx4 %3, %4, 0x600"
-            : "=s"(q0), "=s"(q1), "=s"(q2), "=s"(q3)
-            : "s"(qa));
+        constexpr int NQ = NS / 2;                                  // query registers
+        static_assert(KB == 4, "the score reads two 4-bit codes' centroids by code byte");
+        double(&ac)[G] = acc;
+        int32_t qi[NQ];
+        {
+            const int qh = lane & 3, qc = (lane >> 2) & 3;
 #pragma unroll
-        for (int st2 = 0; st2 < D / 2; ++st2) {
-            if (st2 < NS) {
-                asm volatile("s_waitcnt lgkmcnt(0)"
-                             : "+v"(c0), "+v"(c1), "+s"(q0), "+s"(q1), "+s"(q2), "+s"(q3), "+v"(acc[0]),
-                               "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]));
-                double n0 = 0.0, n1 = 0.0;
-                u32x4 m0 = q0, m1 = q1, m2 = q2, m3 = q3;
-                if (st2 + 1 < NS) {
-                    asm volatile("ds_read_b64 %0, %1" : "=v"(n0) : "v"(caddr(2 * st2 + 2)));
-                    asm volatile("ds_read_b64 %0, %1" : "=v"(n1) : "v"(caddr(2 * st2 + 3)));
-                    asm volatile(
-                        "s_load_dwordx4 %0, %8, %9\n\t"
-                        "s_load_dwordx4 %1, %8, %10\n\t"
-                        "s_load_dwordx4 %2, %8, %11\n\t"
-                        "s_load_dwordx4 %3, %8, %12"
-                        : "=s"(m0), "=s"(m1), "=s"(m2), "=s"(m3), "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]),
-                          "+v"(acc[3])
-                        : "s"(qa), "i"(16 * (st2 + 1)), "i"(512 + 16 * (st2 + 1)), "i"(1024 + 16 * (st2 + 1)),
-                          "i"(1536 + 16 * (st2 + 1)));
-                }
-                const u32x4 qh[G] = {q0, q1, q2, q3};
+            for (int j = 0; j < NQ; ++j) qi[j] = S.qi[qh][slice * cps + 4 * j + qc];
+        }
 #pragma unroll
-                for (int h = 0; h < G; ++h) {
-                    const double qa0 = __builtin_bit_cast(double, (uint64_t)qh[h][0] | ((uint64_t)qh[h][1] << 32));
-                    const double qa1 = __builtin_bit_cast(double, (uint64_t)qh[h][2] | ((uint64_t)qh[h][3] << 32));
-                    acc[h] = fma(qa0, c0, acc[h]);
-                    acc[h] = fma(qa1, c1, acc[h]);
-                }
-                c0 = n0;
-                c1 = n1;
-                q0 = m0;
-                q1 = m1;
-                q2 = m2;
-                q3 = m3;
-            }
+        for (int j = 0; j < NQ; ++j) {
+            // steps 2j and 2j + 1: channels 4j .. 4j + 3, centroids by code bytes 2j and 2j + 1
+            const uint32_t w = kw[j >> 1];
+            const uint32_t b0 = __builtin_amdgcn_ubfe(w, (uint32_t)(16 * (j & 1)), 8u);
+            const uint32_t b1 = __builtin_amdgcn_ubfe(w, (uint32_t)(16 * (j & 1) + 8), 8u);
+            const double c0 = S.kcd[b0][0], c1 = S.kcd[b0][1], c2 = S.kcd[b1][0], c3 = S.kcd[b1][1];
+            double qd;
+            // The conversion writes the DPP operand: two wait states (s_nop 1) before its first
+            // DPP read, which the compiler cannot see inside the asm.
+            asm("v_cvt_f64_i32 %4, %5\n\t"
+                "s_nop 1\n\t"
+                "v_fmac_f64_dpp %0, %4, %6 row_newbcast:0 row_mask:0xf bank_mask:0xf\n\t"
+                "v_fmac_f64_dpp %1, %4, %6 row_newbcast:1 row_mask:0xf bank_mask:0xf\n\t"
+                "v_fmac_f64_dpp %2, %4, %6 row_newbcast:2 row_mask:0xf bank_mask:0xf\n\t"
+                "v_fmac_f64_dpp %3, %4, %6 row_newbcast:3 row_mask:0xf bank_mask:0xf\n\t"
+                "v_fmac_f64_dpp %0, %4, %7 row_newbcast:4 row_mask:0xf bank_mask:0xf\n\t"
+                "v_fmac_f64_dpp %1, %4, %7 row_newbcast:5 row_mask:0xf bank_mask:0xf\n\t"
+                "v_fmac_f64_dpp %2, %4, %7 row_newbcast:6 row_mask:0xf bank_mask:0xf\n\t"
+                "v_fmac_f64_dpp %3, %4, %7 row_newbcast:7 row_mask:0xf bank_mask:0xf\n\t"
+                "v_fmac_f64_dpp %0, %4, %8 row_newbcast:8 row_mask:0xf bank_mask:0xf\n\t"
+                "v_fmac_f64_dpp %1, %4, %8 row_newbcast:9 row_mask:0xf bank_mask:0xf\n\t"
+                "v_fmac_f64_dpp %2, %4, %8 row_newbcast:10 row_mask:0xf bank_mask:0xf\n\t"
+                "v_fmac_f64_dpp %3, %4, %8 row_newbcast:11 row_mask:0xf bank_mask:0xf\n\t"
+                "v_fmac_f64_dpp %0, %4, %9 row_newbcast:12 row_mask:0xf bank_mask:0xf\n\t"
+                "v_fmac_f64_dpp %1, %4, %9 row_newbcast:13 row_mask:0xf bank_mask:0xf\n\t"
+                "v_fmac_f64_dpp %2, %4, %9 row_newbcast:14 row_mask:0xf bank_mask:0xf\n\t"
+                "v_fmac_f64_dpp %3, %4, %9 row_newbcast:15 row_mask:0xf bank_mask:0xf"
+                : "+v"(ac[0]), "+v"(ac[1]), "+v"(ac[2]), "+v"(ac[3]), "=&v"(qd)
+                : "v"(qi[j]), "v"(c0), "v"(c1), "v"(c2), "v"(c3));
         }
     };
     if (ok && scorer) {
@@ -595,6 +593,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         default: score_steps(std::integral_constant<int, 2>{}); break;
         }
     }
+    STAMP(22);
     if (sp > 1) {
         // the slices' partial sums to their token wave, through the (not yet used) tt area
         double *part = (double *)&S.u.ph.tu.tt[0][0];
@@ -630,20 +629,31 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     for (int i = 0; i < VWORDS; ++i) S.u.ph.vw[tid][i] = vwd[i];
     // the wave's maxima (scores lie in [SCORE_LO, SCORE_HI], within +-2^47: 32-bit steps),
     // its overflow count (at most 4 a lane: three ballots) and its largest |score|
+    // (the 4 heads' maxima and the largest |score| - 2^47 reduced together)
+    int64_t wm[G + 1], mv[G + 1];
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-        const int64_t m = wlive ? wave_max_s48(s[h]) : SCORE_LO;
-        if (lane == 0) S.wmax[wv][h] = m;
+        wm[h] = SCORE_LO;
+        mv[h] = s[h];
+    }
+    wm[G] = 0;
+    mv[G] = mabs - (int64_t(1) << 47);
+    if (wlive) wave_max_s48_n<G + 1>(mv, wm);
+    if (lane == 0) {
+#pragma unroll
+        for (int h = 0; h < G; ++h) S.wmax[wv][h] = wm[h];
     }
     if (ok && wlive) {
         ovf = (unsigned long long)(__popcll(__ballot(ovf & 1)) + 2 * __popcll(__ballot(ovf & 2)) +
                                    4 * __popcll(__ballot(ovf & 4)));
-        mabs = wave_max_s48(mabs - (int64_t(1) << 47)) + (int64_t(1) << 47);    // |score| <= 2^47
+        mabs = wm[G] + (int64_t(1) << 47);                      // |score| <= 2^47
         if (lane == 0) {
             if (ovf) atomicAdd(&S.ovf, ovf);
             if (mabs) atomicMax(&S.mabs, (unsigned long long)mabs);
         }
     }
+    if (tid >= 320 && tid < 320 + NV) S.vc9[tid - 320] = (int32_t)tab * 512;   // |centroid| < 2^18
+    if (tid >= 384 && tid < 384 + 256) S.expt[tid - 384] = ex;
     STAMP(3);
     __syncthreads();                                               // B2
     STAMP(4);
@@ -1542,7 +1552,6 @@ static void carve(const Geom &g, int64_t mc, int64_t pool, uint8_t *p, Sck *ck, 
     if (front) *front = o;
     c.meta = (uint64_t *)take(chains * G * pool * 2 * sizeof(uint64_t));
     c.segS = (int32_t *)take(chains * G * pool * D * sizeof(int32_t));
-    c.qst = (double *)take(chains * mc * D * G * sizeof(double));
     c.mc = (int32_t)mc;
     c.pool = (int32_t)pool;
     if (ck) *ck = c;
@@ -1573,12 +1582,11 @@ void step_layout_facts(const Geom &g, int64_t mc, int64_t *f) {
     size_t total = 0, front = 0;
     carve(g, mc, pool, base, &c, &total, &front);
     auto off = [&](const void *q) { return (int64_t)((const uint8_t *)q - base); };
-    const int64_t at[] = {off(c.status), off(c.hdr), off(c.done), off(c.meta), off(c.segS), off(c.qst),
-                          (int64_t)total};
+    const int64_t at[] = {off(c.status), off(c.hdr), off(c.done), off(c.meta), off(c.segS), (int64_t)total};
     const int64_t sz[] = {chains * G * 2 * mc * 8, chains * mc * G * 2 * 8, chains * 4, chains * G * pool * 2 * 8,
-                          chains * G * pool * D * 4, chains * mc * D * G * 8};
+                          chains * G * pool * D * 4};
     bool ok = true;
-    for (int i = 0; i < 6; ++i) ok = ok && at[i] % 256 == 0 && at[i] + sz[i] <= at[i + 1];
+    for (int i = 0; i < 5; ++i) ok = ok && at[i] % 256 == 0 && at[i] + sz[i] <= at[i + 1];
     ok = ok && (int64_t)front == off(c.meta);
     f[0] = mc;
     f[1] = pool;

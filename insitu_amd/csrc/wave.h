@@ -116,6 +116,63 @@ __device__ __forceinline__ int64_t wave_max_s48(int64_t v) {
     return (int64_t)mhi * 65536 + wave_max_i32(lo);
 }
 
+// wave_max_s48 of N values at once, step by step: each DPP step and each readlane round issues
+// N independent operations, so that one value's dependent chain does not stall the wave (a DPP
+// read of a VGPR written by the previous VALU op needs wait states).
+template <int N>
+__device__ __forceinline__ void wave_max_s48_n(const int64_t (&v)[N], int64_t (&out)[N]) {
+    auto mx = [](int32_t a, int32_t b) { return a > b ? a : b; };
+    int32_t hi[N], m[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) m[i] = hi[i] = (int32_t)(v[i] >> 16);
+    auto rowmax = [&](int32_t (&x)[N]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) x[i] = mx(x[i], (int32_t)dpp32<DPP_QUAD_1032>((uint32_t)x[i], (uint32_t)x[i]));
+#pragma unroll
+        for (int i = 0; i < N; ++i) x[i] = mx(x[i], (int32_t)dpp32<DPP_QUAD_2301>((uint32_t)x[i], (uint32_t)x[i]));
+#pragma unroll
+        for (int i = 0; i < N; ++i) x[i] = mx(x[i], (int32_t)dpp32<DPP_ROW_HALF_MIRROR>((uint32_t)x[i], (uint32_t)x[i]));
+#pragma unroll
+        for (int i = 0; i < N; ++i) x[i] = mx(x[i], (int32_t)dpp32<DPP_ROW_MIRROR>((uint32_t)x[i], (uint32_t)x[i]));
+    };
+    rowmax(m);
+    int32_t mhi[N], lo[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        mhi[i] = mx(mx(__builtin_amdgcn_readlane(m[i], 0), __builtin_amdgcn_readlane(m[i], 16)),
+                    mx(__builtin_amdgcn_readlane(m[i], 32), __builtin_amdgcn_readlane(m[i], 48)));
+        lo[i] = hi[i] == mhi[i] ? (int32_t)(v[i] & 0xFFFF) : 0;
+    }
+    rowmax(lo);
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+        const int32_t mlo = mx(mx(__builtin_amdgcn_readlane(lo[i], 0), __builtin_amdgcn_readlane(lo[i], 16)),
+                               mx(__builtin_amdgcn_readlane(lo[i], 32), __builtin_amdgcn_readlane(lo[i], 48)));
+        out[i] = (int64_t)mhi[i] * 65536 + mlo;
+    }
+}
+
+// Sums over the wave of N unsigned 32-bit values at once (each below 2^26 / 64 lanes' worth,
+// so that no sum wraps), wave-uniform, step by step like wave_max_s48_n.
+template <int N>
+__device__ __forceinline__ void wave_sum_u32_n(const uint32_t (&v)[N], uint32_t (&out)[N]) {
+    uint32_t x[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) x[i] = v[i];
+#pragma unroll
+    for (int i = 0; i < N; ++i) x[i] += dpp32<DPP_QUAD_1032>(x[i], x[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) x[i] += dpp32<DPP_QUAD_2301>(x[i], x[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) x[i] += dpp32<DPP_ROW_HALF_MIRROR>(x[i], x[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i) x[i] += dpp32<DPP_ROW_MIRROR>(x[i], x[i]);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+        out[i] = ((uint32_t)__builtin_amdgcn_readlane((int)x[i], 0) + (uint32_t)__builtin_amdgcn_readlane((int)x[i], 16)) +
+                 ((uint32_t)__builtin_amdgcn_readlane((int)x[i], 32) + (uint32_t)__builtin_amdgcn_readlane((int)x[i], 48));
+}
+
 // 32-bit inclusive running maximum (signed) in lane order.
 __device__ __forceinline__ int32_t wave_scan_max32(int32_t v) {
     auto mx = [](int32_t a, int32_t b) { return a > b ? a : b; };
