@@ -49,22 +49,37 @@ extern "C" int insitu_step_stamps_clear() {
     if (hipGetSymbolAddress(&p, HIP_SYMBOL(insitu_step_stamps)) != hipSuccess) return 1;
     return (int)hipMemset(p, 0, sizeof(unsigned long long) * 8192 * 16 * 32);
 }
+// Each wave keeps its stamps in LDS (so that no global store enters the memory counters the
+// kernel waits on) and writes them out once, where it ends (STAMP_FLUSH).
 #define STAMP(k)                                                                                \
     do {                                                                                        \
         const unsigned long long _t = __builtin_amdgcn_s_memrealtime();                         \
-        if ((threadIdx.x & 63) == 0 && blockIdx.x < 8192)                                       \
-            insitu_step_stamps[((size_t)blockIdx.x * 16 + (threadIdx.x >> 6)) * 32 + (k)] = _t; \
+        if ((threadIdx.x & 63) == 0) S.stamps[threadIdx.x >> 6][(k)] = _t;                      \
     } while (0)
 // a count instead of a time, in slots 24 and up
 #define STAMPV(k, v)                                                                            \
     do {                                                                                        \
-        if ((threadIdx.x & 63) == 0 && blockIdx.x < 8192)                                       \
-            insitu_step_stamps[((size_t)blockIdx.x * 16 + (threadIdx.x >> 6)) * 32 + (k)] =      \
-                (unsigned long long)(v);                                                        \
+        if ((threadIdx.x & 63) == 0) S.stamps[threadIdx.x >> 6][(k)] = (unsigned long long)(v); \
+    } while (0)
+#define STAMP_INIT()                                                                            \
+    do {                                                                                        \
+        if ((threadIdx.x & 63) < 32) S.stamps[threadIdx.x >> 6][threadIdx.x & 31] = 0;          \
+    } while (0)
+#define STAMP_FLUSH()                                                                           \
+    do {                                                                                        \
+        if ((threadIdx.x & 63) < 32 && blockIdx.x < 8192)                                       \
+            insitu_step_stamps[((size_t)blockIdx.x * 16 + (threadIdx.x >> 6)) * 32 + (threadIdx.x & 31)] = \
+                S.stamps[threadIdx.x >> 6][threadIdx.x & 31];                                   \
     } while (0)
 #else
 #define STAMPV(k, v) \
     do {             \
+    } while (0)
+#define STAMP_INIT() \
+    do {             \
+    } while (0)
+#define STAMP_FLUSH() \
+    do {              \
     } while (0)
 #define STAMP(k) \
     do {         \
@@ -139,12 +154,14 @@ struct OpOr64 {
 };
 __host__ __device__ __forceinline__ int slot_base(int chunk) { return chunk == 0 ? 0 : 1 + (chunk - 1) * SLOTS; }
 
-// Chunk scratch: look-back words, headers and counters first (the epoch-checked front,
-// zeroed when a launch lays the buffer out differently), then the runs and the query staging.
+// Chunk scratch: look-back words, headers, counters and chunk 0's tagged state first (the
+// epoch-checked front, zeroed when a launch lays the buffer out differently), then the runs.
 struct Sck {
     unsigned long long *status;   // [chain][G][2][mc]: inclusive, aggregate
     uint64_t *hdr;                // [chain][mc][G][2]: w0, w1
     unsigned int *done;           // [chain]: chunks done with their runs
+    uint64_t *st0;                // [chain][G][D + 1]: chunk 0's state, each word tagged with the
+                                  // epoch (<< 48): acc (lane = channel), then l | events << 26
     uint64_t *meta;               // [chain][G][pool][2]: L | f << 32, B
     int32_t *segS;                // [chain][G][pool][D]
     int32_t mc, pool;
@@ -216,6 +233,9 @@ struct StepLds {
     unsigned long long sev, samax;          // the chain's merged statistics (replay)
     int32_t sdone;
     int32_t hfin;                           // head waves done with the finalize
+#ifdef INSITU_STEP_STAMPS
+    unsigned long long stamps[NW][32];      // each wave's phase stamps (timing studies only)
+#endif
 };
 
 // Applies a chunk's runs 0 .. nr - 1 of head h (its LDS run accumulators; run r > 0 opens
@@ -278,6 +298,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     const int64_t T = len[b] + 1;
     const int nch = (int)((T + CHUNK - 1) / CHUNK);
     if (chunk >= nch) return;
+    STAMP_INIT();
     STAMP(0);
     const bool newrow = chunk == nch - 1;     // this chunk holds the step's new token
     const int64_t t0 = (int64_t)chunk * CHUNK;
@@ -423,13 +444,8 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         // Chunk 0 counts the queries' range errors, once per call: values beyond int32
         // after the rotation, and rotated values beyond the 24-bit seam's +-2^27.
         int32_t r[1];
-#ifdef INSITU_STEP_STAMPS
-        asm volatile("" ::"v"(xv));
-        STAMP(29);
-#endif
         const int32_t in[1] = {xv};
         rotate_loaded<1>(in, D, si.rounds, si.sg, r, own ? &st->range_errors : nullptr);
-        STAMP(27);
         // The rotated row, for every wave's score (which reads it from LDS after the barrier)
         // and the serial path. Scores stay exact fp64 integers when ||q||_1 * max|c| < 2^51
         // (attention.py:333-359 computes them in int64); rotated values beyond the 24-bit
@@ -446,7 +462,6 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         if (own && lane == 0 && bad) atomicAdd(&st->range_errors, (unsigned long long)bad);
         const bool okh = (double)l1 * kc_absmax < DOT_LIMIT;
         if (lane == 0) S.qbad[wv] = okh ? 0 : 1;
-        STAMP(28);
     } else if (newrow && wv < G + 2) {
         // the new token: rotate, norm, codes (quantize.py:164-212), pack (:237-252), store
         const int f = wv - G;      // 0: key, 1: value
@@ -1268,9 +1283,13 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             const int64_t hbase = ((int64_t)chain * G + h) * ck.pool;
             int npub = 0;
             if (own) {
-                pub32(&ck.segS[hbase * D + lane], (uint32_t)acc0);
-                if (lane == 0) pub64(&ck.meta[hbase * 2], (uint64_t)(uint32_t)l0 | ((uint64_t)(uint32_t)nev0 << 32));
-                npub = 1;
+                // the state, each word tagged with the epoch: the replayer polls the words
+                // themselves, so they need no wait before the header (l < 2^26: at most 1,024
+                // values of p <= 2^15; events <= 1,024)
+                uint64_t *s0 = ck.st0 + ((int64_t)chain * G + h) * (D + 1);
+                const uint64_t tag = (uint64_t)ck.ep << 48;
+                pub64(&s0[lane], (uint64_t)(uint32_t)acc0 | tag);
+                if (lane == 0) pub64(&s0[D], ((uint64_t)l0 & ((1ull << 26) - 1)) | ((uint64_t)nev0 << 26) | tag);
             } else if ((work || olist) && !(flags & FL_POOL)) {
                 const int nr = nruns[h];
                 const bool empty = nr == 1 && S.runL[h][0] == 0 && S.runB[h][0] == 0;
@@ -1284,7 +1303,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
                     }
                 }
             }
-            stores_done();
+            if (!own) stores_done();
             if (lane == 0) {
                 pub64(hp + 1, ok ? S.mabs : 0ull);
                 pub64(hp, (uint64_t)(uint32_t)npub | ((uint64_t)(uint32_t)flags << 16) |
@@ -1292,6 +1311,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             }
         }
         STAMP(12);
+        STAMP_FLUSH();
         return;
     }
     if (newrow && (wv == G || wv == G + 1)) stores_done();         // the new row, for the serial path
@@ -1300,24 +1320,40 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     STAMP(8);
 
     // -- P6: the replay --------------------------------------------------------------
-    // Wave h < G polls the headers of chunks 0 .. nch - 2 (one per lane and 64 at a time;
-    // the wait is bounded, and a head whose wait gives up goes to the serial path), takes
-    // their statistics and flags, and lists the runs of chunks 1 .. nch - 2 in order. Then
-    // every wave stages runs (lane = channel) in LDS, and wave h walks chunk 0's state
-    // through them and through this chunk's own runs.
+    // Wave h < G polls the headers of chunks 1 .. nch - 2 (one per lane and 64 at a time; the
+    // wait is bounded, and a head whose wait gives up goes to the serial path), takes their
+    // statistics and flags, lists their runs in order and requests them (sums lane = channel,
+    // L, f and bounds lane = run); then it polls chunk 0's header and tagged state, which the
+    // poll itself delivers, while those loads are in flight, and walks chunk 0's state through
+    // the runs and through this chunk's own.
     int32_t aw = acc0;
     int64_t l = l0;
     unsigned long long events = (unsigned long long)nev0;
     int hflags = flags;            // this head's flags over every chunk
     unsigned long long tovf = ok ? S.ovf : 0, tmabs = ok ? S.mabs : 0;
     int total = 0;
+    int spins = 0;
+    bool gaveup = ck.spin_limit == 0;
+    // This chunk's own runs (up to 8), applied last: their sums (lane = channel), factors and L
+    // (lane = run) and the sum of their bounds, read now, while the headers are awaited.
+    const bool own8 = nch > 1 && hw && (work || olist) && nruns[h] <= 8;
+    int32_t vo[8];
+    int32_t fko = 1 << PROB_FRAC;
+    uint32_t lko = 0;
+    int64_t bso = 0;
+    if (own8) {
+        const int nr = nruns[h];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) vo[k] = k < nr ? S.runS[h][k][lane] : 0;
+        if (lane > 0 && lane < nr) fko = S.runf[h][lane];       // run 0 continues the open run
+        if (lane < nr) lko = S.runL[h][lane];
+        bso = wave_sum_i64(lane < nr ? (int64_t)S.runB[h][lane] : 0);
+    }
+    const uint32_t ep = ck.ep;
+    const uint64_t *hdr = ck.hdr + ((int64_t)chain * ck.mc * G + h) * 2;    // chunk c: hdr[c * G * 2]
     if (nch > 1 && hw) {
-        const uint64_t *hdr = ck.hdr + ((int64_t)chain * ck.mc * G + h) * 2;    // chunk c: hdr[c * G * 2]
-        const uint32_t ep = ck.ep;
         uint16_t *rl = S.u.rp.rl[h];
-        int spins = 0;
-        bool gaveup = ck.spin_limit == 0;
-        for (int c0 = 0; c0 < nch - 1; c0 += 64) {
+        for (int c0 = 1; c0 < nch - 1; c0 += 64) {
             const int c = c0 + lane;
             const bool in = c < nch - 1;
             uint64_t w0 = 0, w1 = 0;
@@ -1333,14 +1369,14 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
                 }
                 __builtin_amdgcn_s_sleep(2);
             }
-            // A current header lists at most SLOTS runs (chunk 0: its state, one; a chunk whose
-            // runs did not fit publishes none, with FL_POOL); one that lists more would send the
-            // staging past the chunk's slots: a fault, and the head takes the serial path.
+            // A current header lists at most SLOTS runs (a chunk whose runs did not fit
+            // publishes none, with FL_POOL); one that lists more would send the loads past the
+            // chunk's slots: a fault, and the head takes the serial path.
             const bool cep = in && (uint32_t)(w0 >> 40) == ep;
             const bool over = cep && (int)(w0 & 0xFFFF) > SLOTS;
             if (over && !((w0 >> 16) & FL_POOL)) st->fault = 1;
             const bool cur = cep && !over;
-            const int n = cur && c > 0 ? (int)(w0 & 0xFFFF) : 0;
+            const int n = cur ? (int)(w0 & 0xFFFF) : 0;
             int fl = cur ? (int)((w0 >> 16) & 0xFF) : 0;
             if (over) fl |= FL_POOL;
             if (in && !cep) fl |= FL_LB;
@@ -1365,12 +1401,41 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     } else if (hw && lane == 0) {
         S.total[h] = 0;
     }
+    // Chunk 0's header and state: one poll reads the header (flags, statistics) and the state's
+    // tagged words, until every one carries this call's epoch (bounded like the other waits).
+    auto take_chunk0 = [&]() __attribute__((always_inline)) {
+        const uint64_t *s0 = ck.st0 + ((int64_t)chain * G + h) * (D + 1);
+        uint64_t sa = 0, sm = 0, w0 = 0, w1 = 0;
+        while (true) {
+            sa = get64(&s0[lane]);
+            sm = get64(&s0[D]);
+            w0 = get64(&hdr[0]);
+            w1 = get64(&hdr[1]);
+            const bool cur = (uint32_t)(sa >> 48) == ep && (uint32_t)(sm >> 48) == ep && (uint32_t)(w0 >> 40) == ep;
+            if (!__ballot(!cur)) break;
+            if (gaveup || ++spins > ck.spin_limit) {
+                gaveup = true;
+                hflags |= FL_LB;
+                return;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        hflags |= (int)((w0 >> 16) & 0xF);
+        if (h == 0) {
+            tovf += (uint32_t)((w0 >> 24) & 0xFFFF);
+            tmabs = w1 > tmabs ? w1 : tmabs;
+        }
+        aw = (int32_t)(uint32_t)sa;
+        l = (int64_t)(sm & ((1ull << 26) - 1));
+        events = (sm >> 26) & 0xFFF;
+    };
     // Each head's wave walks its own runs, RMAX at a time: their sums (lane = channel), L, f
     // and bounds (lane = run) loaded into registers together, one round trip, then the walk.
     bool unsafe = false;
     if (hw) {
         const int64_t hbase = ((int64_t)chain * G + h) * ck.pool;
-        // this head's slot 0 (chunk 0's state), lane = channel, and its meta words
+        // this head's slot 0 (unused by the chunks' runs, so that a clamped index reads it),
+        // lane = channel, and its meta words
         const int32_t *segh = ck.segS + hbase * D + lane;
         const uint64_t *metah = ck.meta + hbase * 2;
         bool take_c0 = nch > 1;
@@ -1385,14 +1450,12 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             const int slot = (int)(ent & (RUN_EVENT - 1));
             const bool bad = mine && slot >= ck.pool;
             const bool ld = mine && !bad;
-            // Every load first, none of them conditional, so that all are in flight together
-            // and the first use waits once: chunk 0's state (its header is current: acc, and
-            // l | events << 32 in lane 63's meta word), each run's L | f << 32 and bound (lane
-            // = run) and its sums (lane = channel). A lane past nb, or one whose slot failed
-            // the check, reads slot 0, which lies in the pool, and its values count 0.
+            // Every load first, none of them conditional, so that all are in flight together:
+            // each run's L | f << 32 and bound (lane = run) and its sums (lane = channel). A
+            // lane past nb, or one whose slot failed the check, reads slot 0, which lies in the
+            // pool, and its values count 0.
             const int sl = ld ? slot : 0;
-            const uint32_t acc_c0 = get32(segh);
-            const uint64_t lfr = get64(metah + (lane == 63 ? 0 : 2 * sl));
+            const uint64_t lfr = get64(metah + 2 * sl);
             const uint64_t bbr = get64(metah + 2 * sl + 1);
             int32_t v[RMAX];
 #pragma unroll
@@ -1400,11 +1463,10 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             const uint64_t lf = ld ? lfr : 0ull;
             const int64_t bb = ld ? (int64_t)bbr : 0;
             if (take_c0) {
-                const uint64_t lf0 = readlane64((int64_t)lfr, 63);
-                aw = (int32_t)acc_c0;
-                l = (int64_t)(uint32_t)lf0;
-                events = lf0 >> 32;
+                // chunk 0, polled while these loads are in flight
+                take_chunk0();
                 take_c0 = false;
+                if (hflags) break;
             }
             if (__ballot(bad)) {
                 st->fault = 1;
@@ -1412,16 +1474,58 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
                 break;
             }
             STAMP(15);
-            // The walk. Lane k < nb holds run k's list entry, L, f and bound B; prefix sums over
-            // the lanes give each block's sums. |acc| only shrinks at a rescale and grows by at
-            // most a run's B per run, so |acc at a block's start| + the block's B certifies 8
-            // runs at once; elsewhere the walk goes run by run.
             const uint64_t evm = __ballot(mine && (ent & RUN_EVENT));
+            // The walk. |acc| only shrinks at a rescale and grows by at most a run's bound B per
+            // run, so |acc| + the sum of the nb runs' B certifies them all at once: then a block
+            // of 8 runs with no event adds as one tree, and elsewhere only a run that opens with
+            // an event rescales first; L comes from a prefix sum over the runs.
+            {
+                const int64_t bsum_all = wave_sum_i64(mine ? bb : 0);
+                const int64_t a0 = aw < 0 ? -(int64_t)aw : (int64_t)aw;
+                STAMPV(27, nb);
+                STAMPV(28, __ballot(a0 + bsum_all > ACC_HI) ? 2 : 1);
+                if (!__ballot(a0 + bsum_all > ACC_HI)) {
+                    const uint32_t PLa = wave_scan_add32((uint32_t)lf);   // L < 2^26 a run, 0 past nb
+#pragma unroll
+                    for (int k0 = 0; k0 < RMAX; k0 += 8) {
+                        if (k0 >= nb) break;
+                        const int kn = nb - k0 < 8 ? nb - k0 : 8;
+                        const uint32_t bev = (uint32_t)(evm >> k0) & ((1u << kn) - 1u);
+                        const uint32_t lb = k0 ? (uint32_t)__builtin_amdgcn_readlane((int)PLa, k0 - 1) : 0u;
+                        if (!bev) {
+                            int32_t t[8];
+#pragma unroll
+                            for (int k = 0; k < 8; ++k) t[k] = k < kn ? v[k0 + k] : 0;
+                            aw += ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+                            l += (uint32_t)__builtin_amdgcn_readlane((int)PLa, k0 + kn - 1) - lb;
+                            continue;
+                        }
+#pragma unroll
+                        for (int k = 0; k < 8; ++k) {
+                            if (k < kn) {
+                                if ((bev >> k) & 1u) {
+                                    const int64_t f = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(lf >> 32), k0 + k);
+                                    aw = (int32_t)(((int64_t)aw * f) >> PROB_FRAC);
+                                    l = (l * f) >> PROB_FRAC;
+                                }
+                                aw += v[k0 + k];
+                                l += (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)lf, k0 + k);
+                            }
+                        }
+                    }
+                    events += (unsigned long long)__popcll(evm);
+                    continue;
+                }
+            }
+            // Otherwise block by block: lane k < nb holds run k's list entry, L, f and bound B;
+            // prefix sums over the lanes give each block's sums, |acc at a block's start| + the
+            // block's B certifies 8 runs at once, and elsewhere the walk goes run by run.
             // 32-bit prefix sums: L < 2^26 per run, and bounds below 2^27 (a run with a larger
             // one is checked on its own, by the walk run by run)
             const uint64_t bigm = __ballot(mine && bb >= (1ll << 27));
             const uint32_t PB = wave_scan_add32(bb < (1ll << 27) ? (uint32_t)bb : 0u);
             const uint32_t PL = wave_scan_add32((uint32_t)lf);
+            STAMP(23);
 #pragma unroll
             for (int k0 = 0; k0 < RMAX; k0 += 8) {
                 if (k0 >= nb) break;
@@ -1460,18 +1564,26 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
                 }
             }
         }
-        if (take_c0) {
-            // no runs to walk (or the flags sent the head to the serial path)
-            const uint64_t lf0 = get64(metah);
-            aw = (int32_t)get32(segh);
-            l = (int64_t)(uint32_t)lf0;
-            events = lf0 >> 32;
-        }
+        if (take_c0) take_chunk0();        // no runs, or the flags sent the head to the serial path
     }
+    STAMP(30);
     if (nch > 1 && hw && (work || olist) && !hflags) {
         // this chunk's own runs, last (run 0 continues the run open before it)
         const int nr = nruns[h];
-        const bool cert = fold_runs_certified(S, h, nr, lane, aw, l);
+        const int64_t ao = aw < 0 ? -(int64_t)aw : (int64_t)aw;
+        bool cert = false;
+        if (own8 && !__ballot(ao + bso > ACC_HI)) {
+            // certified by |acc| + their bounds: one chain, no branch (factor 2^15 past nr)
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const int64_t f = __builtin_amdgcn_readlane(fko, k);
+                aw = (int32_t)(((int64_t)aw * f) >> PROB_FRAC) + vo[k];
+                l = ((l * f) >> PROB_FRAC) + (uint32_t)__builtin_amdgcn_readlane((int)lko, k);
+            }
+            cert = true;
+        } else {
+            cert = fold_runs_certified(S, h, nr, lane, aw, l);
+        }
         if (cert) events += (unsigned long long)(nr - 1);
         for (int r = 0; r < nr && !cert; ++r) {
             if (r > 0) {
@@ -1503,6 +1615,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             const Recip rc = reciprocal(l);
             const int64_t acc = aw;
             orow[lane] = (int32_t)(wmul(acc, rc.r) >> rc.shift);
+            STAMP(31);
             const int64_t amax = wave_max_i64(acc < 0 ? -acc : acc);
             if (lane == 0) {
                 if (events) atomicAdd(&S.sev, events);
@@ -1535,6 +1648,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         }
     }
     STAMP(10);
+    STAMP_FLUSH();
 }
 
 static void carve(const Geom &g, int64_t mc, int64_t pool, uint8_t *p, Sck *ck, size_t *total, size_t *front) {
@@ -1549,6 +1663,7 @@ static void carve(const Geom &g, int64_t mc, int64_t pool, uint8_t *p, Sck *ck, 
     c.status = (unsigned long long *)take(chains * G * 2 * mc * sizeof(unsigned long long));
     c.hdr = (uint64_t *)take(chains * mc * G * 2 * sizeof(uint64_t));
     c.done = (unsigned int *)take(chains * sizeof(unsigned int));
+    c.st0 = (uint64_t *)take(chains * G * (D + 1) * sizeof(uint64_t));
     if (front) *front = o;
     c.meta = (uint64_t *)take(chains * G * pool * 2 * sizeof(uint64_t));
     c.segS = (int32_t *)take(chains * G * pool * D * sizeof(int32_t));
@@ -1582,11 +1697,12 @@ void step_layout_facts(const Geom &g, int64_t mc, int64_t *f) {
     size_t total = 0, front = 0;
     carve(g, mc, pool, base, &c, &total, &front);
     auto off = [&](const void *q) { return (int64_t)((const uint8_t *)q - base); };
-    const int64_t at[] = {off(c.status), off(c.hdr), off(c.done), off(c.meta), off(c.segS), (int64_t)total};
-    const int64_t sz[] = {chains * G * 2 * mc * 8, chains * mc * G * 2 * 8, chains * 4, chains * G * pool * 2 * 8,
-                          chains * G * pool * D * 4};
+    const int64_t at[] = {off(c.status), off(c.hdr), off(c.done), off(c.st0), off(c.meta), off(c.segS),
+                          (int64_t)total};
+    const int64_t sz[] = {chains * G * 2 * mc * 8, chains * mc * G * 2 * 8, chains * 4, chains * G * (D + 1) * 8,
+                          chains * G * pool * 2 * 8, chains * G * pool * D * 4};
     bool ok = true;
-    for (int i = 0; i < 5; ++i) ok = ok && at[i] % 256 == 0 && at[i] + sz[i] <= at[i + 1];
+    for (int i = 0; i < 6; ++i) ok = ok && at[i] % 256 == 0 && at[i] + sz[i] <= at[i + 1];
     ok = ok && (int64_t)front == off(c.meta);
     f[0] = mc;
     f[1] = pool;

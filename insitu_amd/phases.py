@@ -50,7 +50,10 @@ PHASES = [
     (8, "P5 own fold or publish"),
     (14, "P6 headers read"),
     (15, "P6 runs staged"),
+    (23, "P6 block sums scanned"),
+    (30, "P6 runs walked (before own runs)"),
     (9, "P6 replay walked"),
+    (31, "P6 output row stored"),
     (10, "end (finalize)"),
 ]
 
@@ -97,7 +100,7 @@ def run(ctx_len: int, n_caches: int, reps: int, flat: bool = False) -> dict:
     nch = (ctx_len + 1023) // 1024
     nblk = nch * 8
     buf = np.zeros(MAXBLK * NWAVES * NSTAMPS, dtype=np.uint64)
-    runs, counts = [], []
+    runs, counts, rcounts = [], [], []
     for i in range(reps + 4):
         c = caches[i % n_caches]
         c.set_length(ctx_len - 1)
@@ -111,7 +114,8 @@ def run(ctx_len: int, n_caches: int, reps: int, flat: bool = False) -> dict:
             continue                                   # warmup
         st = buf[:nblk * NWAVES * NSTAMPS].reshape(nblk, NWAVES, NSTAMPS).astype(np.int64)
         counts.append(st[:, :4, 24:27].copy())          # head waves: list entries, tokens of weight, events
-        st[:, :, 24:] = 0
+        rcounts.append(st[:, :4, 27:29].copy())         # replay: runs walked, certified (1) or not (2)
+        st[:, :, 24:29] = 0
         t0 = st[:, :, 0][st[:, :, 0] > 0].min()
         runs.append(np.where(st > 0, (st - t0) * 0.01, np.nan))
     R = np.stack(runs)                                  # (reps, block, wave, stamp), us
@@ -121,8 +125,9 @@ def run(ctx_len: int, n_caches: int, reps: int, flat: bool = False) -> dict:
         rep_blk = (nch - 1) * 8                                  # chain 0's last chunk
         w0 = np.nanmedian(R[:, rep_blk, 0], axis=0)               # (stamp,)
     C = np.stack(counts[4:]) if len(counts) > 4 else None          # (reps, block, head, 3)
+    RC = np.stack(rcounts[4:])[:, (nch - 1) * 8:] if len(rcounts) > 4 else None    # the replaying workgroups
     return {"ctx": ctx_len, "flat": flat, "reps": reps, "blocks": nblk, "per_blk": per_blk, "replayer_w0": w0,
-            "counts": C}
+            "counts": C, "rcounts": RC}
 
 
 def table(res: dict) -> str:
@@ -150,6 +155,11 @@ def table(res: dict) -> str:
                   f"(max {rest[..., 0].max() if rest.size else 0}), tokens of weight {np.median(c0[..., 1]):.0f} "
                   f"(max {c0[..., 1].max()}) / {np.median(rest[..., 1]) if rest.size else 0:.1f}, "
                   f"events {np.median(c0[..., 2]):.0f} (max {c0[..., 2].max()})"]
+    RC = res.get("rcounts")
+    if RC is not None and (RC[..., 0] > 0).any():
+        walked = RC[..., 0][RC[..., 0] > 0]
+        lines += ["", f"replay per head: runs of the other chunks walked, median {np.median(walked):.0f} "
+                  f"(max {walked.max()}); certified at once in {(RC[..., 1] == 1).sum()} of {(RC[..., 1] > 0).sum()}"]
     pub = res["per_blk"][:, 12]
     if res["blocks"] > 8 and not np.all(np.isnan(pub)):
         order = np.argsort(np.nan_to_num(pub, nan=-1.0))[::-1][:6]
