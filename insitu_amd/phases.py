@@ -31,7 +31,7 @@ NWAVES, NSTAMPS, MAXBLK = 16, 32, 8192
 # stamp index -> the point of the kernel it marks
 PHASES = [
     (0, "start"),
-    (1, "P0 loads, query staging, new row"),
+    (1, "P0 loads, query rotation, new row"),
     (2, "barrier B1"),
     (3, "P1 scores and wave maxima"),
     (4, "barrier B2"),
