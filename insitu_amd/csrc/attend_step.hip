@@ -653,7 +653,8 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     }
     wm[G] = 0;
     mv[G] = mabs - (int64_t(1) << 47);
-    if (wlive) wave_max_s48_n<G + 1>(mv, wm);
+    static_assert(G + 1 == 5, "the 4 heads' maxima and max |score| reduce as 5 values");
+    if (wlive) wave_max_s48_x5(mv, wm);
     if (lane == 0) {
 #pragma unroll
         for (int h = 0; h < G; ++h) S.wmax[wv][h] = wm[h];

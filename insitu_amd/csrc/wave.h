@@ -152,6 +152,47 @@ __device__ __forceinline__ void wave_max_s48_n(const int64_t (&v)[N], int64_t (&
     }
 }
 
+// The signed 32-bit maximum over the wave of 5 values at once, wave-uniform: fused v_max_i32_dpp
+// steps, 4 within each row of 16 lanes and 2 that carry rows 0-1 into 1 and 3, then rows 0-2
+// into 3 (row_bcast), so that lane 63 holds the maximum. One asm block, the 5 values' steps
+// interleaved: a value's next DPP read comes 4 instructions after its write (2 wait states are
+// needed), and s_nop 1 covers the writes before the block.
+__device__ __forceinline__ void wave_max_i32_x5(int32_t (&x)[5]) {
+#define INSITU_MAX5(CTRL)                                                              \
+    "v_max_i32_dpp %0, %0, %0 " CTRL "\n\t"                                             \
+    "v_max_i32_dpp %1, %1, %1 " CTRL "\n\t"                                             \
+    "v_max_i32_dpp %2, %2, %2 " CTRL "\n\t"                                             \
+    "v_max_i32_dpp %3, %3, %3 " CTRL "\n\t"                                             \
+    "v_max_i32_dpp %4, %4, %4 " CTRL "\n\t"
+    asm volatile("s_nop 1\n\t"
+                 INSITU_MAX5("quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf")
+                 INSITU_MAX5("quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf")
+                 INSITU_MAX5("row_half_mirror row_mask:0xf bank_mask:0xf")
+                 INSITU_MAX5("row_mirror row_mask:0xf bank_mask:0xf")
+                 INSITU_MAX5("row_bcast:15 row_mask:0xa bank_mask:0xf")
+                 INSITU_MAX5("row_bcast:31 row_mask:0xc bank_mask:0xf")
+                 "s_nop 1"
+                 : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]));
+#undef INSITU_MAX5
+#pragma unroll
+    for (int i = 0; i < 5; ++i) x[i] = __builtin_amdgcn_readlane(x[i], 63);
+}
+
+// wave_max_s48 of 5 values at once with the fused steps above: the largest v >> 16, then the
+// largest low 16 bits among the lanes that hold it.
+__device__ __forceinline__ void wave_max_s48_x5(const int64_t (&v)[5], int64_t (&out)[5]) {
+    int32_t hi[5], m[5];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) m[i] = hi[i] = (int32_t)(v[i] >> 16);
+    wave_max_i32_x5(m);
+    int32_t lo[5];
+#pragma unroll
+    for (int i = 0; i < 5; ++i) lo[i] = hi[i] == m[i] ? (int32_t)(v[i] & 0xFFFF) : 0;
+    wave_max_i32_x5(lo);
+#pragma unroll
+    for (int i = 0; i < 5; ++i) out[i] = (int64_t)m[i] * 65536 + lo[i];
+}
+
 // Sums over the wave of N unsigned 32-bit values at once (each below 2^26 / 64 lanes' worth,
 // so that no sum wraps), wave-uniform, step by step like wave_max_s48_n.
 template <int N>
