@@ -279,14 +279,21 @@ enum {
     INSITU_DEBUG_SPIN_LIMIT = 3,     /* polls before a wait on another workgroup gives up; 0 gives
                                         up at once, sending every chain with a predecessor to the
                                         exact serial path                                       */
-    INSITU_DEBUG_PATH = 4            /* the kernel of a sequential-mode attend: 0 automatic (the
+    INSITU_DEBUG_PATH = 4,           /* the kernel of a sequential-mode attend: 0 automatic (the
                                         decode step on its own kernel where it handles the cache,
                                         the chunked attend where it handles the cache, the scan
                                         attend elsewhere), 1 the scan attend, 2 the chunked attend
                                         (the decode step too), 3 the decode step's own kernel;
                                         INSITU_EINVAL if the kernel does not handle the cache   */
+    INSITU_DEBUG_APPEND = 5          /* the append's kernel: 0 automatic (lane = row where it
+                                        handles the format: d = 64, 4/2- or 2/2-bit codes), 1 the
+                                        lane-per-channel kernel for every format                */
 };
 int insitu_cache_debug(insitu_cache *cache, int32_t what, int64_t value);
+/* The statistics the cache's kernels have gathered since they were last cleared (an
+ * attend that returns statistics clears them first; an append's range errors are
+ * otherwise seen nowhere), copied into stats_host and then cleared. Synchronises. */
+int insitu_cache_stats(insitu_cache *cache, insitu_stats *stats_host);
 /* The invariants of a scratch layout, computed on the host without a GPU: kernel 0 the
  * chunked attend (1,024-token chunks), 1 the chunked attend (512), 2 the decode step's own
  * kernel (d = 64), for a cache of `capacity` tokens, batch sequences and n_kv KV heads of

@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(HERE, "libinsitu_hip.so")
 
 OK, EBADLEN, ERANGE, EHIP, EINVAL, ECAPACITY, ENOMEM, EFAULT = range(8)
 SEQUENTIAL, TWO_PASS, SPLIT, SERIAL = range(4)
-DEBUG_DECODE_CALLS, DEBUG_PREFILL_CALLS, DEBUG_SPIN_LIMIT, DEBUG_PATH = 1, 2, 3, 4
+DEBUG_DECODE_CALLS, DEBUG_PREFILL_CALLS, DEBUG_SPIN_LIMIT, DEBUG_PATH, DEBUG_APPEND = 1, 2, 3, 4, 5
 PATH_AUTO, PATH_SCAN, PATH_CHUNKED, PATH_STEP = 0, 1, 2, 3
 MODES = {"online": SEQUENTIAL, "sequential": SEQUENTIAL, "two_pass": TWO_PASS,
          "split": SPLIT, "serial": SERIAL}
@@ -31,6 +31,7 @@ EXPORTS = (
     "insitu_append_wire", "insitu_attend", "insitu_attend_causal", "insitu_attend_causal_head", "insitu_attend_causal_static", "insitu_step", "insitu_project", "insitu_seam_wire",
     "insitu_output_projection", "insitu_read_rows", "insitu_load_rows", "insitu_read_image",
     "insitu_load_image", "insitu_probe_read", "insitu_probe_empty", "insitu_cache_debug",
+    "insitu_cache_stats",
     "insitu_debug_scratch_layout", "insitu_last_error",
 )
 
@@ -133,6 +134,7 @@ def load(path: str | None = None):
         "insitu_probe_read": (i32, [vp, vp, i64, i32, i32, vp]),
         "insitu_probe_empty": (i32, [vp, i32, vp]),
         "insitu_cache_debug": (i32, [vp, i32, i64]),
+        "insitu_cache_stats": (i32, [vp, P(Stats)]),
         "insitu_debug_scratch_layout": (i32, [i32, i64, i32, i32, i32, P(i64), i32]),
         "insitu_last_error": (ctypes.c_char_p, []),
     }

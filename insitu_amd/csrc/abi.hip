@@ -191,6 +191,7 @@ struct insitu_cache {
     int64_t *prefill_len = nullptr;
     int32_t spin_limit = 1 << 20;         // insitu_cache_debug
     int32_t path = 0;                     // insitu_cache_debug: 0 auto, 1 scan, 2 chunked, 3 step kernel
+    int32_t append_path = 0;              // insitu_cache_debug: 0 auto, 1 the lane-per-channel kernel
 };
 
 namespace {
@@ -662,7 +663,8 @@ static int append_impl(insitu_cache *k, int seq_lo, int seq_hi, const int32_t *k
     HIP_TRY(hipSetDevice(k->ctx->device), "hipSetDevice");
     HIP_TRY(launch_append(k->ctx->stream, k->g, k->tabs, kr, vr, n_tok, seq_lo, seq_hi,
                           k->len_dev[k->cur], k->len_dev[k->cur ^ 1], k->stats,
-                          wire ? k->desc.fmt.rot_rounds : 0, wire ? k->desc.fmt.rot_signs : nullptr),
+                          wire ? k->desc.fmt.rot_rounds : 0, wire ? k->desc.fmt.rot_signs : nullptr,
+                          k->append_path == 0 ? &k->tabs_host : nullptr),
             "append launch");
     k->cur ^= 1;
     for (int b = seq_lo; b < seq_hi; ++b) k->len_host[b] += n_tok;
@@ -1059,9 +1061,21 @@ int insitu_cache_debug(insitu_cache *k, int32_t what, int64_t value) {
             return fail(INSITU_EINVAL, "path is 0 (auto), 1 (scan), 2 (chunked) or 3 (step kernel)");
         k->path = (int32_t)value;
         return INSITU_OK;
+    case INSITU_DEBUG_APPEND:
+        if (value < 0 || value > 1) return fail(INSITU_EINVAL, "append kernel is 0 (auto) or 1 (lane per channel)");
+        k->append_path = (int32_t)value;
+        return INSITU_OK;
     default:
         return fail(INSITU_EINVAL, "unknown debug setting");
     }
+}
+
+int insitu_cache_stats(insitu_cache *k, insitu_stats *stats) {
+    if (!k || !stats) return fail(INSITU_EINVAL, "null argument");
+    HIP_TRY(hipSetDevice(k->ctx->device), "hipSetDevice");
+    const int rc = copy_stats(k, stats);
+    const int rz = zero_stats(k);
+    return rc != INSITU_OK ? rc : rz;
 }
 
 int insitu_read_rows(insitu_cache *k, int32_t seq, int32_t head, int64_t t0, int64_t n,

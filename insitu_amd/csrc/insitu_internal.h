@@ -203,7 +203,7 @@ hipError_t launch_finalize(hipStream_t s, const int64_t *acc, const int64_t *l, 
 hipError_t launch_append(hipStream_t s, const Geom &g, const Tables *t, const int32_t *k,
                          const int32_t *v, int n_tok, int seq_lo, int seq_hi, const int64_t *len_in,
                          int64_t *len_out, DevStats *st, int rounds = 0,
-                         const uint64_t (*signs)[2] = nullptr);
+                         const uint64_t (*signs)[2] = nullptr, const Tables *host_tabs = nullptr);
 bool chunked_supported(const Geom &g, int64_t capacity);
 int64_t chunked_max_chunks(int64_t capacity);
 int64_t chunked_pool_slots(int64_t max_chunks);

@@ -223,6 +223,283 @@ __global__ void __launch_bounds__(64 * APPEND_WAVES) append_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// append, lane = row (d = 64, code widths 1, 2 or 4 bits)
+// ---------------------------------------------------------------------------
+//
+// A wave takes 64 consecutive rows of the input's (sequence, token, KV head) order, which
+// are 16 KB of contiguous k (and of v): loaded with whole-wave 16-byte loads, turned round
+// through LDS (a row per 66 dwords, so that the row reads spread over the banks) and read
+// back one row per lane. Each lane then rotates, measures and encodes its own row in
+// registers: no cross-lane step at all. The arithmetic is fp64 on integers, exact while
+// every value stays below 2^53:
+//   - the rotation's values stay below 2^31 * 2^6 * 2^6 * 2^3 (two rounds);
+//   - sum(x^2) is exact when the computed sum is below 2^53 (below that every square and
+//     partial sum is an integer that a double holds; at or above it, the computed sum is at
+//     least 2^53, since rounding to nearest never crosses a representable number); rows at
+//     or above take the int64 path, wrapping as the lane-per-channel kernel does;
+//   - isqrt by the correctly rounded fp64 sqrt, then corrected as quantize.py:42-60 does;
+//   - the half-even requantize is rint of the scaled root (quantize.py:164-181);
+//   - a threshold compare (x << e) > n * b_i is x > floor(n * b_i / 2^e) for integer x, in
+//     int32 (|n * b_i / 2^e| < 2^31 when |b_i| < 2^24: the launcher checks).
+// Rotated values outside int32 are counted as range errors and wrap to int32, as the
+// lane-per-channel kernel's rotate_loaded does.
+constexpr int AR_WAVES = 4;
+constexpr int AR_STRIDE = 66;
+
+// x negated where bit c of the signs is set: the sign bit of the high dword flipped by a
+// scalar mask (sw: the 32-bit half of the sign word that holds bit c)
+__device__ __forceinline__ double ar_flip(double x, uint32_t sw, int c) {
+    const uint32_t m = ((sw >> (c & 31)) & 1u) << 31;
+    const uint64_t u = (uint64_t)__double_as_longlong(x) ^ ((uint64_t)m << 32);
+    return __longlong_as_double((long long)u);
+}
+
+// The 64-point FWHT of the row (hadamard butterflies, fixed.py fwht), in place.
+__device__ __forceinline__ void ar_fwht64(double (&x)[64]) {
+#pragma unroll
+    for (int H = 1; H < 64; H <<= 1) {
+#pragma unroll
+        for (int i = 0; i < 64; ++i) {
+            if (i & H) continue;
+            const double a = x[i], b = x[i + H];
+            x[i] = a + b;
+            x[i + H] = a - b;
+        }
+    }
+}
+
+// The int64 sum of squares of the row, wrapping, and the norm from it as norm_wire does.
+__device__ __forceinline__ int32_t ar_norm_int64(const int32_t (&x)[64], int norm_frac) {
+    uint64_t sq = 0;
+#pragma unroll
+    for (int c = 0; c < 64; ++c) {
+        const int64_t xi = x[c];
+        sq += (uint64_t)xi * (uint64_t)xi;
+    }
+    const int64_t mean = (int64_t)sq >> 6;
+    int64_t w = rshift_even(isqrt64(mean), QK_FRAC - norm_frac);
+    if (w > 32767) w = 32767;
+    if (w < -32768) w = -32768;
+    return (int32_t)w;
+}
+
+// The rotated row's values outside int32, recounted by the whole wave (lane = channel, the
+// rotation of rotate_loaded) from the wire row in memory: the rows of the lanes in `need`
+// (live lanes whose largest |value| reached 2^31, which is rare), one after another, so that
+// the lane = row path keeps no unwrapped copy of its row. Returns this lane's count; adds
+// each recounted row's count to range_err.
+__device__ __forceinline__ unsigned long long ar_range_recount(uint64_t need, const int32_t *__restrict__ rows0,
+                                                               int rounds,
+                                                               const RotSigns &sg,
+                                                               unsigned long long *range_err) {
+    const int lane = threadIdx.x & 63;
+    unsigned long long mine = 0;
+    while (need) {
+        const int j = __builtin_ctzll(need);
+        need &= need - 1;
+        int64_t x[1] = {rows0[(int64_t)j * 64 + lane]};
+        for (int r = 0; r < rounds; ++r) {
+            const uint64_t w = r == 0 ? sg.s0a : sg.s1a;
+            if ((w >> lane) & 1) x[0] = -x[0];
+            fwht_wave<1>(x, 64);
+            x[0] = rot_scale(x[0], 64);
+        }
+        const unsigned long long cnt =
+            (unsigned long long)__popcll(__ballot(x[0] < INT32_MIN || x[0] > INT32_MAX));
+        if (lane == j) mine = cnt;
+        if (lane == 0 && cnt) atomicAdd(range_err, cnt);
+    }
+    return mine;
+}
+
+// One field of a lane's row: xi (int32, the row as loaded) rotated when ROT, its norm
+// returned and its codes packed into w (BITS-wide, LSB first, quantize.py:271-289). A lane
+// that is not live (past the tile's rows) counts no range errors; rows0 is the tile's first
+// row in memory (for the recount).
+template <int BITS, bool ROT>
+__device__ __forceinline__ int32_t ar_field(const int32_t (&xi)[64], int rounds, const RotSigns &sg,
+                                            const int64_t *__restrict__ bnd, int norm_frac, bool live,
+                                            const int32_t *rows0, unsigned long long *range_err,
+                                            uint32_t (&w)[2 * BITS]) {
+    // xr: the row as int32 (rotated and wrapped when ROT); S: sum(x^2) in fp64, in four
+    // partial sums (exact below 2^53; +inf sends the row to the int64 path)
+    int32_t xr[64];
+    double S;
+    if constexpr (ROT) {
+        double x[64];
+#pragma unroll
+        for (int c = 0; c < 64; ++c) x[c] = (double)xi[c];
+        // a round: the signs, the FWHT, >> 3 (rotate.py:190-191); rounds is 1 or 2
+        auto round = [&](uint64_t s) {
+            const uint32_t slo = (uint32_t)s, shi = (uint32_t)(s >> 32);
+            // in groups of 8 channels, so that the masks are made where they are used
+#pragma unroll
+            for (int c = 0; c < 64; ++c) {
+                x[c] = ar_flip(x[c], c < 32 ? slo : shi, c);
+                if ((c & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+            }
+            ar_fwht64(x);
+#pragma unroll
+            for (int c = 0; c < 64; ++c) x[c] = floor(x[c] * 0.125);
+        };
+        round(sg.s0a);
+        if (rounds > 1) round(sg.s1a);
+        double amax = 0.0, s4[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+        for (int c = 0; c < 64; ++c) {
+            amax = fmax(amax, fabs(x[c]));
+            s4[c & 3] = fma(x[c], x[c], s4[c & 3]);
+            // |x| < 2^51: the low dword of x + 1.5 * 2^52 is x mod 2^32, the int32 wrap
+            xr[c] = (int32_t)(uint32_t)__double_as_longlong(x[c] + 6755399441055744.0);
+        }
+        S = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+        // rare: values may have wrapped (live lanes only: the others' rows are not stored, and
+        // a recount reads rows0 + 64 j only for j below the tile's row count)
+        const uint64_t need = __ballot(live && amax >= 2147483648.0);
+        if (need) {
+            const unsigned long long cnt = ar_range_recount(need, rows0, rounds, sg, range_err);
+            if (cnt) S = __builtin_inf();           // the squares are of the wrapped values
+        }
+    } else {
+        double s4[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+        for (int c = 0; c < 64; ++c) {
+            xr[c] = xi[c];
+            const double xd = (double)xi[c];
+            s4[c & 3] = fma(xd, xd, s4[c & 3]);
+        }
+        S = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+    }
+    int32_t n;
+    if (S < 9007199254740992.0) {
+        const double m = floor(S * (1.0 / 64.0));
+        double r = floor(sqrt(m));
+        if (r * r > m) r -= 1.0;
+        if ((r + 1.0) * (r + 1.0) <= m) r += 1.0;
+        const double wn = rint(r * __builtin_ldexp(1.0, norm_frac - QK_FRAC));
+        n = (int32_t)(wn < 32767.0 ? wn : 32767.0);
+    } else {
+        n = ar_norm_int64(xr, norm_frac);
+    }
+    constexpr int NB = (1 << BITS) - 1, PER = 32 / BITS;
+    const double sc = __builtin_ldexp(1.0, QK_FRAC - CENT_FRAC - norm_frac);
+    const double nd = (double)n;
+    int32_t th[NB];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) th[i] = (int32_t)floor(nd * ((double)bnd[i] * sc));
+#pragma unroll
+    for (int j = 0; j < 2 * BITS; ++j) w[j] = 0;
+#pragma unroll
+    for (int c = 0; c < 64; ++c) {
+        const int32_t xv = xr[c];
+        uint32_t code = 0;
+#pragma unroll
+        for (int i = 0; i < NB; ++i) code += xv > th[i] ? 1u : 0u;
+        w[c / PER] |= code << (BITS * (c % PER));
+    }
+    return n;
+}
+
+template <int KB, int VB, bool ROT>
+__global__ void __launch_bounds__(64 * AR_WAVES) append_rows_kernel(
+        Geom g, const Tables *__restrict__ tabs, const int32_t *__restrict__ k, const int32_t *__restrict__ v,
+        int n_tok, int seq_lo, const int64_t *__restrict__ len_in, int64_t *len_out, int seq_hi, int rounds,
+        RotSigns sg, DevStats *st, int rows) {
+    static_assert(32 % KB == 0 && 32 % VB == 0 && KB <= 4 && VB <= 4, "code widths of 1, 2 or 4 bits");
+    constexpr int NW = 2 * KB + 2 * VB + 1;            // the row's dwords: key codes, value codes, norms
+    __shared__ int32_t tile[AR_WAVES][64 * AR_STRIDE];
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // the length bookkeeping rides on workgroup 0 (as in append_kernel)
+    if (blockIdx.x == 0) {
+        for (int i = threadIdx.x; i < g.batch; i += blockDim.x)
+            len_out[i] = len_in[i] + ((i >= seq_lo && i < seq_hi) ? n_tok : 0);
+    }
+    const int r0 = (blockIdx.x * AR_WAVES + wv) * 64;
+    if (r0 >= rows) return;
+    const int nr = rows - r0 < 64 ? rows - r0 : 64;    // rows of this tile
+    // load i, lane l: row 4 i + l / 16 of the tile, dwords 4 (l % 16) .. + 3 (rows past the
+    // input's end read its last row, and are not stored)
+    const int sub = lane >> 4, q4 = (lane & 15) * 4;
+    uint4 rk[16], rv[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int r = 4 * i + sub < nr ? 4 * i + sub : nr - 1;
+        rk[i] = *(const uint4 *)(k + ((int64_t)r0 + r) * 64 + q4);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int r = 4 * i + sub < nr ? 4 * i + sub : nr - 1;
+        rv[i] = *(const uint4 *)(v + ((int64_t)r0 + r) * 64 + q4);
+    }
+    // this lane's row: (sequence, token, KV head) and where it goes
+    const int R = r0 + (lane < nr ? lane : nr - 1);
+    const int hh = R % g.n_kv, tt = R / g.n_kv;
+    const int t = tt % n_tok, b = seq_lo + tt / n_tok;
+    const int64_t pos = len_in[b] + t;
+    WordLoc loc[NW];
+#pragma unroll
+    for (int j = 0; j < NW; ++j) loc[j] = word_loc(g, j);
+    int32_t *T = tile[wv];
+    auto to_lds = [&](const uint4 (&raw)[16]) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            int32_t *p = T + (4 * i + sub) * AR_STRIDE + q4;
+            *(uint2 *)p = make_uint2(raw[i].x, raw[i].y);
+            *(uint2 *)(p + 2) = make_uint2(raw[i].z, raw[i].w);
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    // each field's row is read where its arithmetic starts (a read moved up would keep two
+    // rows in registers at once)
+    auto row_from_lds = [&](int32_t (&x)[64]) {
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            const uint2 u = *(const uint2 *)(T + lane * AR_STRIDE + 2 * j);
+            x[2 * j] = (int32_t)u.x;
+            x[2 * j + 1] = (int32_t)u.y;
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    int32_t x[64];
+    to_lds(rk);
+    row_from_lds(x);
+    to_lds(rv);                                          // the key rows have been read
+    uint32_t word[NW];
+    uint32_t kw[2 * KB], vw[2 * VB];
+    // (lanes past the tile's rows hold its last row again: their recount reads that row)
+    int32_t nk = ar_field<KB, ROT>(x, rounds, sg, tabs->kbnd, g.norm_frac, lane < nr, k + (int64_t)r0 * 64,
+                                   &st->range_errors, kw);
+    // the key field's codes are finished here (left to the compiler, their arithmetic sinks
+    // to the stores and keeps the key row live through the value field)
+#pragma unroll
+    for (int j = 0; j < 2 * KB; ++j) asm volatile("" : "+v"(kw[j]));
+    asm volatile("" : "+v"(nk));
+    row_from_lds(x);
+    const int32_t nv = ar_field<VB, ROT>(x, rounds, sg, tabs->vbnd, g.norm_frac, lane < nr, v + (int64_t)r0 * 64,
+                                         &st->range_errors, vw);
+#pragma unroll
+    for (int j = 0; j < 2 * KB; ++j) word[j] = kw[j];
+#pragma unroll
+    for (int j = 0; j < 2 * VB; ++j) word[2 * KB + j] = vw[j];
+    word[NW - 1] = (uint32_t)(nk & 0xFFFF) | ((uint32_t)(nv & 0xFFFF) << 16);
+    if (lane < nr) {
+        if (pos >= g.capacity) {         // the host checks capacity first; this only guards memory
+            atomicAdd(&st->fault, 1ull);
+        } else {
+#pragma unroll
+            for (int j = 0; j < NW; ++j) *word_ptr(g, loc[j], b, hh, pos) = word[j];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // the fused decode step's writes (kernel.py:271-284): rotate k, v and q,
 // encode and append every (sequence, KV head)'s row, stage the query rows
 // ---------------------------------------------------------------------------
@@ -311,13 +588,46 @@ hipError_t launch_step_write(hipStream_t s, const Geom &g, const Tables *t, cons
     return hipGetLastError();
 }
 
+// The lane = row kernel takes the append when: d = 64; key and value codes of 1, 2 or 4
+// bits (instantiated here for 4/2 and 2/2); every boundary below 2^24 in magnitude and the
+// encoder's shift CENT_FRAC + norm_frac - QK_FRAC at least 0 (its int32 thresholds are then
+// exact); k and v 16-byte aligned (whole-wave 16-byte loads); fewer than 2^31 rows.
+bool append_rows_ok(const Geom &g, const Tables &th, const int32_t *k, const int32_t *v, int64_t rows) {
+    if (g.d != 64 || rows >= (int64_t(1) << 31) - 64) return false;
+    if (!((g.kb == 4 && g.vb == 2) || (g.kb == 2 && g.vb == 2))) return false;
+    if (CENT_FRAC + g.norm_frac - QK_FRAC < 0 || g.norm_frac > QK_FRAC) return false;
+    if (((uintptr_t)k | (uintptr_t)v) & 15) return false;
+    const int64_t lim = int64_t(1) << 24;
+    for (int i = 0; i + 1 < (1 << g.kb); ++i)
+        if (th.kbnd[i] >= lim || th.kbnd[i] <= -lim) return false;
+    for (int i = 0; i + 1 < (1 << g.vb); ++i)
+        if (th.vbnd[i] >= lim || th.vbnd[i] <= -lim) return false;
+    return true;
+}
+
 hipError_t launch_append(hipStream_t s, const Geom &g, const Tables *t, const int32_t *k,
                          const int32_t *v, int n_tok, int seq_lo, int seq_hi, const int64_t *len_in,
-                         int64_t *len_out, DevStats *st, int rounds, const uint64_t (*signs)[2]) {
+                         int64_t *len_out, DevStats *st, int rounds, const uint64_t (*signs)[2],
+                         const Tables *host_tabs) {
     const int64_t rows = (int64_t)(seq_hi - seq_lo) * n_tok * g.n_kv;
     if (rows <= 0) return hipSuccess;
     if (rounds < 0 || rounds > 2 || (rounds && !signs)) return hipErrorInvalidValue;
     const RotSigns sg = rounds ? rot_signs(rounds, signs) : RotSigns{};
+    if (host_tabs && append_rows_ok(g, *host_tabs, k, v, rows)) {
+        const int waves = (int)((rows + 63) / 64);
+        dim3 grid((unsigned)((waves + AR_WAVES - 1) / AR_WAVES)), block(64 * AR_WAVES);
+        const int nr = (int)rows;
+#define INSITU_AR(KB, VB, ROT)                                                                     \
+    hipLaunchKernelGGL((append_rows_kernel<KB, VB, ROT>), grid, block, 0, s, g, t, k, v, n_tok, seq_lo, \
+                       len_in, len_out, seq_hi, rounds, sg, st, nr)
+        if (g.kb == 4) {
+            if (rounds) INSITU_AR(4, 2, true); else INSITU_AR(4, 2, false);
+        } else {
+            if (rounds) INSITU_AR(2, 2, true); else INSITU_AR(2, 2, false);
+        }
+#undef INSITU_AR
+        return hipGetLastError();
+    }
     // about 8 rows a wave at the most, 4 waves a workgroup, up to 8 workgroups a CU
     int64_t blocks = (rows + 8 * APPEND_WAVES - 1) / (8 * APPEND_WAVES);
     if (blocks > 2048) blocks = 2048;
