@@ -246,12 +246,12 @@ __global__ void __launch_bounds__(64 * APPEND_WAVES) append_kernel(
 constexpr int AR_WAVES = 4;
 constexpr int AR_STRIDE = 66;
 
-// x negated where bit c of the signs is set: the sign bit of the high dword flipped by a
-// scalar mask (sw: the 32-bit half of the sign word that holds bit c)
-__device__ __forceinline__ double ar_flip(double x, uint32_t sw, int c) {
-    const uint32_t m = ((sw >> (c & 31)) & 1u) << 31;
-    const uint64_t u = (uint64_t)__double_as_longlong(x) ^ ((uint64_t)m << 32);
-    return __longlong_as_double((long long)u);
+// x * s_c / 8, s_c = -1 where bit c of the signs is set (sw: the 32-bit half of the sign
+// word that holds bit c): the rotation's sign and its 1/sqrt(64) in one exact multiply. The
+// FWHT of x / 8 is FWHT(x) / 8 exactly (its sums keep 3 fractional bits, far below 2^53),
+// so floor of it is rotate.py's floor(FWHT(x) / 8).
+__device__ __forceinline__ double ar_sign_scale(double x, uint32_t sw, int c) {
+    return x * (((sw >> (c & 31)) & 1u) ? -0.125 : 0.125);
 }
 
 // The 64-point FWHT of the row (hadamard butterflies, fixed.py fwht), in place.
@@ -329,18 +329,21 @@ __device__ __forceinline__ int32_t ar_field(const int32_t (&xi)[64], int rounds,
         double x[64];
 #pragma unroll
         for (int c = 0; c < 64; ++c) x[c] = (double)xi[c];
-        // a round: the signs, the FWHT, >> 3 (rotate.py:190-191); rounds is 1 or 2
+        // a round: the signs and 1/8, the FWHT, the floor (rotate.py:170-197); rounds is 1 or 2
         auto round = [&](uint64_t s) {
-            const uint32_t slo = (uint32_t)s, shi = (uint32_t)(s >> 32);
-            // in groups of 8 channels, so that the masks are made where they are used
+            // (a fresh copy of the word each round: the key and value fields share it, and
+            // factors the compiler shared between them would stay live from one to the other)
+            uint32_t slo = (uint32_t)s, shi = (uint32_t)(s >> 32);
+            asm volatile("" : "+s"(slo), "+s"(shi));
+            // in groups of 8 channels, so that the scalar factors are made where they are used
 #pragma unroll
             for (int c = 0; c < 64; ++c) {
-                x[c] = ar_flip(x[c], c < 32 ? slo : shi, c);
+                x[c] = ar_sign_scale(x[c], c < 32 ? slo : shi, c);
                 if ((c & 7) == 7) __builtin_amdgcn_sched_barrier(0);
             }
             ar_fwht64(x);
 #pragma unroll
-            for (int c = 0; c < 64; ++c) x[c] = floor(x[c] * 0.125);
+            for (int c = 0; c < 64; ++c) x[c] = floor(x[c]);
         };
         round(sg.s0a);
         if (rounds > 1) round(sg.s1a);
@@ -392,9 +395,22 @@ __device__ __forceinline__ int32_t ar_field(const int32_t (&xi)[64], int rounds,
 #pragma unroll
     for (int c = 0; c < 64; ++c) {
         const int32_t xv = xr[c];
-        uint32_t code = 0;
+        uint32_t code;
+        if constexpr (BITS == 4) {
+            // #{i : xv > th[i]} by bisection over the sorted thresholds (a prefix of them is
+            // below xv): each step halves the candidates, the next threshold chosen by select
+            const bool c3 = xv > th[7];
+            const bool c2 = xv > (c3 ? th[11] : th[3]);
+            const bool c1 = xv > (c3 ? (c2 ? th[13] : th[9]) : (c2 ? th[5] : th[1]));
+            const int32_t hi = c2 ? (c1 ? th[14] : th[12]) : (c1 ? th[10] : th[8]);
+            const int32_t lo = c2 ? (c1 ? th[6] : th[4]) : (c1 ? th[2] : th[0]);
+            const bool c0 = xv > (c3 ? hi : lo);
+            code = (uint32_t)c3 * 8u + (uint32_t)c2 * 4u + (uint32_t)c1 * 2u + (uint32_t)c0;
+        } else {
+            code = 0;
 #pragma unroll
-        for (int i = 0; i < NB; ++i) code += xv > th[i] ? 1u : 0u;
+            for (int i = 0; i < NB; ++i) code += xv > th[i] ? 1u : 0u;
+        }
         w[c / PER] |= code << (BITS * (c % PER));
     }
     return n;
@@ -436,9 +452,6 @@ __global__ void __launch_bounds__(64 * AR_WAVES) append_rows_kernel(
     const int hh = R % g.n_kv, tt = R / g.n_kv;
     const int t = tt % n_tok, b = seq_lo + tt / n_tok;
     const int64_t pos = len_in[b] + t;
-    WordLoc loc[NW];
-#pragma unroll
-    for (int j = 0; j < NW; ++j) loc[j] = word_loc(g, j);
     int32_t *T = tile[wv];
     auto to_lds = [&](const uint4 (&raw)[16]) {
 #pragma unroll
@@ -489,6 +502,11 @@ __global__ void __launch_bounds__(64 * AR_WAVES) append_rows_kernel(
 #pragma unroll
     for (int j = 0; j < 2 * VB; ++j) word[2 * KB + j] = vw[j];
     word[NW - 1] = (uint32_t)(nk & 0xFFFF) | ((uint32_t)(nv & 0xFFFF) << 16);
+    // where each of the row's dwords goes (scalar; found here, after the arithmetic, so that
+    // it holds no scalar registers through it)
+    WordLoc loc[NW];
+#pragma unroll
+    for (int j = 0; j < NW; ++j) loc[j] = word_loc(g, j);
     if (lane < nr) {
         if (pos >= g.capacity) {         // the host checks capacity first; this only guards memory
             atomicAdd(&st->fault, 1ull);
@@ -589,7 +607,8 @@ hipError_t launch_step_write(hipStream_t s, const Geom &g, const Tables *t, cons
 }
 
 // The lane = row kernel takes the append when: d = 64; key and value codes of 1, 2 or 4
-// bits (instantiated here for 4/2 and 2/2); every boundary below 2^24 in magnitude and the
+// bits (instantiated here for 4/2 and 2/2); the boundaries non-decreasing (4-bit codes are
+// found by bisection); every boundary below 2^24 in magnitude and the
 // encoder's shift CENT_FRAC + norm_frac - QK_FRAC at least 0 (its int32 thresholds are then
 // exact); k and v 16-byte aligned (whole-wave 16-byte loads); fewer than 2^31 rows.
 bool append_rows_ok(const Geom &g, const Tables &th, const int32_t *k, const int32_t *v, int64_t rows) {
@@ -597,6 +616,7 @@ bool append_rows_ok(const Geom &g, const Tables &th, const int32_t *k, const int
     if (!((g.kb == 4 && g.vb == 2) || (g.kb == 2 && g.vb == 2))) return false;
     if (CENT_FRAC + g.norm_frac - QK_FRAC < 0 || g.norm_frac > QK_FRAC) return false;
     if (((uintptr_t)k | (uintptr_t)v) & 15) return false;
+    if (!th.bnd_sorted) return false;
     const int64_t lim = int64_t(1) << 24;
     for (int i = 0; i + 1 < (1 << g.kb); ++i)
         if (th.kbnd[i] >= lim || th.kbnd[i] <= -lim) return false;
