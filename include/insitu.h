@@ -236,6 +236,17 @@ int insitu_seam_wire(insitu_ctx *ctx, const float *p_dev, const float *bias_dev,
                      int32_t cast_after_rope, int32_t *q_dev, int32_t *k_dev, int32_t *v_dev,
                      unsigned long long *counts_host);
 
+/* insitu_project then insitu_seam_wire (kernel.py:198-249) in one launch where the decode
+ * projection takes it (n <= 4 tokens, in_f a multiple of 8, d even): the q|k|v
+ * projections of x_dev fp32 (n, in_f) by w_dev fp16 ((n_q + 2 n_kv) d, in_f) into p_dev
+ * fp32 (n, (n_q + 2 n_kv) d), unbiased, then the seam as insitu_seam_wire (bias_dev added
+ * there) into q/k/v_dev, and counts_host as there. Elsewhere the two calls. */
+int insitu_project_seam(insitu_ctx *ctx, const uint16_t *w_dev, int32_t in_f, const float *x_dev, int64_t n,
+                        const float *bias_dev, int32_t n_q, int32_t n_kv, int32_t d, const int64_t *pos_dev,
+                        int64_t pos0, const int64_t *cos_dev, const int64_t *sin_dev, int64_t max_pos,
+                        int32_t frac, double attn_scale, int32_t cast_after_rope, float *p_dev, int32_t *q_dev,
+                        int32_t *k_dev, int32_t *v_dev, unsigned long long *counts_host);
+
 /* The output side (kernel.py:348-356): out_dev int32 (n, width) Q(frac) -> float ->
  * fp16, then y_dev fp32 (n, hidden) = that @ wo_dev^T + bias_dev with W_o' fp16
  * (hidden, width), R^-1 folded in (ops/output.py:49-78). bias_dev may be NULL. */

@@ -29,6 +29,7 @@ EXPORTS = (
     "insitu_cache_create", "insitu_cache_destroy", "insitu_cache_reset", "insitu_cache_length",
     "insitu_cache_set_length", "insitu_cache_layout", "insitu_append", "insitu_append_seq",
     "insitu_append_wire", "insitu_attend", "insitu_attend_causal", "insitu_attend_causal_head", "insitu_attend_causal_static", "insitu_step", "insitu_project", "insitu_seam_wire",
+    "insitu_project_seam",
     "insitu_output_projection", "insitu_read_rows", "insitu_load_rows", "insitu_read_image",
     "insitu_load_image", "insitu_probe_read", "insitu_probe_empty", "insitu_cache_debug",
     "insitu_cache_stats",
@@ -125,6 +126,8 @@ def load(path: str | None = None):
         "insitu_project": (i32, [vp, vp, i32, i32, vp, i64, vp, vp]),
         "insitu_seam_wire": (i32, [vp, vp, vp, i64, i32, i32, i32, vp, i64, vp, vp, i64, i32,
                                    ctypes.c_double, i32, vp, vp, vp, P(ctypes.c_uint64)]),
+        "insitu_project_seam": (i32, [vp, vp, i32, vp, i64, vp, i32, i32, i32, vp, i64, vp, vp, i64, i32,
+                                      ctypes.c_double, i32, vp, vp, vp, vp, P(ctypes.c_uint64)]),
         "insitu_output_projection": (i32, [vp, vp, i64, i32, i32, vp, i32, vp, vp]),
         "insitu_step": (i32, [vp, vp, vp, vp, vp, i32, P(Stats)]),
         "insitu_read_rows": (i32, [vp, i32, i32, i64, i64, vp]),

@@ -48,16 +48,10 @@ __global__ void add_bias_kernel(float *__restrict__ y, const float *__restrict__
 }
 
 // y (n, out_f) = fp16(x) (n, in_f) . W^T, W fp16 (out_f, in_f) row-major, for n <= GEMV_N
-// tokens: the products are exact in fp32 (11 x 11 significant bits) and each is
-// added with one rounding (fmaf). The block stages fp16(x) in LDS (as float):
-// from fp32 (FIXED = false) or from Q(frac) int32 through float64 (FIXED = true,
-// one rounding, kernel.py:354 to_float). Wave = GEMV_RPW rows, lane = 8
-// consecutive columns per 16-byte load; DPP row steps and readlane sum the lanes.
-// One row per wave (twice the workgroups of two) measured 8.8 -> 7.2 us for the
-// 3,072 x 2,048 projection; two rows a wave, or 8 waves a workgroup, were no faster than
-// one row and 4 waves; staging the inputs before the weight loads are issued was 4 %
-// faster than after.
-constexpr int GEMV_N = 4, GEMV_RPW = 1, GEMV_WAVES = 4, GEMV_UNR = 4;
+// tokens: the products are exact in fp32 (11 x 11 significant bits) and each is added with
+// one rounding (fmaf). fp16(x) from fp32 (FIXED = false) or from Q(frac) int32 through
+// float64 (FIXED = true, one rounding, kernel.py:354 to_float).
+constexpr int GEMV_N = 4;
 
 // The sum of a float over the wave's 64 lanes (in lane 0; a fixed order): within each
 // row of 16 lanes by quad permutes and mirrors, then the four rows by readlane.
@@ -75,93 +69,97 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
     };
     return (rl(v, 0) + rl(v, 16)) + (rl(v, 32) + rl(v, 48));
 }
-constexpr int64_t GEMV_LDS_FLOATS = 16384;     // n * in_f staged, 64 KB
-
-template <bool FIXED>
-__global__ __launch_bounds__(64 * GEMV_WAVES) void gemv_f16_kernel(
-    const uint16_t *__restrict__ w, int32_t out_f, int32_t in_f, const void *__restrict__ xin, int32_t n,
-    double fscale, const float *__restrict__ bias, float *__restrict__ y) {
-    extern __shared__ float xs[];
-    const int lane = threadIdx.x & 63;
-    const int row0 = (blockIdx.x * GEMV_WAVES + (threadIdx.x >> 6)) * GEMV_RPW;
-    // GEMV_UNR 16-byte chunks of each row per batch: for in_f <= 2,048 one batch, all of the
-    // wave's weight loads in flight at once
-    uint4 wv[GEMV_UNR][GEMV_RPW];
-    auto load = [&](int cb) __attribute__((always_inline)) {
+// The columns are split over the workgroup: a workgroup takes GV_RB rows, its 256 lanes 8
+// consecutive columns each (2,048 columns a pass). Every lane issues its 16-byte weight loads
+// of all GV_RB rows first, then reads its 8 columns of each token's x straight into
+// registers, fp16-rounded: no staging of x and no barrier before the arithmetic, so that the
+// whole matrix is in flight at once. Each row's partial sums reduce over the wave (DPP,
+// readlane) and then over the 4 waves through LDS. GV_RB = 2 for fp32 x and 4 for Q16 x
+// (whose conversion through float64 costs more per workgroup): 4.9-5.2 and 5.5 us for the
+// 3,072 x 2,048 and 2,048 x 2,048 decode projections, against 6.9 and 6.1 us for one row
+// per wave with x staged in LDS first, and 5.9-6.1 / 6.6-6.7 us for 8 rows a workgroup.
+// The workgroup's rows row0 + r * rstride (r < GV_RB): each wave's partial sums of row r and
+// token t into part[wave][r][t]; the workgroup has passed a barrier when it returns. The
+// row's sum is then (part[0] + part[1]) + (part[2] + part[3]).
+template <bool FIXED, int GV_RB>
+__device__ __forceinline__ void gemv_partials(const uint16_t *__restrict__ w, int32_t out_f, int32_t in_f,
+                                              const void *__restrict__ xin, int32_t n, double fscale, int row0,
+                                              int rstride, float (*part)[GV_RB][GEMV_N]) {
+    const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+    float acc[GV_RB][GEMV_N];
 #pragma unroll
-        for (int u = 0; u < GEMV_UNR; ++u) {
-            const int c = cb + 512 * u;
-#pragma unroll
-            for (int r = 0; r < GEMV_RPW; ++r) {
-                const int row = row0 + r < out_f ? row0 + r : out_f - 1;     // clamped: in bounds
-                wv[u][r] = c < in_f ? *(const uint4 *)(w + (int64_t)row * in_f + c) : make_uint4(0, 0, 0, 0);
-            }
-        }
-    };
-    // the inputs first, 4 values per 16-byte load and 4 loads per thread in flight (n * in_f
-    // is a multiple of 8), then the weights
-    const int total = n * in_f;
-    for (int i0 = threadIdx.x * 4; i0 < total; i0 += 64 * GEMV_WAVES * 16) {
-        uint4 xv[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int i = i0 + u * 64 * GEMV_WAVES * 4;
-            xv[u] = i < total ? *(const uint4 *)((const char *)xin + (int64_t)i * 4) : make_uint4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int i = i0 + u * 64 * GEMV_WAVES * 4;
-            if (i < total) {
-                const uint32_t wd[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    _Float16 hv;
-                    if (FIXED)
-                        hv = (_Float16)((double)(int32_t)wd[e] * fscale);
-                    else
-                        hv = (_Float16)__builtin_bit_cast(float, wd[e]);
-                    xs[i + e] = (float)hv;
-                }
-            }
-        }
-    }
-    load(lane * 8);
-    __syncthreads();
-    float acc[GEMV_RPW][GEMV_N];
-#pragma unroll
-    for (int r = 0; r < GEMV_RPW; ++r)
+    for (int r = 0; r < GV_RB; ++r)
 #pragma unroll
         for (int t = 0; t < GEMV_N; ++t) acc[r][t] = 0.0f;
-    for (int cb = lane * 8; cb < in_f; cb += 512 * GEMV_UNR) {
+    for (int c0 = 0; c0 < in_f; c0 += 2048) {
+        const int c = c0 + tid * 8;
+        const bool on = c < in_f;                     // in_f is a multiple of 8
+        uint4 wq[GV_RB];
 #pragma unroll
-        for (int u = 0; u < GEMV_UNR; ++u) {
-            const int c = cb + 512 * u;
-            if (c < in_f) {
+        for (int r = 0; r < GV_RB; ++r) {
+            const int row = row0 + r * rstride < out_f ? row0 + r * rstride : out_f - 1;   // clamped: in bounds
+            wq[r] = on ? *(const uint4 *)(w + (int64_t)row * in_f + c) : make_uint4(0, 0, 0, 0);
+        }
+        float xs[GEMV_N][8];
 #pragma unroll
-                for (int r = 0; r < GEMV_RPW; ++r) {
-                    _Float16 hw[8];
-                    __builtin_memcpy(hw, &wv[u][r], 16);
+        for (int t = 0; t < GEMV_N; ++t) {
 #pragma unroll
-                    for (int t = 0; t < GEMV_N; ++t) {
-                        if (t < n) {
+            for (int e = 0; e < 8; ++e) xs[t][e] = 0.0f;
+            if (t >= n) continue;                    // uniform: only the tokens there are converted
+            uint4 a = make_uint4(0, 0, 0, 0), b = make_uint4(0, 0, 0, 0);
+            if (on) {
+                const uint4 *src = (const uint4 *)((const char *)xin + ((int64_t)t * in_f + c) * 4);
+                a = src[0];
+                b = src[1];
+            }
+            const uint32_t wd[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-                            for (int e = 0; e < 8; ++e)
-                                acc[r][t] = fmaf((float)hw[e], xs[t * in_f + c + e], acc[r][t]);
-                        }
-                    }
+            for (int e = 0; e < 8; ++e) {
+                _Float16 hv;
+                if (FIXED)
+                    hv = (_Float16)((double)(int32_t)wd[e] * fscale);
+                else
+                    hv = (_Float16)__builtin_bit_cast(float, wd[e]);
+                xs[t][e] = (float)hv;
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < GV_RB; ++r) {
+            _Float16 hw[8];
+            __builtin_memcpy(hw, &wq[r], 16);
+#pragma unroll
+            for (int t = 0; t < GEMV_N; ++t) {
+                if (t < n) {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[r][t] = fmaf((float)hw[e], xs[t][e], acc[r][t]);
                 }
             }
         }
-        if (cb + 512 * GEMV_UNR < in_f) load(cb + 512 * GEMV_UNR);
     }
 #pragma unroll
-    for (int r = 0; r < GEMV_RPW; ++r) {
+    for (int r = 0; r < GV_RB; ++r) {
 #pragma unroll
         for (int t = 0; t < GEMV_N; ++t) {
             if (t >= n) break;                       // uniform: only the tokens there are
             const float v = wave_sum_f32(acc[r][t]);
-            const int row = row0 + r;
-            if (lane == 0 && row < out_f) y[(int64_t)t * out_f + row] = bias ? v + bias[row] : v;
+            if (lane == 0) part[wv][r][t] = v;
+        }
+    }
+    __syncthreads();
+}
+
+template <bool FIXED, int GV_RB>
+__global__ __launch_bounds__(256) void gemv_f16_rows_kernel(
+    const uint16_t *__restrict__ w, int32_t out_f, int32_t in_f, const void *__restrict__ xin, int32_t n,
+    double fscale, const float *__restrict__ bias, float *__restrict__ y) {
+    __shared__ float part[4][GV_RB][GEMV_N];
+    const int row0 = blockIdx.x * GV_RB, tid = threadIdx.x;
+    gemv_partials<FIXED, GV_RB>(w, out_f, in_f, xin, n, fscale, row0, 1, part);
+    if (tid < GV_RB * GEMV_N) {
+        const int r = tid / GEMV_N, t = tid % GEMV_N, row = row0 + r;
+        if (t < n && row < out_f) {
+            const float v = (part[0][r][t] + part[1][r][t]) + (part[2][r][t] + part[3][r][t]);
+            y[(int64_t)t * out_f + row] = bias ? v + bias[row] : v;
         }
     }
 }
@@ -183,62 +181,96 @@ __device__ __forceinline__ int64_t to_fixed_q16(double a, unsigned long long *sa
 // the attention scale in float64; then either to_fixed and fixed-point RoPE
 // (cast_after_rope = 0, the board's order) or float RoPE and to_fixed (1).
 // RoPE pairs channel j with j + d/2 (the half split, rope.py:144-174).
-__global__ void seam_wire_kernel(const float *__restrict__ p, const float *__restrict__ bias, int64_t n,
-                                 int32_t n_q, int32_t n_kv, int32_t d, const int64_t *__restrict__ pos,
-                                 int64_t pos0, const int64_t *__restrict__ cos_t, const int64_t *__restrict__ sin_t,
-                                 int64_t max_pos, int32_t frac, double attn_scale, int32_t cast_after_rope,
-                                 int32_t *__restrict__ q, int32_t *__restrict__ k, int32_t *__restrict__ v,
-                                 unsigned long long *sat, unsigned long long *range_err) {
+struct SeamArgs {
+    const float *bias;
+    int32_t n_q, n_kv, d;
+    const int64_t *pos;
+    int64_t pos0;
+    const int64_t *cos_t, *sin_t;
+    int64_t max_pos;
+    int32_t frac;
+    double attn_scale;
+    int32_t cast_after_rope;
+    int32_t *q, *k, *v;
+    unsigned long long *sat, *range_err;
+};
+
+// The seam of one channel pair (j, j + d/2) of head h, token t, from its fp32 projections.
+__device__ __forceinline__ void seam_pair(float lo32, float hi32, int64_t t, int h, int j, const SeamArgs &a) {
 #pragma clang fp contract(off)
-    const int heads = n_q + 2 * n_kv;
-    const int64_t wave = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (wave >= n * heads) return;
-    const int64_t t = wave / heads;
-    const int h = (int)(wave % heads);
+    const int n_q = a.n_q, n_kv = a.n_kv, d = a.d;
     const int half = d / 2;
     const int kind = h < n_q ? 0 : (h < n_q + n_kv ? 1 : 2);       // q, k, v
     const int hh = kind == 0 ? h : (kind == 1 ? h - n_q : h - n_q - n_kv);
-    const int64_t width = (int64_t)heads * d;
-    const float *row = p + t * width + (int64_t)h * d;
-    int32_t *dst = kind == 0 ? q + (t * n_q + hh) * d : (kind == 1 ? k + (t * n_kv + hh) * d
-                                                                     : v + (t * n_kv + hh) * d);
-    const int64_t ps = pos ? pos[t] : pos0 + t;
+    int32_t *dst = kind == 0 ? a.q + (t * n_q + hh) * d : (kind == 1 ? a.k + (t * n_kv + hh) * d
+                                                                     : a.v + (t * n_kv + hh) * d);
+    const int64_t ps = a.pos ? a.pos[t] : a.pos0 + t;
     const bool rope = kind != 2;
-    if (rope && (ps < 0 || ps >= max_pos)) {
-        if (lane == 0) atomicAdd(range_err, 1ull);
+    if (rope && (ps < 0 || ps >= a.max_pos)) {
+        if (j == 0) atomicAdd(a.range_err, 1ull);                  // once a row
         return;
     }
-    for (int j = lane; j < half; j += 64) {
-        float lo32 = row[j], hi32 = row[j + half];
-        if (bias) {
-            lo32 = lo32 + bias[h * d + j];
-            hi32 = hi32 + bias[h * d + j + half];
-        }
-        double lo = (double)lo32, hi = (double)hi32;
-        if (kind == 0) {
-            lo = lo * attn_scale;
-            hi = hi * attn_scale;
-        }
-        if (!rope) {
-            dst[j] = (int32_t)to_fixed_q16(lo, sat);
-            dst[j + half] = (int32_t)to_fixed_q16(hi, sat);
-            continue;
-        }
-        const int64_t c = cos_t[ps * half + j], s = sin_t[ps * half + j];
-        if (cast_after_rope) {
-            const double cf = (double)c / (double)(1ll << frac), sf = (double)s / (double)(1ll << frac);
-            const double a = lo * cf, b = hi * sf, e = lo * sf, f = hi * cf;
-            dst[j] = (int32_t)to_fixed_q16(a - b, sat);
-            dst[j + half] = (int32_t)to_fixed_q16(e + f, sat);
-        } else {
-            const int64_t li = to_fixed_q16(lo, sat), hi_ = to_fixed_q16(hi, sat);
-            // Q(16 + frac), one floor shift at the end; not clamped (the RTL flags range)
-            const int64_t ol = (li * c - hi_ * s) >> frac;
-            const int64_t oh = (li * s + hi_ * c) >> frac;
-            dst[j] = (int32_t)ol;
-            dst[j + half] = (int32_t)oh;
-        }
+    if (a.bias) {
+        lo32 = lo32 + a.bias[h * d + j];
+        hi32 = hi32 + a.bias[h * d + j + half];
+    }
+    double lo = (double)lo32, hi = (double)hi32;
+    if (kind == 0) {
+        lo = lo * a.attn_scale;
+        hi = hi * a.attn_scale;
+    }
+    if (!rope) {
+        dst[j] = (int32_t)to_fixed_q16(lo, a.sat);
+        dst[j + half] = (int32_t)to_fixed_q16(hi, a.sat);
+        return;
+    }
+    const int64_t c = a.cos_t[ps * half + j], s = a.sin_t[ps * half + j];
+    if (a.cast_after_rope) {
+        const double cf = (double)c / (double)(1ll << a.frac), sf = (double)s / (double)(1ll << a.frac);
+        const double e0 = lo * cf, e1 = hi * sf, e2 = lo * sf, e3 = hi * cf;
+        dst[j] = (int32_t)to_fixed_q16(e0 - e1, a.sat);
+        dst[j + half] = (int32_t)to_fixed_q16(e2 + e3, a.sat);
+    } else {
+        const int64_t li = to_fixed_q16(lo, a.sat), hi_ = to_fixed_q16(hi, a.sat);
+        // Q(16 + frac), one floor shift at the end; not clamped (the RTL flags range)
+        const int64_t ol = (li * c - hi_ * s) >> a.frac;
+        const int64_t oh = (li * s + hi_ * c) >> a.frac;
+        dst[j] = (int32_t)ol;
+        dst[j + half] = (int32_t)oh;
+    }
+}
+
+__global__ void seam_wire_kernel(const float *__restrict__ p, int64_t n, SeamArgs a) {
+    const int heads = a.n_q + 2 * a.n_kv;
+    const int64_t wave = (int64_t)blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
+    if (wave >= n * heads) return;
+    const int64_t t = wave / heads;
+    const int h = (int)(wave % heads), half = a.d / 2;
+    const float *row = p + t * heads * a.d + (int64_t)h * a.d;
+    for (int j = threadIdx.x & 63; j < half; j += 64) seam_pair(row[j], row[j + half], t, h, j, a);
+}
+
+// The decode projection of q|k|v fused with the seam epilogue (kernel.py:198-249 for n <=
+// GEMV_N tokens). RoPE pairs channel j of a head with j + d/2 and nothing else, so a
+// workgroup that computes exactly those two rows (h d + j and h d + j + d/2) has all the
+// seam needs: thread t of it adds the bias, scales, rotates and casts token t's pair, and
+// writes p as well. No workgroup waits for another. (A ticket per head, the last of its
+// workgroups running the head's seam, took 15.6 us against 4.9 + 4.2 for the two launches:
+// each workgroup waited out its stores and its ticket.)
+__global__ __launch_bounds__(256) void gemv_seam_kernel(const uint16_t *__restrict__ w, int32_t out_f, int32_t in_f,
+                                                        const float *__restrict__ x, int32_t n, float *p, SeamArgs a) {
+    __shared__ float part[4][2][GEMV_N];
+    const int half = a.d / 2;
+    const int h = blockIdx.x / half, j = blockIdx.x % half;
+    const int row0 = h * a.d + j;
+    gemv_partials<false, 2>(w, out_f, in_f, x, n, 0.0, row0, half, part);
+    const int t = threadIdx.x;
+    if (t < n) {
+        const float lo = (part[0][0][t] + part[1][0][t]) + (part[2][0][t] + part[3][0][t]);
+        const float hi = (part[0][1][t] + part[1][1][t]) + (part[2][1][t] + part[3][1][t]);
+        p[(int64_t)t * out_f + row0] = lo;
+        p[(int64_t)t * out_f + row0 + half] = hi;
+        seam_pair(lo, hi, t, h, j, a);
     }
 }
 
@@ -295,17 +327,15 @@ int ensure_x16(insitu_ctx *c, size_t n) {
 }
 
 bool gemv_fits(int64_t n, int32_t in_f) {
-    return n <= GEMV_N && in_f % 8 == 0 && n * in_f <= GEMV_LDS_FLOATS;
+    return n <= GEMV_N && in_f % 8 == 0;
 }
 
 template <bool FIXED>
 int gemv(insitu_ctx *c, const uint16_t *w, int32_t out_f, int32_t in_f, const void *x, int64_t n, double fscale,
          const float *bias, float *y) {
-    const int rows_per_block = GEMV_WAVES * GEMV_RPW;
-    const unsigned blocks = (unsigned)((out_f + rows_per_block - 1) / rows_per_block);
-    hipLaunchKernelGGL(gemv_f16_kernel<FIXED>, dim3(blocks), dim3(64 * GEMV_WAVES),
-                       (size_t)n * in_f * sizeof(float), ctx_stream(c), w, out_f, in_f, x, (int32_t)n, fscale,
-                       bias, y);
+    constexpr int RB = FIXED ? 4 : 2;
+    hipLaunchKernelGGL((gemv_f16_rows_kernel<FIXED, RB>), dim3((unsigned)((out_f + RB - 1) / RB)), dim3(256), 0,
+                       ctx_stream(c), w, out_f, in_f, x, (int32_t)n, fscale, bias, y);
     HIP_TRY(hipGetLastError(), "gemv");
     return INSITU_OK;
 }
@@ -326,6 +356,21 @@ Blas &blas_of(insitu_ctx *c) {
             b.counters = nullptr;
     }
     return b;
+}
+}  // namespace
+
+namespace {
+// The seam's counts into counts_host (when given): {saturated, rows beyond the RoPE table}.
+int seam_counts(insitu_ctx *c, unsigned long long *counts_host) {
+    Blas &b = blas_of(c);
+    if (counts_host) {
+        HIP_TRY(hipMemcpyAsync(counts_host, b.counters, 2 * sizeof(unsigned long long), hipMemcpyDeviceToHost,
+                               ctx_stream(c)),
+                "counts");
+        HIP_TRY(hipStreamSynchronize(ctx_stream(c)), "sync");
+        if (counts_host[1]) return fail(INSITU_ERANGE, "a position beyond the RoPE table (rope.py:163-167)");
+    }
+    return INSITU_OK;
 }
 }  // namespace
 
@@ -379,19 +424,43 @@ int insitu_seam_wire(insitu_ctx *c, const float *p, const float *bias, int64_t n
     if (counts_host) HIP_TRY(hipMemsetAsync(b.counters, 0, 2 * sizeof(unsigned long long), ctx_stream(c)), "memset");
     if (n) {
         const int64_t waves = n * (n_q + 2 * n_kv);
-        hipLaunchKernelGGL(seam_wire_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, ctx_stream(c), p,
-                           bias, n, n_q, n_kv, d, pos, pos0, cos_t, sin_t, max_pos, frac, attn_scale, cast_after_rope, q,
-                           k, v, b.counters, b.counters + 1);
+        const SeamArgs a{bias, n_q, n_kv, d, pos, pos0, cos_t, sin_t, max_pos, frac, attn_scale, cast_after_rope,
+                         q, k, v, b.counters, b.counters + 1};
+        hipLaunchKernelGGL(seam_wire_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, ctx_stream(c), p, n,
+                           a);
         HIP_TRY(hipGetLastError(), "seam epilogue");
     }
-    if (counts_host) {
-        HIP_TRY(hipMemcpyAsync(counts_host, b.counters, 2 * sizeof(unsigned long long), hipMemcpyDeviceToHost,
-                               ctx_stream(c)),
-                "counts");
-        HIP_TRY(hipStreamSynchronize(ctx_stream(c)), "sync");
-        if (counts_host[1]) return fail(INSITU_ERANGE, "a position beyond the RoPE table (rope.py:163-167)");
+    return seam_counts(c, counts_host);
+}
+
+int insitu_project_seam(insitu_ctx *c, const uint16_t *w, int32_t in_f, const float *x, int64_t n,
+                        const float *bias, int32_t n_q, int32_t n_kv, int32_t d, const int64_t *pos, int64_t pos0,
+                        const int64_t *cos_t, const int64_t *sin_t, int64_t max_pos, int32_t frac, double attn_scale,
+                        int32_t cast_after_rope, float *p, int32_t *q, int32_t *k, int32_t *v,
+                        unsigned long long *counts_host) {
+    if (!c || !w || (n && (!x || !p || !cos_t || !sin_t || !q || !k || !v))) return fail(INSITU_EINVAL, "null argument");
+    if (in_f <= 0 || n < 0 || n_q <= 0 || n_kv <= 0 || d <= 0 || d % 2 || frac < 0 || frac > 30 || max_pos <= 0)
+        return fail(INSITU_EBADLEN, "bad projection or seam shape");
+    const int32_t heads = n_q + 2 * n_kv;
+    const int32_t out_f = heads * d;
+    if (!gemv_fits(n, in_f)) {
+        const int rc = insitu_project(c, w, out_f, in_f, x, n, nullptr, p);
+        if (rc) return rc;
+        return insitu_seam_wire(c, p, bias, n, n_q, n_kv, d, pos, pos0, cos_t, sin_t, max_pos, frac, attn_scale,
+                                cast_after_rope, q, k, v, counts_host);
     }
-    return INSITU_OK;
+    HIP_TRY(hipSetDevice(ctx_device(c)), "hipSetDevice");
+    Blas &b = blas_of(c);
+    if (!b.counters) return fail(INSITU_EHIP, "counters");
+    if (counts_host) HIP_TRY(hipMemsetAsync(b.counters, 0, 2 * sizeof(unsigned long long), ctx_stream(c)), "memset");
+    if (n) {
+        const SeamArgs a{bias, n_q, n_kv, d, pos, pos0, cos_t, sin_t, max_pos, frac, attn_scale, cast_after_rope,
+                         q, k, v, b.counters, b.counters + 1};
+        hipLaunchKernelGGL(gemv_seam_kernel, dim3((unsigned)(out_f / 2)), dim3(256), 0, ctx_stream(c), w, out_f,
+                           in_f, x, (int32_t)n, p, a);
+        HIP_TRY(hipGetLastError(), "projection and seam");
+    }
+    return seam_counts(c, counts_host);
 }
 
 int insitu_output_projection(insitu_ctx *c, const int32_t *out, int64_t n, int32_t width, int32_t frac,

@@ -186,8 +186,8 @@ class HostHalf:
         q (n, Hq, d), k and v (n, Hkv, d), int32 torch tensors on the device."""
         import torch
         m = self.model
-        p = self.project_qkv(x)
-        n = p.shape[0]
+        x = self.ctx.to_device(x, torch.float32).reshape(-1, m.hidden_size).contiguous()
+        n = int(x.shape[0])
         positions = np.asarray(positions, dtype=np.int64).reshape(n)
         if n and (positions.min() < 0 or positions.max() >= m.max_position):
             # rope.py:163-167; checked here so that counts=False needs no read-back
@@ -203,14 +203,18 @@ class HostHalf:
         v = torch.empty_like(k)
         cnt = (ctypes.c_uint64 * 2)() if counts else None
         bias = self.weights.qkv_bias
-        _lib.check(self.ctx.lib.insitu_seam_wire(
-            self.ctx.handle, ptr(p), ptr(bias) if bias is not None else None, n, m.num_heads,
-            m.num_kv_heads, m.head_dim, ptr(pos) if pos is not None else None, pos0, ptr(self._cos),
-            ptr(self._sin), m.max_position, ROPE_FRAC,
-            self.attn_scale, 1 if self.cast_after_rope else 0, ptr(q), ptr(k), ptr(v), cnt))
+        width = m.q_out_features + 2 * m.kv_out_features
+        p = torch.empty((n, width), dtype=torch.float32, device=dev)
+        # the projection and the seam in one launch for a decode step (kernel.py:198-249)
+        _lib.check(self.ctx.lib.insitu_project_seam(
+            self.ctx.handle, ptr(self.weights.qkv), m.hidden_size, ptr(x), n,
+            ptr(bias) if bias is not None else None, m.num_heads, m.num_kv_heads, m.head_dim,
+            ptr(pos) if pos is not None else None, pos0, ptr(self._cos), ptr(self._sin),
+            m.max_position, ROPE_FRAC, self.attn_scale, 1 if self.cast_after_rope else 0, ptr(p),
+            ptr(q), ptr(k), ptr(v), cnt))
         if cnt is not None:
             self.last_saturated = int(cnt[0])
-        self._keep = (p, pos)
+        self._keep = (x, p, pos)
         return q, k, v
 
     def output(self, out):

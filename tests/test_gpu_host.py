@@ -268,3 +268,66 @@ def test_two_contexts_on_one_device_keep_their_own_blas_state(ctx, golden_half):
     with torch.cuda.stream(streams[1]):
         q, _, _ = halves[1].wire(xs[3], pos[3])
         np.testing.assert_array_equal(q.cpu().numpy(), ref[3][0])
+
+
+@pytest.mark.parametrize("cast_after_rope", [True, False])
+@pytest.mark.parametrize("n", [1, 2, 4])
+def test_fused_decode_seam_is_exact_on_its_projections(ctx, cast_after_rope, n):
+    """insitu_project_seam for a decode step (n <= 4 tokens: gemv_seam_kernel, the last
+    workgroup of each head running its seam): the wire rows are the oracle's seam of the
+    projections the same call wrote, bit for bit, with biases, positions across the table
+    (given, and consecutive from pos0) and saturating rows; the projections within the
+    fp32 bound."""
+    import ctypes
+    import torch
+    from insitu_amd import _lib
+    from insitu_amd.host import ROPE_FRAC, HostHalf, Weights
+    from insitu_amd.runtime import ptr
+    model = _model()
+    rng = np.random.default_rng(50 + n)
+    biases = [rng.standard_normal(m).astype(np.float32) * 0.05 for m in (NQ * D, NKV * D, NKV * D)]
+    wq, wk, wv, wo = oh.random_weights(HIDDEN, NQ, NKV, D, seed=5)
+    w = Weights(wq, wk, wv, wo, model, matrix(signs_from_seed(D, 0, 1)), q_bias=biases[0],
+                k_bias=biases[1], v_bias=biases[2], ctx=ctx)
+    half = HostHalf(model, w, cast_after_rope=cast_after_rope, ctx=ctx)
+    cos, sin = oh.rope_tables(D, model.max_position, model.rope_theta)
+    for trial, scale in enumerate((0.02, 300.0, 3000.0)):      # the last ones saturate
+        x = (rng.standard_normal((n, HIDDEN)) * scale).astype(np.float32)
+        for consecutive in (False, True):
+            pos = (np.arange(n) + [7, model.max_position - n][trial % 2]) if consecutive else \
+                rng.integers(0, model.max_position, n)
+            q, k, v = half.wire(x, pos)
+            p = half._keep[1].cpu().numpy()
+            _check_gemm(p, np.concatenate([wq, wk, wv]), x)
+            (wq_, wk_, wv_), sat = oh.seam(p, NQ, NKV, D, pos, cos, sin, bias=np.concatenate(biases),
+                                           cast_after_rope=cast_after_rope)
+            np.testing.assert_array_equal(q.cpu().numpy(), wq_)
+            np.testing.assert_array_equal(k.cpu().numpy(), wk_)
+            np.testing.assert_array_equal(v.cpu().numpy(), wv_)
+            assert half.last_saturated == sat
+            if trial:
+                assert sat > 0
+    np.testing.assert_array_equal(half.rope.cos, cos)
+    # a position beyond the table, found on the device: ERANGE, and the per-head tickets
+    # are left ready for the next call
+    from insitu_amd._lib import FormatError
+    dev = ctx.torch_device
+    xd = torch.from_numpy(x).to(dev)
+    bad = torch.from_numpy(np.full(n, model.max_position, np.int64)).to(dev)
+    pd = torch.empty((n, (NQ + 2 * NKV) * D), dtype=torch.float32, device=dev)
+    qd = torch.empty((n, NQ, D), dtype=torch.int32, device=dev)
+    kd = torch.empty((n, NKV, D), dtype=torch.int32, device=dev)
+    vd = torch.empty((n, NKV, D), dtype=torch.int32, device=dev)
+    cnt = (ctypes.c_uint64 * 2)()
+    bias = w.qkv_bias
+    with pytest.raises(FormatError):
+        _lib.check(ctx.lib.insitu_project_seam(
+            ctx.handle, ptr(w.qkv), HIDDEN, ptr(xd), n, ptr(bias), NQ, NKV, D, ptr(bad), 0,
+            ptr(half._cos), ptr(half._sin), model.max_position, ROPE_FRAC, half.attn_scale,
+            1 if cast_after_rope else 0, ptr(pd), ptr(qd), ptr(kd), ptr(vd), cnt))
+    assert cnt[1] == n * (NQ + NKV)                 # every q and k row of every token
+    q2, _, _ = half.wire(x, np.arange(n))
+    p = half._keep[1].cpu().numpy()
+    (wq_, _, _), _ = oh.seam(p, NQ, NKV, D, np.arange(n), cos, sin, bias=np.concatenate(biases),
+                             cast_after_rope=cast_after_rope)
+    np.testing.assert_array_equal(q2.cpu().numpy(), wq_)
