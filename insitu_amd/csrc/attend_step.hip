@@ -627,16 +627,42 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     if (ok && slice == 0 && scorer) {
         if (live) {
             const int64_t kn = sext16(nw);
+            // (acc kn) >> score_shift in fp64: acc * (kn / 2^shift) is exact while |acc kn| <
+            // 2^53, and a computed |product| below 2^(53 - shift) proves it (rounding never
+            // crosses the power of two); floor is then the arithmetic shift. A lane past the
+            // bound takes the int64 product, which wraps as the reference's does.
+            const double kns = (double)kn * __builtin_ldexp(1.0, -score_shift);
+            const double lim = __builtin_ldexp(1.0, 53 - score_shift);
+            double pr[G];
+            bool fast = true;
 #pragma unroll
             for (int h = 0; h < G; ++h) {
-                int64_t v = wmul(dbl_to_i64(acc[h]), kn) >> score_shift;
-                if (v < SCORE_LO || v > SCORE_HI) {
-                    ++ovf;
-                    v = v < SCORE_LO ? SCORE_LO : SCORE_HI;
+                pr[h] = acc[h] * kns;
+                fast = fast && fabs(pr[h]) < lim;
+            }
+            if (fast) {
+                double am = 0.0;
+#pragma unroll
+                for (int h = 0; h < G; ++h) {
+                    const double f = floor(pr[h]);
+                    const double v = fmax(fmin(f, (double)SCORE_HI), (double)SCORE_LO);
+                    ovf += f != v ? 1 : 0;
+                    am = fmax(am, fabs(v));
+                    s[h] = dbl_to_i64(v);                          // |v| <= 2^47
                 }
-                const int64_t a = v < 0 ? -v : v;
-                mabs = a > mabs ? a : mabs;
-                s[h] = v;
+                mabs = dbl_to_i64(am);
+            } else {
+#pragma unroll
+                for (int h = 0; h < G; ++h) {
+                    int64_t v = wmul(dbl_to_i64(acc[h]), kn) >> score_shift;
+                    if (v < SCORE_LO || v > SCORE_HI) {
+                        ++ovf;
+                        v = v < SCORE_LO ? SCORE_LO : SCORE_HI;
+                    }
+                    const int64_t a = v < 0 ? -v : v;
+                    mabs = a > mabs ? a : mabs;
+                    s[h] = v;
+                }
             }
         }
     }
