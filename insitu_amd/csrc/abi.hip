@@ -106,7 +106,7 @@ struct insitu_ctx {
 // stand-in; the device address comes from hipGetSymbolAddress, once per device,
 // in insitu_ctx_create.
 constexpr size_t STATIC_SCRATCH_BYTES = (size_t)64 << 20;
-constexpr size_t STATIC_LEN_BYTES = 4096;      // PREFILL_QB int64 lengths, rounded up
+constexpr size_t STATIC_LEN_BYTES = 8192;      // PREFILL_QB int64 lengths, rounded up
 static __device__ __align__(256) uint8_t scratch[STATIC_SCRATCH_BYTES];
 
 namespace {
@@ -786,7 +786,7 @@ int insitu_attend(insitu_cache *k, const int32_t *q, int32_t *out, int32_t mode,
 // fit PREFILL_SCRATCH_BUDGET (at most PREFILL_QB): at ctx 32k and d = 64 about
 // 2.2 MB per query, so 116 queries per launch; at d = 128 and ctx 131,072 about
 // 17 MB per query, so 15.
-constexpr int64_t PREFILL_QB = 256;
+constexpr int64_t PREFILL_QB = 1024;
 constexpr size_t PREFILL_SCRATCH_BUDGET = (size_t)256 << 20;
 
 __global__ void prefill_lengths_kernel(int64_t *len, int64_t first, int64_t n) {
