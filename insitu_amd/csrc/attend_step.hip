@@ -95,6 +95,7 @@ constexpr int CHUNK = NT;         // tokens per workgroup, one per thread
 constexpr int D = 64;
 constexpr int G = GF;             // query heads per KV head
 constexpr int RMAX = 32;          // runs per head a chunk sums in LDS
+constexpr int RPB = 64;           // runs per head the replay loads in one round trip (lane = run)
 constexpr int SLOTS = 16;         // runs per head a chunk after chunk 0 publishes
 constexpr int HMAX = 512;         // chunks per sequence
 constexpr int NSEG = 2048;        // runs per head the replay lists
@@ -1456,7 +1457,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         l = (int64_t)(sm & ((1ull << 26) - 1));
         events = (sm >> 26) & 0xFFF;
     };
-    // Each head's wave walks its own runs, RMAX at a time: their sums (lane = channel), L, f
+    // Each head's wave walks its own runs, RPB at a time: their sums (lane = channel), L, f
     // and bounds (lane = run) loaded into registers together, one round trip, then the walk.
     bool unsafe = false;
     if (hw) {
@@ -1467,8 +1468,8 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         const uint64_t *metah = ck.meta + hbase * 2;
         bool take_c0 = nch > 1;
         const int tot_h = S.total[h];
-        for (int g0 = 0; g0 < tot_h && !hflags; g0 += RMAX) {
-            const int nb = tot_h - g0 < RMAX ? tot_h - g0 : RMAX;
+        for (int g0 = 0; g0 < tot_h && !hflags; g0 += RPB) {
+            const int nb = tot_h - g0 < RPB ? tot_h - g0 : RPB;
             const bool mine = lane < nb;
             const uint32_t ent = mine ? (uint32_t)S.u.rp.rl[h][g0 + lane] : 0u;
             // every slot index is checked against the pool before it is read: one past it (a
@@ -1484,9 +1485,9 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             const int sl = ld ? slot : 0;
             const uint64_t lfr = get64(metah + 2 * sl);
             const uint64_t bbr = get64(metah + 2 * sl + 1);
-            int32_t v[RMAX];
+            int32_t v[RPB];
 #pragma unroll
-            for (int k = 0; k < RMAX; ++k) v[k] = (int32_t)get32(segh + (int64_t)__builtin_amdgcn_readlane(sl, k) * D);
+            for (int k = 0; k < RPB; ++k) v[k] = (int32_t)get32(segh + (int64_t)__builtin_amdgcn_readlane(sl, k) * D);
             const uint64_t lf = ld ? lfr : 0ull;
             const int64_t bb = ld ? (int64_t)bbr : 0;
             if (take_c0) {
@@ -1514,7 +1515,7 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
                 if (!__ballot(a0 + bsum_all > ACC_HI)) {
                     const uint32_t PLa = wave_scan_add32((uint32_t)lf);   // L < 2^26 a run, 0 past nb
 #pragma unroll
-                    for (int k0 = 0; k0 < RMAX; k0 += 8) {
+                    for (int k0 = 0; k0 < RPB; k0 += 8) {
                         if (k0 >= nb) break;
                         const int kn = nb - k0 < 8 ? nb - k0 : 8;
                         const uint32_t bev = (uint32_t)(evm >> k0) & ((1u << kn) - 1u);
@@ -1547,14 +1548,15 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             // Otherwise block by block: lane k < nb holds run k's list entry, L, f and bound B;
             // prefix sums over the lanes give each block's sums, |acc at a block's start| + the
             // block's B certifies 8 runs at once, and elsewhere the walk goes run by run.
-            // 32-bit prefix sums: L < 2^26 per run, and bounds below 2^27 (a run with a larger
-            // one is checked on its own, by the walk run by run)
-            const uint64_t bigm = __ballot(mine && bb >= (1ll << 27));
-            const uint32_t PB = wave_scan_add32(bb < (1ll << 27) ? (uint32_t)bb : 0u);
+            // 32-bit prefix sums over the RPB = 64 runs: L < 2^26 per run, and bounds below 2^26
+            // (a run with a larger one is checked on its own, by the walk run by run)
+            static_assert(RPB <= 64, "64 bounds below 2^26 sum below 2^32");
+            const uint64_t bigm = __ballot(mine && bb >= (1ll << 26));
+            const uint32_t PB = wave_scan_add32(bb < (1ll << 26) ? (uint32_t)bb : 0u);
             const uint32_t PL = wave_scan_add32((uint32_t)lf);
             STAMP(23);
 #pragma unroll
-            for (int k0 = 0; k0 < RMAX; k0 += 8) {
+            for (int k0 = 0; k0 < RPB; k0 += 8) {
                 if (k0 >= nb) break;
                 const int kn = nb - k0 < 8 ? nb - k0 : 8;
                 const uint32_t bmask = (1u << kn) - 1u;
