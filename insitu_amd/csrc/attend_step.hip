@@ -214,9 +214,6 @@ struct StepLds {
     uint32_t runL[G][RMAX];
     int32_t runf[G][RMAX];
     int32_t qi[G][D];                       // the rotated query rows (the score, the serial path)
-    // the head waves' planes (key words, value words, norm word a lane), loaded for them by
-    // waves G .. 2G - 1, so that a head wave's first load is its query row
-    uint32_t hpl[G][D * KB / 32 + D * VB / 32 + 1][64];
     uint8_t codes[2][MAX_D];                // the new token's key and value codes
     uint32_t nk[D * 4 / 32 + 1], nv[D * 2 / 32 + 1], nn;   // the new row: key words, value words, norms
     int64_t wmax[NW][G];
@@ -358,29 +355,19 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     for (int i = 0; i <= KWORDS; ++i) kw[i] = 0;
 #pragma unroll
     for (int i = 0; i < VWORDS; ++i) vwd[i] = 0;
-    // Wave w's planes (key words, value words, norm word) into (k, v, n): a token wave's own
-    // token, or a helper's slice of its token wave's token; nothing for a token past the
-    // context or the step's new one (its row arrives through LDS).
+    // Wave w's planes (key words, value words, norm word) into (k, v, n): the row of its
+    // token wave's token (a helper picks its slice's words after barrier B1).
     auto load_planes = [&](int w, uint32_t(&k)[KWORDS + 1], uint32_t(&v)[VWORDS], uint32_t &n)
         __attribute__((always_inline)) {
-        const int sl = w / ntw, tww = w - sl * ntw;
-        if (sl > 0) {
-            // a helper: the key words of its slice of token hx, from word 0 on
-            const int hx = 64 * tww + lane;
-            if (!(w < ntw * sp && t0 + hx < T) || (newrow && hx == tln)) return;
-            const int w0 = cps >= 8 ? sl * cps / 8 : sl / 2;       // the slice's first word
-            const uint4 x = *(const uint4 *)(hb + (w0 >> 2) * g.span + (t0 + hx) * 16);
-            // slices of 4 words start at a plane, of 2 at an even word, of 1 or half anywhere
-            const uint32_t x0 = (w0 & 2) ? x.z : x.x, x1 = (w0 & 2) ? x.w : x.y;
-            k[0] = ((w0 & 1) ? x1 : x0) >> (cps >= 8 ? 0 : 16 * (sl & 1));
-            k[1] = x1;
-            k[2] = x.z;
-            k[3] = x.w;
-            return;
-        }
-        const int lt = 64 * w + lane;
-        if (!(t0 + lt < T) || (newrow && lt == tln)) return;
-        const int64_t t = t0 + lt;
+        const int tww = w % ntw;
+        // Every lane loads, with no branch: a lane past the context reads the chunk's row t0
+        // (its values are never used: the score, the list and the walk take live tokens only,
+        // a helper's partial sums go to dead lanes), and the step's new token is replaced by
+        // its row from LDS after barrier B1. (Lanes that returned early, and a helper path of
+        // its own, made the compiler join the paths with copies of the loaded registers, so
+        // that every wave waited for its planes before B1.)
+        const int lt = 64 * tww + lane;
+        const int64_t t = t0 + lt < T ? t0 + lt : t0;
 #pragma unroll
         for (int p = 0; p < NFULL; ++p) {
             const uint4 x = *(const uint4 *)(hb + p * g.span + t * 16);
@@ -408,20 +395,6 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         n = *(const uint32_t *)(hb + (KPL + 1) * g.span + t * 4);
     };
     if (wv >= G) load_planes(wv, kw, vwd, nw);
-    if (wv >= G && wv < 2 * G) {
-        // head wave wv - G's planes, handed over in LDS
-        uint32_t k2[KWORDS + 1], v2[VWORDS], n2 = 0;
-#pragma unroll
-        for (int i = 0; i <= KWORDS; ++i) k2[i] = 0;
-#pragma unroll
-        for (int i = 0; i < VWORDS; ++i) v2[i] = 0;
-        load_planes(wv - G, k2, v2, n2);
-#pragma unroll
-        for (int i = 0; i < KWORDS; ++i) S.hpl[wv - G][i][lane] = k2[i];
-#pragma unroll
-        for (int i = 0; i < VWORDS; ++i) S.hpl[wv - G][KWORDS + i][lane] = v2[i];
-        S.hpl[wv - G][KWORDS + VWORDS][lane] = n2;
-    }
     // zero the run accumulators (LDS atomics add into them)
     for (int i = tid; i < G * RMAX * D; i += NT) (&S.runS[0][0][0])[i] = 0;
     if (tid < G * RMAX) {
@@ -509,6 +482,10 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             ((uint16_t *)&S.nn)[f] = (uint16_t)(n & 0xFFFF);
         }
     }
+    // The head waves' own planes, requested after their rotation (so that it waits for the
+    // query row alone); they land while the other waves of their SIMDs score. (Loaded for them
+    // by waves 4-7 and handed over in LDS instead, barrier B1 waited for those loads.)
+    if (wv < G) load_planes(wv, kw, vwd, nw);
     STAMP(1);
     __syncthreads();                                               // B1
     STAMP(2);
@@ -519,12 +496,21 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     int32_t ex = 0;
     if (tid >= 320 && tid < 320 + NV) tab = tabs->vc[tid - 320];
     if (tid >= 384 && tid < 384 + 256) ex = tabs->exp_table[tid - 384];
-    if (wv < G) {
+    if (slice > 0) {
+        // a helper's slice of its token's key words: word w0 on (uniform selects over the row)
+        const int w0 = cps >= 8 ? slice * cps / 8 : slice / 2;
+        // x[i] = word (w0 + i) mod KWORDS, with constant register indices only (a runtime index
+        // into kw would put the array in scratch memory)
+        uint32_t x[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int i = 0; i < KWORDS; ++i) kw[i] = S.hpl[wv][i][lane];
+        for (int j = 0; j < KWORDS; ++j) {
+            const int d = (j - w0) & (KWORDS - 1);
 #pragma unroll
-        for (int i = 0; i < VWORDS; ++i) vwd[i] = S.hpl[wv][KWORDS + i][lane];
-        nw = S.hpl[wv][KWORDS + VWORDS][lane];
+            for (int i = 0; i < 4; ++i) x[i] = d == i ? kw[j] : x[i];
+        }
+        kw[0] = x[0] >> (cps >= 8 ? 0 : 16 * (slice & 1));
+#pragma unroll
+        for (int i = 1; i < 4; ++i) kw[i] = x[i];
     }
     if (fresh) {
 #pragma unroll
