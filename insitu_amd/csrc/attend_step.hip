@@ -328,11 +328,13 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     // -- P0: loads, rotations, the new row ---------------------------------------
     // The small loads first (wire rows, tables), then the chunk's planes: the vector
     // memory counter drains in order, so the rotations wait only for their rows.
-    int32_t xv = 0;
-    if (wv < G)
-        xv = si.qw[((int64_t)b * g.n_q + kvh * G + wv) * D + lane];
-    else if (newrow && wv < G + 2)
-        xv = (wv == G ? si.kw : si.vw)[((int64_t)b * g.n_kv + kvh) * D + lane];
+    // The loads of P0 go out in order: the wire row (unconditional: a wave that needs none
+    // reads one it ignores), the new row's boundaries (their waves wait for them where the
+    // paths join, before their planes go out), the score's table, the planes. A wait for a
+    // later load waits for every earlier one.
+    const int32_t *xsrc = wv < G ? si.qw + ((int64_t)b * g.n_q + kvh * G + wv) * D
+                                 : (wv == G + 1 ? si.vw : si.kw) + ((int64_t)b * g.n_kv + kvh) * D;
+    const int32_t xv = xsrc[lane];
     // the new token's encoder: lane i < 2^bits - 1 of wave G (keys) and G + 1 (values) holds
     // boundary i (quantize.py:183-196)
     int64_t bl = 0;
@@ -343,11 +345,8 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
     const double kc_absmax = tabs->kc_absmax;
     // The score's table by code byte (two channels' key centroids in one LDS read), loaded by
     // waves past the head waves, whose one load before the rotation is their query row.
-    int64_t kp0 = 0, kp1 = 0;
-    if (tid >= 512 && tid < 512 + 256) {
-        kp0 = tabs->kc[(tid - 512) & 15];
-        kp1 = tabs->kc[(tid - 512) >> 4];
-    }
+    const int64_t kp0 = tabs->kc[tid & 15], kp1 = tabs->kc[(tid >> 4) & 15];   // used by tid 512 .. 767
+    __builtin_amdgcn_sched_barrier(0);          // (these before the planes: see above)
     uint32_t kw[KWORDS + 1];
     uint32_t vwd[VWORDS];
     uint32_t nw = 0;
@@ -394,7 +393,11 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
         }
         n = *(const uint32_t *)(hb + (KPL + 1) * g.span + t * 4);
     };
-    if (wv >= G) load_planes(wv, kw, vwd, nw);
+    // Every wave's planes, right after its wire row: the loads are unconditional, so that a
+    // rotation waits for its row alone (the vector memory counter drains in order), and no
+    // wave waits for its planes before barrier B1. (Loaded for the head waves by waves 4-7 and
+    // handed over in LDS, or branching per lane, B1 waited for the planes.)
+    load_planes(wv, kw, vwd, nw);
     // zero the run accumulators (LDS atomics add into them)
     for (int i = tid; i < G * RMAX * D; i += NT) (&S.runS[0][0][0])[i] = 0;
     if (tid < G * RMAX) {
@@ -482,10 +485,6 @@ __global__ void __launch_bounds__(NT, 1) step_kernel(Geom g, const Tables *__res
             ((uint16_t *)&S.nn)[f] = (uint16_t)(n & 0xFFFF);
         }
     }
-    // The head waves' own planes, requested after their rotation (so that it waits for the
-    // query row alone); they land while the other waves of their SIMDs score. (Loaded for them
-    // by waves 4-7 and handed over in LDS instead, barrier B1 waited for those loads.)
-    if (wv < G) load_planes(wv, kw, vwd, nw);
     STAMP(1);
     __syncthreads();                                               // B1
     STAMP(2);
