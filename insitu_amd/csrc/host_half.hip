@@ -53,6 +53,22 @@ __global__ void add_bias_kernel(float *__restrict__ y, const float *__restrict__
 // float64 (FIXED = true, one rounding, kernel.py:354 to_float).
 constexpr int GEMV_N = 4;
 
+// fp16(x / 2^16) for int32 x, rounded to nearest even, in integer steps: |x| rounded to 11
+// significant bits (half to even), then scaled, which is exact in fp32 and in fp16 (|x| / 2^16
+// < 2^15, inside fp16's range; below 2^-14 the value has at most 2 bits, on fp16's subnormal
+// grid). The same value as (_Float16)((double)x / 2^16), for ~20 instructions instead of a
+// float64-to-fp16 conversion.
+__device__ __forceinline__ float q16_to_f16f(int32_t x) {
+    const uint32_t a = x < 0 ? 0u - (uint32_t)x : (uint32_t)x;
+    const int msb = 31 - __builtin_clz(a | 1u);
+    const int sh = msb > 10 ? msb - 10 : 0;
+    uint32_t r = a >> sh;
+    const uint32_t rem = a & ((1u << sh) - 1u), half = sh ? 1u << (sh - 1) : 1u;
+    r += (sh && (rem > half || (rem == half && (r & 1u)))) ? 1u : 0u;
+    const float m = __builtin_ldexpf((float)r, sh - 16);
+    return (float)(_Float16)(x < 0 ? -m : m);
+}
+
 // The sum of a float over the wave's 64 lanes (in lane 0; a fixed order): within each
 // row of 16 lanes by quad permutes and mirrors, then the four rows by readlane.
 __device__ __forceinline__ float wave_sum_f32(float v) {
@@ -86,6 +102,7 @@ __device__ __forceinline__ void gemv_partials(const uint16_t *__restrict__ w, in
                                               const void *__restrict__ xin, int32_t n, double fscale, int row0,
                                               int rstride, float (*part)[GV_RB][GEMV_N]) {
     const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63;
+    const bool q16 = FIXED && fscale == 1.0 / 65536.0;        // the seam's Q16 (uniform)
     float acc[GV_RB][GEMV_N];
 #pragma unroll
     for (int r = 0; r < GV_RB; ++r)
@@ -115,12 +132,11 @@ __device__ __forceinline__ void gemv_partials(const uint16_t *__restrict__ w, in
             const uint32_t wd[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                _Float16 hv;
                 if (FIXED)
-                    hv = (_Float16)((double)(int32_t)wd[e] * fscale);
+                    xs[t][e] = q16 ? q16_to_f16f((int32_t)wd[e])
+                                   : (float)(_Float16)((double)(int32_t)wd[e] * fscale);
                 else
-                    hv = (_Float16)__builtin_bit_cast(float, wd[e]);
-                xs[t][e] = (float)hv;
+                    xs[t][e] = (float)(_Float16)__builtin_bit_cast(float, wd[e]);
             }
         }
 #pragma unroll
@@ -333,7 +349,7 @@ bool gemv_fits(int64_t n, int32_t in_f) {
 template <bool FIXED>
 int gemv(insitu_ctx *c, const uint16_t *w, int32_t out_f, int32_t in_f, const void *x, int64_t n, double fscale,
          const float *bias, float *y) {
-    constexpr int RB = FIXED ? 4 : 2;
+    constexpr int RB = 2;
     hipLaunchKernelGGL((gemv_f16_rows_kernel<FIXED, RB>), dim3((unsigned)((out_f + RB - 1) / RB)), dim3(256), 0,
                        ctx_stream(c), w, out_f, in_f, x, (int32_t)n, fscale, bias, y);
     HIP_TRY(hipGetLastError(), "gemv");
