@@ -148,7 +148,7 @@ def copy_calibration() -> None:
 
 def cpu_baseline(cache, q_rot_all, out_gpu, wire, budget_s: float = 20.0):
     """The oracle's numpy restatement of the decode step, timed on this box's host cores
-    (BASELINE.md's CPU plan): rotate the step's q/k/v, encode and pack its k/v row, then
+    (the reference's CPU path for the step): rotate the step's q/k/v, encode and pack its k/v row, then
     attend_online (the per-token loop, the parity golden) on the step's cache, KV group
     by KV group within `budget_s` (at least one group; the GPU output of every timed
     group is checked bit for bit), and the vectorized attend_two_pass on every group.
