@@ -30,19 +30,6 @@ __global__ void __launch_bounds__(64) rotate_kernel(const int32_t *__restrict__ 
 }
 
 
-hipError_t launch_rotate(hipStream_t s, const int32_t *x, int32_t *y, int64_t n_vec, int d,
-                         int rounds, const uint64_t (*signs)[2], unsigned long long *range_err) {
-    if (n_vec <= 0) return hipSuccess;
-    if (rounds > 2) return hipErrorInvalidValue;  // the kernel carries two sign diagonals
-    const RotSigns sg = rot_signs(rounds, signs);
-    dim3 grid((unsigned)n_vec), block(64);
-    if (d <= 64)
-        hipLaunchKernelGGL(rotate_kernel<1>, grid, block, 0, s, x, y, n_vec, d, rounds, sg, range_err);
-    else
-        hipLaunchKernelGGL(rotate_kernel<2>, grid, block, 0, s, x, y, n_vec, d, rounds, sg, range_err);
-    return hipGetLastError();
-}
-
 // ---------------------------------------------------------------------------
 // norm + encode
 // ---------------------------------------------------------------------------
@@ -307,9 +294,58 @@ __device__ __forceinline__ unsigned long long ar_range_recount(uint64_t need, co
         const unsigned long long cnt =
             (unsigned long long)__popcll(__ballot(x[0] < INT32_MIN || x[0] > INT32_MAX));
         if (lane == j) mine = cnt;
-        if (lane == 0 && cnt) atomicAdd(range_err, cnt);
+        if (lane == 0 && cnt && range_err) atomicAdd(range_err, cnt);
     }
     return mine;
+}
+
+// The rotation of a row in registers, lane = row (rotate.py:170-197, rounds 1 or 2): the
+// sign and 1/8 in one exact multiply, the FWHT's butterflies, the floor, all in fp64 on
+// integers; xr the rotated row as int32 (wrapped), S (when WANT_S) its sum of squares in fp64
+// partial sums (exact below 2^53; +inf when values wrapped, so that the caller takes the
+// int64 path). Values beyond int32 are counted into range_err for live lanes (recounted by the
+// whole wave, lane = channel, from rows0: the fast path keeps no unwrapped copy of the row).
+template <bool WANT_S>
+__device__ __forceinline__ void ar_rotate_row(const int32_t (&xi)[64], int rounds, const RotSigns &sg, bool live,
+                                             const int32_t *rows0, unsigned long long *range_err,
+                                             int32_t (&xr)[64], double &S) {
+    double x[64];
+#pragma unroll
+    for (int c = 0; c < 64; ++c) x[c] = (double)xi[c];
+    // a round: the signs and 1/8, the FWHT, the floor (rotate.py:170-197); rounds is 1 or 2
+    auto round = [&](uint64_t s) {
+        // (a fresh copy of the word each round: the key and value fields share it, and
+        // factors the compiler shared between them would stay live from one to the other)
+        uint32_t slo = (uint32_t)s, shi = (uint32_t)(s >> 32);
+        asm volatile("" : "+s"(slo), "+s"(shi));
+        // in groups of 8 channels, so that the scalar factors are made where they are used
+#pragma unroll
+        for (int c = 0; c < 64; ++c) {
+            x[c] = ar_sign_scale(x[c], c < 32 ? slo : shi, c);
+            if ((c & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+        }
+        ar_fwht64(x);
+#pragma unroll
+        for (int c = 0; c < 64; ++c) x[c] = floor(x[c]);
+    };
+    round(sg.s0a);
+    if (rounds > 1) round(sg.s1a);
+    double amax = 0.0, s4[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int c = 0; c < 64; ++c) {
+        amax = fmax(amax, fabs(x[c]));
+        if (WANT_S) s4[c & 3] = fma(x[c], x[c], s4[c & 3]);
+        // |x| < 2^51: the low dword of x + 1.5 * 2^52 is x mod 2^32, the int32 wrap
+        xr[c] = (int32_t)(uint32_t)__double_as_longlong(x[c] + 6755399441055744.0);
+    }
+    S = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+    // rare: values may have wrapped (live lanes only: the others' rows are not stored, and
+    // a recount reads rows0 + 64 j only for j below the tile's row count)
+    const uint64_t need = __ballot(live && amax >= 2147483648.0);
+    if (need) {
+        const unsigned long long cnt = ar_range_recount(need, rows0, rounds, sg, range_err);
+        if (cnt) S = __builtin_inf();               // the squares are of the wrapped values
+    }
 }
 
 // One field of a lane's row: xi (int32, the row as loaded) rotated when ROT, its norm
@@ -326,43 +362,7 @@ __device__ __forceinline__ int32_t ar_field(const int32_t (&xi)[64], int rounds,
     int32_t xr[64];
     double S;
     if constexpr (ROT) {
-        double x[64];
-#pragma unroll
-        for (int c = 0; c < 64; ++c) x[c] = (double)xi[c];
-        // a round: the signs and 1/8, the FWHT, the floor (rotate.py:170-197); rounds is 1 or 2
-        auto round = [&](uint64_t s) {
-            // (a fresh copy of the word each round: the key and value fields share it, and
-            // factors the compiler shared between them would stay live from one to the other)
-            uint32_t slo = (uint32_t)s, shi = (uint32_t)(s >> 32);
-            asm volatile("" : "+s"(slo), "+s"(shi));
-            // in groups of 8 channels, so that the scalar factors are made where they are used
-#pragma unroll
-            for (int c = 0; c < 64; ++c) {
-                x[c] = ar_sign_scale(x[c], c < 32 ? slo : shi, c);
-                if ((c & 7) == 7) __builtin_amdgcn_sched_barrier(0);
-            }
-            ar_fwht64(x);
-#pragma unroll
-            for (int c = 0; c < 64; ++c) x[c] = floor(x[c]);
-        };
-        round(sg.s0a);
-        if (rounds > 1) round(sg.s1a);
-        double amax = 0.0, s4[4] = {0.0, 0.0, 0.0, 0.0};
-#pragma unroll
-        for (int c = 0; c < 64; ++c) {
-            amax = fmax(amax, fabs(x[c]));
-            s4[c & 3] = fma(x[c], x[c], s4[c & 3]);
-            // |x| < 2^51: the low dword of x + 1.5 * 2^52 is x mod 2^32, the int32 wrap
-            xr[c] = (int32_t)(uint32_t)__double_as_longlong(x[c] + 6755399441055744.0);
-        }
-        S = (s4[0] + s4[1]) + (s4[2] + s4[3]);
-        // rare: values may have wrapped (live lanes only: the others' rows are not stored, and
-        // a recount reads rows0 + 64 j only for j below the tile's row count)
-        const uint64_t need = __ballot(live && amax >= 2147483648.0);
-        if (need) {
-            const unsigned long long cnt = ar_range_recount(need, rows0, rounds, sg, range_err);
-            if (cnt) S = __builtin_inf();           // the squares are of the wrapped values
-        }
+        ar_rotate_row<true>(xi, rounds, sg, live, rows0, range_err, xr, S);
     } else {
         double s4[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
@@ -414,6 +414,83 @@ __device__ __forceinline__ int32_t ar_field(const int32_t (&xi)[64], int rounds,
         w[c / PER] |= code << (BITS * (c % PER));
     }
     return n;
+}
+
+// insitu_rotate at d = 64 with one or two rounds, lane = row: a wave takes 64 consecutive
+// vectors (16 KB), turned round through LDS as the append does, rotates one per lane
+// (ar_rotate_row) and writes them back through LDS with whole-wave 16-byte stores.
+__global__ void __launch_bounds__(64 * AR_WAVES) rotate_rows_kernel(const int32_t *__restrict__ x, int32_t *y,
+                                                                   int n_vec, int rounds, RotSigns sg,
+                                                                   unsigned long long *range_err) {
+    __shared__ int32_t tile[AR_WAVES][64 * AR_STRIDE];
+    const int lane = threadIdx.x & 63, wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r0 = (blockIdx.x * AR_WAVES + wv) * 64;
+    if (r0 >= n_vec) return;
+    const int nr = n_vec - r0 < 64 ? n_vec - r0 : 64;
+    const int sub = lane >> 4, q4 = (lane & 15) * 4;
+    uint4 raw[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int r = 4 * i + sub < nr ? 4 * i + sub : nr - 1;
+        raw[i] = *(const uint4 *)(x + ((int64_t)r0 + r) * 64 + q4);
+    }
+    int32_t *T = tile[wv];
+    auto sync = [&]() {
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        int32_t *p = T + (4 * i + sub) * AR_STRIDE + q4;
+        *(uint2 *)p = make_uint2(raw[i].x, raw[i].y);
+        *(uint2 *)(p + 2) = make_uint2(raw[i].z, raw[i].w);
+    }
+    sync();
+    int32_t xi[64];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+        const uint2 u = *(const uint2 *)(T + lane * AR_STRIDE + 2 * j);
+        xi[2 * j] = (int32_t)u.x;
+        xi[2 * j + 1] = (int32_t)u.y;
+    }
+    sync();
+    int32_t xr[64];
+    double S;
+    ar_rotate_row<false>(xi, rounds, sg, lane < nr, x + (int64_t)r0 * 64, range_err, xr, S);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) *(uint2 *)(T + lane * AR_STRIDE + 2 * j) = make_uint2(xr[2 * j], xr[2 * j + 1]);
+    sync();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int r = 4 * i + sub;
+        if (r < nr) {
+            const int32_t *p = T + r * AR_STRIDE + q4;
+            const uint2 a = *(const uint2 *)p, b = *(const uint2 *)(p + 2);
+            *(uint4 *)(y + ((int64_t)r0 + r) * 64 + q4) = make_uint4(a.x, a.y, b.x, b.y);
+        }
+    }
+}
+
+hipError_t launch_rotate(hipStream_t s, const int32_t *x, int32_t *y, int64_t n_vec, int d,
+                         int rounds, const uint64_t (*signs)[2], unsigned long long *range_err) {
+    if (n_vec <= 0) return hipSuccess;
+    if (rounds > 2) return hipErrorInvalidValue;  // the kernel carries two sign diagonals
+    const RotSigns sg = rot_signs(rounds, signs);
+    // d = 64, one or two rounds, 16-byte aligned vectors, x and y apart: lane = row
+    if (d == 64 && rounds >= 1 && n_vec < 0x7fffffff - 64 && !(((uintptr_t)x | (uintptr_t)y) & 15) &&
+        (y + n_vec * 64 <= x || x + n_vec * 64 <= y)) {
+        const int waves = (int)((n_vec + 63) / 64);
+        hipLaunchKernelGGL(rotate_rows_kernel, dim3((unsigned)((waves + AR_WAVES - 1) / AR_WAVES)),
+                           dim3(64 * AR_WAVES), 0, s, x, y, (int)n_vec, rounds, sg, range_err);
+        return hipGetLastError();
+    }
+    dim3 grid((unsigned)n_vec), block(64);
+    if (d <= 64)
+        hipLaunchKernelGGL(rotate_kernel<1>, grid, block, 0, s, x, y, n_vec, d, rounds, sg, range_err);
+    else
+        hipLaunchKernelGGL(rotate_kernel<2>, grid, block, 0, s, x, y, n_vec, d, rounds, sg, range_err);
+    return hipGetLastError();
 }
 
 template <int KB, int VB, bool ROT>

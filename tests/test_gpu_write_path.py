@@ -182,3 +182,17 @@ def test_lane_row_append_batch_and_offsets(ctx):
         kr = rotate(seqk.reshape(-1, d), sg).reshape(m, 8, d)
         vr = rotate(seqv.reshape(-1, d), sg).reshape(m, 8, d)
         np.testing.assert_array_equal(_rows(c, b, m), pack(encode(kr, vr, f), f))
+
+
+@pytest.mark.parametrize("rounds", [1, 2])
+@pytest.mark.parametrize("n", [1, 63, 64, 65, 777])
+def test_lane_row_rotation_against_the_oracle(ctx, rounds, n):
+    # insitu_rotate at d = 64 runs rotate_rows_kernel (a row per lane, fp64 FWHT): every
+    # vector against the oracle's rotation wrapped to int32, on ordinary and extreme rows
+    # (values leaving int32, INT32_MIN/MAX entries, zero and one-channel rows)
+    from insitu_amd.rotate import Rotation
+    rng = np.random.default_rng(31 * rounds + n)
+    x = _extreme_rows(rng, n).reshape(-1, 64)[: max(n, 1)]
+    rot = Rotation.from_seed(64, 0, rounds)
+    want = _wrap32(rotate(x, signs_from_seed(64, 0, rounds)))
+    np.testing.assert_array_equal(rot.apply(x, ctx).cpu().numpy(), want)
